@@ -1,0 +1,135 @@
+// hale_device.h -- device-side helpers shared by the gfx950 kernels.
+//
+// Arithmetic follows Hale-Token's Rust CPU path bit for bit: every
+// translation unit is compiled with -ffp-contract=off (no fused
+// multiply-add), f32 division is correctly rounded, denormals are kept.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define HALE_EXPF_FN static __device__ __forceinline__
+#define HALE_EXPF_TABLE static __constant__ const
+#include "glibc_expf.h"
+
+namespace hale {
+
+constexpr int QK = 32;         // elements per quantization block
+constexpr int TILE = 32;       // rows per tile of the HBM weight layout
+constexpr int GROUP = 64;      // rows one wave covers (two tiles)
+constexpr int WAVE = 64;
+
+enum DType : int { F32 = 0, F16 = 1, BF16 = 2, Q8_0 = 3, Q4_0 = 4 };
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One q8 activation block as the kernels read it: the 32 codes and f32
+// scale of Q8Activations (src/tensor/quant.rs:69-93) plus the code sum used
+// by the q4 kernels (sum_j (n_j - 8) x_j = sum_j n_j x_j - 8 sum_j x_j).
+struct alignas(16) ActBlock {
+  int8_t q[QK];
+  float scale;
+  int32_t qsum;
+  int32_t pad[2];
+};
+static_assert(sizeof(ActBlock) == 48, "ActBlock is 48 bytes");
+
+// ---- scalar conversions -------------------------------------------------
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return (float)v;  // v_cvt_f32_f16: exact, keeps subnormals
+}
+
+__device__ __forceinline__ uint16_t f2h(float f) {
+  _Float16 v = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+  uint16_t h;
+  __builtin_memcpy(&h, &v, 2);
+  return h;
+}
+
+// Rust `v as i8`: saturating, NaN -> 0.
+__device__ __forceinline__ int sat_i8(float v) {
+  if (v != v) return 0;
+  if (v >= 127.0f) return 127;
+  if (v <= -128.0f) return -128;
+  return (int)v;
+}
+
+// Rust `v as i32`: saturating, NaN -> 0.
+__device__ __forceinline__ int sat_i32(float v) {
+  if (v != v) return 0;
+  if (v >= 2147483648.0f) return 2147483647;
+  if (v <= -2147483648.0f) return (int)0x80000000u;
+  return (int)v;
+}
+
+// silu, src/ops/activation.rs:5-7: x / (1 + exp(-x)).
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + hale_expf(-x)); }
+
+// f32::total_cmp as a signed integer key.
+__device__ __forceinline__ int total_key(float v) {
+  int b = __float_as_int(v);
+  return b ^ (int)(((unsigned)(b >> 31)) >> 1);
+}
+
+// ---- wave helpers ---------------------------------------------------------
+
+__device__ __forceinline__ float half_wave_max(float v) {
+  // 32-lane groups (lanes 0-31 and 32-63 reduce separately)
+  v = fmaxf(v, __shfl_xor(v, 16, 32));
+  v = fmaxf(v, __shfl_xor(v, 8, 32));
+  v = fmaxf(v, __shfl_xor(v, 4, 32));
+  v = fmaxf(v, __shfl_xor(v, 2, 32));
+  v = fmaxf(v, __shfl_xor(v, 1, 32));
+  return v;
+}
+
+__device__ __forceinline__ int half_wave_sum(int v) {
+  v += __shfl_xor(v, 16, 32);
+  v += __shfl_xor(v, 8, 32);
+  v += __shfl_xor(v, 4, 32);
+  v += __shfl_xor(v, 2, 32);
+  v += __shfl_xor(v, 1, 32);
+  return v;
+}
+
+// Quantizes one 32-element block held one value per lane of a 32-lane
+// group (Q8Activations::quantize, src/tensor/quant.rs:85-91).  The max is
+// order independent; the scale stays f32.  Returns the code of this lane.
+__device__ __forceinline__ int quant_block_lane(float v, float* scale_out, int* qsum_out) {
+  float amax = half_wave_max(fabsf(v));
+  float scale = amax / 127.0f;
+  float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  int q = sat_i8(roundf(v * inv));
+  *scale_out = scale;
+  *qsum_out = half_wave_sum(q);
+  return q;
+}
+
+// ---- weight layout ---------------------------------------------------------
+//
+// A quantized matrix [rows][cols] lives in HBM as two planes, rows padded to
+// a multiple of 64 (zero rows):
+//   codes : [rows/32][nb][CH][32 rows][16 B]   CH = 2 (q8_0) or 1 (q4_0)
+//   scales: [rows/32][nb][32 rows] f16
+// so the 16-byte chunks of one block for 32 consecutive rows are contiguous
+// (512 B).  The q4_0 chunk keeps the reference's nibble order: byte j holds
+// element j (low) and element j+16 (high).
+
+template <int DT> struct Layout;
+template <> struct Layout<Q8_0> { static constexpr int CH = 2; };
+template <> struct Layout<Q4_0> { static constexpr int CH = 1; };
+
+__host__ __device__ inline size_t padded_rows(size_t rows) { return (rows + 63) / 64 * 64; }
+
+__host__ __device__ inline size_t code_plane_bytes(int dtype, size_t rows, size_t cols) {
+  return padded_rows(rows) * (cols / QK) * (dtype == Q8_0 ? 32 : 16);
+}
+__host__ __device__ inline size_t scale_plane_bytes(size_t rows, size_t cols) {
+  return padded_rows(rows) * (cols / QK) * 2;
+}
+
+}  // namespace hale

@@ -1,0 +1,87 @@
+// kernels.h -- launch interface between the host runtime and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace hale {
+
+struct ActBlock;
+
+enum Epilogue : int { EPI_PLAIN = 0, EPI_GATE_UP = 1, EPI_COMBINE = 2 };
+
+// Arguments of the exact tile GEMV (kernels_decode.hip).  Expert e's planes
+// start at codes + e * codes_stride / scales + e * scales_stride; the
+// expert of slot s is route_idx[s] (expert 0 when route_idx is null).
+struct GemvArgs {
+  const uint8_t* codes;
+  const uint16_t* scales;
+  const uint8_t* codes2;   // up-projection planes (EPI_GATE_UP)
+  const uint16_t* scales2;
+  size_t codes_stride;     // bytes
+  size_t scales_stride;    // f16 elements
+  int nb;                  // quantization blocks per row
+  int rows;                // real rows (outputs beyond are not written)
+  const ActBlock* act;     // [slot][act_stride] activation blocks
+  int act_stride;          // 0: one activation shared by all slots
+  const int* route_idx;    // [slots]
+  const float* route_w;    // [slots] (EPI_COMBINE)
+  float* out;              // [rows]
+  float* ytmp;             // [slots][padded rows] (EPI_COMBINE)
+  unsigned* counters;      // [row groups], zero between launches (EPI_COMBINE)
+  ActBlock* hact;          // [slots][hact_stride] (EPI_GATE_UP)
+  int hact_stride;
+  int slots;
+};
+
+hipError_t launch_repack(int dtype, const uint8_t* aos, size_t rows, size_t cols, uint8_t* codes,
+                         uint16_t* scales, hipStream_t st);
+hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales, size_t rows,
+                         size_t cols, uint8_t* aos, hipStream_t st);
+hipError_t launch_encode(int dtype, const float* values, size_t nblocks, uint8_t* out,
+                         hipStream_t st);
+hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipStream_t st);
+hipError_t launch_route(const float* router, const float* logits_in, const float* x, int H, int E,
+                        int k, int normalize, int T, ActBlock* act, float* logits,
+                        unsigned* counters, int* route_idx, float* route_w,
+                        unsigned long long* stats, hipStream_t st);
+hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int slots,
+                       hipStream_t st);
+hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,
+                             size_t cols, int32_t* isums, hipStream_t st);
+hipError_t launch_fill(float* p, size_t n, float v, hipStream_t st);
+hipError_t launch_fill_normal(float* p, size_t n, uint64_t seed, float mean, float std,
+                              hipStream_t st);
+
+// Kernel kinds for per-kernel timing (hale_profile_*).
+enum KernelKind : int {
+  K_ROUTE = 0,
+  K_GATE_UP,
+  K_DOWN,
+  K_ACT_QUANT,
+  K_GEMV,
+  K_ENCODE,
+  K_REPACK,
+  K_FILL,
+  K_GROUP,
+  K_GROUPED_GATE_UP,
+  K_GROUPED_DOWN,
+  K_COMBINE,
+  K_KINDS
+};
+
+// Lets code outside the runtime bracket its launches for the profiler.
+struct LaunchHook {
+  void (*begin)(void* self, int kind) = nullptr;
+  void (*end)(void* self) = nullptr;
+  void* self = nullptr;
+  void on_begin(int kind) const {
+    if (begin) begin(self, kind);
+  }
+  void on_end() const {
+    if (end) end(self);
+  }
+};
+
+}  // namespace hale

@@ -1,0 +1,1169 @@
+// runtime.hip -- host runtime behind include/hale_moe.h.
+//
+// Owns device memory (weights repacked into the tile planes, per-layer
+// scratch), the context's stream and the error strings, and sequences the
+// kernels of kernels_decode.hip / kernels_prefill.hip.  Reference items are
+// cited per entry point in the public header.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/hale_moe.h"
+#include "hale_device.h"
+#include "kernels.h"
+#include "prefill.h"
+
+using namespace hale;
+
+// ---------------------------------------------------------------------------
+// handles
+// ---------------------------------------------------------------------------
+
+struct ProfRecord {
+  int kind;
+  hipEvent_t start, stop;
+};
+
+struct hale_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::recursive_mutex mu;
+  std::string err;
+  // scratch of the synchronous single-matrix / single-expert entry points
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  // wall timer
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  // per-kernel profiler
+  bool prof_on = false;
+  std::vector<hipEvent_t> ev_pool;
+  std::vector<ProfRecord> recs;
+  hipEvent_t open_start = nullptr;
+  int open_kind = -1;
+  double prof_ms[K_KINDS] = {};
+  uint64_t prof_n[K_KINDS] = {};
+};
+
+struct hale_graph {
+  hale_ctx* ctx = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+struct hale_matrix {
+  hale_ctx* ctx = nullptr;
+  int dtype = 0;
+  size_t rows = 0, cols = 0;
+  uint8_t* codes = nullptr;    // quantized: tile planes
+  uint16_t* scales = nullptr;
+  float* f32 = nullptr;        // F32: row-major copy
+};
+
+struct hale_moe {
+  hale_ctx* ctx = nullptr;
+  uint32_t layer = 0;
+  size_t E = 0, H = 0, I = 0, k = 0;
+  int dtype = 0;
+  int normalize = 0;
+  float* router = nullptr;  // [E][H] f32, or null
+  // resident experts, [E][plane]
+  uint8_t *gate_c = nullptr, *up_c = nullptr, *down_c = nullptr;
+  uint16_t *gate_s = nullptr, *up_s = nullptr, *down_s = nullptr;
+  size_t gc_bytes = 0, gs_elems = 0, dc_bytes = 0, ds_elems = 0;
+  std::vector<char> present;
+  unsigned long long* stats = nullptr;  // [E] routing counts
+  // decode scratch
+  ActBlock* act = nullptr;  // [cap_tok][H/32]
+  float* logits = nullptr;  // [cap_tok][E]
+  unsigned* tok_counters = nullptr;  // [cap_tok]
+  int* route_idx = nullptr;  // [cap_tok][k]
+  float* route_w = nullptr;  // [cap_tok][k]
+  ActBlock* hact = nullptr;  // [k][I/32]
+  float* ytmp = nullptr;     // [k][padded H]
+  unsigned* grp_counters = nullptr;  // [padded H / 64]
+  size_t cap_tok = 0;
+  // grouped prefill workspace
+  PrefillWorkspace pw;
+};
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+
+static thread_local std::string g_create_err;
+
+static int fail(hale_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c)
+    c->err = buf;
+  else
+    g_create_err = buf;
+  return code;
+}
+
+#define HIPCHK(ctx, call)                                                                  \
+  do {                                                                                     \
+    hipError_t e_ = (call);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      return fail((ctx), HALE_EHIP, "%s failed: %s", #call, hipGetErrorString(e_));        \
+  } while (0)
+
+static bool quantized(int dtype) { return dtype == HALE_Q8_0 || dtype == HALE_Q4_0; }
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+
+extern "C" int hale_ctx_create(int device, hale_ctx** out) {
+  if (!out) return fail(nullptr, HALE_EINVAL, "hale_ctx_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return fail(nullptr, HALE_EHIP, "no HIP device available (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n) return fail(nullptr, HALE_EINVAL, "device %d of %d", device, n);
+  hale_ctx* c = new (std::nothrow) hale_ctx;
+  if (!c) return fail(nullptr, HALE_ENOMEM, "out of host memory");
+  c->device = device;
+  if ((e = hipSetDevice(device)) != hipSuccess ||
+      (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+    delete c;
+    return fail(nullptr, HALE_EHIP, "stream creation failed: %s", hipGetErrorString(e));
+  }
+  *out = c;
+  return HALE_OK;
+}
+
+extern "C" void hale_ctx_destroy(hale_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  if (c->scratch) (void)hipFree(c->scratch);
+  for (auto& r : c->recs) {
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
+  if (c->t0) (void)hipEventDestroy(c->t0);
+  if (c->t1) (void)hipEventDestroy(c->t1);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+extern "C" const char* hale_last_error(const hale_ctx* c) {
+  return c ? c->err.c_str() : g_create_err.c_str();
+}
+
+extern "C" void* hale_ctx_stream(hale_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+extern "C" int hale_ctx_synchronize(hale_ctx* c) {
+  if (!c) return HALE_EINVAL;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// Grows the context scratch to at least `bytes` (synchronous).
+static int ctx_scratch(hale_ctx* c, size_t bytes, void** p) {
+  if (c->scratch_bytes < bytes) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (c->scratch) (void)hipFree(c->scratch);
+    c->scratch = nullptr;
+    c->scratch_bytes = 0;
+    if (hipMalloc(&c->scratch, bytes) != hipSuccess)
+      return fail(c, HALE_ENOMEM, "device scratch of %zu bytes", bytes);
+    c->scratch_bytes = bytes;
+  }
+  *p = c->scratch;
+  return HALE_OK;
+}
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---------------------------------------------------------------------------
+// per-kernel profiler (events on the context's stream around each launch)
+// ---------------------------------------------------------------------------
+
+static hipEvent_t prof_event(hale_ctx* c) {
+  if (!c->ev_pool.empty()) {
+    hipEvent_t e = c->ev_pool.back();
+    c->ev_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+static void prof_begin(hale_ctx* c, int kind) {
+  if (!c->prof_on) return;
+  hipEvent_t e = prof_event(c);
+  if (!e) return;
+  (void)hipEventRecord(e, c->stream);
+  c->open_start = e;
+  c->open_kind = kind;
+}
+
+static void prof_end(hale_ctx* c) {
+  if (!c->prof_on || !c->open_start) return;
+  hipEvent_t e = prof_event(c);
+  if (!e) return;
+  (void)hipEventRecord(e, c->stream);
+  c->recs.push_back({c->open_kind, c->open_start, e});
+  c->open_start = nullptr;
+}
+
+static void hook_begin(void* self, int kind) { prof_begin((hale_ctx*)self, kind); }
+static void hook_end(void* self) { prof_end((hale_ctx*)self); }
+
+static LaunchHook ctx_hook(hale_ctx* c) {
+  LaunchHook h;
+  h.begin = hook_begin;
+  h.end = hook_end;
+  h.self = c;
+  return h;
+}
+
+// Launches `call` (returning hipError_t) bracketed for the profiler.
+#define LAUNCH(ctx, kind, call)   \
+  do {                            \
+    prof_begin((ctx), (kind));    \
+    hipError_t le_ = (call);      \
+    prof_end((ctx));              \
+    HIPCHK((ctx), le_);           \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// geometry
+// ---------------------------------------------------------------------------
+
+extern "C" size_t hale_block_bytes(int dtype) {
+  switch (dtype) {
+    case HALE_F32: return 4;
+    case HALE_F16:
+    case HALE_BF16: return 2;
+    case HALE_Q8_0: return 34;
+    case HALE_Q4_0: return 18;
+    default: return 0;
+  }
+}
+
+extern "C" long long hale_row_bytes(int dtype, size_t cols) {
+  size_t bb = hale_block_bytes(dtype);
+  if (bb == 0) return -1;
+  size_t bl = quantized(dtype) ? HALE_QK : 1;
+  if (cols % bl) return -1;
+  return (long long)(cols / bl * bb);
+}
+
+// ---------------------------------------------------------------------------
+// matrices
+// ---------------------------------------------------------------------------
+
+static int matrix_create(hale_ctx* c, int dtype, size_t rows, size_t cols, const void* bytes,
+                         size_t nbytes, bool on_device, hale_matrix** out) {
+  if (!c || !out) return fail(c, HALE_EINVAL, "matrix upload: NULL argument");
+  *out = nullptr;
+  if (dtype != HALE_F32 && !quantized(dtype))
+    return fail(c, HALE_EINVAL, "matrix upload: dtype %d not supported (q8_0, q4_0, f32)", dtype);
+  long long rb = hale_row_bytes(dtype, cols);
+  if (rb < 0) return fail(c, HALE_EINVAL, "dtype %d needs row length divisible by 32, got %zu", dtype, cols);
+  if (nbytes != rows * (size_t)rb)
+    return fail(c, HALE_EINVAL, "matrix %zux%zu needs %zu bytes, got %zu", rows, cols,
+                rows * (size_t)rb, nbytes);
+  if (rows == 0 || cols == 0) return fail(c, HALE_EINVAL, "empty matrix %zux%zu", rows, cols);
+  if (!bytes) return fail(c, HALE_EINVAL, "matrix upload: bytes is NULL");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  hale_matrix* m = new (std::nothrow) hale_matrix;
+  if (!m) return fail(c, HALE_ENOMEM, "out of host memory");
+  m->ctx = c;
+  m->dtype = dtype;
+  m->rows = rows;
+  m->cols = cols;
+  hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  if (dtype == HALE_F32) {
+    if (hipMalloc(&m->f32, nbytes) != hipSuccess) {
+      delete m;
+      return fail(c, HALE_ENOMEM, "device allocation of %zu bytes", nbytes);
+    }
+    hipError_t e = hipMemcpyAsync(m->f32, bytes, nbytes, kind, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+      (void)hipFree(m->f32);
+      delete m;
+      return fail(c, HALE_EHIP, "upload: %s", hipGetErrorString(e));
+    }
+    *out = m;
+    return HALE_OK;
+  }
+  size_t cb = code_plane_bytes(dtype, rows, cols), sb = scale_plane_bytes(rows, cols);
+  uint8_t* staging = nullptr;
+  hipError_t e = hipMalloc(&m->codes, cb);
+  if (e == hipSuccess) e = hipMalloc(&m->scales, sb);
+  if (e == hipSuccess && !on_device) e = hipMalloc(&staging, nbytes);
+  if (e != hipSuccess) {
+    (void)hipFree(m->codes);
+    (void)hipFree(m->scales);
+    (void)hipFree(staging);
+    delete m;
+    return fail(c, HALE_ENOMEM, "device allocation for a %zux%zu matrix", rows, cols);
+  }
+  const uint8_t* src = (const uint8_t*)bytes;
+  if (!on_device) {
+    e = hipMemcpyAsync(staging, bytes, nbytes, hipMemcpyHostToDevice, c->stream);
+    src = staging;
+  }
+  if (e == hipSuccess) e = launch_repack(dtype, src, rows, cols, m->codes, m->scales, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  (void)hipFree(staging);
+  if (e != hipSuccess) {
+    (void)hipFree(m->codes);
+    (void)hipFree(m->scales);
+    delete m;
+    return fail(c, HALE_EHIP, "upload/repack: %s", hipGetErrorString(e));
+  }
+  *out = m;
+  return HALE_OK;
+}
+
+extern "C" int hale_matrix_upload(hale_ctx* c, int dtype, size_t rows, size_t cols,
+                                  const void* bytes, size_t nbytes, hale_matrix** out) {
+  return matrix_create(c, dtype, rows, cols, bytes, nbytes, false, out);
+}
+
+extern "C" int hale_matrix_upload_device(hale_ctx* c, int dtype, size_t rows, size_t cols,
+                                         const void* d_bytes, size_t nbytes, hale_matrix** out) {
+  return matrix_create(c, dtype, rows, cols, d_bytes, nbytes, true, out);
+}
+
+extern "C" void hale_matrix_destroy(hale_matrix* m) {
+  if (!m) return;
+  std::lock_guard<std::recursive_mutex> g(m->ctx->mu);
+  (void)hipSetDevice(m->ctx->device);
+  (void)hipStreamSynchronize(m->ctx->stream);
+  (void)hipFree(m->codes);
+  (void)hipFree(m->scales);
+  (void)hipFree(m->f32);
+  delete m;
+}
+
+extern "C" int hale_matrix_shape(const hale_matrix* m, int* dtype, size_t* rows, size_t* cols) {
+  if (!m) return HALE_EINVAL;
+  if (dtype) *dtype = m->dtype;
+  if (rows) *rows = m->rows;
+  if (cols) *cols = m->cols;
+  return HALE_OK;
+}
+
+extern "C" int hale_matrix_download(hale_ctx* c, const hale_matrix* m, void* bytes, size_t nbytes) {
+  if (!c || !m || !bytes) return fail(c, HALE_EINVAL, "matrix download: NULL argument");
+  size_t need = m->rows * (size_t)hale_row_bytes(m->dtype, m->cols);
+  if (nbytes != need) return fail(c, HALE_EINVAL, "matrix download needs %zu bytes, got %zu", need, nbytes);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  if (m->dtype == HALE_F32) {
+    HIPCHK(c, hipMemcpyAsync(bytes, m->f32, nbytes, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return HALE_OK;
+  }
+  void* tmp;
+  int rc = ctx_scratch(c, nbytes, &tmp);
+  if (rc) return rc;
+  LAUNCH(c, K_REPACK, launch_unpack(m->dtype, m->codes, m->scales, m->rows, m->cols, (uint8_t*)tmp, c->stream));
+  HIPCHK(c, hipMemcpyAsync(bytes, tmp, nbytes, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// quantization
+// ---------------------------------------------------------------------------
+
+extern "C" int hale_quantize_q8_act(hale_ctx* c, const float* x, size_t n, float* scales,
+                                    int8_t* quants) {
+  if (!c || !x || !scales || !quants) return fail(c, HALE_EINVAL, "quantize: NULL argument");
+  if (n % HALE_QK) return fail(c, HALE_EINVAL, "activation length must be a multiple of 32, got %zu", n);
+  if (n == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t nb = n / HALE_QK;
+  size_t xoff = 0, aoff = align_up(n * 4, 256);
+  void* s;
+  int rc = ctx_scratch(c, aoff + nb * sizeof(ActBlock), &s);
+  if (rc) return rc;
+  float* dx = (float*)((char*)s + xoff);
+  ActBlock* act = (ActBlock*)((char*)s + aoff);
+  HIPCHK(c, hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nb, act, c->stream));
+  std::vector<ActBlock> h(nb);
+  HIPCHK(c, hipMemcpyAsync(h.data(), act, nb * sizeof(ActBlock), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  for (size_t b = 0; b < nb; b++) {
+    scales[b] = h[b].scale;
+    memcpy(quants + b * HALE_QK, h[b].q, HALE_QK);
+  }
+  return HALE_OK;
+}
+
+static int encode_check(hale_ctx* c, int dtype, size_t rows, size_t cols) {
+  if (!quantized(dtype)) return fail(c, HALE_EINVAL, "encode: dtype %d is not q8_0/q4_0", dtype);
+  if (cols % HALE_QK) return fail(c, HALE_EINVAL, "encode: row length %zu not a multiple of 32", cols);
+  (void)rows;
+  return HALE_OK;
+}
+
+extern "C" int hale_encode_rows_device(hale_ctx* c, int dtype, size_t rows, size_t cols,
+                                       const float* d_values, void* d_bytes) {
+  if (!c || !d_values || !d_bytes) return fail(c, HALE_EINVAL, "encode: NULL argument");
+  int rc = encode_check(c, dtype, rows, cols);
+  if (rc) return rc;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  LAUNCH(c, K_ENCODE, launch_encode(dtype, d_values, rows * (cols / HALE_QK), (uint8_t*)d_bytes, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_encode_rows(hale_ctx* c, int dtype, size_t rows, size_t cols,
+                                const float* values, void* bytes) {
+  if (!c || !values || !bytes) return fail(c, HALE_EINVAL, "encode: NULL argument");
+  int rc = encode_check(c, dtype, rows, cols);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t nin = rows * cols * 4, nout = rows * (size_t)hale_row_bytes(dtype, cols);
+  void* s;
+  rc = ctx_scratch(c, align_up(nin, 256) + nout, &s);
+  if (rc) return rc;
+  float* dv = (float*)s;
+  uint8_t* db = (uint8_t*)s + align_up(nin, 256);
+  HIPCHK(c, hipMemcpyAsync(dv, values, nin, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_ENCODE, launch_encode(dtype, dv, rows * (cols / HALE_QK), db, c->stream));
+  HIPCHK(c, hipMemcpyAsync(bytes, db, nout, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// matvec
+// ---------------------------------------------------------------------------
+
+static GemvArgs plain_args(const hale_matrix* m, const ActBlock* act, float* out) {
+  GemvArgs a{};
+  a.codes = m->codes;
+  a.scales = m->scales;
+  a.nb = (int)(m->cols / HALE_QK);
+  a.rows = (int)m->rows;
+  a.act = act;
+  a.out = out;
+  a.slots = 1;
+  return a;
+}
+
+// Enqueues out = m x for device x/out.  F32 matrices use the router kernel's
+// 8-lane dot (one work-group per row, logits-only mode is not needed here).
+static int matvec_enqueue(hale_ctx* c, const hale_matrix* m, const float* dx, float* dout,
+                          ActBlock* act) {
+  if (m->dtype == HALE_F32)
+    return fail(c, HALE_EINVAL, "matvec on f32 matrices is not part of the quantized path");
+  size_t nb = m->cols / HALE_QK;
+  LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nb, act, c->stream));
+  GemvArgs a = plain_args(m, act, dout);
+  LAUNCH(c, K_GEMV, launch_gemv(m->dtype, EPI_PLAIN, a, (int)(padded_rows(m->rows) / 64), 1, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_matvec(hale_ctx* c, const hale_matrix* m, const float* x, size_t xlen,
+                           float* out, size_t outlen) {
+  if (!c || !m || !x || !out) return fail(c, HALE_EINVAL, "matvec: NULL argument");
+  if (xlen != m->cols) return fail(c, HALE_EINVAL, "matvec input length %zu != cols %zu", xlen, m->cols);
+  if (outlen != m->rows) return fail(c, HALE_EINVAL, "matvec output length %zu != rows %zu", outlen, m->rows);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t nb = m->cols / HALE_QK;
+  size_t o1 = align_up(xlen * 4, 256), o2 = o1 + align_up(outlen * 4, 256);
+  void* s;
+  int rc = ctx_scratch(c, o2 + nb * sizeof(ActBlock), &s);
+  if (rc) return rc;
+  float* dx = (float*)s;
+  float* dout = (float*)((char*)s + o1);
+  ActBlock* act = (ActBlock*)((char*)s + o2);
+  HIPCHK(c, hipMemcpyAsync(dx, x, xlen * 4, hipMemcpyHostToDevice, c->stream));
+  rc = matvec_enqueue(c, m, dx, dout, act);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync(out, dout, outlen * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_matvec_device(hale_ctx* c, const hale_matrix* m, const float* d_x, float* d_out) {
+  if (!c || !m || !d_x || !d_out) return fail(c, HALE_EINVAL, "matvec: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  void* s;
+  int rc = ctx_scratch(c, (m->cols / HALE_QK) * sizeof(ActBlock), &s);
+  if (rc) return rc;
+  return matvec_enqueue(c, m, d_x, d_out, (ActBlock*)s);
+}
+
+extern "C" int hale_matvec_block_sums(hale_ctx* c, const hale_matrix* m, const float* x,
+                                      size_t xlen, int32_t* isums) {
+  if (!c || !m || !x || !isums) return fail(c, HALE_EINVAL, "block_sums: NULL argument");
+  if (!quantized(m->dtype)) return fail(c, HALE_EINVAL, "block sums need a quantized matrix");
+  if (xlen != m->cols) return fail(c, HALE_EINVAL, "input length %zu != cols %zu", xlen, m->cols);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t nb = m->cols / HALE_QK;
+  size_t n = m->rows * nb;
+  size_t o1 = align_up(xlen * 4, 256), o2 = o1 + align_up(nb * sizeof(ActBlock), 256);
+  void* s;
+  int rc = ctx_scratch(c, o2 + n * 4, &s);
+  if (rc) return rc;
+  float* dx = (float*)s;
+  ActBlock* act = (ActBlock*)((char*)s + o1);
+  int32_t* dsum = (int32_t*)((char*)s + o2);
+  HIPCHK(c, hipMemcpyAsync(dx, x, xlen * 4, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nb, act, c->stream));
+  LAUNCH(c, K_GEMV, launch_block_sums(m->dtype, m->codes, act, m->rows, m->cols, dsum, c->stream));
+  HIPCHK(c, hipMemcpyAsync(isums, dsum, n * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// expert
+// ---------------------------------------------------------------------------
+
+extern "C" int hale_expert_forward(hale_ctx* c, const hale_matrix* gate, const hale_matrix* up,
+                                   const hale_matrix* down, const float* x, float* out) {
+  if (!c || !gate || !up || !down || !x || !out) return fail(c, HALE_EINVAL, "expert_forward: NULL argument");
+  if (!quantized(gate->dtype) || gate->dtype != up->dtype || gate->dtype != down->dtype)
+    return fail(c, HALE_EINVAL, "expert matrices must share one quantized dtype");
+  size_t I = gate->rows, H = gate->cols;
+  if (up->rows != I || up->cols != H || down->rows != H || down->cols != I)
+    return fail(c, HALE_EINVAL, "expert shapes: gate %zux%zu up %zux%zu down %zux%zu", gate->rows,
+                gate->cols, up->rows, up->cols, down->rows, down->cols);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t nbh = H / HALE_QK, nbi = I / HALE_QK;
+  size_t o1 = align_up(H * 4, 256), o2 = o1 + align_up(H * 4, 256);
+  size_t o3 = o2 + align_up(nbh * sizeof(ActBlock), 256);
+  void* s;
+  int rc = ctx_scratch(c, o3 + nbi * sizeof(ActBlock), &s);
+  if (rc) return rc;
+  float* dx = (float*)s;
+  float* dout = (float*)((char*)s + o1);
+  ActBlock* act = (ActBlock*)((char*)s + o2);
+  ActBlock* hact = (ActBlock*)((char*)s + o3);
+  HIPCHK(c, hipMemcpyAsync(dx, x, H * 4, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nbh, act, c->stream));
+  GemvArgs a{};
+  a.codes = gate->codes;
+  a.scales = gate->scales;
+  a.codes2 = up->codes;
+  a.scales2 = up->scales;
+  a.nb = (int)nbh;
+  a.rows = (int)I;
+  a.act = act;
+  a.hact = hact;
+  a.hact_stride = (int)nbi;
+  a.slots = 1;
+  LAUNCH(c, K_GATE_UP, launch_gemv(gate->dtype, EPI_GATE_UP, a, (int)nbi, 1, c->stream));
+  GemvArgs d = plain_args(down, hact, dout);
+  LAUNCH(c, K_DOWN, launch_gemv(down->dtype, EPI_PLAIN, d, (int)(padded_rows(H) / 64), 1, c->stream));
+  HIPCHK(c, hipMemcpyAsync(out, dout, H * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MoE layer
+// ---------------------------------------------------------------------------
+
+static void moe_free_scratch(hale_moe* m) {
+  (void)hipFree(m->act);
+  (void)hipFree(m->logits);
+  (void)hipFree(m->tok_counters);
+  (void)hipFree(m->route_idx);
+  (void)hipFree(m->route_w);
+  m->act = nullptr;
+  m->logits = nullptr;
+  m->tok_counters = nullptr;
+  m->route_idx = nullptr;
+  m->route_w = nullptr;
+  m->cap_tok = 0;
+}
+
+// Per-token scratch for ntok tokens; counters are zeroed once here and the
+// kernels leave them zero.
+static int moe_reserve(hale_moe* m, size_t ntok) {
+  hale_ctx* c = m->ctx;
+  if (m->cap_tok >= ntok) return HALE_OK;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  moe_free_scratch(m);
+  size_t nbh = m->H / HALE_QK;
+  hipError_t e = hipMalloc(&m->act, ntok * nbh * sizeof(ActBlock));
+  if (e == hipSuccess) e = hipMalloc(&m->logits, ntok * m->E * 4);
+  if (e == hipSuccess) e = hipMalloc(&m->tok_counters, ntok * 4);
+  if (e == hipSuccess) e = hipMalloc(&m->route_idx, ntok * m->k * 4);
+  if (e == hipSuccess) e = hipMalloc(&m->route_w, ntok * m->k * 4);
+  if (e == hipSuccess) e = hipMemsetAsync(m->tok_counters, 0, ntok * 4, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    moe_free_scratch(m);
+    return fail(c, HALE_ENOMEM, "MoE scratch for %zu tokens: %s", ntok, hipGetErrorString(e));
+  }
+  m->cap_tok = ntok;
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, size_t I, int dtype,
+                               size_t top_k, int normalize, const hale_matrix* router,
+                               hale_moe** out) {
+  if (!c || !out) return fail(c, HALE_EINVAL, "moe_create: NULL argument");
+  *out = nullptr;
+  if (!quantized(dtype)) return fail(c, HALE_EINVAL, "expert dtype %d is not q8_0/q4_0", dtype);
+  if (E == 0 || E > 1024) return fail(c, HALE_EINVAL, "num_experts %zu outside 1..1024", E);
+  if (H == 0 || I == 0 || H % HALE_QK || I % HALE_QK)
+    return fail(c, HALE_EINVAL, "hidden %zu / inter %zu must be non-zero multiples of 32", H, I);
+  if (H > 8192) return fail(c, HALE_EINVAL, "hidden %zu above 8192", H);
+  if (std::min(top_k, E) > 64) return fail(c, HALE_EINVAL, "top_k %zu above 64", top_k);
+  if (router && (router->dtype != HALE_F32 || router->rows != E || router->cols != H))
+    return fail(c, HALE_EINVAL, "router must be f32 [%zu x %zu]", E, H);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  hale_moe* m = new (std::nothrow) hale_moe;
+  if (!m) return fail(c, HALE_ENOMEM, "out of host memory");
+  m->ctx = c;
+  m->layer = layer;
+  m->E = E;
+  m->H = H;
+  m->I = I;
+  m->k = std::min(top_k, E);  // top_k clamps k to the number of scores
+  m->dtype = dtype;
+  m->normalize = normalize;
+  m->gc_bytes = code_plane_bytes(dtype, I, H);
+  m->gs_elems = scale_plane_bytes(I, H) / 2;
+  m->dc_bytes = code_plane_bytes(dtype, H, I);
+  m->ds_elems = scale_plane_bytes(H, I) / 2;
+  m->present.assign(E, 0);
+  size_t hp = padded_rows(H);
+  hipError_t e = hipSuccess;
+#define ALLOC(p, n) \
+  if (e == hipSuccess) e = hipMalloc(&(p), (n))
+  ALLOC(m->gate_c, E * m->gc_bytes);
+  ALLOC(m->up_c, E * m->gc_bytes);
+  ALLOC(m->down_c, E * m->dc_bytes);
+  ALLOC(m->gate_s, E * m->gs_elems * 2);
+  ALLOC(m->up_s, E * m->gs_elems * 2);
+  ALLOC(m->down_s, E * m->ds_elems * 2);
+  ALLOC(m->stats, E * 8);
+  ALLOC(m->hact, std::max<size_t>(m->k, 1) * (I / HALE_QK) * sizeof(ActBlock));
+  ALLOC(m->ytmp, std::max<size_t>(m->k, 1) * hp * 4);
+  ALLOC(m->grp_counters, (hp / 64) * 4);
+  if (router) ALLOC(m->router, E * H * 4);
+#undef ALLOC
+  if (e == hipSuccess) e = hipMemsetAsync(m->stats, 0, E * 8, c->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(m->grp_counters, 0, (hp / 64) * 4, c->stream);
+  if (e == hipSuccess && router)
+    e = hipMemcpyAsync(m->router, router->f32, E * H * 4, hipMemcpyDeviceToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    hale_moe_destroy(m);
+    return fail(c, HALE_ENOMEM, "MoE layer allocation (%zu experts): %s", E, hipGetErrorString(e));
+  }
+  *out = m;
+  return HALE_OK;
+}
+
+extern "C" void hale_moe_destroy(hale_moe* m) {
+  if (!m) return;
+  hale_ctx* c = m->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  moe_free_scratch(m);
+  prefill_free(m->pw);
+  (void)hipFree(m->gate_c);
+  (void)hipFree(m->up_c);
+  (void)hipFree(m->down_c);
+  (void)hipFree(m->gate_s);
+  (void)hipFree(m->up_s);
+  (void)hipFree(m->down_s);
+  (void)hipFree(m->stats);
+  (void)hipFree(m->hact);
+  (void)hipFree(m->ytmp);
+  (void)hipFree(m->grp_counters);
+  (void)hipFree(m->router);
+  delete m;
+}
+
+static int set_expert(hale_moe* m, uint32_t e, const void* gate, const void* up, const void* down,
+                      size_t ng, size_t nd, bool on_device) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !gate || !up || !down) return fail(c, HALE_EINVAL, "set_expert: NULL argument");
+  if (e >= m->E) return fail(c, HALE_EINVAL, "expert %u of %zu", e, m->E);
+  size_t need_g = m->I * (size_t)hale_row_bytes(m->dtype, m->H);
+  size_t need_d = m->H * (size_t)hale_row_bytes(m->dtype, m->I);
+  if (ng != need_g || nd != need_d)
+    return fail(c, HALE_EINVAL, "expert bytes gate/up %zu (need %zu), down %zu (need %zu)", ng,
+                need_g, nd, need_d);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  const uint8_t *sg = (const uint8_t*)gate, *su = (const uint8_t*)up, *sd = (const uint8_t*)down;
+  if (!on_device) {
+    void* s;
+    int rc = ctx_scratch(c, 2 * align_up(need_g, 256) + need_d, &s);
+    if (rc) return rc;
+    uint8_t* b = (uint8_t*)s;
+    HIPCHK(c, hipMemcpyAsync(b, gate, need_g, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(b + align_up(need_g, 256), up, need_g, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(b + 2 * align_up(need_g, 256), down, need_d, hipMemcpyHostToDevice, c->stream));
+    sg = b;
+    su = b + align_up(need_g, 256);
+    sd = b + 2 * align_up(need_g, 256);
+  }
+  LAUNCH(c, K_REPACK, launch_repack(m->dtype, sg, m->I, m->H, m->gate_c + e * m->gc_bytes, m->gate_s + e * m->gs_elems, c->stream));
+  LAUNCH(c, K_REPACK, launch_repack(m->dtype, su, m->I, m->H, m->up_c + e * m->gc_bytes, m->up_s + e * m->gs_elems, c->stream));
+  LAUNCH(c, K_REPACK, launch_repack(m->dtype, sd, m->H, m->I, m->down_c + e * m->dc_bytes, m->down_s + e * m->ds_elems, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  m->present[e] = 1;
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_set_expert(hale_moe* m, uint32_t e, const void* gate, const void* up,
+                                   const void* down, size_t ng, size_t nd) {
+  return set_expert(m, e, gate, up, down, ng, nd, false);
+}
+
+extern "C" int hale_moe_set_expert_device(hale_moe* m, uint32_t e, const void* gate, const void* up,
+                                          const void* down, size_t ng, size_t nd) {
+  return set_expert(m, e, gate, up, down, ng, nd, true);
+}
+
+extern "C" int hale_moe_set_expert_matrices(hale_moe* m, uint32_t e, const hale_matrix* gate,
+                                            const hale_matrix* up, const hale_matrix* down) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !gate || !up || !down) return fail(c, HALE_EINVAL, "set_expert: NULL argument");
+  if (e >= m->E) return fail(c, HALE_EINVAL, "expert %u of %zu", e, m->E);
+  for (const hale_matrix* x : {gate, up, down})
+    if (x->dtype != m->dtype) return fail(c, HALE_EINVAL, "expert dtype %d != layer dtype %d", x->dtype, m->dtype);
+  if (gate->rows != m->I || gate->cols != m->H || up->rows != m->I || up->cols != m->H ||
+      down->rows != m->H || down->cols != m->I)
+    return fail(c, HALE_EINVAL, "expert shapes do not match the layer");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  // identical padded geometry, so the planes copy as they are
+  HIPCHK(c, hipMemcpyAsync(m->gate_c + e * m->gc_bytes, gate->codes, m->gc_bytes, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(m->up_c + e * m->gc_bytes, up->codes, m->gc_bytes, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(m->down_c + e * m->dc_bytes, down->codes, m->dc_bytes, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(m->gate_s + e * m->gs_elems, gate->scales, m->gs_elems * 2, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(m->up_s + e * m->gs_elems, up->scales, m->gs_elems * 2, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(m->down_s + e * m->ds_elems, down->scales, m->ds_elems * 2, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  m->present[e] = 1;
+  return HALE_OK;
+}
+
+static int check_all_present(hale_moe* m) {
+  for (size_t e = 0; e < m->E; e++)
+    if (!m->present[e])
+      return fail(m->ctx, HALE_ENOTFOUND, "expert L%uE%zu is not registered", m->layer, e);
+  return HALE_OK;
+}
+
+// Enqueues the decode path for ntok tokens (token t's route in slot range
+// [t*k, t*k+k)).  x/logits/out are device pointers.
+static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
+                              float* dout) {
+  hale_ctx* c = m->ctx;
+  const int k = (int)m->k;
+  const size_t nbh = m->H / HALE_QK, nbi = m->I / HALE_QK;
+  if (!m->router && !dlogits) return fail(c, HALE_EINVAL, "layer has no router: logits are required");
+  LAUNCH(c, K_ROUTE, launch_route(dlogits ? nullptr : m->router, dlogits, dx, (int)m->H, (int)m->E, k,
+                         m->normalize, (int)ntok, m->act, m->logits, m->tok_counters, m->route_idx,
+                         m->route_w, m->stats, c->stream));
+  for (size_t t = 0; t < ntok; t++) {
+    float* out_t = dout + t * m->H;
+    if (k == 0) {
+      LAUNCH(c, K_FILL, launch_fill(out_t, m->H, 0.0f, c->stream));
+      continue;
+    }
+    GemvArgs a{};
+    a.codes = m->gate_c;
+    a.scales = m->gate_s;
+    a.codes2 = m->up_c;
+    a.scales2 = m->up_s;
+    a.codes_stride = m->gc_bytes;
+    a.scales_stride = m->gs_elems;
+    a.nb = (int)nbh;
+    a.rows = (int)m->I;
+    a.act = m->act + t * nbh;
+    a.act_stride = 0;
+    a.route_idx = m->route_idx + t * k;
+    a.hact = m->hact;
+    a.hact_stride = (int)nbi;
+    a.slots = k;
+    LAUNCH(c, K_GATE_UP, launch_gemv(m->dtype, EPI_GATE_UP, a, (int)nbi, k, c->stream));
+    GemvArgs d{};
+    d.codes = m->down_c;
+    d.scales = m->down_s;
+    d.codes_stride = m->dc_bytes;
+    d.scales_stride = m->ds_elems;
+    d.nb = (int)nbi;
+    d.rows = (int)m->H;
+    d.act = m->hact;
+    d.act_stride = (int)nbi;
+    d.route_idx = m->route_idx + t * k;
+    d.route_w = m->route_w + t * k;
+    d.out = out_t;
+    d.ytmp = m->ytmp;
+    d.counters = m->grp_counters;
+    d.slots = k;
+    LAUNCH(c, K_DOWN, launch_gemv(m->dtype, EPI_COMBINE, d, (int)(padded_rows(m->H) / 64), k, c->stream));
+  }
+  return HALE_OK;
+}
+
+static PrefillLayer prefill_layer(hale_moe* m) {
+  PrefillLayer L{};
+  L.dtype = m->dtype;
+  L.E = (int)m->E;
+  L.H = (int)m->H;
+  L.I = (int)m->I;
+  L.k = (int)m->k;
+  L.normalize = m->normalize;
+  L.router = m->router;
+  L.gate_c = m->gate_c;
+  L.up_c = m->up_c;
+  L.down_c = m->down_c;
+  L.gate_s = m->gate_s;
+  L.up_s = m->up_s;
+  L.down_s = m->down_s;
+  L.gc_bytes = m->gc_bytes;
+  L.gs_elems = m->gs_elems;
+  L.dc_bytes = m->dc_bytes;
+  L.ds_elems = m->ds_elems;
+  L.act = m->act;
+  L.logits = m->logits;
+  L.tok_counters = m->tok_counters;
+  L.route_idx = m->route_idx;
+  L.route_w = m->route_w;
+  L.stats = m->stats;
+  return L;
+}
+
+static int moe_forward_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
+                               float* dout) {
+  int rc = check_all_present(m);
+  if (rc) return rc;
+  rc = moe_reserve(m, ntok);
+  if (rc) return rc;
+  if (ntok >= prefill_min_tokens(m->k)) {
+    if (!m->router && !dlogits)
+      return fail(m->ctx, HALE_EINVAL, "layer has no router: logits are required");
+    PrefillLayer L = prefill_layer(m);
+    hipError_t e = prefill_enqueue(L, m->pw, ntok, dx, dlogits, dout, m->ctx->stream,
+                                   ctx_hook(m->ctx));
+    if (e != hipSuccess) return fail(m->ctx, HALE_EHIP, "grouped prefill: %s", hipGetErrorString(e));
+    return HALE_OK;
+  }
+  return moe_decode_enqueue(m, ntok, dx, dlogits, dout);
+}
+
+extern "C" int hale_moe_forward_device(hale_moe* m, size_t ntok, const float* d_x,
+                                       const float* d_logits, float* d_out, uint32_t* d_index,
+                                       float* d_weight) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !d_x || !d_out) return fail(c, HALE_EINVAL, "moe_forward: NULL argument");
+  if (ntok == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_forward_enqueue(m, ntok, d_x, d_logits, d_out);
+  if (rc) return rc;
+  if (d_index)
+    HIPCHK(c, hipMemcpyAsync(d_index, m->route_idx, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (d_weight)
+    HIPCHK(c, hipMemcpyAsync(d_weight, m->route_w, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_forward(hale_moe* m, size_t ntok, const float* x, const float* logits,
+                                float* out, uint32_t* index, float* weight) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !x || !out) return fail(c, HALE_EINVAL, "moe_forward: NULL argument");
+  if (ntok == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  size_t xb = ntok * m->H * 4, lb = logits ? ntok * m->E * 4 : 0;
+  size_t o1 = align_up(xb, 256), o2 = o1 + align_up(xb, 256);
+  void* s;
+  int rc = ctx_scratch(c, o2 + lb, &s);
+  if (rc) return rc;
+  float* dx = (float*)s;
+  float* dout = (float*)((char*)s + o1);
+  float* dl = logits ? (float*)((char*)s + o2) : nullptr;
+  HIPCHK(c, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream));
+  if (logits) HIPCHK(c, hipMemcpyAsync(dl, logits, lb, hipMemcpyHostToDevice, c->stream));
+  rc = moe_forward_enqueue(m, ntok, dx, dl, dout);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync(out, dout, xb, hipMemcpyDeviceToHost, c->stream));
+  if (index) HIPCHK(c, hipMemcpyAsync(index, m->route_idx, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  if (weight) HIPCHK(c, hipMemcpyAsync(weight, m->route_w, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, float* weight) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !x || !index || !weight) return fail(c, HALE_EINVAL, "moe_route: NULL argument");
+  if (!m->router) return fail(c, HALE_EINVAL, "layer has no router matrix");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_reserve(m, 1);
+  if (rc) return rc;
+  void* s;
+  rc = ctx_scratch(c, m->H * 4, &s);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync(s, x, m->H * 4, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_ROUTE, launch_route(m->router, nullptr, (const float*)s, (int)m->H, (int)m->E, (int)m->k,
+                         m->normalize, 1, m->act, m->logits, m->tok_counters, m->route_idx,
+                         m->route_w, nullptr, c->stream));
+  HIPCHK(c, hipMemcpyAsync(index, m->route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpyAsync(weight, m->route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_routing_counts(hale_moe* m, uint64_t* counts) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !counts) return fail(c, HALE_EINVAL, "routing_counts: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(counts, m->stats, m->E * 8, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// bulk expert registration
+// ---------------------------------------------------------------------------
+
+extern "C" int hale_moe_set_experts_device(hale_moe* m, uint32_t first, uint32_t count,
+                                           const void* d_gate, const void* d_up,
+                                           const void* d_down) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !d_gate || !d_up || !d_down) return fail(c, HALE_EINVAL, "set_experts: NULL argument");
+  if ((size_t)first + count > m->E) return fail(c, HALE_EINVAL, "experts %u..%u of %zu", first, first + count, m->E);
+  size_t ng = m->I * (size_t)hale_row_bytes(m->dtype, m->H);
+  size_t nd = m->H * (size_t)hale_row_bytes(m->dtype, m->I);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  for (uint32_t i = 0; i < count; i++) {
+    size_t e = first + i;
+    LAUNCH(c, K_REPACK, launch_repack(m->dtype, (const uint8_t*)d_gate + i * ng, m->I, m->H,
+                                      m->gate_c + e * m->gc_bytes, m->gate_s + e * m->gs_elems, c->stream));
+    LAUNCH(c, K_REPACK, launch_repack(m->dtype, (const uint8_t*)d_up + i * ng, m->I, m->H,
+                                      m->up_c + e * m->gc_bytes, m->up_s + e * m->gs_elems, c->stream));
+    LAUNCH(c, K_REPACK, launch_repack(m->dtype, (const uint8_t*)d_down + i * nd, m->H, m->I,
+                                      m->down_c + e * m->dc_bytes, m->down_s + e * m->ds_elems, c->stream));
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  for (uint32_t i = 0; i < count; i++) m->present[first + i] = 1;
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// support entry points
+// ---------------------------------------------------------------------------
+
+extern "C" int hale_device_malloc(hale_ctx* c, size_t bytes, void** out) {
+  if (!c || !out) return fail(c, HALE_EINVAL, "device_malloc: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  *out = nullptr;
+  if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess) return fail(c, HALE_ENOMEM, "device allocation of %zu bytes", bytes);
+  return HALE_OK;
+}
+
+extern "C" int hale_device_free(hale_ctx* c, void* p) {
+  if (!c) return HALE_EINVAL;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipFree(p));
+  return HALE_OK;
+}
+
+extern "C" int hale_memcpy_htod(hale_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c || (n && (!dst || !src))) return fail(c, HALE_EINVAL, "memcpy: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_memcpy_dtoh(hale_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c || (n && (!dst || !src))) return fail(c, HALE_EINVAL, "memcpy: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_fill_normal_device(hale_ctx* c, uint64_t seed, float mean, float std,
+                                       float* d_out, size_t n) {
+  if (!c || (n && !d_out)) return fail(c, HALE_EINVAL, "fill_normal: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  LAUNCH(c, K_FILL, launch_fill_normal(d_out, n, seed, mean, std, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_timer_start(hale_ctx* c) {
+  if (!c) return HALE_EINVAL;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  if (!c->t0) HIPCHK(c, hipEventCreate(&c->t0));
+  if (!c->t1) HIPCHK(c, hipEventCreate(&c->t1));
+  HIPCHK(c, hipEventRecord(c->t0, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_timer_stop(hale_ctx* c, double* ms) {
+  if (!c || !ms || !c->t0) return fail(c, HALE_EINVAL, "timer_stop without timer_start");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipEventRecord(c->t1, c->stream));
+  HIPCHK(c, hipEventSynchronize(c->t1));
+  float f = 0.0f;
+  HIPCHK(c, hipEventElapsedTime(&f, c->t0, c->t1));
+  *ms = f;
+  return HALE_OK;
+}
+
+extern "C" int hale_profile_enable(hale_ctx* c, int on) {
+  if (!c) return HALE_EINVAL;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  c->prof_on = on != 0;
+  return HALE_OK;
+}
+
+static int prof_collect(hale_ctx* c) {
+  if (c->recs.empty()) return HALE_OK;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  for (auto& r : c->recs) {
+    float f = 0.0f;
+    HIPCHK(c, hipEventElapsedTime(&f, r.start, r.stop));
+    if (r.kind >= 0 && r.kind < K_KINDS) {
+      c->prof_ms[r.kind] += f;
+      c->prof_n[r.kind] += 1;
+    }
+    c->ev_pool.push_back(r.start);
+    c->ev_pool.push_back(r.stop);
+  }
+  c->recs.clear();
+  return HALE_OK;
+}
+
+extern "C" int hale_profile_read(hale_ctx* c, int kind, double* total_ms, uint64_t* launches) {
+  if (!c || kind < 0 || kind >= K_KINDS) return fail(c, HALE_EINVAL, "profile_read: bad kind %d", kind);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = prof_collect(c);
+  if (rc) return rc;
+  if (total_ms) *total_ms = c->prof_ms[kind];
+  if (launches) *launches = c->prof_n[kind];
+  return HALE_OK;
+}
+
+extern "C" int hale_profile_reset(hale_ctx* c) {
+  if (!c) return HALE_EINVAL;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = prof_collect(c);
+  if (rc) return rc;
+  for (int k = 0; k < K_KINDS; k++) {
+    c->prof_ms[k] = 0.0;
+    c->prof_n[k] = 0;
+  }
+  return HALE_OK;
+}
+
+extern "C" int hale_kernel_kinds(void) { return K_KINDS; }
+
+extern "C" const char* hale_kernel_name(int kind) {
+  static const char* names[K_KINDS] = {"route", "gate_up", "down", "act_quant", "gemv", "encode",
+                                       "repack", "fill", "group", "grouped_gate_up",
+                                       "grouped_down", "combine"};
+  return kind >= 0 && kind < K_KINDS ? names[kind] : "";
+}
+
+extern "C" int hale_graph_begin(hale_ctx* c) {
+  if (!c) return HALE_EINVAL;
+  c->mu.lock();  // held until hale_graph_end: nothing else may enqueue meanwhile
+  hipError_t e = hipSetDevice(c->device);
+  if (e == hipSuccess) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) {
+    c->mu.unlock();
+    return fail(c, HALE_EHIP, "begin capture: %s", hipGetErrorString(e));
+  }
+  return HALE_OK;
+}
+
+extern "C" int hale_graph_end(hale_ctx* c, hale_graph** out) {
+  if (!c || !out) return HALE_EINVAL;
+  *out = nullptr;
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &graph);
+  c->mu.unlock();
+  if (e != hipSuccess) return fail(c, HALE_EHIP, "end capture: %s", hipGetErrorString(e));
+  hale_graph* g = new (std::nothrow) hale_graph;
+  if (!g) {
+    (void)hipGraphDestroy(graph);
+    return fail(c, HALE_ENOMEM, "out of host memory");
+  }
+  g->ctx = c;
+  g->graph = graph;
+  e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    delete g;
+    return fail(c, HALE_EHIP, "instantiate: %s", hipGetErrorString(e));
+  }
+  *out = g;
+  return HALE_OK;
+}
+
+extern "C" int hale_graph_launch(hale_graph* g) {
+  if (!g) return HALE_EINVAL;
+  hale_ctx* c = g->ctx;
+  std::lock_guard<std::recursive_mutex> lk(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipGraphLaunch(g->exec, c->stream));
+  return HALE_OK;
+}
+
+extern "C" void hale_graph_destroy(hale_graph* g) {
+  if (!g) return;
+  std::lock_guard<std::recursive_mutex> lk(g->ctx->mu);
+  (void)hipStreamSynchronize(g->ctx->stream);
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  delete g;
+}

@@ -1,0 +1,596 @@
+"""Python view of the MI355X quantized MoE expert path (lib/libhale_moe.so).
+
+The classes mirror the Hale-Token surface this path replaces, with the same
+names and argument meaning:
+
+=====================  ==========================================================
+``WeightMatrix``       ``WeightMatrix::{new, from_f32, matvec, bytes}``
+                       (src/tensor/matrix.rs:19-126)
+``Q8Activations``      ``Q8Activations::quantize`` (src/tensor/quant.rs:77-93)
+``encode_row(s)``      ``encode_row`` (src/tensor/quant.rs:274-321)
+``Expert``             ``Expert::forward`` (src/expert/mod.rs:91-103)
+``MoeLayer``           ``MoeLayer::{route, forward}`` (src/model/moe.rs:36-70)
+``HbmExpertProvider``  ``ExpertProvider::{fetch, stats, routing_stats}``
+                       (src/expert/mod.rs:128-137), all experts resident in HBM
+=====================  ==========================================================
+
+Errors follow the reference: shape and length violations (which panic in
+Rust) raise ``ValueError``; runtime failures raise ``HaleError``; a missing
+expert raises ``KeyError``.  Every computation runs on the GPU through the C
+ABI in include/hale_moe.h; there is no host fallback, and importing this
+module on a machine without the built library raises at first use.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libhale_moe.so")
+
+F32, F16, BF16, Q8_0, Q4_0 = 0, 1, 2, 3, 4
+QK = 32
+_NAMES = {"f32": F32, "f16": F16, "bf16": BF16, "q8_0": Q8_0, "q8": Q8_0, "q4_0": Q4_0, "q4": Q4_0}
+OK, EINVAL, EHIP, ENOMEM, ENOTFOUND = 0, 1, 2, 3, 4
+
+_vp = C.c_void_p
+_fp = C.POINTER(C.c_float)
+_i8p = C.POINTER(C.c_int8)
+_i32p = C.POINTER(C.c_int32)
+_u32p = C.POINTER(C.c_uint32)
+_u64p = C.POINTER(C.c_uint64)
+_sz = C.c_size_t
+
+# name -> (restype, argtypes); the exported surface of include/hale_moe.h
+SIGNATURES = {
+    "hale_ctx_create": (C.c_int, [C.c_int, C.POINTER(_vp)]),
+    "hale_ctx_destroy": (None, [_vp]),
+    "hale_last_error": (C.c_char_p, [_vp]),
+    "hale_ctx_stream": (_vp, [_vp]),
+    "hale_ctx_synchronize": (C.c_int, [_vp]),
+    "hale_row_bytes": (C.c_longlong, [C.c_int, _sz]),
+    "hale_block_bytes": (_sz, [C.c_int]),
+    "hale_matrix_upload": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _sz, C.POINTER(_vp)]),
+    "hale_matrix_upload_device": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _sz, C.POINTER(_vp)]),
+    "hale_matrix_destroy": (None, [_vp]),
+    "hale_matrix_shape": (C.c_int, [_vp, C.POINTER(C.c_int), C.POINTER(_sz), C.POINTER(_sz)]),
+    "hale_matrix_download": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "hale_quantize_q8_act": (C.c_int, [_vp, _fp, _sz, _fp, _i8p]),
+    "hale_encode_rows": (C.c_int, [_vp, C.c_int, _sz, _sz, _fp, _vp]),
+    "hale_encode_rows_device": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _vp]),
+    "hale_matvec": (C.c_int, [_vp, _vp, _fp, _sz, _fp, _sz]),
+    "hale_matvec_device": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "hale_matvec_block_sums": (C.c_int, [_vp, _vp, _fp, _sz, _i32p]),
+    "hale_expert_forward": (C.c_int, [_vp, _vp, _vp, _vp, _fp, _fp]),
+    "hale_moe_create": (C.c_int, [_vp, C.c_uint32, _sz, _sz, _sz, C.c_int, _sz, C.c_int, _vp,
+                                  C.POINTER(_vp)]),
+    "hale_moe_destroy": (None, [_vp]),
+    "hale_moe_set_expert": (C.c_int, [_vp, C.c_uint32, _vp, _vp, _vp, _sz, _sz]),
+    "hale_moe_set_expert_device": (C.c_int, [_vp, C.c_uint32, _vp, _vp, _vp, _sz, _sz]),
+    "hale_moe_set_expert_matrices": (C.c_int, [_vp, C.c_uint32, _vp, _vp, _vp]),
+    "hale_moe_route": (C.c_int, [_vp, _fp, _u32p, _fp]),
+    "hale_moe_forward": (C.c_int, [_vp, _sz, _fp, _fp, _fp, _u32p, _fp]),
+    "hale_moe_forward_device": (C.c_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
+    "hale_moe_set_experts_device": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _vp, _vp, _vp]),
+    "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
+    "hale_device_malloc": (C.c_int, [_vp, _sz, C.POINTER(_vp)]),
+    "hale_device_free": (C.c_int, [_vp, _vp]),
+    "hale_memcpy_htod": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "hale_memcpy_dtoh": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "hale_fill_normal_device": (C.c_int, [_vp, C.c_uint64, C.c_float, C.c_float, _vp, _sz]),
+    "hale_timer_start": (C.c_int, [_vp]),
+    "hale_timer_stop": (C.c_int, [_vp, C.POINTER(C.c_double)]),
+    "hale_profile_enable": (C.c_int, [_vp, C.c_int]),
+    "hale_profile_read": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_double), _u64p]),
+    "hale_profile_reset": (C.c_int, [_vp]),
+    "hale_kernel_kinds": (C.c_int, []),
+    "hale_kernel_name": (C.c_char_p, [C.c_int]),
+    "hale_graph_begin": (C.c_int, [_vp]),
+    "hale_graph_end": (C.c_int, [_vp, C.POINTER(_vp)]),
+    "hale_graph_launch": (C.c_int, [_vp]),
+    "hale_graph_destroy": (None, [_vp]),
+}
+
+_LIB = None
+
+
+class HaleError(RuntimeError):
+    """A runtime failure reported by the library (HaleError in the reference)."""
+
+
+def lib():
+    """The loaded native library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise HaleError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def parse_dtype(d) -> int:
+    """DType::parse (src/tensor/dtype.rs:89-100)."""
+    if isinstance(d, int):
+        return d
+    try:
+        return _NAMES[str(d).lower()]
+    except KeyError:
+        raise ValueError(f"unknown dtype `{d}` (expected f32, f16, bf16, q8_0 or q4_0)") from None
+
+
+def row_bytes(dtype, cols: int) -> int:
+    """DType::row_bytes (src/tensor/dtype.rs:53-61); ValueError when cols is
+    not a multiple of the block length."""
+    n = lib().hale_row_bytes(parse_dtype(dtype), cols)
+    if n < 0:
+        raise ValueError(f"{dtype} needs row length divisible by 32, got {cols}")
+    return int(n)
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Context:
+    """One GPU and one stream.  Ref: the engine-wide state behind
+    WeightMatrix / Expert / MoeLayer (which in Rust are CPU objects)."""
+
+    def __init__(self, device: int = 0):
+        h = _vp()
+        rc = lib().hale_ctx_create(device, C.byref(h))
+        if rc != OK:
+            raise HaleError(lib().hale_last_error(None).decode())
+        self.handle = h
+
+    def check(self, rc: int, what: str = ""):
+        if rc == OK:
+            return
+        msg = lib().hale_last_error(self.handle).decode()
+        if what:
+            msg = f"{what}: {msg}"
+        if rc == EINVAL:
+            raise ValueError(msg)
+        if rc == ENOTFOUND:
+            raise KeyError(msg)
+        if rc == ENOMEM:
+            raise MemoryError(msg)
+        raise HaleError(msg)
+
+    @property
+    def stream(self) -> int:
+        return int(lib().hale_ctx_stream(self.handle) or 0)
+
+    def synchronize(self):
+        self.check(lib().hale_ctx_synchronize(self.handle), "synchronize")
+
+    # ---- device memory, timing and graphs (support entry points) ----------
+    def malloc(self, nbytes: int) -> "DeviceBuffer":
+        p = _vp()
+        self.check(lib().hale_device_malloc(self.handle, nbytes, C.byref(p)), "malloc")
+        return DeviceBuffer(self, p, nbytes)
+
+    def timer_start(self):
+        self.check(lib().hale_timer_start(self.handle), "timer_start")
+
+    def timer_stop(self) -> float:
+        ms = C.c_double()
+        self.check(lib().hale_timer_stop(self.handle, C.byref(ms)), "timer_stop")
+        return ms.value
+
+    def profile(self, on: bool):
+        self.check(lib().hale_profile_enable(self.handle, int(on)), "profile")
+
+    def profile_reset(self):
+        self.check(lib().hale_profile_reset(self.handle), "profile_reset")
+
+    def profile_read(self) -> dict:
+        """{kernel kind name: (total ms, launches)} since the last reset."""
+        out = {}
+        for k in range(lib().hale_kernel_kinds()):
+            ms, n = C.c_double(), C.c_uint64()
+            self.check(lib().hale_profile_read(self.handle, k, C.byref(ms), C.byref(n)), "profile")
+            if n.value:
+                out[lib().hale_kernel_name(k).decode()] = (ms.value, int(n.value))
+        return out
+
+    def capture(self, fn) -> "Graph":
+        """Records the device work `fn()` enqueues into a replayable graph."""
+        self.check(lib().hale_graph_begin(self.handle), "graph_begin")
+        try:
+            fn()
+        finally:
+            g = _vp()
+            rc = lib().hale_graph_end(self.handle, C.byref(g))
+        self.check(rc, "graph_end")
+        return Graph(self, g)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().hale_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """Device memory owned by the library's HIP runtime."""
+
+    def __init__(self, ctx: Context, ptr, nbytes: int):
+        self.ctx, self.ptr, self.nbytes = ctx, ptr, nbytes
+
+    @property
+    def address(self) -> int:
+        return int(self.ptr.value or 0)
+
+    def offset(self, nbytes: int) -> int:
+        return self.address + nbytes
+
+    def upload(self, arr: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(arr)
+        if offset + a.nbytes > self.nbytes:
+            raise ValueError("upload past the end of the buffer")
+        self.ctx.check(lib().hale_memcpy_htod(self.ctx.handle, _vp(self.address + offset),
+                                              a.ctypes.data_as(_vp), a.nbytes), "upload")
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.zeros(count, dtype=dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download past the end of the buffer")
+        self.ctx.check(lib().hale_memcpy_dtoh(self.ctx.handle, out.ctypes.data_as(_vp),
+                                              _vp(self.address + offset), out.nbytes), "download")
+        return out
+
+    def fill_normal(self, seed: int, count: int, mean: float = 0.0, std: float = 1.0,
+                    offset: int = 0):
+        if offset + 4 * count > self.nbytes:
+            raise ValueError("fill past the end of the buffer")
+        self.ctx.check(lib().hale_fill_normal_device(self.ctx.handle, seed, mean, std,
+                                                     _vp(self.address + offset), count),
+                       "fill_normal")
+
+    def free(self):
+        if self.ptr:
+            lib().hale_device_free(self.ctx.handle, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Graph:
+    """A captured sequence of device work (hale_graph)."""
+
+    def __init__(self, ctx: Context, handle):
+        self.ctx, self.handle = ctx, handle
+
+    def launch(self):
+        self.ctx.check(lib().hale_graph_launch(self.handle), "graph_launch")
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().hale_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Q8Activations:
+    """Q8Activations::quantize (src/tensor/quant.rs:77-93) on the GPU."""
+
+    def __init__(self, scales: np.ndarray, quants: np.ndarray):
+        self.scales, self.quants = scales, quants
+
+    @classmethod
+    def quantize(cls, ctx: Context, x) -> "Q8Activations":
+        v = _f32(x)
+        if v.size % QK:
+            raise ValueError(f"activation length must be a multiple of {QK}")
+        scales = np.zeros(v.size // QK, dtype=np.float32)
+        quants = np.zeros(v.size, dtype=np.int8)
+        ctx.check(lib().hale_quantize_q8_act(ctx.handle, _p(v, _fp), v.size, _p(scales, _fp),
+                                             _p(quants, _i8p)), "quantize")
+        return cls(scales, quants)
+
+
+def encode_rows(ctx: Context, dtype, values: np.ndarray) -> np.ndarray:
+    """encode_row over every row of a [rows][cols] f32 matrix, on the GPU
+    (src/tensor/quant.rs:274-321 via WeightMatrix::from_f32, matrix.rs:48-61)."""
+    dt = parse_dtype(dtype)
+    v = _f32(values)
+    if v.ndim == 1:
+        v = v.reshape(1, -1)
+    rows, cols = v.shape
+    out = np.zeros(rows * row_bytes(dt, cols), dtype=np.uint8)
+    ctx.check(lib().hale_encode_rows(ctx.handle, dt, rows, cols, _p(v, _fp),
+                                     out.ctypes.data_as(_vp)), "encode_rows")
+    return out
+
+
+def encode_row(ctx: Context, dtype, values) -> np.ndarray:
+    return encode_rows(ctx, dtype, _f32(values).reshape(1, -1))
+
+
+class WeightMatrix:
+    """A rows x cols matrix resident in HBM (src/tensor/matrix.rs:19-25)."""
+
+    def __init__(self, ctx: Context, handle, rows: int, cols: int, dtype: int):
+        self.ctx, self.handle = ctx, handle
+        self._rows, self._cols, self._dtype = rows, cols, dtype
+
+    @classmethod
+    def new(cls, ctx: Context, rows: int, cols: int, dtype, data) -> "WeightMatrix":
+        """WeightMatrix::new (src/tensor/matrix.rs:27-47): reference-layout
+        bytes, checked against the shape."""
+        dt = parse_dtype(dtype)
+        b = np.ascontiguousarray(data, dtype=np.uint8)
+        h = _vp()
+        ctx.check(lib().hale_matrix_upload(ctx.handle, dt, rows, cols, b.ctypes.data_as(_vp),
+                                           b.size, C.byref(h)), "WeightMatrix::new")
+        return cls(ctx, h, rows, cols, dt)
+
+    @classmethod
+    def from_f32(cls, ctx: Context, rows: int, cols: int, dtype, values) -> "WeightMatrix":
+        """WeightMatrix::from_f32 (src/tensor/matrix.rs:48-61): quantized on
+        the GPU for q8_0/q4_0."""
+        v = _f32(values)
+        if v.size != rows * cols:
+            raise ValueError(f"expected {rows * cols} values for a {rows}x{cols} matrix, got {v.size}")
+        dt = parse_dtype(dtype)
+        data = v.view(np.uint8) if dt == F32 else encode_rows(ctx, dt, v.reshape(rows, cols))
+        return cls.new(ctx, rows, cols, dt, data)
+
+    def rows(self) -> int:
+        return self._rows
+
+    def cols(self) -> int:
+        return self._cols
+
+    def dtype(self) -> int:
+        return self._dtype
+
+    def size_bytes(self) -> int:
+        return self._rows * row_bytes(self._dtype, self._cols)
+
+    def bytes(self) -> np.ndarray:
+        """The matrix in the reference block layout (WeightMatrix::bytes)."""
+        out = np.zeros(self.size_bytes(), dtype=np.uint8)
+        self.ctx.check(lib().hale_matrix_download(self.ctx.handle, self.handle,
+                                                  out.ctypes.data_as(_vp), out.size), "bytes")
+        return out
+
+    def matvec(self, x, out: np.ndarray | None = None) -> np.ndarray:
+        """WeightMatrix::matvec (src/tensor/matrix.rs:115-126)."""
+        v = _f32(x)
+        if out is None:
+            out = np.zeros(self._rows, dtype=np.float32)
+        self.ctx.check(lib().hale_matvec(self.ctx.handle, self.handle, _p(v, _fp), v.size,
+                                         _p(out, _fp), out.size), "matvec")
+        return out
+
+    matvec_serial = matvec  # the reference's serial and parallel forms agree bit for bit
+
+    def block_sums(self, x) -> np.ndarray:
+        """Per-block i32 sums [rows][cols/32] (the isum of dot_q8_0/dot_q4_0)."""
+        v = _f32(x)
+        out = np.zeros((self._rows, self._cols // QK), dtype=np.int32)
+        self.ctx.check(lib().hale_matvec_block_sums(self.ctx.handle, self.handle, _p(v, _fp),
+                                                    v.size, _p(out, _i32p)), "block_sums")
+        return out
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().hale_matrix_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Expert:
+    """A SwiGLU expert: down(silu(gate x) * up x) (src/expert/mod.rs:75-103)."""
+
+    def __init__(self, gate: WeightMatrix, up: WeightMatrix, down: WeightMatrix):
+        self.gate, self.up, self.down = gate, up, down
+
+    def size_bytes(self) -> int:
+        return self.gate.size_bytes() + self.up.size_bytes() + self.down.size_bytes()
+
+    def forward(self, x, out: np.ndarray | None = None) -> np.ndarray:
+        ctx = self.gate.ctx
+        v = _f32(x)
+        if out is None:
+            out = np.zeros(self.down.rows(), dtype=np.float32)
+        ctx.check(lib().hale_expert_forward(ctx.handle, self.gate.handle, self.up.handle,
+                                            self.down.handle, _p(v, _fp), _p(out, _fp)),
+                  "Expert::forward")
+        return out
+
+
+@dataclass(frozen=True)
+class ExpertKey:
+    """(layer, expert index within the layer) (src/expert/mod.rs:50-62)."""
+
+    layer: int
+    expert: int
+
+    def __str__(self):
+        return f"L{self.layer}E{self.expert}"
+
+
+@dataclass
+class Route:
+    """One routing decision (src/model/moe.rs:8-12)."""
+
+    key: ExpertKey
+    weight: float
+
+
+class HbmExpertProvider:
+    """ExpertProvider whose tiers are all HBM: every expert of the layer is
+    resident, so fetch never misses (src/expert/mod.rs:128-137)."""
+
+    def __init__(self, layer: "MoeLayer"):
+        self._layer = layer
+
+    def fetch(self, keys):
+        """Returns the keys' experts in request order; KeyError if absent."""
+        for k in keys:
+            if k.layer != self._layer.layer or not (0 <= k.expert < self._layer.num_experts) \
+                    or not self._layer._present[k.expert]:
+                raise KeyError(f"expert {k} is not resident")
+        return [self._layer.expert_ref(k.expert) for k in keys]
+
+    def stats(self) -> dict:
+        counts = self.routing_counts()
+        n = int(counts.sum())
+        return {"pinned_hits": n, "lru_hits": 0, "misses": 0, "bytes_loaded": 0,
+                "pinned_experts": int(sum(self._layer._present)),
+                "pinned_bytes": int(sum(self._layer._present)) * self._layer.expert_bytes(),
+                "passthrough": False}
+
+    def routing_counts(self) -> np.ndarray:
+        out = np.zeros(self._layer.num_experts, dtype=np.uint64)
+        ctx = self._layer.ctx
+        ctx.check(lib().hale_moe_routing_counts(self._layer.handle, _p(out, _u64p)), "routing_stats")
+        return out
+
+    def routing_stats(self) -> dict:
+        """RoutingStats counters of this layer as {ExpertKey: count}."""
+        c = self.routing_counts()
+        return {ExpertKey(self._layer.layer, e): int(v) for e, v in enumerate(c) if v}
+
+
+class MoeLayer:
+    """Router plus HBM-resident experts (src/model/moe.rs:25-70)."""
+
+    def __init__(self, ctx: Context, layer: int, num_experts: int, hidden: int, inter: int,
+                 dtype, experts_per_token: int, normalize_topk: bool,
+                 router: WeightMatrix | None = None):
+        self.ctx = ctx
+        self.layer, self.num_experts, self.hidden, self.inter = layer, num_experts, hidden, inter
+        self.dtype = parse_dtype(dtype)
+        self.experts_per_token = experts_per_token
+        self.top_k = min(experts_per_token, num_experts)
+        self.normalize_topk = bool(normalize_topk)
+        self.router = router
+        h = _vp()
+        ctx.check(lib().hale_moe_create(ctx.handle, layer, num_experts, hidden, inter, self.dtype,
+                                        experts_per_token, int(bool(normalize_topk)),
+                                        router.handle if router is not None else None,
+                                        C.byref(h)), "MoeLayer")
+        self.handle = h
+        self._present = [False] * num_experts
+        self.experts = HbmExpertProvider(self)
+
+    def expert_bytes(self) -> int:
+        return 2 * self.inter * row_bytes(self.dtype, self.hidden) + \
+            self.hidden * row_bytes(self.dtype, self.inter)
+
+    def expert_ref(self, e: int) -> ExpertKey:
+        return ExpertKey(self.layer, e)
+
+    def set_expert(self, e: int, gate, up, down):
+        """Registers expert e from reference-layout bytes (gate/up [I][H],
+        down [H][I])."""
+        g, u, d = (np.ascontiguousarray(a, dtype=np.uint8) for a in (gate, up, down))
+        if g.size != u.size:
+            raise ValueError("gate and up must have the same size")
+        self.ctx.check(lib().hale_moe_set_expert(self.handle, e, g.ctypes.data_as(_vp),
+                                                 u.ctypes.data_as(_vp), d.ctypes.data_as(_vp),
+                                                 g.size, d.size), "set_expert")
+        self._present[e] = True
+
+    def set_experts_device(self, first: int, count: int, d_gate: int, d_up: int, d_down: int):
+        """Registers experts first..first+count-1 from device buffers of
+        back-to-back reference-layout bytes."""
+        self.ctx.check(lib().hale_moe_set_experts_device(self.handle, first, count, _vp(d_gate),
+                                                         _vp(d_up), _vp(d_down)), "set_experts")
+        for e in range(first, first + count):
+            self._present[e] = True
+
+    def forward_device(self, ntok: int, d_x: int, d_out: int, d_logits: int = 0,
+                       d_index: int = 0, d_weight: int = 0):
+        """MoeLayer::forward on device buffers, enqueued on the context stream."""
+        self.ctx.check(lib().hale_moe_forward_device(self.handle, ntok, _vp(d_x),
+                                                     _vp(d_logits) if d_logits else None,
+                                                     _vp(d_out),
+                                                     _vp(d_index) if d_index else None,
+                                                     _vp(d_weight) if d_weight else None),
+                       "MoeLayer::forward")
+
+    def set_expert_matrices(self, e: int, expert: Expert):
+        self.ctx.check(lib().hale_moe_set_expert_matrices(self.handle, e, expert.gate.handle,
+                                                          expert.up.handle, expert.down.handle),
+                       "set_expert")
+        self._present[e] = True
+
+    def route(self, x) -> list[Route]:
+        """MoeLayer::route (src/model/moe.rs:36-53)."""
+        v = _f32(x)
+        if v.size != self.hidden:
+            raise ValueError("route input length")
+        idx = np.zeros(max(self.top_k, 1), dtype=np.uint32)
+        w = np.zeros(max(self.top_k, 1), dtype=np.float32)
+        self.ctx.check(lib().hale_moe_route(self.handle, _p(v, _fp), _p(idx, _u32p), _p(w, _fp)),
+                       "route")
+        return [Route(ExpertKey(self.layer, int(i)), float(wt))
+                for i, wt in zip(idx[:self.top_k], w[:self.top_k])]
+
+    def forward(self, x, logits=None, return_routes: bool = False):
+        """MoeLayer::forward (src/model/moe.rs:56-70).  x is [H] (decode) or
+        [T][H] (token-at-a-time prefill semantics, computed as one batch).
+        logits, when given, replace the router matvec output ([T][E])."""
+        v = _f32(x)
+        single = v.ndim == 1
+        v = v.reshape(-1, self.hidden)
+        T = v.shape[0]
+        lg = None
+        if logits is not None:
+            lg = _f32(logits).reshape(T, self.num_experts)
+        out = np.zeros((T, self.hidden), dtype=np.float32)
+        idx = np.zeros((T, max(self.top_k, 1)), dtype=np.uint32)
+        w = np.zeros((T, max(self.top_k, 1)), dtype=np.float32)
+        self.ctx.check(lib().hale_moe_forward(self.handle, T, _p(v, _fp),
+                                              None if lg is None else _p(lg, _fp), _p(out, _fp),
+                                              _p(idx, _u32p), _p(w, _fp)), "MoeLayer::forward")
+        idx, w = idx[:, :self.top_k], w[:, :self.top_k]
+        if single:
+            out, idx, w = out[0], idx[0], w[0]
+        return (out, idx, w) if return_routes else out
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().hale_moe_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

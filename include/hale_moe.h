@@ -1,0 +1,246 @@
+/*
+ * hale_moe.h -- C ABI of the MI355X (gfx950) quantized MoE expert path.
+ *
+ * This is the drop-in seam behind Hale-Token's Rust surface for the path:
+ * WeightMatrix::matvec, Q8Activations::quantize, encode_row,
+ * Expert::forward, MoeLayer::{route, forward} and the ExpertProvider trait.
+ * Every declaration names the reference item it replaces (Hale-Token
+ * file:line).  The ABI uses plain pointers, sizes and opaque handles only.
+ *
+ * Conventions
+ *   - Every fallible call returns an int status (hale_status).  Nothing
+ *     unwinds across the ABI.  The message of the last failure on a context
+ *     is available from hale_last_error().  A Rust wrapper maps
+ *     HALE_EINVAL to the reference's panics/asserts (length checks,
+ *     `len % 32`, float dtype in dot_quantized) and everything else to
+ *     HaleError.
+ *   - Entry points without a `_device` suffix take HOST buffers and are
+ *     synchronous, matching the Rust semantics (the result is in `out` when
+ *     the call returns).  `_device` entry points take device pointers, are
+ *     enqueued on the context's stream (hale_ctx_stream) and return at once.
+ *   - Weight bytes are accepted in the reference's block layout
+ *     (src/tensor/quant.rs:20-26: q8_0 = [f16 scale][32 x i8], 34 B;
+ *     q4_0 = [f16 scale][16 B nibbles], 18 B, byte j = element j low nibble,
+ *     element j+16 high nibble).  They are copied to HBM once and repacked
+ *     into an aligned tile layout; the bytes read per matvec are unchanged.
+ *   - A context serialises its own calls; distinct contexts may run
+ *     concurrently.  All calls on one context share its stream.
+ */
+#ifndef HALE_MOE_H
+#define HALE_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Ref: HaleError (src/error.rs:11-60) and the panics listed
+ * above. */
+typedef enum {
+  HALE_OK = 0,
+  HALE_EINVAL = 1,   /* bad shape, dtype, length or argument            */
+  HALE_EHIP = 2,     /* HIP runtime error (message in hale_last_error)  */
+  HALE_ENOMEM = 3,   /* device or host allocation failed                */
+  HALE_ENOTFOUND = 4 /* expert not registered (ExpertProvider::fetch)   */
+} hale_status;
+
+/* Element formats.  Ref: DType (src/tensor/dtype.rs:15-25), same order. */
+typedef enum {
+  HALE_F32 = 0,
+  HALE_F16 = 1,
+  HALE_BF16 = 2,
+  HALE_Q8_0 = 3,
+  HALE_Q4_0 = 4
+} hale_dtype;
+
+#define HALE_QK 32 /* Ref: QK (src/tensor/dtype.rs:28) */
+
+typedef struct hale_ctx hale_ctx;       /* device + stream + scratch      */
+typedef struct hale_matrix hale_matrix; /* Ref: WeightMatrix              */
+typedef struct hale_moe hale_moe;       /* Ref: MoeLayer + its provider   */
+
+/* ---- context --------------------------------------------------------- */
+
+/* Creates a context on HIP device `device` (one stream, default priority). */
+int hale_ctx_create(int device, hale_ctx **out);
+void hale_ctx_destroy(hale_ctx *ctx);
+/* Message of the last failed call on ctx ("" if none).  NULL ctx gives the
+ * message of the last failed hale_ctx_create in this thread. */
+const char *hale_last_error(const hale_ctx *ctx);
+/* The hipStream_t the context enqueues on (for the _device entry points). */
+void *hale_ctx_stream(hale_ctx *ctx);
+int hale_ctx_synchronize(hale_ctx *ctx);
+
+/* ---- geometry -------------------------------------------------------- */
+
+/* Ref: DType::row_bytes (src/tensor/dtype.rs:53-61); -1 when cols is not a
+ * multiple of the block length or dtype is unknown. */
+long long hale_row_bytes(int dtype, size_t cols);
+/* Ref: DType::block_bytes (src/tensor/dtype.rs:40-47); 0 if unknown. */
+size_t hale_block_bytes(int dtype);
+
+/* ---- weight matrices ------------------------------------------------- */
+
+/* Ref: WeightMatrix::new (src/tensor/matrix.rs:19-47).  `bytes` holds
+ * rows x row_bytes(cols) bytes in the reference layout (host memory).
+ * Supported dtypes: Q8_0, Q4_0 (expert weights) and F32 (router). */
+int hale_matrix_upload(hale_ctx *ctx, int dtype, size_t rows, size_t cols,
+                       const void *bytes, size_t nbytes, hale_matrix **out);
+/* Same, with the reference-layout bytes already in device memory (for
+ * example written by hale_encode_rows_device). */
+int hale_matrix_upload_device(hale_ctx *ctx, int dtype, size_t rows,
+                              size_t cols, const void *d_bytes, size_t nbytes,
+                              hale_matrix **out);
+void hale_matrix_destroy(hale_matrix *m);
+/* Ref: WeightMatrix::{rows, cols, dtype} (src/tensor/matrix.rs:65-77). */
+int hale_matrix_shape(const hale_matrix *m, int *dtype, size_t *rows,
+                      size_t *cols);
+/* Ref: WeightMatrix::bytes (src/tensor/matrix.rs:78-81): the matrix back in
+ * the reference layout (undoes the HBM repack). */
+int hale_matrix_download(hale_ctx *ctx, const hale_matrix *m, void *bytes,
+                         size_t nbytes);
+
+/* ---- quantization ---------------------------------------------------- */
+
+/* Ref: Q8Activations::quantize (src/tensor/quant.rs:77-93).  n % 32 == 0;
+ * scales[n/32] (f32, not rounded to f16), quants[n]. */
+int hale_quantize_q8_act(hale_ctx *ctx, const float *x, size_t n,
+                         float *scales, int8_t *quants);
+/* Ref: encode_row for Q8_0 / Q4_0 (src/tensor/quant.rs:274-321), applied to
+ * each row of a row-major rows x cols f32 matrix (WeightMatrix::from_f32,
+ * src/tensor/matrix.rs:48-61).  Host buffers; bytes gets rows*row_bytes. */
+int hale_encode_rows(hale_ctx *ctx, int dtype, size_t rows, size_t cols,
+                     const float *values, void *bytes);
+int hale_encode_rows_device(hale_ctx *ctx, int dtype, size_t rows,
+                            size_t cols, const float *d_values,
+                            void *d_bytes);
+
+/* ---- matvec ---------------------------------------------------------- */
+
+/* Ref: WeightMatrix::matvec (src/tensor/matrix.rs:115-126) and
+ * matvec_serial (:130-143), which return identical bits.  xlen must equal
+ * cols and outlen rows (the reference asserts both). */
+int hale_matvec(hale_ctx *ctx, const hale_matrix *m, const float *x,
+                size_t xlen, float *out, size_t outlen);
+int hale_matvec_device(hale_ctx *ctx, const hale_matrix *m, const float *d_x,
+                       float *d_out);
+/* The per-block i32 sums of dot_q8_0 / dot_q4_0 (src/tensor/quant.rs:
+ * 115-144, `isum`) for every row: isums[rows][cols/32].  For parity tests. */
+int hale_matvec_block_sums(hale_ctx *ctx, const hale_matrix *m,
+                           const float *x, size_t xlen, int32_t *isums);
+
+/* ---- expert ---------------------------------------------------------- */
+
+/* Ref: Expert::forward (src/expert/mod.rs:91-103): gate.matvec(x) and
+ * up.matvec(x), h = silu(g)*u, down.matvec(h).  gate/up are [I][H], down is
+ * [H][I], all of one quantized dtype.  x[H] -> out[H]. */
+int hale_expert_forward(hale_ctx *ctx, const hale_matrix *gate,
+                        const hale_matrix *up, const hale_matrix *down,
+                        const float *x, float *out);
+
+/* ---- MoE layer and its HBM-resident expert provider ------------------ */
+
+/* Ref: MoeLayer (src/model/moe.rs:25-32) with an ExpertProvider
+ * (src/expert/mod.rs:128-137) that keeps all E experts of the layer
+ * resident in HBM.  `router` is the f32 [E][H] router matrix, or NULL for a
+ * layer whose router logits are supplied to hale_moe_forward.
+ * normalize_topk: ModelConfig::normalize_topk (src/config.rs:205-208). */
+int hale_moe_create(hale_ctx *ctx, uint32_t layer, size_t num_experts,
+                    size_t hidden, size_t inter, int dtype, size_t top_k,
+                    int normalize_topk, const hale_matrix *router,
+                    hale_moe **out);
+void hale_moe_destroy(hale_moe *moe);
+
+/* Registers expert `expert` from reference-layout bytes (host memory):
+ * gate/up [I][H], down [H][I].  Ref: ExpertSource::load + the pinned tier
+ * of ExpertCache (src/expert/cache.rs:82-115), which here is all of HBM. */
+int hale_moe_set_expert(hale_moe *moe, uint32_t expert, const void *gate,
+                        const void *up, const void *down, size_t nbytes_gate,
+                        size_t nbytes_down);
+/* Same with the reference-layout bytes already in device memory. */
+int hale_moe_set_expert_device(hale_moe *moe, uint32_t expert,
+                               const void *d_gate, const void *d_up,
+                               const void *d_down, size_t nbytes_gate,
+                               size_t nbytes_down);
+/* Registers an expert from uploaded matrices (copied into the layer). */
+int hale_moe_set_expert_matrices(hale_moe *moe, uint32_t expert,
+                                 const hale_matrix *gate,
+                                 const hale_matrix *up,
+                                 const hale_matrix *down);
+
+/* Ref: MoeLayer::route (src/model/moe.rs:36-53): router matvec (8-lane f32
+ * order), softmax_in_place, top_k (ties to the lower index), renormalise.
+ * index[top_k], weight[top_k], best first. */
+int hale_moe_route(hale_moe *moe, const float *x, uint32_t *index,
+                   float *weight);
+
+/* Ref: MoeLayer::forward (src/model/moe.rs:56-70) for ntok tokens.  ntok
+ * == 1 is decode; ntok > 1 is the reference's token-at-a-time prefill
+ * (src/model/transformer.rs:231-239) computed as one expert-grouped batch:
+ * token t's output equals MoeLayer::forward(x_t).  x and out are
+ * [ntok][H].  logits: NULL to run the router matvec, else [ntok][E] router
+ * outputs used as given.  index/weight: NULL or [ntok][top_k]. */
+int hale_moe_forward(hale_moe *moe, size_t ntok, const float *x,
+                     const float *logits, float *out, uint32_t *index,
+                     float *weight);
+int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
+                            const float *d_logits, float *d_out,
+                            uint32_t *d_index, float *d_weight);
+
+/* Registers experts first .. first+count-1 from device buffers holding
+ * their reference-layout bytes back to back: d_gate/d_up [count][I][H],
+ * d_down [count][H][I] (bulk form of hale_moe_set_expert_device). */
+int hale_moe_set_experts_device(hale_moe *moe, uint32_t first, uint32_t count,
+                                const void *d_gate, const void *d_up,
+                                const void *d_down);
+
+/* Ref: ExpertProvider::routing_stats (src/expert/mod.rs:136) /
+ * RoutingStats::count (src/expert/stats.rs:53-55): selections per expert
+ * of this layer since creation.  counts[num_experts]. */
+int hale_moe_routing_counts(hale_moe *moe, uint64_t *counts);
+
+/* ---- support entry points -------------------------------------------
+ * No counterpart in the reference: device memory, timing and graph capture
+ * for benchmarks and tests, so that a caller needs no second HIP runtime. */
+
+int hale_device_malloc(hale_ctx *ctx, size_t bytes, void **out);
+int hale_device_free(hale_ctx *ctx, void *p);
+/* Synchronous copies between host and device memory. */
+int hale_memcpy_htod(hale_ctx *ctx, void *dst, const void *src, size_t n);
+int hale_memcpy_dtoh(hale_ctx *ctx, void *dst, const void *src, size_t n);
+/* Fills d_out[n] with seeded N(mean, std^2) values (counter-based
+ * generator, enqueued on the context's stream). */
+int hale_fill_normal_device(hale_ctx *ctx, uint64_t seed, float mean,
+                            float std, float *d_out, size_t n);
+
+/* Wall time of the work enqueued between start and stop, from HIP events
+ * recorded on the context's stream; stop waits for that work. */
+int hale_timer_start(hale_ctx *ctx);
+int hale_timer_stop(hale_ctx *ctx, double *ms);
+
+/* Per-kernel timing: while enabled, every kernel the context launches is
+ * bracketed by HIP events on its stream.  hale_profile_read waits for the
+ * stream and returns the summed duration and launch count of one kernel
+ * kind since the last reset; hale_kernel_name names the kinds
+ * (0 .. hale_kernel_kinds()-1). */
+int hale_profile_enable(hale_ctx *ctx, int on);
+int hale_profile_read(hale_ctx *ctx, int kind, double *total_ms,
+                      uint64_t *launches);
+int hale_profile_reset(hale_ctx *ctx);
+int hale_kernel_kinds(void);
+const char *hale_kernel_name(int kind);
+
+/* Graph capture of the context's stream: the _device entry points called
+ * between begin and end are recorded (not run) and replayed by launch. */
+typedef struct hale_graph hale_graph;
+int hale_graph_begin(hale_ctx *ctx);
+int hale_graph_end(hale_ctx *ctx, hale_graph **out);
+int hale_graph_launch(hale_graph *g);
+void hale_graph_destroy(hale_graph *g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HALE_MOE_H */

@@ -1,0 +1,228 @@
+"""GPU parity of the decode path against the CPU oracle, through the C ABI.
+
+Bar: bit-exact.  Quantization codes and scales, per-block i32 sums and the
+f32 outputs of matvec, Expert::forward and MoeLayer::forward all equal the
+oracle's bits (the kernels keep the reference's left-to-right block order).
+The north-star tolerance for f32 outputs, rel-L2 <= 1e-5, is asserted as
+well, so a failure reports both.
+"""
+import numpy as np
+import pytest
+
+import hale_moe as H
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-5
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return a.shape == b.shape and bool((a.view(np.uint32) == b.view(np.uint32)).all())
+
+
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def assert_parity(got, want):
+    assert rel_l2(got, want) <= REL_L2
+    assert same_bits(got, want)
+
+
+# ---------------------------------------------------------------------------
+# quantization
+# ---------------------------------------------------------------------------
+
+def test_act_quant_bit_exact(ctx):
+    x = O.normal(1, 4096)
+    x[32:64] = 0.0                          # zero block
+    x[64:96] *= 1e-30                       # subnormal products
+    x[96:128] = O.test_values(32, 3) * 127  # scale exactly near 1
+    x[128] = np.inf                         # inf block: scale inf, codes 0
+    q = H.Q8Activations.quantize(ctx, x)
+    s, c = O.q8_quantize(x)
+    assert same_bits(q.scales, s)
+    assert (q.quants == c).all()
+    with pytest.raises(ValueError):
+        H.Q8Activations.quantize(ctx, np.zeros(33, np.float32))
+
+
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+def test_encode_rows_bit_exact(ctx, dtype):
+    rows, cols = 96, 256
+    v = O.normal(4, rows * cols, 0.0, 0.02).reshape(rows, cols)
+    v[0, :32] = 0.0
+    v[1, :32] = 1e-6 * O.normal(5, 32)       # f16 subnormal scales
+    v[2, :32] = [-8.0, 8.0] + [0.0] * 30     # q4 tie: first wins
+    v[3, :32] = [2.5, -2.5, 127.0] + [0.0] * 29
+    v[4, :32] = 7e4                          # scale overflows f16 for q4 -> inf
+    got = H.encode_rows(ctx, dtype, v)
+    want = O.encode_matrix(dtype, v)
+    assert (got == want).all()
+
+
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+def test_upload_download_round_trip(ctx, dtype):
+    rows, cols = 100, 96   # rows not a multiple of the 64-row group
+    w = O.encode_matrix(dtype, O.normal(6, rows * cols, 0, 0.02).reshape(rows, cols))
+    m = H.WeightMatrix.new(ctx, rows, cols, dtype, w)
+    assert (m.bytes() == w).all()
+    with pytest.raises(ValueError):
+        H.WeightMatrix.new(ctx, rows, cols, dtype, w[:-1])
+
+
+# ---------------------------------------------------------------------------
+# matvec
+# ---------------------------------------------------------------------------
+
+SHAPES = [(768, 2048), (2048, 768), (1536, 4096), (4096, 1536), (32, 64), (100, 96), (4096, 14336)]
+
+
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_matvec_bit_exact(ctx, dtype, rows, cols):
+    w = O.encode_matrix(dtype, O.normal(rows + cols, rows * cols, 0, 0.02).reshape(rows, cols))
+    x = O.normal(7, cols)
+    m = H.WeightMatrix.new(ctx, rows, cols, dtype, w)
+    got = m.matvec(x)
+    want = O.matvec(dtype, rows, cols, w, x, nthreads=8)
+    assert_parity(got, want)
+    if rows * cols <= 2048 * 768:
+        assert (m.block_sums(x) == O.matvec_block_sums(dtype, rows, cols, w, x)).all()
+
+
+def test_matvec_rejects_wrong_lengths(ctx):
+    w = O.encode_matrix(H.Q8_0, O.normal(1, 64 * 64).reshape(64, 64))
+    m = H.WeightMatrix.new(ctx, 64, 64, H.Q8_0, w)
+    with pytest.raises(ValueError):
+        m.matvec(np.zeros(63, np.float32))
+    with pytest.raises(ValueError):
+        m.matvec(np.zeros(64, np.float32), out=np.zeros(10, np.float32))
+
+
+def test_from_f32_quantizes_on_the_gpu(ctx):
+    v = O.normal(8, 64 * 128, 0, 0.5)
+    m = H.WeightMatrix.from_f32(ctx, 64, 128, "q4_0", v)
+    assert (m.bytes() == O.encode_matrix(O.Q4_0, v.reshape(64, 128))).all()
+
+
+# ---------------------------------------------------------------------------
+# Expert::forward
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+@pytest.mark.parametrize("hidden,inter", [(2048, 768), (64, 32), (4096, 1536)])
+def test_expert_forward_bit_exact(ctx, dtype, hidden, inter):
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, 1, 1, seed=hidden + inter, with_router=False)
+    gate = H.WeightMatrix.new(ctx, inter, hidden, dtype, L.gate[0])
+    up = H.WeightMatrix.new(ctx, inter, hidden, dtype, L.up[0])
+    down = H.WeightMatrix.new(ctx, hidden, inter, dtype, L.down[0])
+    x = O.normal(9, hidden)
+    got = H.Expert(gate, up, down).forward(x)
+    want = O.expert_forward(dtype, hidden, inter, L.gate[0], L.up[0], L.down[0], x, nthreads=8)
+    assert_parity(got, want)
+
+
+# ---------------------------------------------------------------------------
+# MoeLayer
+# ---------------------------------------------------------------------------
+
+def make_layer(ctx, L: "O.OracleMoe", layer_id=0):
+    router = None
+    if L.router is not None:
+        router = H.WeightMatrix.new(ctx, L.num_experts, L.hidden, "f32", L.router.view(np.uint8))
+    moe = H.MoeLayer(ctx, layer_id, L.num_experts, L.hidden, L.inter, L.dtype, L.top_k,
+                     L.normalize, router)
+    for e in range(L.num_experts):
+        moe.set_expert(e, L.gate[e], L.up[e], L.down[e])
+    return moe
+
+
+@pytest.fixture(scope="module")
+def qwen30b_q4(ctx):
+    """128 experts, H 2048, I 768, q4_0, top-8 renormalised, f32 router."""
+    L = O.OracleMoe.synthetic(O.Q4_0, 2048, 768, 128, 8, normalize_topk=True, seed=101)
+    return L, make_layer(ctx, L)
+
+
+def test_moe_route_matches_oracle(ctx, qwen30b_q4):
+    L, moe = qwen30b_q4
+    for seed in range(5):
+        x = O.normal(1000 + seed, 2048)
+        routes = moe.route(x)
+        idx, w = L.route(x)
+        assert [r.key.expert for r in routes] == list(idx)
+        assert same_bits([r.weight for r in routes], w)
+
+
+def test_moe_decode_qwen30b_q4_bit_exact(ctx, qwen30b_q4):
+    L, moe = qwen30b_q4
+    for seed in range(4):
+        x = O.normal(2000 + seed, 2048)
+        out, idx, w = moe.forward(x, return_routes=True)
+        o_out, o_idx, o_w = L.forward(x, nthreads=8)
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+
+
+def test_moe_multi_token_equals_per_token(ctx, qwen30b_q4):
+    L, moe = qwen30b_q4
+    xs = O.normal(3000, 6 * 2048).reshape(6, 2048)
+    out, idx, w = moe.forward(xs, return_routes=True)
+    o_out, o_idx, o_w = L.prefill(xs, nthreads=8)
+    assert (idx == o_idx).all()
+    assert same_bits(w, o_w)
+    assert_parity(out, o_out)
+
+
+def test_routing_stats_count_selections(ctx):
+    L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 8, 3, seed=5)
+    moe = make_layer(ctx, L, layer_id=3)
+    xs = O.normal(6, 10 * 64).reshape(10, 64)
+    _, idx, _ = moe.forward(xs, return_routes=True)
+    counts = moe.experts.routing_counts()
+    assert counts.sum() == 30
+    for e in range(8):
+        assert counts[e] == int((idx == e).sum())
+    assert moe.experts.fetch([H.ExpertKey(3, 1)]) == [H.ExpertKey(3, 1)]
+    with pytest.raises(KeyError):
+        moe.experts.fetch([H.ExpertKey(3, 8)])
+
+
+def test_missing_expert_is_reported(ctx):
+    moe = H.MoeLayer(ctx, 0, 4, 64, 32, "q8_0", 2, True, None)
+    with pytest.raises(KeyError):
+        moe.forward(np.zeros(64, np.float32), logits=np.zeros(4, np.float32))
+
+
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+def test_moe_logits_given_zipf_routing(ctx, dtype):
+    """Router logits supplied directly (the skewed-routing workloads)."""
+    E, Hd, I, k, T = 32, 256, 64, 4, 8
+    L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
+    moe = make_layer(ctx, L)
+    rng = np.random.default_rng(1)
+    p = np.arange(1, E + 1, dtype=np.float64) ** -1.1
+    logits = (np.log(p / p.sum())[rng.permutation(E)] + rng.gumbel(size=(T, E))).astype(np.float32)
+    xs = O.normal(8, T * Hd).reshape(T, Hd)
+    out, idx, w = moe.forward(xs, logits=logits, return_routes=True)
+    o_out, o_idx, o_w = L.prefill(xs, logits=logits, nthreads=8)
+    assert (idx == o_idx).all()
+    assert same_bits(w, o_w)
+    assert_parity(out, o_out)
+
+
+def test_moe_top_k_clamped_and_unnormalised(ctx):
+    L = O.OracleMoe.synthetic(O.Q4_0, 64, 32, 4, 6, normalize_topk=False, seed=3)
+    moe = make_layer(ctx, L)
+    x = O.normal(4, 64)
+    out, idx, w = moe.forward(x, return_routes=True)
+    o_out, o_idx, o_w = L.forward(x)
+    assert len(idx) == 4 and list(idx) == list(o_idx)
+    assert same_bits(w, o_w)
+    assert_parity(out, o_out)

@@ -1,0 +1,481 @@
+"""Pins of the CPU oracle (oracle/hale_oracle.c) against things other than
+itself: the reference's own unit tests and known answers, closed forms,
+library routines (numpy's IEEE half conversion) and brute force.
+
+Each test names the oracle function it pins and the mistake it would catch.
+No GPU is needed.
+"""
+import math
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+F2 = np.float32
+
+
+def f16_bits(v: float) -> int:
+    """IEEE binary16 bits of v by numpy (round to nearest even)."""
+    return int(np.array([v], dtype=np.float32).astype(np.float16).view(np.uint16)[0])
+
+
+def q8_block(scale_bits: int, codes) -> np.ndarray:
+    b = np.zeros(34, dtype=np.uint8)
+    b[0], b[1] = scale_bits & 0xFF, scale_bits >> 8
+    b[2:] = np.asarray(codes, dtype=np.int8).view(np.uint8)
+    return b
+
+
+# ---------------------------------------------------------------------------
+# geometry: DType::row_bytes (src/tensor/dtype.rs:53-61)
+# ---------------------------------------------------------------------------
+
+def test_row_bytes_known_answers():
+    # src/tensor/dtype.rs:120-127
+    assert O.row_bytes(O.F32, 64) == 256
+    assert O.row_bytes(O.BF16, 64) == 128
+    assert O.row_bytes(O.Q8_0, 64) == 68
+    assert O.row_bytes(O.Q4_0, 64) == 36
+    assert O.row_bytes(O.Q4_0, 33) == -1
+    # bits_per_weight 4.5 for q4_0 (dtype.rs:140)
+    assert O.block_bytes(O.Q4_0) * 8 / 32 == 4.5
+
+
+# ---------------------------------------------------------------------------
+# f16 conversion (half 2.7.1, used at src/tensor/quant.rs:44-46,299,316)
+# ---------------------------------------------------------------------------
+
+def test_f32_to_f16_matches_f16c_on_every_float(tmp_path):
+    """Exhaustive over all 2^32 bit patterns against the F16C instruction
+    (NaN payloads excluded): catches truncation instead of RNE, a missing
+    subnormal path or a wrong overflow threshold."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    exe = tmp_path / "f16c_check"
+    odir = os.path.dirname(O.__file__)
+    subprocess.run(["gcc", "-O2", "-mf16c", "-mavx", os.path.join(here, "native", "f16c_check.c"),
+                    "-o", str(exe), f"-L{odir}", "-lhale_oracle", f"-Wl,-rpath,{odir}", "-lm"],
+                   check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    assert int(out.strip()) == 0
+
+
+def test_f32_to_f16_matches_numpy_on_a_sample():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    bits[:65536] = (np.arange(65536, dtype=np.uint32) << 13) + 0x1000  # ties
+    vals = bits.view(np.float32)
+    ours = np.array([O.f32_to_f16(float(v)) for v in vals[:4096]], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        ref = vals[:4096].astype(np.float16).view(np.uint16)
+    ok = (ours == ref) | np.isnan(vals[:4096])
+    assert ok.all()
+
+
+def test_f16_to_f32_is_exact_for_all_halves():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    ours = np.array([O.f16_to_f32(int(v)) for v in h], dtype=np.float32)
+    same = (ours.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(ours) & np.isnan(ref))
+    assert same.all()
+
+
+# ---------------------------------------------------------------------------
+# encode / decode (src/tensor/quant.rs:236-321)
+# ---------------------------------------------------------------------------
+
+def test_q8_encode_known_answer_rounds_half_away_from_zero():
+    """amax = 127 makes scale = inv = 1, so codes = round(v): 2.5 -> 3 and
+    -2.5 -> -3 (banker's rounding would give 2 / -2)."""
+    v = np.zeros(32, dtype=np.float32)
+    v[:8] = [127, -126.5, 2.5, -2.5, 0.5, -0.5, 0.49999997, 1.5]
+    b = O.encode_row(O.Q8_0, v)
+    assert b.size == 34
+    assert (int(b[0]) | (int(b[1]) << 8)) == 0x3C00  # f16(1.0)
+    codes = b[2:].view(np.int8)
+    assert list(codes[:8]) == [127, -127, 3, -3, 1, -1, 0, 2]
+    assert (codes[8:] == 0).all()
+
+
+def test_q8_encode_scale_is_f16_of_unrounded_f32_scale():
+    v = O.test_values(32, 5)
+    b = O.encode_row(O.Q8_0, v)
+    amax = np.max(np.abs(v))
+    s = F2(amax) / F2(127.0)
+    assert (int(b[0]) | (int(b[1]) << 8)) == f16_bits(float(s))
+
+
+def test_q4_encode_known_answers():
+    """extreme = -8 gives scale 1: q = trunc(v + 8.5) clamped to 0..15;
+    element j sits in the low nibble of byte j, element j+16 in the high."""
+    v = np.zeros(32, dtype=np.float32)
+    v[0] = -8.0
+    v[1:8] = [7.0, -0.5, -0.6, 3.4, 3.5, 7.6, -7.9]
+    v[16:20] = [1.0, 2.0, -1.0, 7.4]
+    b = O.encode_row(O.Q4_0, v)
+    assert b.size == 18
+    assert (int(b[0]) | (int(b[1]) << 8)) == 0x3C00
+    lo = [int(x) & 0xF for x in b[2:]]
+    hi = [int(x) >> 4 for x in b[2:]]
+    # v+8.5 truncated: -8->0, 7->15, -0.5->8, -0.6->7, 3.4->11, 3.5->12, 7.6->15(clamp), -7.9->0
+    assert lo[:8] == [0, 15, 8, 7, 11, 12, 15, 0]
+    assert hi[:4] == [9, 10, 7, 15]
+    assert lo[8:] == [8] * 8 and hi[4:] == [8] * 12
+
+
+def test_q4_encode_positive_extreme_gives_negative_scale_and_first_tie_wins():
+    v = np.zeros(32, dtype=np.float32)
+    v[0], v[1] = 8.0, -8.0   # |8| == |-8|: the first one is the extreme
+    b = O.encode_row(O.Q4_0, v)
+    assert (int(b[0]) | (int(b[1]) << 8)) == 0xBC00  # f16(-1.0)
+    # inv = -1: 8 -> trunc(-8 + 8.5) = 0; -8 -> trunc(8 + 8.5) = 16 -> 15
+    assert int(b[2]) & 0xF == 0 and int(b[3]) & 0xF == 15
+    v[0], v[1] = -8.0, 8.0
+    b = O.encode_row(O.Q4_0, v)
+    assert (int(b[0]) | (int(b[1]) << 8)) == 0x3C00
+
+
+def test_every_dtype_round_trips_within_its_precision():
+    # src/tensor/quant.rs:344-366 (values(96, 7), the reference's tolerances)
+    v = O.test_values(96, 7)
+    for dtype, tol in [(O.F32, 0.0), (O.F16, 1e-3), (O.BF16, 1e-2), (O.Q8_0, 1e-2), (O.Q4_0, 0.15)]:
+        b = O.encode_row(dtype, v)
+        assert b.size == O.row_bytes(dtype, v.size)
+        back = O.decode_row(dtype, b, v.size)
+        assert np.max(np.abs(v - back)) <= tol, dtype
+
+
+def test_zero_block_quantizes_to_zero():
+    # src/tensor/quant.rs:422-432.  q8_0 stores f16(0/127) = +0; q4_0 stores
+    # f16(0 / -8) = -0 (0x8000); both decode to zeros.
+    z = np.zeros(32, dtype=np.float32)
+    for dtype, bits in ((O.Q8_0, 0x0000), (O.Q4_0, 0x8000)):
+        b = O.encode_row(dtype, z)
+        assert (int(b[0]) | (int(b[1]) << 8)) == bits
+        assert (b[2:] == (0 if dtype == O.Q8_0 else 0x88)).all()
+        assert (O.decode_row(dtype, b, 32) == 0).all()
+
+
+def test_decode_q4_nibble_order():
+    b = np.zeros(18, dtype=np.uint8)
+    b[0], b[1] = 0x00, 0x3C
+    b[2] = 0x9F   # element 0 = 15-8 = 7, element 16 = 9-8 = 1
+    b[17] = 0x30  # element 15 = 0-8 = -8, element 31 = 3-8 = -5
+    d = O.decode_row(O.Q4_0, b, 32)
+    assert d[0] == 7 and d[16] == 1 and d[15] == -8 and d[31] == -5
+
+
+# ---------------------------------------------------------------------------
+# activation quantization: Q8Activations::quantize (quant.rs:77-93)
+# ---------------------------------------------------------------------------
+
+def test_activation_scale_stays_f32_and_codes_round_half_away():
+    x = np.zeros(64, dtype=np.float32)
+    x[0:4] = [1.0, -0.25, 0.5, 0.0]              # amax 1 -> scale 1/127 (f32)
+    x[32:36] = [127.0, 2.5, -2.5, -126.5]        # amax 127 -> scale 1
+    s, q = O.q8_quantize(x)
+    assert s[0] == F2(1.0) / F2(127.0)            # not rounded to f16
+    assert f16_bits(float(s[0])) != int(np.float32(s[0]).view(np.uint32) >> 16)
+    assert s[1] == 1.0
+    assert list(q[32:36]) == [127, 3, -3, -127]
+    assert q[0] == 127 and q[3] == 0
+    with pytest.raises(ValueError):
+        O.q8_quantize(np.zeros(33, dtype=np.float32))
+
+
+# ---------------------------------------------------------------------------
+# block dot products: dot_q8_0 / dot_q4_0 (quant.rs:115-144)
+# ---------------------------------------------------------------------------
+
+def test_block_sums_equal_brute_force_int64():
+    """isum_b from the decoded codes in int64 (scale 1 blocks make decode
+    return the codes themselves); catches a wrong nibble pairing."""
+    rng = np.random.default_rng(3)
+    for dtype in (O.Q8_0, O.Q4_0):
+        nb = 5
+        row = np.zeros(nb * O.block_bytes(dtype), dtype=np.uint8)
+        for b in range(nb):
+            blk = row[b * O.block_bytes(dtype):(b + 1) * O.block_bytes(dtype)]
+            blk[0], blk[1] = 0x00, 0x3C
+            blk[2:] = rng.integers(0, 256, blk.size - 2, dtype=np.uint8)
+        x = rng.normal(size=nb * 32).astype(np.float32)
+        xs, xq = O.q8_quantize(x)
+        _, isums = O.dot_quantized(dtype, row, xs, xq)
+        codes = O.decode_row(dtype, row, nb * 32).astype(np.int64)
+        brute = (codes.reshape(nb, 32) * xq.astype(np.int64).reshape(nb, 32)).sum(axis=1)
+        assert (isums == brute).all()
+
+
+def test_block_terms_are_summed_left_to_right():
+    """Terms t = [1, 2^24, 1, -2^24]: left to right gives 0 (1 is absorbed
+    twice by round-to-even), a pairwise sum gives 1, right-to-left gives 2."""
+    x = np.zeros(4 * 32, dtype=np.float32)
+    for b in range(4):
+        x[b * 32:b * 32 + 3] = [127.0, 127.0, 1.0]   # scale 1, codes [127,127,1,0..]
+    xs, xq = O.q8_quantize(x)
+    assert (xs == 1.0).all()
+    # isum = 127*(a0+a1) + a2; (dw, codes) per wanted term
+    blocks = [
+        q8_block(0x3C00, [0, 0, 1] + [0] * 29),           # 1 * 1
+        q8_block(0x6400, [127, 2, 1] + [0] * 29),         # 1024 * 16384 = 2^24
+        q8_block(0x3C00, [0, 0, 1] + [0] * 29),           # 1
+        q8_block(0xE400, [127, 2, 1] + [0] * 29),         # -1024 * 16384
+    ]
+    row = np.concatenate(blocks)
+    total, isums = O.dot_quantized(O.Q8_0, row, xs, xq)
+    assert list(isums) == [1, 16384, 1, 16384]
+    assert total == 0.0
+
+
+def test_block_term_is_scale_product_times_isum():
+    """(d_w * d_x) * isum, not d_w * (d_x * isum): search a case where the two
+    differ in f32 and check the oracle follows the reference's grouping."""
+    rng = np.random.default_rng(11)
+    for _ in range(2000):
+        dw_bits = int(rng.integers(0x2000, 0x3C00))
+        dw = np.float32(np.uint16(dw_bits).view(np.float16))
+        x = rng.normal(size=32).astype(np.float32)
+        xs, xq = O.q8_quantize(x)
+        codes = rng.integers(-127, 128, 32)
+        isum = int((codes * xq.astype(np.int64)).sum())
+        a = (dw * xs[0]) * F2(isum)
+        b = dw * (xs[0] * F2(isum))
+        if a != b:
+            total, _ = O.dot_quantized(O.Q8_0, q8_block(dw_bits, codes), xs, xq)
+            assert total == F2(0.0) + a
+            return
+    pytest.fail("no distinguishing case found")
+
+
+def test_dot_equals_dot_of_decoded_row():
+    # src/tensor/quant.rs:368-398
+    w, x = O.test_values(64, 3), O.test_values(64, 11)
+    for dtype in (O.F32, O.F16, O.BF16, O.Q8_0, O.Q4_0):
+        b = O.encode_row(dtype, w)
+        dec = O.decode_row(dtype, b, 64)
+        expect = float(np.dot(dec.astype(np.float64), x.astype(np.float64)))
+        got = O.dot(dtype, b, x)
+        tol = 2e-2 * max(abs(expect), 1.0) if dtype in (O.Q8_0, O.Q4_0) else 1e-4
+        assert abs(expect - got) < tol, dtype
+    w13, x13 = O.test_values(13, 5), O.test_values(13, 9)
+    assert abs(O.dot(O.F32, O.encode_row(O.F32, w13), x13) - float(np.dot(w13, x13))) < 1e-5
+
+
+def test_dot_f32_uses_eight_lane_order():
+    """w = [1,1,0,0,2^24,0,0,0], x = 1: lanes give (1 + 2^24) + 1 -> 2^24
+    after two round-to-even steps; a left-to-right sum gives 2^24 + 2."""
+    w = np.array([1, 1, 0, 0, 2 ** 24, 0, 0, 0], dtype=np.float32)
+    assert O.dot_f32(w, np.ones(8, dtype=np.float32)) == 16777216.0
+    # a 4-element tail is summed after the lanes: (2^24) + (1 + 1) = 2^24 + 2
+    w2 = np.concatenate([w, np.array([1, 1, 0, 0], dtype=np.float32)])
+    assert O.dot_f32(w2, np.ones(12, dtype=np.float32)) == 16777218.0
+
+
+# ---------------------------------------------------------------------------
+# matvec (src/tensor/matrix.rs:115-143, tests :150-189)
+# ---------------------------------------------------------------------------
+
+def test_matvec_parallel_equals_serial_and_naive():
+    rows, cols = 70, 64
+    i = np.arange(rows * cols)
+    w = (((i * 37) % 101).astype(np.float32) - 50.0) / 50.0
+    x = (np.arange(cols, dtype=np.float32) / cols) - 0.5
+    expect = w.reshape(rows, cols).astype(np.float64) @ x.astype(np.float64)
+    data = w.astype(np.float32).view(np.uint8)
+    par = O.matvec(O.F32, rows, cols, data, x, nthreads=4)
+    ser = O.matvec(O.F32, rows, cols, data, x, nthreads=1)
+    assert (par.view(np.uint32) == ser.view(np.uint32)).all()
+    assert np.max(np.abs(par - expect)) < 1e-4
+    for dtype in (O.Q8_0, O.Q4_0):
+        wq = O.encode_matrix(dtype, np.sin(np.arange(96 * 128, dtype=np.float32)).reshape(96, 128))
+        xr = O.test_values(128, 2)
+        a = O.matvec(dtype, 96, 128, wq, xr, nthreads=4)
+        b = O.matvec(dtype, 96, 128, wq, xr, nthreads=1)
+        assert (a.view(np.uint32) == b.view(np.uint32)).all()
+
+
+def test_convert_quantizes_and_keeps_shape():
+    # src/tensor/matrix.rs:182-189: q8 size < f32 size / 3
+    assert O.row_bytes(O.Q8_0, 64) * 4 < O.row_bytes(O.F32, 64) * 4 / 3
+
+
+def test_matvec_rejects_bad_shapes():
+    with pytest.raises(ValueError):
+        O.matvec(O.Q4_0, 2, 33, np.zeros(100, np.uint8), np.zeros(33, np.float32))
+
+
+# ---------------------------------------------------------------------------
+# ops (src/ops/activation.rs, src/ops/topk.rs)
+# ---------------------------------------------------------------------------
+
+def test_softmax_reference_cases_and_closed_forms():
+    # activation.rs:38-44
+    p = O.softmax([1000.0, 1001.0, 1002.0])
+    assert abs(float(p.sum()) - 1.0) < 1e-6 and p[2] > p[1] > p[0]
+    # equal logits: exp(0) = 1 each, 1/4 exactly
+    assert (O.softmax([3.0, 3.0, 3.0, 3.0]) == 0.25).all()
+    # [0, ln2] up to rounding of ln2 in f32: ratio 2
+    q = O.softmax([0.0, math.log(2.0)])
+    assert abs(q[1] / q[0] - 2.0) < 1e-6
+
+
+def test_expf_is_glibc():
+    for v in (-103.0, -20.5, -1.0, 0.0, 1e-7, 0.5, 1.0, 10.0, 88.5, 89.0):
+        assert O.expf(v) == float(np.float32(math.exp(np.float32(v)))) or \
+            abs(O.expf(v) / math.exp(np.float32(v)) - 1) < 1.2e-7
+
+
+def test_silu_and_argmax_basics():
+    # activation.rs:46-51
+    assert O.silu(0.0) == 0.0
+    assert abs(O.silu(10.0) - 10.0) < 1e-3
+    assert O.argmax([1.0, 3.0, 3.0, -1.0]) == 1
+    for v in np.linspace(-30, 30, 601, dtype=np.float32):
+        exact = float(v) / (1.0 + math.exp(-float(v)))
+        assert abs(O.silu(float(v)) - exact) <= 4e-7 * max(abs(exact), 1e-30) + 1e-38
+
+
+def test_top_k_matches_full_sort():
+    # topk.rs:67-76
+    scores = np.array([((i * 73) % 128) * 0.37 - 20.0 for i in range(128)], dtype=np.float32)
+    order = sorted(range(128), key=lambda i: (-scores[i], i))
+    idx, sc = O.top_k(scores, 8)
+    assert list(idx) == order[:8]
+    assert list(sc) == [scores[i] for i in order[:8]]
+
+
+def test_top_k_ties_prefer_lower_index_and_k_is_clamped():
+    # topk.rs:78-87
+    idx, _ = O.top_k([1.0, 5.0, 5.0, 5.0], 2)
+    assert list(idx) == [1, 2]
+    assert len(O.top_k([1.0, 2.0], 10)[0]) == 2
+    assert len(O.top_k([1.0], 0)[0]) == 0
+    # total_cmp: +0.0 ranks above -0.0
+    assert list(O.top_k([-0.0, 0.0], 1)[0]) == [1]
+
+
+def test_top_k_equals_stable_sort_on_random_ties():
+    rng = np.random.default_rng(5)
+    for _ in range(50):
+        s = rng.integers(0, 6, 40).astype(np.float32)
+        k = int(rng.integers(1, 40))
+        order = sorted(range(40), key=lambda i: (-s[i], i))
+        assert list(O.top_k(s, k)[0]) == order[:k]
+
+
+# ---------------------------------------------------------------------------
+# route / expert / MoE layer
+# ---------------------------------------------------------------------------
+
+def _tiny_layer(dtype, normalize=True, E=8, H=64, I=32, k=3, seed=7):
+    return O.OracleMoe.synthetic(dtype, H, I, E, k, normalize_topk=normalize, seed=seed)
+
+
+def test_route_closed_form_for_equal_logits():
+    L = _tiny_layer(O.Q8_0, normalize=True, E=4, k=2)
+    idx, w = L.route(np.zeros(64, np.float32), logits=np.zeros(4, np.float32))
+    assert list(idx) == [0, 1] and list(w) == [0.5, 0.5]
+    L2 = _tiny_layer(O.Q8_0, normalize=False, E=4, k=2)
+    idx, w = L2.route(np.zeros(64, np.float32), logits=np.zeros(4, np.float32))
+    assert list(w) == [0.25, 0.25]
+
+
+def test_route_uses_router_matvec_softmax_topk_renorm():
+    L = _tiny_layer(O.Q4_0)
+    x = O.normal(99, 64)
+    logits = np.array([O.dot_f32(L.router[e], x) for e in range(8)], dtype=np.float32)
+    p = O.softmax(logits)
+    order = sorted(range(8), key=lambda i: (-p[i], i))[:3]
+    idx, w = L.route(x)
+    assert list(idx) == order
+    norm = F2(-0.0)
+    for i in order:
+        norm = F2(norm + p[i])
+    assert list(w) == [F2(p[i] / norm) for i in order]
+
+
+def test_expert_forward_close_to_float64_model():
+    """Only the q8 activation rounding separates the oracle from an f64 SwiGLU
+    on the dequantized weights."""
+    H, I = 256, 64
+    for dtype in (O.Q8_0, O.Q4_0):
+        L = O.OracleMoe.synthetic(dtype, H, I, 1, 1, seed=3, with_router=False)
+        x = O.normal(5, H)
+        got = O.expert_forward(dtype, H, I, L.gate[0], L.up[0], L.down[0], x)
+        dq = lambda data, r, c: np.stack([O.decode_row(dtype, data[i * O.row_bytes(dtype, c):(i + 1) * O.row_bytes(dtype, c)], c) for i in range(r)]).astype(np.float64)
+        G, U, D = dq(L.gate[0], I, H), dq(L.up[0], I, H), dq(L.down[0], H, I)
+        g, u = G @ x, U @ x
+        h = g / (1 + np.exp(-g)) * u
+        ref = D @ h
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert rel < 0.02, (dtype, rel)
+
+
+def test_moe_forward_is_weighted_sum_of_experts_in_route_order():
+    L = _tiny_layer(O.Q8_0, E=8, k=3)
+    x = O.normal(17, 64)
+    out, idx, w = L.forward(x)
+    acc = np.zeros(64, dtype=np.float32)
+    for e, wt in zip(idx, w):
+        y = O.expert_forward(O.Q8_0, 64, 32, L.gate[e], L.up[e], L.down[e], x)
+        acc = (acc + F2(wt) * y).astype(np.float32)
+    assert (out.view(np.uint32) == acc.view(np.uint32)).all()
+
+
+def test_prefill_equals_token_by_token_forward():
+    # tests/litmus.rs:47-59: prefill == per-token forward, bit for bit
+    L = _tiny_layer(O.Q4_0, E=8, k=2)
+    xs = O.normal(23, 5 * 64).reshape(5, 64)
+    out, idx, w = L.prefill(xs, nthreads=3)
+    for t in range(5):
+        o1, i1, w1 = L.forward(xs[t])
+        assert (o1.view(np.uint32) == out[t].view(np.uint32)).all()
+        assert list(i1) == list(idx[t]) and list(w1) == list(w[t])
+
+
+def test_threads_do_not_change_bits():
+    L = O.OracleMoe.synthetic(O.Q4_0, 256, 64, 16, 4, seed=9)
+    x = O.normal(2, 256)
+    a = L.forward(x, nthreads=1)[0]
+    b = L.forward(x, nthreads=6)[0]
+    c = L.forward(x, nthreads=6, variant="_v3")[0]
+    assert (a.view(np.uint32) == b.view(np.uint32)).all()
+    assert (a.view(np.uint32) == c.view(np.uint32)).all()
+
+
+# ---------------------------------------------------------------------------
+# seeded generators
+# ---------------------------------------------------------------------------
+
+def test_xorshift64star_matches_its_definition():
+    # src/generate/sampler.rs:135-140 restated with Python integers
+    s = 42
+    want = []
+    for _ in range(5):
+        s ^= s >> 12
+        s ^= (s << 25) & (2 ** 64 - 1)
+        s ^= s >> 27
+        want.append((s * 0x2545F4914F6CDD1D) & (2 ** 64 - 1))
+    assert O.xorshift64star(42, 5) == want
+    assert O.xorshift64star(0, 1) == O.xorshift64star(1, 1)  # seed.max(1)
+
+
+def test_values_helper_matches_reference_definition():
+    # src/tensor/quant.rs:328-338
+    seed = 7
+    s = (seed * 2654435761) & 0xFFFFFFFF
+    s = max(s, 1)
+    want = []
+    for _ in range(6):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        want.append(F2(F2(s) / F2(4294967295.0)) * F2(2.0) - F2(1.0))
+    assert list(O.test_values(6, 7)) == want
+
+
+def test_normals_have_the_requested_moments():
+    v = O.normal(1, 200000, 0.0, 0.02)
+    assert abs(float(v.mean())) < 2e-4 and abs(float(v.std()) - 0.02) < 2e-4
