@@ -45,28 +45,37 @@ HALE_EXPF_TABLE uint64_t hale_exp2_tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-HALE_EXPF_FN float hale_expf(float x) {
+/* Range reduction and special cases.  Returns 1 with the final result in
+ * *res for |x| >= 88, inf and nan; otherwise returns 0 with the table index
+ * (*ki % 32), ki and r for hale_expf_finish. */
+HALE_EXPF_FN int hale_expf_reduce(float x, float *res, uint64_t *ki_out, double *r_out) {
   const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
   const double shift = 0x1.8p+52;
-  const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
-  const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
-  const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
   uint32_t ix;
   __builtin_memcpy(&ix, &x, 4);
   uint32_t abstop = (ix >> 20) & 0x7ffu;
   if (abstop >= 0x42bu) { /* |x| >= 88, or inf / nan */
-    if (ix == 0xff800000u) return 0.0f; /* -inf */
-    if (abstop >= 0x7f8u) return x + x; /* inf or nan */
-    if (x > 0x1.62e42ep6f) return __builtin_huge_valf(); /* overflow */
-    if (x < -0x1.9fe368p6f) return 0.0f;                /* underflow */
+    if (ix == 0xff800000u) { *res = 0.0f; return 1; }             /* -inf */
+    if (abstop >= 0x7f8u) { *res = x + x; return 1; }             /* inf or nan */
+    if (x > 0x1.62e42ep6f) { *res = __builtin_huge_valf(); return 1; } /* overflow */
+    if (x < -0x1.9fe368p6f) { *res = 0.0f; return 1; }            /* underflow */
   }
   double xd = (double)x;
   double kd = __builtin_fma(inv_ln2_n, xd, shift);
   uint64_t ki;
   __builtin_memcpy(&ki, &kd, 8);
   kd -= shift;
-  double r = __builtin_fma(inv_ln2_n, xd, -kd);
-  uint64_t t = hale_exp2_tab[ki % 32] + (ki << 47);
+  *ki_out = ki;
+  *r_out = __builtin_fma(inv_ln2_n, xd, -kd);
+  return 0;
+}
+
+/* 2^(k/32) from the table entry of ki % 32, times the polynomial for r. */
+HALE_EXPF_FN float hale_expf_finish(uint64_t ki, double r, uint64_t tab_entry) {
+  const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  uint64_t t = tab_entry + (ki << 47);
   double s;
   __builtin_memcpy(&s, &t, 8);
   double z = __builtin_fma(c0, r, c1);
@@ -75,6 +84,14 @@ HALE_EXPF_FN float hale_expf(float x) {
   y = __builtin_fma(z, r2, y);
   y = y * s;
   return (float)y;
+}
+
+HALE_EXPF_FN float hale_expf(float x) {
+  float res;
+  uint64_t ki;
+  double r;
+  if (hale_expf_reduce(x, &res, &ki, &r)) return res;
+  return hale_expf_finish(ki, r, hale_exp2_tab[ki % 32]);
 }
 
 #endif /* HALE_GLIBC_EXPF_H */

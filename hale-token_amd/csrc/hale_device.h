@@ -44,6 +44,10 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 }
 
 __device__ __forceinline__ uint16_t f2h(float f) {
+  // The empty asm keeps f a rounded f32 value: without it the compiler may
+  // fold a producing multiply into v_fma_mix* with a +0 addend, which rounds
+  // the exact product straight to f16 and turns a -0 product into +0.
+  asm volatile("" : "+v"(f));
   _Float16 v = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
   uint16_t h;
   __builtin_memcpy(&h, &v, 2);
@@ -66,8 +70,30 @@ __device__ __forceinline__ int sat_i32(float v) {
   return (int)v;
 }
 
+// exp for a whole wave (all lanes active): the 2^(i/32) table entry comes
+// from a register of lane i (ExpTable, loaded once per kernel) through a
+// lane shuffle instead of a per-lane memory lookup.
+struct ExpTable {
+  uint64_t entry;  // hale_exp2_tab[lane % 32]
+  __device__ __forceinline__ void load() {
+    entry = hale_exp2_tab[__lane_id() & 31];
+  }
+};
+
+__device__ __forceinline__ float wave_expf(float x, const ExpTable& tab) {
+  float res;
+  uint64_t ki = 0;
+  double r = 0.0;
+  const int fin = hale_expf_reduce(x, &res, &ki, &r);
+  const uint64_t te = __shfl(tab.entry, (int)(ki & 31));  // every lane takes part
+  return fin ? res : hale_expf_finish(ki, r, te);
+}
+
 // silu, src/ops/activation.rs:5-7: x / (1 + exp(-x)).
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + hale_expf(-x)); }
+__device__ __forceinline__ float wave_silu(float x, const ExpTable& tab) {
+  return x / (1.0f + wave_expf(-x, tab));
+}
 
 // f32::total_cmp as a signed integer key.
 __device__ __forceinline__ int total_key(float v) {
@@ -77,22 +103,82 @@ __device__ __forceinline__ int total_key(float v) {
 
 // ---- wave helpers ---------------------------------------------------------
 
+// Reductions over a full wave (all 64 lanes active): DPP within 16-lane rows
+// (xor 1, xor 2, half mirror, mirror), ds_swizzle across the two rows of a
+// 32-lane half, readlane across the halves.  The result is wave-uniform.
+template <typename Op>
+__device__ __forceinline__ unsigned wave_reduce_u32(unsigned x, Op op) {
+  x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));   // xor 1
+  x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));   // xor 2
+  x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false));  // half mirror
+  x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false));  // mirror
+  x = op(x, (unsigned)__builtin_amdgcn_ds_swizzle((int)x, 0x401F));                     // xor 16
+  unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)x, 0);
+  unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)x, 32);
+  return op(lo, hi);
+}
+
+struct OpMaxU { __device__ unsigned operator()(unsigned a, unsigned b) const { return a > b ? a : b; } };
+struct OpMinU { __device__ unsigned operator()(unsigned a, unsigned b) const { return a < b ? a : b; } };
+struct OpOrU { __device__ unsigned operator()(unsigned a, unsigned b) const { return a | b; } };
+struct OpAndU { __device__ unsigned operator()(unsigned a, unsigned b) const { return a & b; } };
+struct OpMaxF {
+  __device__ unsigned operator()(unsigned a, unsigned b) const {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }
+};
+
+// Maximum of a u64 over the full wave (all lanes active), wave-uniform.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
+  auto step = [&](unsigned lo, unsigned hi) {
+    const unsigned long long y = ((unsigned long long)hi << 32) | lo;
+    x = y > x ? y : x;
+  };
+#define HALE_DPP_MAX64(ctrl)                                                              \
+  step((unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)x, ctrl, 0xF, 0xF, false), \
+       (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(x >> 32), ctrl, 0xF, 0xF, false))
+  HALE_DPP_MAX64(0xB1);   // xor 1
+  HALE_DPP_MAX64(0x4E);   // xor 2
+  HALE_DPP_MAX64(0x141);  // half mirror
+  HALE_DPP_MAX64(0x140);  // mirror
+#undef HALE_DPP_MAX64
+  step((unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)x, 0x401F),
+       (unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)(x >> 32), 0x401F));  // xor 16
+  const unsigned long long a = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(x >> 32), 0) << 32) |
+                               (unsigned)__builtin_amdgcn_readlane((int)(unsigned)x, 0);
+  const unsigned long long b = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(x >> 32), 32) << 32) |
+                               (unsigned)__builtin_amdgcn_readlane((int)(unsigned)x, 32);
+  return a > b ? a : b;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  return __uint_as_float(wave_reduce_u32(__float_as_uint(v), OpMaxF()));
+}
+
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Reductions within each 32-lane half of a wave (all lanes active): DPP
+// inside 16-lane rows, ds_swizzle across the two rows of a half.  Every lane
+// of a half gets its half's result.
+#define HALE_DPP_F32(x, ctrl) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false))
 __device__ __forceinline__ float half_wave_max(float v) {
-  // 32-lane groups (lanes 0-31 and 32-63 reduce separately)
-  v = fmaxf(v, __shfl_xor(v, 16, 32));
-  v = fmaxf(v, __shfl_xor(v, 8, 32));
-  v = fmaxf(v, __shfl_xor(v, 4, 32));
-  v = fmaxf(v, __shfl_xor(v, 2, 32));
-  v = fmaxf(v, __shfl_xor(v, 1, 32));
+  v = fmaxf(v, HALE_DPP_F32(v, 0xB1));
+  v = fmaxf(v, HALE_DPP_F32(v, 0x4E));
+  v = fmaxf(v, HALE_DPP_F32(v, 0x141));
+  v = fmaxf(v, HALE_DPP_F32(v, 0x140));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
   return v;
 }
 
 __device__ __forceinline__ int half_wave_sum(int v) {
-  v += __shfl_xor(v, 16, 32);
-  v += __shfl_xor(v, 8, 32);
-  v += __shfl_xor(v, 4, 32);
-  v += __shfl_xor(v, 2, 32);
-  v += __shfl_xor(v, 1, 32);
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  v += __builtin_amdgcn_ds_swizzle(v, 0x401F);
   return v;
 }
 

@@ -33,7 +33,34 @@ struct GemvArgs {
   ActBlock* hact;          // [slots][hact_stride] (EPI_GATE_UP)
   int hact_stride;
   int slots;
+  // EPI_GATE_UP with routing in the prologue: when logits is set, the
+  // slot's expert is selected from logits[E] (softmax, top-k, renormalise)
+  // and published to route_out_idx / route_out_w (and counted in stats).
+  const float* logits;
+  int E;
+  int normalize;
+  int* route_out_idx;
+  float* route_out_w;
+  unsigned long long* stats;
 };
+
+// Arguments of the down projection + combine (k_down_combine).
+struct DownArgs {
+  const uint8_t* codes;
+  const uint16_t* scales;
+  size_t codes_stride;     // bytes per expert
+  size_t scales_stride;    // f16 elements per expert
+  int nb;                  // blocks per row (inter / 32)
+  int rows;                // hidden
+  const ActBlock* hact;    // [slots][hact_stride]
+  int hact_stride;
+  const int* route_idx;    // [slots]
+  const float* route_w;    // [slots]
+  int slots;
+  float* out;              // [rows]
+};
+
+hipError_t launch_down_combine(int dtype, const DownArgs& a, int groups, hipStream_t st);
 
 hipError_t launch_repack(int dtype, const uint8_t* aos, size_t rows, size_t cols, uint8_t* codes,
                          uint16_t* scales, hipStream_t st);
@@ -42,10 +69,11 @@ hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales
 hipError_t launch_encode(int dtype, const float* values, size_t nblocks, uint8_t* out,
                          hipStream_t st);
 hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipStream_t st);
-hipError_t launch_route(const float* router, const float* logits_in, const float* x, int H, int E,
-                        int k, int normalize, int T, ActBlock* act, float* logits,
-                        unsigned* counters, int* route_idx, float* route_w,
-                        unsigned long long* stats, hipStream_t st);
+hipError_t launch_route_logits(const float* router, const float* x, int H, int E, int T,
+                               ActBlock* act, float* logits, hipStream_t st);
+hipError_t launch_route_select(const float* logits, int E, int k, int normalize, int T,
+                               int* route_idx, float* route_w, unsigned long long* stats,
+                               hipStream_t st);
 hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int slots,
                        hipStream_t st);
 hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,

@@ -161,27 +161,22 @@ __global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, 
 // Router: MoeLayer::route (src/model/moe.rs:36-53)
 // ===========================================================================
 //
-// grid (gx, T), 64 threads.  With a router matrix gx == E and work-group e
-// computes logit e of token t with the 8-lane f32 order of dot_f32
-// (quant.rs:37-41,152-194); otherwise the logits are given and gx == 1.
-// Every work-group also quantizes a share of token t's activation blocks.
-// The last work-group of a token (counter) runs softmax, top-k and the
-// renormalisation in one wave and resets the counter for the next launch.
+// Two parts.  k_route_logits (grid (E, T), 64 threads) computes logit e of
+// token t with the 8-lane f32 order of dot_f32 (quant.rs:37-41,152-194) and
+// quantizes a share of token t's activation blocks.  route_select (one
+// wave) turns E logits into the top-k experts and their weights; the
+// gate/up kernel runs it in every work-group's prologue, so no work-group
+// ever waits for another.
 
 constexpr int ROUTE_MAX_H = 8192;
 constexpr int ROUTE_MAX_E = 1024;
+constexpr int GEMV_MAX_NB = 512;  // blocks per row the GEMV stages in LDS
 
-__global__ __launch_bounds__(64) void k_route(const float* __restrict__ router,
-                                              const float* __restrict__ logits_in,
-                                              const float* __restrict__ x, int H, int E, int k,
-                                              int normalize, ActBlock* __restrict__ act,
-                                              float* __restrict__ logits, unsigned* counters,
-                                              int* __restrict__ route_idx,
-                                              float* __restrict__ route_w,
-                                              unsigned long long* __restrict__ stats) {
-  __shared__ __attribute__((aligned(16))) float prod[ROUTE_MAX_H + 32];  // products, chain-major
-  __shared__ float sm[ROUTE_MAX_E];
-  __shared__ int last_flag;
+__global__ __launch_bounds__(64) void k_route_logits(const float* __restrict__ router,
+                                                     const float* __restrict__ x, int H, int E,
+                                                     ActBlock* __restrict__ act,
+                                                     float* __restrict__ logits) {
+  __shared__ __attribute__((aligned(16))) float prod[ROUTE_MAX_H + 32];  // chain-major
   const int lane = threadIdx.x;
   const int t = blockIdx.y;
   const int gx = gridDim.x;
@@ -189,7 +184,7 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ router,
   const float* xt = x + (size_t)t * H;
   const int nb = H / QK;
 
-  // ---- activation quantization share: half-wave h takes block 2*(e+gx*i)+h
+  // activation quantization share: half-wave h takes block 2*(e + gx*i) + h
   for (int bb = 2 * e + (lane >> 5); bb < nb; bb += 2 * gx) {
     float v = xt[bb * QK + (lane & 31)];
     float scale;
@@ -202,105 +197,178 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ router,
       ab->qsum = qsum;
     }
   }
+  if (e >= E) return;
 
-  if (router != nullptr) {
-    // ---- logit e: 8 accumulators, acc[l] += w[8i+l]*x[8i+l] in order of i
-    const float* w = router + (size_t)e * H;
-    const int steps = H / 8;
-    const int stride = steps + 4;  // keeps 16 B alignment, spreads banks
-    for (int i = lane; i < steps * 8; i += 64) prod[(i & 7) * stride + (i >> 3)] = w[i] * xt[i];
-    __syncthreads();
-    float acc = 0.0f;
-    if (lane < 8) {
-      const float* p = prod + lane * stride;
-      int s = 0;
-      for (; s + 4 <= steps; s += 4) {
-        f32x4 q = *(const f32x4*)(p + s);
-        acc = acc + q.x;
-        acc = acc + q.y;
-        acc = acc + q.z;
-        acc = acc + q.w;
-      }
-      for (; s < steps; s++) acc = acc + p[s];
-    }
-    float a0 = __shfl(acc, 0), a1 = __shfl(acc, 1), a2 = __shfl(acc, 2), a3 = __shfl(acc, 3);
-    float a4 = __shfl(acc, 4), a5 = __shfl(acc, 5), a6 = __shfl(acc, 6), a7 = __shfl(acc, 7);
-    if (lane == 0) {
-      float tail = -0.0f;  // Iterator::sum over the H % 8 leftover products
-      for (int i = steps * 8; i < H; i++) tail = tail + w[i] * xt[i];
-      float s0 = (a0 + a4) + (a1 + a5);
-      float s1 = (a2 + a6) + (a3 + a7);
-      logits[(size_t)t * E + e] = (s0 + s1) + tail;
-    }
+  // products w[i]*x[i] (each one rounding, order free) into chain-major LDS:
+  // chain l holds i = 8s + l at prod[l * stride + s]
+  const float* w = router + (size_t)e * H;
+  const int steps = H / 8;
+  const int stride = steps + 4;  // 16 B aligned rows, chains on distinct banks
+  const int nvec = steps * 2;    // float4 chunks covering the 8-lane part
+  for (int c = lane; c < nvec; c += 64) {
+    f32x4 wv = *(const f32x4*)(w + 4 * c);
+    f32x4 xv = *(const f32x4*)(xt + 4 * c);
+    const int sidx = c >> 1, l0 = (c & 1) * 4;
+    prod[(l0 + 0) * stride + sidx] = wv.x * xv.x;
+    prod[(l0 + 1) * stride + sidx] = wv.y * xv.y;
+    prod[(l0 + 2) * stride + sidx] = wv.z * xv.z;
+    prod[(l0 + 3) * stride + sidx] = wv.w * xv.w;
   }
-
-  // ---- completion: the last work-group of token t continues
-  const float* lg = logits_in ? logits_in + (size_t)t * E : logits + (size_t)t * E;
-  if (gx > 1) {
-    __threadfence();
-    if (lane == 0) last_flag = (atomicAdd(&counters[t], 1u) == (unsigned)(gx - 1));
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    if (lane == 0) counters[t] = 0u;
-  } else {
-    __threadfence();
-    __syncthreads();  // lane 0's logit store is visible to the whole group
+  __syncthreads();
+  // acc[l] += w[8i+l]*x[8i+l] in order of i, 16 values per batch of reads
+  float acc = 0.0f;
+  if (lane < 8) {
+    const float* p = prod + lane * stride;
+    int s0 = 0;
+    for (; s0 + 16 <= steps; s0 += 16) {
+      f32x4 q0 = *(const f32x4*)(p + s0), q1 = *(const f32x4*)(p + s0 + 4);
+      f32x4 q2 = *(const f32x4*)(p + s0 + 8), q3 = *(const f32x4*)(p + s0 + 12);
+      acc = acc + q0.x; acc = acc + q0.y; acc = acc + q0.z; acc = acc + q0.w;
+      acc = acc + q1.x; acc = acc + q1.y; acc = acc + q1.z; acc = acc + q1.w;
+      acc = acc + q2.x; acc = acc + q2.y; acc = acc + q2.z; acc = acc + q2.w;
+      acc = acc + q3.x; acc = acc + q3.y; acc = acc + q3.z; acc = acc + q3.w;
+    }
+    for (; s0 < steps; s0++) acc = acc + p[s0];
   }
+  float a0 = __shfl(acc, 0), a1 = __shfl(acc, 1), a2 = __shfl(acc, 2), a3 = __shfl(acc, 3);
+  float a4 = __shfl(acc, 4), a5 = __shfl(acc, 5), a6 = __shfl(acc, 6), a7 = __shfl(acc, 7);
+  if (lane == 0) {
+    float tail = -0.0f;  // Iterator::sum over the H % 8 leftover products
+    for (int i = steps * 8; i < H; i++) tail = tail + w[i] * xt[i];
+    float s0v = (a0 + a4) + (a1 + a5);
+    float s1v = (a2 + a6) + (a3 + a7);
+    logits[(size_t)t * E + e] = (s0v + s1v) + tail;
+  }
+}
 
-  // ---- softmax_in_place (src/ops/activation.rs:11-21)
+// softmax_in_place (src/ops/activation.rs:11-21), top_k (src/ops/topk.rs:
+// 44-61) and the renormalisation of MoeLayer::route, run by one whole wave
+// (all 64 lanes active).  Element i lives in lane i % 64, slot i / 64.
+//   - the sum of exp(l_i - max) is taken strictly in index order by one lane
+//     reading LDS in batches;
+//   - top-k: each probability gets the unique key (total_cmp key, then the
+//     complement of its index) so that larger key = better; k rounds of a
+//     wave-wide maximum pick the experts best first.
+// The k chosen experts and renormalised weights go to sel_idx / sel_w
+// (LDS), best first.  rs is LDS scratch of ROUTE_MAX_E + 3*64 words.
+constexpr int RS_SCRATCH = ROUTE_MAX_E + 4 * 64;
+
+template <int PER>  // elements per lane: E <= 64 * PER
+__device__ __forceinline__ void route_select_t(const float* lg, int E, int k, int normalize,
+                                               int* sel_idx, float* sel_w, const ExpTable& tab,
+                                               float* rs) {
+  const int lane = threadIdx.x & 63;
+  float* e_lds = rs;  // [E]
+  float v[PER];
   float mx = -__builtin_huge_valf();
-  for (int i = lane; i < E; i += 64) {
-    float v = __builtin_nontemporal_load(lg + i);
-    sm[i] = v;
-    mx = fmaxf(mx, v);
+#pragma unroll
+  for (int m = 0; m < PER; m++) {
+    const int i = lane + 64 * m;
+    v[m] = (i < E) ? lg[i] : -__builtin_huge_valf();
+    mx = fmaxf(mx, v[m]);
   }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  __syncthreads();
-  for (int i = lane; i < E; i += 64) sm[i] = hale_expf(sm[i] - mx);
-  __syncthreads();
-  float sum = 0.0f;
-  if (lane == 0)
-    for (int i = 0; i < E; i++) sum = sum + sm[i];
-  sum = __shfl(sum, 0);
-  for (int i = lane; i < E; i += 64) sm[i] = sm[i] / sum;
-  __syncthreads();
-
-  // ---- top_k (src/ops/topk.rs:44-61): best total_cmp score, ties to lower index
-  unsigned long long taken = 0;  // bit m: element lane + 64*m already chosen
-  float norm = -0.0f;
-  float chosen_score = 0.0f;
-  int chosen_idx = 0;
+  mx = wave_max_f32(mx);  // max is order independent
+#pragma unroll
+  for (int m = 0; m < PER; m++) {
+    const int i = lane + 64 * m;
+    v[m] = wave_expf(v[m] - mx, tab);
+    if (i < E) e_lds[i] = v[m];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float sum = 0.0f;  // sum += exp(v - max), index order
+  if (lane == 0) {
+    int i = 0;
+    for (; i + 16 <= E; i += 16) {
+      f32x4 a = *(const f32x4*)(e_lds + i), b = *(const f32x4*)(e_lds + i + 4);
+      f32x4 c = *(const f32x4*)(e_lds + i + 8), d = *(const f32x4*)(e_lds + i + 12);
+      sum = sum + a.x; sum = sum + a.y; sum = sum + a.z; sum = sum + a.w;
+      sum = sum + b.x; sum = sum + b.y; sum = sum + b.z; sum = sum + b.w;
+      sum = sum + c.x; sum = sum + c.y; sum = sum + c.z; sum = sum + c.w;
+      sum = sum + d.x; sum = sum + d.y; sum = sum + d.z; sum = sum + d.w;
+    }
+    for (; i < E; i++) sum = sum + e_lds[i];
+  }
+  sum = lane_value(sum, 0);
+  unsigned long long key[PER];
+#pragma unroll
+  for (int m = 0; m < PER; m++) {
+    const int i = lane + 64 * m;
+    key[m] = 0ull;  // below every real key
+    if (i < E) {
+      v[m] = v[m] / sum;
+      const unsigned k32 = (unsigned)total_key(v[m]) ^ 0x80000000u;  // order-preserving
+      key[m] = ((unsigned long long)k32 << 32) | (0xffffffffu - (unsigned)i);
+    }
+  }
+  // k rounds: the wave's largest untaken key is the next best expert; its
+  // probability is decoded from the key's high word
   for (int r = 0; r < k; r++) {
-    int bk = (int)0x80000000u, bi = 0x7fffffff;
-    for (int m = 0, i = lane; i < E; m++, i += 64) {
-      if (taken >> m & 1ull) continue;
-      int key = total_key(sm[i]);
-      if (key > bk || (key == bk && i < bi)) {
-        bk = key;
-        bi = i;
-      }
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int m = 0; m < PER; m++) best = key[m] > best ? key[m] : best;
+    best = wave_max_u64(best);
+#pragma unroll
+    for (int m = 0; m < PER; m++)
+      if (key[m] == best) key[m] = 0ull;  // unique keys: only the winner matches
+    if (lane == 0) {
+      const int bits = (int)((unsigned)(best >> 32) ^ 0x80000000u);
+      sel_idx[r] = (int)(0xffffffffu - (unsigned)best);
+      sel_w[r] = __int_as_float(bits ^ (int)(((unsigned)(bits >> 31)) >> 1));  // inverse of total_key
     }
-    for (int o = 32; o > 0; o >>= 1) {
-      int ok = __shfl_xor(bk, o), oi = __shfl_xor(bi, o);
-      if (ok > bk || (ok == bk && oi < bi)) {
-        bk = ok;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1ull << (bi >> 6);
-    float sc = sm[bi];
-    if (lane == r) {
-      chosen_idx = bi;
-      chosen_score = sc;
-    }
-    norm = norm + sc;  // Iterator::sum in best-first order (every lane)
   }
-  if (!normalize) norm = 1.0f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float norm = 1.0f;
+  if (normalize) {
+    norm = -0.0f;  // Iterator::sum in best-first order
+    for (int r = 0; r < k; r++) norm = norm + sel_w[r];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < k) sel_w[lane] = sel_w[lane] / norm;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void route_select(const float* lg, int E, int k, int normalize,
+                                             int* sel_idx, float* sel_w, const ExpTable& tab,
+                                             float* rs) {
+  if (E <= 64)
+    route_select_t<1>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
+  else if (E <= 128)
+    route_select_t<2>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
+  else if (E <= 256)
+    route_select_t<4>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
+  else if (E <= 512)
+    route_select_t<8>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
+  else
+    route_select_t<16>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
+}
+
+// Standalone routing (MoeLayer::route without the experts, and the grouped
+// path): one wave per token.
+__global__ __launch_bounds__(64) void k_route_select(const float* __restrict__ logits, int E, int k,
+                                                     int normalize, int* __restrict__ route_idx,
+                                                     float* __restrict__ route_w,
+                                                     unsigned long long* __restrict__ stats) {
+  __shared__ int sel_idx[64];
+  __shared__ float sel_w[64];
+  __shared__ __attribute__((aligned(16))) float rs[RS_SCRATCH];
+  const int t = blockIdx.x;
+  ExpTable tab;
+  tab.load();
+  route_select(logits + (size_t)t * E, E, k, normalize, sel_idx, sel_w, tab, rs);
+  __syncthreads();
+  const int lane = threadIdx.x;
   if (lane < k) {
-    route_idx[(size_t)t * k + lane] = chosen_idx;
-    route_w[(size_t)t * k + lane] = chosen_score / norm;
-    if (stats) atomicAdd(&stats[chosen_idx], 1ull);
+    route_idx[(size_t)t * k + lane] = sel_idx[lane];
+    route_w[(size_t)t * k + lane] = sel_w[lane];
+    if (stats) atomicAdd(&stats[sel_idx[lane]], 1ull);
   }
 }
 
@@ -309,25 +377,25 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ router,
 // ===========================================================================
 //
 // A work-group of 4 waves owns a group of 64 output rows (two 32-row tiles)
-// and loops over the row's quantization blocks: wave w takes blocks
-// w, w+4, w+8, ...  For one block a wave reads 2 x 512 B of codes (q4_0)
-// or 2 x 1 KB (q8_0), all lanes use the same activation block (scalar
-// loads), and lane l produces the term (d_w * d_x) * isum of row l.  Terms
-// go to LDS in chunks of CB blocks; wave 0 folds each chunk into its 64
-// running row sums in block order, so the total is the reference's
-// left-to-right sum.  Two LDS buffers let the other waves fill chunk c+1
-// while wave 0 folds chunk c.
+// and loops over the rows' quantization blocks in chunks: in a chunk wave w
+// takes blocks w, w+4, w+8, ... and issues all of their loads at once (16
+// per lane, 16 B each).  For one block a wave reads 2 x 512 B of codes
+// (q4_0) or 2 x 1 KB (q8_0), every lane uses the same activation block
+// (scalar loads), and lane l forms the block term (d_w * d_x) * isum of row
+// l.  Terms go to LDS; wave 0 adds them to its 64 running row sums in block
+// order, so each total is the reference's left-to-right sum.  The next
+// chunk's loads are issued before the fold, and two LDS buffers let the
+// other waves fill chunk c+1 while wave 0 folds chunk c.
 //
 // Epilogues:
 //   EPI_PLAIN    out[row] = total                      (WeightMatrix::matvec)
 //   EPI_GATE_UP  rows 0-31 gate, 32-63 up of one I-tile; h = silu(g)*u is
 //                quantized to its q8 block for the down projection
-//                (Expert::forward, src/expert/mod.rs:95-102)
+//                (Expert::forward, src/expert/mod.rs:95-102).  With router
+//                logits given, the prologue selects the slot's expert.
 //   EPI_COMBINE  per-slot results to ytmp; the last slot's work-group of the
 //                row group adds them in route order: out = 0, then
 //                out = out + w_s * y_s (MoeLayer::forward, moe.rs:63-68)
-
-constexpr int CB = 32;  // blocks per LDS chunk
 
 template <int DT>
 __device__ __forceinline__ float block_term(const u32x4* c, uint16_t sc, const ActBlock* ab) {
@@ -381,14 +449,50 @@ __device__ __forceinline__ int block_isum(const u32x4* c, const ActBlock* ab) {
 template <int DT, int EPI>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   constexpr int CH = Layout<DT>::CH;
+  constexpr int NW = 4;             // waves per work-group
+  constexpr int UPW = 16 / CH;      // blocks per wave per chunk (16 loads in flight)
+  constexpr int CB = UPW * NW;      // blocks per chunk
   __shared__ float terms[2][CB][GROUP];
+  __shared__ ActBlock s_act[GEMV_MAX_NB];
+  __shared__ int sel_idx[64];
+  __shared__ float sel_w[64];
+  __shared__ __attribute__((aligned(16))) float rs[EPI == EPI_GATE_UP ? RS_SCRATCH : 4];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x;
   const int slot = blockIdx.y;
   const int nb = a.nb;
-  const int expert = a.route_idx ? a.route_idx[slot] : 0;
+
+  // the activation blocks of this slot: loads issued first, stored to LDS
+  // once the weight loads are in flight
+  constexpr int APER = (GEMV_MAX_NB * 3 + 64 * NW - 1) / (64 * NW);
+  u32x4 av[APER];
+  {
+    const u32x4* src = (const u32x4*)(a.act + (size_t)slot * a.act_stride);
+#pragma unroll
+    for (int j = 0; j < APER; j++) {
+      const int i = threadIdx.x + j * 64 * NW;
+      if (i < nb * 3) av[j] = src[i];
+    }
+  }
+  ExpTable tab;
+  if constexpr (EPI == EPI_GATE_UP) tab.load();
+  int expert = a.route_idx ? a.route_idx[slot] : 0;
+  if constexpr (EPI == EPI_GATE_UP) {
+    if (a.logits) {  // choose this token's experts from the router logits
+      if (wave == 0) {
+        route_select(a.logits, a.E, a.slots, a.normalize, sel_idx, sel_w, tab, rs);
+        if (g == 0 && lane == 0) {  // one work-group per slot publishes it
+          a.route_out_idx[slot] = sel_idx[slot];
+          a.route_out_w[slot] = sel_w[slot];
+          if (a.stats) atomicAdd(&a.stats[sel_idx[slot]], 1ull);
+        }
+      }
+      __syncthreads();
+      expert = sel_idx[slot];
+    }
+  }
 
   // tile and matrix of this lane's row
   const uint8_t* cbase;
@@ -406,35 +510,63 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   const int r = lane & 31;
   const uint8_t* crow = cbase + (tile * nb * CH * TILE + r) * 16;
   const uint16_t* srow = sbase + tile * nb * TILE + r;
-  const ActBlock* act = a.act + (size_t)slot * a.act_stride;
+  const ActBlock* act = s_act;
+
+  u32x4 cw[UPW][CH];
+  uint16_t sw[UPW];
+  // Blocks past the end of the row are clamped to the last block (an
+  // in-bounds load whose term is never stored), so the chunk loop has no
+  // branches and all of its loads are in flight together.
+  auto load_chunk = [&](int ch) {
+    const int b0 = ch * CB;
+#pragma unroll
+    for (int s = 0; s < UPW; s++) {
+      const int b = min(b0 + wave + NW * s, nb - 1);
+#pragma unroll
+      for (int c = 0; c < CH; c++)
+        cw[s][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
+      sw[s] = srow[(size_t)b * TILE];
+    }
+  };
 
   float total = 0.0f;
   const int nchunks = (nb + CB - 1) / CB;
+  load_chunk(0);
+  {
+    u32x4* dst = (u32x4*)s_act;
+#pragma unroll
+    for (int j = 0; j < APER; j++) {
+      const int i = threadIdx.x + j * 64 * NW;
+      if (i < nb * 3) dst[i] = av[j];
+    }
+  }
+  __syncthreads();
   for (int ch = 0; ch < nchunks; ch++) {
     const int b0 = ch * CB;
     const int bend = min(nb, b0 + CB);
     float(*tb)[GROUP] = terms[ch & 1];
-    // issue every load of this wave's share of the chunk, then compute
-    u32x4 cw[CB / 4][CH];
-    uint16_t sw[CB / 4];
+    float tv[UPW];
 #pragma unroll
-    for (int s = 0; s < CB / 4; s++) {
-      const int b = b0 + wave + 4 * s;
-      if (b < bend) {
+    for (int s = 0; s < UPW; s++) tv[s] = block_term<DT>(cw[s], sw[s], act + min(b0 + wave + NW * s, nb - 1));
+    if (ch + 1 < nchunks) load_chunk(ch + 1);
 #pragma unroll
-        for (int c = 0; c < CH; c++)
-          cw[s][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
-        sw[s] = srow[(size_t)b * TILE];
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < CB / 4; s++) {
-      const int b = b0 + wave + 4 * s;
-      if (b < bend) tb[b - b0][lane] = block_term<DT>(cw[s], sw[s], act + b);
+    for (int s = 0; s < UPW; s++) {
+      const int b = b0 + wave + NW * s;
+      if (b < bend) tb[b - b0][lane] = tv[s];
     }
     __syncthreads();
-    if (wave == 0)
-      for (int b = 0; b < bend - b0; b++) total = total + tb[b][lane];
+    if (wave == 0) {
+      const int n = bend - b0;
+      int b = 0;
+      for (; b + 8 <= n; b += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = tb[b + u][lane];
+#pragma unroll
+        for (int u = 0; u < 8; u++) total = total + v[u];
+      }
+      for (; b < n; b++) total = total + tb[b][lane];
+    }
   }
   if (wave != 0) return;
 
@@ -443,7 +575,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     if (row < (size_t)a.rows) a.out[row] = total;
   } else if constexpr (EPI == EPI_GATE_UP) {
     float u = __shfl(total, lane + 32);
-    float h = silu(total) * u;  // lanes 0-31: *g = silu(*g) * u
+    float h = wave_silu(total, tab) * u;  // lanes 0-31: *g = silu(*g) * u
     float scale;
     int qsum;
     int q = quant_block_lane(h, &scale, &qsum);
@@ -469,6 +601,141 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     float acc = 0.0f;
     for (int s = 0; s < a.slots; s++)
       acc = acc + a.route_w[s] * __builtin_nontemporal_load(a.ytmp + (size_t)s * prow + row);
+    if (row < (size_t)a.rows) a.out[row] = acc;
+  }
+}
+
+// ===========================================================================
+// Down projection and combine in one work-group per row group
+// ===========================================================================
+//
+// MoeLayer::forward (src/model/moe.rs:63-68) for one token: out = 0, then
+// for each route in best-first order out = out + w_s * down_s(h_s).  A
+// work-group owns DR = 16 output rows for every slot, so the combine needs
+// no other work-group.  Its units are the (slot, block) pairs in slot-major
+// order.  A wave covers 16 rows x 4 units per load (4 x 256 B); a chunk of
+// CB units loads at once (weights and activation blocks), terms go to LDS,
+// and lanes 0-15 of wave 0 fold them in unit order: a row's sum for slot s
+// is complete at the slot's last block, where it is scaled by w_s and added
+// to the output.
+
+constexpr int DR = 16;          // rows per work-group of k_down_combine
+constexpr int DOWN_WAVES = 4;   // waves per work-group of k_down_combine
+
+template <int DT>
+__global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
+  constexpr int CH = Layout<DT>::CH;
+  constexpr int NW = DOWN_WAVES;
+  constexpr int J = 64 / DR;        // units side by side in one wave
+  constexpr int UPW = 16 / CH;      // 16 loads of 16 B in flight per lane
+  constexpr int CB = NW * J * UPW;  // units per chunk: 256 (q4_0), 128 (q8_0)
+  constexpr int AQ = (CB * 3 + 64 * NW - 1) / (64 * NW);
+  __shared__ float terms[2][CB][DR];
+  __shared__ ActBlock s_act[2][CB];
+  __shared__ int s_exp[64];
+  __shared__ float s_w[64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x;
+  const int nb = a.nb;
+  const int slots = a.slots;
+  const int nunits = slots * nb;
+  if (threadIdx.x < slots) {
+    s_exp[threadIdx.x] = a.route_idx[threadIdx.x];
+    s_w[threadIdx.x] = a.route_w[threadIdx.x];
+  }
+  __syncthreads();
+
+  const int r = lane % DR;          // row within the group
+  const int jl = lane / DR;         // unit lane
+  const size_t row0 = (size_t)g * DR;
+  const size_t tile = row0 / TILE;
+  const int rt = (int)(row0 % TILE) + r;  // row within its 32-row tile
+  const size_t row_off = (tile * nb * CH * TILE + rt) * 16;
+  const size_t srow_off = tile * nb * TILE + rt;
+
+  u32x4 cw[UPW][CH];
+  uint16_t sw[UPW];
+  u32x4 av[AQ];
+  // units past the end are clamped to the last unit (loaded, never stored)
+  auto unit_of = [&](int u0, int s) { return min(u0 + (wave + NW * s) * J + jl, nunits - 1); };
+  auto load_chunk = [&](int ch) {
+    const int u0 = ch * CB;
+#pragma unroll
+    for (int s = 0; s < UPW; s++) {
+      const int u = unit_of(u0, s);
+      const int sl = u / nb, b = u - sl * nb;
+      const size_t e = (size_t)s_exp[sl];
+      const uint8_t* c0 = a.codes + e * a.codes_stride + row_off;
+#pragma unroll
+      for (int c = 0; c < CH; c++)
+        cw[s][c] = __builtin_nontemporal_load((const u32x4*)(c0 + ((size_t)b * CH + c) * TILE * 16));
+      sw[s] = a.scales[e * a.scales_stride + srow_off + (size_t)b * TILE];
+    }
+#pragma unroll
+    for (int q = 0; q < AQ; q++) {
+      const int i = threadIdx.x + q * 64 * NW;
+      const int u = u0 + i / 3;
+      if (i < CB * 3 && u < nunits) {
+        const int sl = u / nb, b = u - sl * nb;
+        av[q] = ((const u32x4*)(a.hact + (size_t)sl * a.hact_stride + b))[i % 3];
+      }
+    }
+  };
+
+  float total = 0.0f, acc = 0.0f;
+  int fs = 0, fb = 0;  // slot and block of the next unit the fold takes
+  const int nchunks = (nunits + CB - 1) / CB;
+  load_chunk(0);
+  for (int ch = 0; ch < nchunks; ch++) {
+    const int u0 = ch * CB;
+    const int uend = min(nunits, u0 + CB);
+    ActBlock* sa = s_act[ch & 1];
+#pragma unroll
+    for (int q = 0; q < AQ; q++) {
+      const int i = threadIdx.x + q * 64 * NW;
+      if (i < CB * 3 && u0 + i / 3 < nunits) ((u32x4*)sa)[i] = av[q];
+    }
+    __syncthreads();
+    float tv[UPW];
+#pragma unroll
+    for (int s = 0; s < UPW; s++) tv[s] = block_term<DT>(cw[s], sw[s], sa + (unit_of(u0, s) - u0));
+    if (ch + 1 < nchunks) load_chunk(ch + 1);
+    float(*tb)[DR] = terms[ch & 1];
+#pragma unroll
+    for (int s = 0; s < UPW; s++) {
+      const int u = u0 + (wave + NW * s) * J + jl;
+      if (u < uend) tb[u - u0][r] = tv[s];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < DR) {
+      int j = 0;
+      const int n = uend - u0;
+      while (j < n) {
+        const int run = min(n - j, nb - fb);  // units left in this slot and chunk
+        int q = 0;
+        for (; q + 8 <= run; q += 8) {
+          float v[8];
+#pragma unroll
+          for (int z = 0; z < 8; z++) v[z] = tb[j + q + z][lane];
+#pragma unroll
+          for (int z = 0; z < 8; z++) total = total + v[z];
+        }
+        for (; q < run; q++) total = total + tb[j + q][lane];
+        j += run;
+        fb += run;
+        if (fb == nb) {
+          acc = acc + s_w[fs] * total;
+          total = 0.0f;
+          fb = 0;
+          fs++;
+        }
+      }
+    }
+  }
+  if (wave == 0 && lane < DR) {
+    const size_t row = row0 + lane;
     if (row < (size_t)a.rows) a.out[row] = acc;
   }
 }
@@ -568,20 +835,28 @@ hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipSt
   return hipGetLastError();
 }
 
-hipError_t launch_route(const float* router, const float* logits_in, const float* x, int H, int E,
-                        int k, int normalize, int T, ActBlock* act, float* logits,
-                        unsigned* counters, int* route_idx, float* route_w,
-                        unsigned long long* stats, hipStream_t st) {
-  if (H > ROUTE_MAX_H || E > ROUTE_MAX_E || k > 64 || k > E || H % QK) return hipErrorInvalidValue;
-  dim3 grid(router ? E : 1, T);
-  k_route<<<grid, 64, 0, st>>>(router, logits_in, x, H, E, k, normalize, act, logits, counters,
-                               route_idx, route_w, stats);
+hipError_t launch_route_logits(const float* router, const float* x, int H, int E, int T,
+                               ActBlock* act, float* logits, hipStream_t st) {
+  if (H > ROUTE_MAX_H || E > ROUTE_MAX_E || H % QK || E < 1 || T < 1) return hipErrorInvalidValue;
+  dim3 grid(E, T);
+  k_route_logits<<<grid, 64, 0, st>>>(router, x, H, E, act, logits);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_select(const float* logits, int E, int k, int normalize, int T,
+                               int* route_idx, float* route_w, unsigned long long* stats,
+                               hipStream_t st) {
+  if (E > ROUTE_MAX_E || k > 64 || k > E || k < 1 || T < 1) return hipErrorInvalidValue;
+  k_route_select<<<T, 64, 0, st>>>(logits, E, k, normalize, route_idx, route_w, stats);
   return hipGetLastError();
 }
 
 hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int slots,
                        hipStream_t st) {
   if (groups == 0 || slots == 0) return hipSuccess;
+  if (a.nb < 1 || a.nb > GEMV_MAX_NB) return hipErrorInvalidValue;
+  if (a.logits && (epi != EPI_GATE_UP || a.E > ROUTE_MAX_E || slots > 64 || slots > a.E))
+    return hipErrorInvalidValue;
   dim3 grid(groups, slots);
 #define HALE_GEMV_CASE(D, E)                                  \
   if (dtype == D && epi == E) {                               \
@@ -596,6 +871,18 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   HALE_GEMV_CASE(Q4_0, EPI_COMBINE)
 #undef HALE_GEMV_CASE
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_down_combine(int dtype, const DownArgs& a, int groups, hipStream_t st) {
+  if (groups == 0) return hipSuccess;
+  if (a.nb < 1 || a.slots < 1 || a.slots > 64) return hipErrorInvalidValue;
+  if (dtype == Q8_0)
+    k_down_combine<Q8_0><<<groups, 64 * DOWN_WAVES, 0, st>>>(a);
+  else if (dtype == Q4_0)
+    k_down_combine<Q4_0><<<groups, 64 * DOWN_WAVES, 0, st>>>(a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,

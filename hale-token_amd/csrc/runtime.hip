@@ -793,9 +793,12 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
   const int k = (int)m->k;
   const size_t nbh = m->H / HALE_QK, nbi = m->I / HALE_QK;
   if (!m->router && !dlogits) return fail(c, HALE_EINVAL, "layer has no router: logits are required");
-  LAUNCH(c, K_ROUTE, launch_route(dlogits ? nullptr : m->router, dlogits, dx, (int)m->H, (int)m->E, k,
-                         m->normalize, (int)ntok, m->act, m->logits, m->tok_counters, m->route_idx,
-                         m->route_w, m->stats, c->stream));
+  if (dlogits)
+    LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, ntok * nbh, m->act, c->stream));
+  else
+    LAUNCH(c, K_ROUTE, launch_route_logits(m->router, dx, (int)m->H, (int)m->E, (int)ntok, m->act,
+                                           m->logits, c->stream));
+  const float* lg = dlogits ? dlogits : m->logits;
   for (size_t t = 0; t < ntok; t++) {
     float* out_t = dout + t * m->H;
     if (k == 0) {
@@ -813,27 +816,31 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     a.rows = (int)m->I;
     a.act = m->act + t * nbh;
     a.act_stride = 0;
-    a.route_idx = m->route_idx + t * k;
+    a.route_idx = nullptr;  // the prologue selects the experts from the logits
+    a.logits = lg + t * m->E;
+    a.E = (int)m->E;
+    a.normalize = m->normalize;
+    a.route_out_idx = m->route_idx + t * k;
+    a.route_out_w = m->route_w + t * k;
+    a.stats = m->stats;
     a.hact = m->hact;
     a.hact_stride = (int)nbi;
     a.slots = k;
     LAUNCH(c, K_GATE_UP, launch_gemv(m->dtype, EPI_GATE_UP, a, (int)nbi, k, c->stream));
-    GemvArgs d{};
+    DownArgs d{};
     d.codes = m->down_c;
     d.scales = m->down_s;
     d.codes_stride = m->dc_bytes;
     d.scales_stride = m->ds_elems;
     d.nb = (int)nbi;
     d.rows = (int)m->H;
-    d.act = m->hact;
-    d.act_stride = (int)nbi;
+    d.hact = m->hact;
+    d.hact_stride = (int)nbi;
     d.route_idx = m->route_idx + t * k;
     d.route_w = m->route_w + t * k;
-    d.out = out_t;
-    d.ytmp = m->ytmp;
-    d.counters = m->grp_counters;
     d.slots = k;
-    LAUNCH(c, K_DOWN, launch_gemv(m->dtype, EPI_COMBINE, d, (int)(padded_rows(m->H) / 64), k, c->stream));
+    d.out = out_t;
+    LAUNCH(c, K_DOWN, launch_down_combine(m->dtype, d, (int)(padded_rows(m->H) / 16), c->stream));
   }
   return HALE_OK;
 }
@@ -939,9 +946,11 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
   rc = ctx_scratch(c, m->H * 4, &s);
   if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync(s, x, m->H * 4, hipMemcpyHostToDevice, c->stream));
-  LAUNCH(c, K_ROUTE, launch_route(m->router, nullptr, (const float*)s, (int)m->H, (int)m->E, (int)m->k,
-                         m->normalize, 1, m->act, m->logits, m->tok_counters, m->route_idx,
-                         m->route_w, nullptr, c->stream));
+  LAUNCH(c, K_ROUTE, launch_route_logits(m->router, (const float*)s, (int)m->H, (int)m->E, 1,
+                                         m->act, m->logits, c->stream));
+  if (m->k > 0)
+    LAUNCH(c, K_ROUTE, launch_route_select(m->logits, (int)m->E, (int)m->k, m->normalize, 1,
+                                           m->route_idx, m->route_w, nullptr, c->stream));
   HIPCHK(c, hipMemcpyAsync(index, m->route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipMemcpyAsync(weight, m->route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));

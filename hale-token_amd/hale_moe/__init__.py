@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -153,6 +154,12 @@ class Context:
         if rc != OK:
             raise HaleError(lib().hale_last_error(None).decode())
         self.handle = h
+        # objects that hold device state of this context; closed before it
+        self._children = weakref.WeakSet()
+
+    def adopt(self, obj):
+        self._children.add(obj)
+        return obj
 
     def check(self, rc: int, what: str = ""):
         if rc == OK:
@@ -218,8 +225,14 @@ class Context:
 
     def close(self):
         if getattr(self, "handle", None):
+            for child in list(self._children):
+                child.close()
             lib().hale_ctx_destroy(self.handle)
             self.handle = None
+
+    @property
+    def alive(self) -> bool:
+        return bool(getattr(self, "handle", None))
 
     def __del__(self):
         try:
@@ -233,6 +246,7 @@ class DeviceBuffer:
 
     def __init__(self, ctx: Context, ptr, nbytes: int):
         self.ctx, self.ptr, self.nbytes = ctx, ptr, nbytes
+        ctx.adopt(self)
 
     @property
     def address(self) -> int:
@@ -265,9 +279,11 @@ class DeviceBuffer:
                        "fill_normal")
 
     def free(self):
-        if self.ptr:
+        if self.ptr and self.ctx.alive:
             lib().hale_device_free(self.ctx.handle, self.ptr)
-            self.ptr = None
+        self.ptr = None
+
+    close = free
 
     def __del__(self):
         try:
@@ -281,14 +297,15 @@ class Graph:
 
     def __init__(self, ctx: Context, handle):
         self.ctx, self.handle = ctx, handle
+        ctx.adopt(self)
 
     def launch(self):
         self.ctx.check(lib().hale_graph_launch(self.handle), "graph_launch")
 
     def close(self):
-        if getattr(self, "handle", None):
+        if getattr(self, "handle", None) and self.ctx.alive:
             lib().hale_graph_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:
@@ -339,6 +356,7 @@ class WeightMatrix:
     def __init__(self, ctx: Context, handle, rows: int, cols: int, dtype: int):
         self.ctx, self.handle = ctx, handle
         self._rows, self._cols, self._dtype = rows, cols, dtype
+        ctx.adopt(self)
 
     @classmethod
     def new(cls, ctx: Context, rows: int, cols: int, dtype, data) -> "WeightMatrix":
@@ -401,9 +419,9 @@ class WeightMatrix:
         return out
 
     def close(self):
-        if getattr(self, "handle", None):
+        if getattr(self, "handle", None) and self.ctx.alive:
             lib().hale_matrix_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:
@@ -505,6 +523,7 @@ class MoeLayer:
                                         router.handle if router is not None else None,
                                         C.byref(h)), "MoeLayer")
         self.handle = h
+        ctx.adopt(self)
         self._present = [False] * num_experts
         self.experts = HbmExpertProvider(self)
 
@@ -585,9 +604,9 @@ class MoeLayer:
         return (out, idx, w) if return_routes else out
 
     def close(self):
-        if getattr(self, "handle", None):
+        if getattr(self, "handle", None) and self.ctx.alive:
             lib().hale_moe_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:

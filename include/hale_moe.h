@@ -65,6 +65,8 @@ typedef struct hale_moe hale_moe;       /* Ref: MoeLayer + its provider   */
 
 /* Creates a context on HIP device `device` (one stream, default priority). */
 int hale_ctx_create(int device, hale_ctx **out);
+/* Destroys the context; matrices, layers, graphs and buffers created on it
+ * must be destroyed first. */
 void hale_ctx_destroy(hale_ctx *ctx);
 /* Message of the last failed call on ctx ("" if none).  NULL ctx gives the
  * message of the last failed hale_ctx_create in this thread. */
