@@ -1,6 +1,21 @@
-// kernels_prefill.hip -- expert-grouped multi-token MoE layer (placeholder:
-// the grouped path is not enabled yet, every token count runs the decode
-// kernels token by token).
+// kernels_prefill.hip -- expert-grouped multi-token MoE layer on gfx950.
+//
+// The reference feeds a prompt one token at a time (Transformer::prefill,
+// src/model/transformer.rs:231-239), so at the MoE layer token t's output is
+// MoeLayer::forward(x_t) (src/model/moe.rs:56-70), independent of the other
+// tokens.  Here the T*k (token, slot) assignments are grouped by expert and
+// each expert's group runs as an int8 MFMA matrix product; every output
+// keeps the reference's bits:
+//   - one v_mfma_i32_32x32x32_i8 covers exactly one 32-element quantization
+//     block, so it yields the block's exact i32 dot sums (dot_q8_0 /
+//     dot_q4_0, src/tensor/quant.rs:115-144);
+//   - each output element then adds (d_w * d_x) * isum to its f32 sum block
+//     after block, the reference's left-to-right order;
+//   - SiLU, the q8 requantization of h, the route-order combine and the
+//     routing itself are the decode path's exact formulas.
+//
+// Pipeline: route (per token) -> group (counts, prefix sums, stable scatter,
+// tile list) -> grouped gate/up -> grouped down -> combine.
 #pragma clang fp contract(off)
 
 #include "hale_device.h"
@@ -9,13 +24,456 @@
 
 namespace hale {
 
-size_t prefill_min_tokens(size_t) { return (size_t)-1; }
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
-size_t prefill_workspace_bytes(const PrefillLayer&, size_t) { return 0; }
+constexpr int TM = 32;          // assignments (rows) per tile
+constexpr int TN = 128;         // output columns per work-group (4 waves x 32)
+constexpr int GROUP_WAVES = 16;  // waves of the grouping kernel
+constexpr int GROUP_MAX_E = 1024;
 
-hipError_t prefill_enqueue(const PrefillLayer&, PrefillWorkspace&, size_t, const float*,
-                           const float*, float*, hipStream_t, const LaunchHook&) {
-  return hipErrorNotSupported;
+struct Tile {
+  int expert;
+  int row0;  // first sorted position
+  int rows;  // 1..TM
+  int pad;
+};
+
+// ---------------------------------------------------------------------------
+// grouping: histogram, prefix sums, stable scatter, tile list
+// ---------------------------------------------------------------------------
+//
+// One work-group of 16 waves.  Assignment a = t*k + s is routed to expert
+// route_idx[a].  Sorted position of a = (assignments to lower experts) +
+// (earlier assignments to the same expert), so each expert's group keeps
+// token order.  Wave w owns a contiguous slice of the assignments; lanes
+// with equal experts in a 64-wide chunk are found with ballots over the
+// expert's bits.
+
+__device__ __forceinline__ unsigned long long match_mask(int e, int nbits, bool valid) {
+  unsigned long long m = __ballot(valid);
+  for (int b = 0; b < nbits; b++) {
+    const unsigned long long v = __ballot(((e >> b) & 1) != 0);
+    m &= ((e >> b) & 1) ? v : ~v;
+  }
+  return valid ? m : 0ull;
+}
+
+__global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restrict__ route_idx, int A,
+                                                            int E, int* __restrict__ perm,
+                                                            int* __restrict__ pos_of,
+                                                            Tile* __restrict__ tiles,
+                                                            int* __restrict__ ntiles) {
+  __shared__ int cnt[GROUP_WAVES][GROUP_MAX_E];
+  __shared__ int scan_a[GROUP_MAX_E];
+  __shared__ int scan_t[GROUP_MAX_E];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  int nbits = 0;
+  while ((1 << nbits) < E) nbits++;
+  for (int i = tid; i < GROUP_WAVES * GROUP_MAX_E; i += 64 * GROUP_WAVES) (&cnt[0][0])[i] = 0;
+  __syncthreads();
+  const int slice = (A + GROUP_WAVES * 64 - 1) / (GROUP_WAVES * 64) * 64;
+  const int a0 = w * slice, a1 = min(A, a0 + slice);
+  const unsigned long long lt = (1ull << lane) - 1ull;
+
+  // pass 1: per-wave counts
+  for (int c = a0; c < a1; c += 64) {
+    const int a = c + lane;
+    const bool valid = a < a1;
+    const int e = valid ? route_idx[a] : 0;
+    const unsigned long long m = match_mask(e, nbits, valid);
+    if (valid && (m >> lane) == 1ull) cnt[w][e] += __popcll(m);  // highest lane of its group
+  }
+  __syncthreads();
+
+  // totals, expert offsets and tile offsets (inclusive scans over experts)
+  for (int e = tid; e < GROUP_MAX_E; e += 64 * GROUP_WAVES) {
+    int tot = 0;
+    if (e < E)
+      for (int q = 0; q < GROUP_WAVES; q++) tot += cnt[q][e];
+    scan_a[e] = tot;
+    scan_t[e] = (tot + TM - 1) / TM;
+  }
+  __syncthreads();
+  for (int off = 1; off < GROUP_MAX_E; off <<= 1) {
+    int va = 0, vt = 0;
+    for (int e = tid; e < GROUP_MAX_E; e += 64 * GROUP_WAVES) {
+      if (e >= off) {
+        va = scan_a[e - off];
+        vt = scan_t[e - off];
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < GROUP_MAX_E; e += 64 * GROUP_WAVES) {
+      if (e >= off) {
+        scan_a[e] += va;
+        scan_t[e] += vt;
+      }
+    }
+    __syncthreads();
+  }
+  // per-wave bases: offset(e) + counts of lower waves; tile list
+  for (int e = tid; e < E; e += 64 * GROUP_WAVES) {
+    const int total = cnt[0][e];
+    int base = e ? scan_a[e - 1] : 0;
+    const int tot_e = scan_a[e] - base;
+    int run = base;
+    for (int q = 0; q < GROUP_WAVES; q++) {
+      const int c = q ? cnt[q][e] : total;
+      cnt[q][e] = run;
+      run += c;
+    }
+    const int t0 = e ? scan_t[e - 1] : 0;
+    for (int i = 0; i * TM < tot_e; i++) {
+      Tile tl;
+      tl.expert = e;
+      tl.row0 = base + i * TM;
+      tl.rows = min(TM, tot_e - i * TM);
+      tl.pad = 0;
+      tiles[t0 + i] = tl;
+    }
+  }
+  if (tid == 0) *ntiles = scan_t[E - 1];
+  __syncthreads();
+
+  // pass 2: stable positions
+  for (int c = a0; c < a1; c += 64) {
+    const int a = c + lane;
+    const bool valid = a < a1;
+    const int e = valid ? route_idx[a] : 0;
+    const unsigned long long m = match_mask(e, nbits, valid);
+    if (valid) {
+      const int pos = cnt[w][e] + __popcll(m & lt);
+      perm[pos] = a;
+      pos_of[a] = pos;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (valid && (m >> lane) == 1ull) cnt[w][e] += __popcll(m);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// ---------------------------------------------------------------------------
+// grouped matrix products
+// ---------------------------------------------------------------------------
+//
+// A work-group takes one tile (expert e, 32 sorted rows) and 128 output
+// columns; wave w owns columns [n0, n0+32).  Per quantization block b a wave
+// issues one 32x32x32 int8 MFMA (two for gate/up): lane l supplies row
+// l%32's 16 activation codes of K half l/32 and column l%32's 16 weight codes
+// of the same half, which is exactly one 16-byte chunk of the tile layout
+// (q4_0: the low nibbles are K 0-15, the high nibbles K 16-31).  Result
+// element j of lane l is row (j%4) + 4*(l/32) + 8*(j/4), column l%32.
+
+// 16 signed weight codes of K half `h` of (column, block)
+template <int DT>
+__device__ __forceinline__ v4i weight_half(const uint8_t* chunk0, int h) {
+  if constexpr (DT == Q8_0) {
+    u32x4 v = __builtin_nontemporal_load((const u32x4*)(chunk0 + h * TILE * 16));
+    v4i r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+  } else {
+    u32x4 v = __builtin_nontemporal_load((const u32x4*)chunk0);
+    // nibble n -> signed code n - 8: (n | 0x80) - 8 keeps each byte apart,
+    // then ^ 0x80 maps n + 120 to n - 8 (mod 256)
+    u32x4 n = h ? ((v >> 4) & 0x0f0f0f0fu) : (v & 0x0f0f0f0fu);
+    n = ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+    v4i r;
+    __builtin_memcpy(&r, &n, 16);
+    return r;
+  }
+}
+
+struct GroupedArgs {
+  // weights of the layer, expert e at base + e * stride
+  const uint8_t* codes;
+  const uint16_t* scales;
+  const uint8_t* codes2;  // up (gate/up kernel)
+  const uint16_t* scales2;
+  size_t codes_stride, scales_stride;
+  int nb;        // K blocks
+  int ncols;     // N (I for gate/up, H for down)
+  const Tile* tiles;
+  const int* ntiles;
+  const int* perm;        // sorted position -> assignment
+  int k;                  // slots per token
+  const ActBlock* act;    // gate/up: [T][nb] by token; down: [A][nb] by sorted position
+  ActBlock* hact;         // gate/up output: [A][ncols/32] by sorted position
+  float* y;               // down output: [A][ncols] by sorted position
+};
+
+template <int DT, bool GATE_UP>
+__global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
+  constexpr int CH = Layout<DT>::CH;
+  __shared__ float s_dx[4][2][TM];  // per wave, double buffer: row scales of a block
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int ti = blockIdx.x;
+  if (ti >= *a.ntiles) return;
+  const Tile tl = a.tiles[ti];
+  const int n0 = blockIdx.y * TN + wave * 32;
+  if (n0 >= a.ncols) return;
+  const int h = lane >> 5;
+  const int n = n0 + (lane & 31);  // this lane's output column (weight row)
+  const int nb = a.nb;
+
+  // activation row of A operand lane (row lane % 32, clamped into the tile)
+  const int arow = tl.row0 + min(lane & 31, tl.rows - 1);
+  const ActBlock* arow_act;
+  if constexpr (GATE_UP)
+    arow_act = a.act + (size_t)(a.perm[arow] / a.k) * nb;
+  else
+    arow_act = a.act + (size_t)arow * nb;
+
+  const size_t tile_n = (size_t)n / TILE;
+  const int rn = n % TILE;
+  const size_t e = (size_t)tl.expert;
+  const uint8_t* cg = a.codes + e * a.codes_stride + (tile_n * nb * CH * TILE + rn) * 16;
+  const uint16_t* sg = a.scales + e * a.scales_stride + tile_n * nb * TILE + rn;
+  const uint8_t* cu = nullptr;
+  const uint16_t* su = nullptr;
+  if constexpr (GATE_UP) {
+    cu = a.codes2 + e * a.codes_stride + (tile_n * nb * CH * TILE + rn) * 16;
+    su = a.scales2 + e * a.scales_stride + tile_n * nb * TILE + rn;
+  }
+
+  float accg[16], accu[16];
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    accg[j] = 0.0f;
+    accu[j] = 0.0f;
+  }
+
+  // software pipeline: the operands of block b+1 load while block b computes
+  v4i xa, wg, wu = {0, 0, 0, 0};
+  uint16_t dg, du = 0;
+  float dxl;
+  auto load = [&](int b) {
+    const ActBlock* ab = arow_act + b;
+    u32x4 q = *(const u32x4*)(ab->q + 16 * h);
+    __builtin_memcpy(&xa, &q, 16);
+    dxl = ab->scale;
+    wg = weight_half<DT>(cg + (size_t)b * CH * TILE * 16, h);
+    dg = sg[(size_t)b * TILE];
+    if constexpr (GATE_UP) {
+      wu = weight_half<DT>(cu + (size_t)b * CH * TILE * 16, h);
+      du = su[(size_t)b * TILE];
+    }
+  };
+  load(0);
+  for (int b = 0; b < nb; b++) {
+    const v4i cxa = xa, cwg = wg, cwu = wu;
+    const uint16_t cdg = dg, cdu = du;
+    float* sdx = s_dx[wave][b & 1];
+    if (lane < 32) sdx[lane] = dxl;  // row lane's d_x for this block
+    if (b + 1 < nb) load(b + 1);
+    v16i ig = {};
+    ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(cxa, cwg, ig, 0, 0, 0);
+    v16i iu = {};
+    if constexpr (GATE_UP) iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(cxa, cwu, iu, 0, 0, 0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float wgf = h2f(cdg);
+    const float wuf = h2f(cdu);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const f32x4 dx4 = *(const f32x4*)(sdx + 8 * q + 4 * h);  // rows 8q+4h .. +3
+#pragma unroll
+      for (int z = 0; z < 4; z++) {
+        const int j = 4 * q + z;
+        const float d = wgf * dx4[z];
+        accg[j] = accg[j] + d * (float)ig[j];
+        if constexpr (GATE_UP) {
+          const float du_ = wuf * dx4[z];
+          accu[j] = accu[j] + du_ * (float)iu[j];
+        }
+      }
+    }
+  }
+
+  if constexpr (GATE_UP) {
+    // h = silu(g) * u, quantized per (row, 32-column block): the 32 columns
+    // of a row sit in the 32 lanes of one half
+    ExpTable tab;
+    tab.load();
+    const int nblk = n0 / QK;
+    const int nbo = a.ncols / QK;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int row = (j % 4) + 4 * h + 8 * (j / 4);
+      const float hv = wave_silu(accg[j], tab) * accu[j];
+      float scale;
+      int qsum;
+      const int qv = quant_block_lane(hv, &scale, &qsum);
+      if (row < tl.rows) {
+        ActBlock* hb = a.hact + (size_t)(tl.row0 + row) * nbo + nblk;
+        hb->q[lane & 31] = (int8_t)qv;
+        if ((lane & 31) == 0) {
+          hb->scale = scale;
+          hb->qsum = qsum;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int row = (j % 4) + 4 * h + 8 * (j / 4);
+      if (row < tl.rows) a.y[(size_t)(tl.row0 + row) * a.ncols + n] = accg[j];
+    }
+  }
+}
+
+// out[t] = 0, then out[t] = out[t] + w[t][s] * y[pos(t, s)] for s in route
+// order (MoeLayer::forward's combine, src/model/moe.rs:63-68).
+__global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y,
+                                                 const int* __restrict__ pos_of,
+                                                 const float* __restrict__ route_w, int k, int H,
+                                                 float* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= H) return;
+  float acc = 0.0f;
+  for (int s = 0; s < k; s++)
+    acc = acc + route_w[(size_t)t * k + s] * y[(size_t)pos_of[(size_t)t * k + s] * H + i];
+  out[(size_t)t * H + i] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+size_t prefill_min_tokens(size_t) { return 8; }
+
+static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+struct WsLayout {
+  size_t perm, pos_of, tiles, ntiles, hact, y, total;
+  size_t max_tiles;
+};
+
+static WsLayout ws_layout(const PrefillLayer& L, size_t T) {
+  WsLayout w{};
+  const size_t A = T * (size_t)L.k;
+  w.max_tiles = (A + TM - 1) / TM + (size_t)L.E;
+  size_t o = 0;
+  w.perm = o;
+  o += align256(A * 4);
+  w.pos_of = o;
+  o += align256(A * 4);
+  w.tiles = o;
+  o += align256(w.max_tiles * sizeof(Tile));
+  w.ntiles = o;
+  o += 256;
+  w.hact = o;
+  o += align256(A * (size_t)(L.I / QK) * sizeof(ActBlock));
+  w.y = o;
+  o += align256(A * (size_t)L.H * 4);
+  w.total = o;
+  return w;
+}
+
+size_t prefill_workspace_bytes(const PrefillLayer& L, size_t T) { return ws_layout(L, T).total; }
+
+hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T, const float* x,
+                           const float* logits, float* out, hipStream_t st,
+                           const LaunchHook& hook) {
+  if (L.E > GROUP_MAX_E || L.k < 1 || L.H % QK || L.I % QK) return hipErrorInvalidValue;
+  const WsLayout w = ws_layout(L, T);
+  if (ws.bytes < w.total) {
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return e;
+    if (ws.base) (void)hipFree(ws.base);
+    ws.base = nullptr;
+    ws.bytes = 0;
+    e = hipMalloc(&ws.base, w.total);
+    if (e != hipSuccess) return e;
+    ws.bytes = w.total;
+  }
+  char* b = (char*)ws.base;
+  int* perm = (int*)(b + w.perm);
+  int* pos_of = (int*)(b + w.pos_of);
+  Tile* tiles = (Tile*)(b + w.tiles);
+  int* ntiles = (int*)(b + w.ntiles);
+  ActBlock* hact = (ActBlock*)(b + w.hact);
+  float* y = (float*)(b + w.y);
+  const int nbh = L.H / QK, nbi = L.I / QK;
+  const size_t A = T * (size_t)L.k;
+  hipError_t e;
+#define HALE_STEP(kind, call)       \
+  do {                              \
+    hook.on_begin(kind);            \
+    e = (call);                     \
+    hook.on_end();                  \
+    if (e != hipSuccess) return e;  \
+  } while (0)
+
+  // 1. route every token and quantize its activations
+  if (logits) {
+    HALE_STEP(K_ACT_QUANT, launch_act_quant(x, T * nbh, L.act, st));
+  } else {
+    HALE_STEP(K_ROUTE, launch_route_logits(L.router, x, L.H, L.E, (int)T, L.act, L.logits, st));
+    logits = L.logits;
+  }
+  HALE_STEP(K_ROUTE, launch_route_select(logits, L.E, L.k, L.normalize, (int)T, L.route_idx,
+                                         L.route_w, L.stats, st));
+  // 2. group assignments by expert
+  HALE_STEP(K_GROUP, (k_group<<<1, 64 * GROUP_WAVES, 0, st>>>(L.route_idx, (int)A, L.E, perm,
+                                                               pos_of, tiles, ntiles),
+                      hipGetLastError()));
+  // 3. grouped gate/up with SiLU and requantization
+  GroupedArgs g{};
+  g.codes = L.gate_c;
+  g.scales = L.gate_s;
+  g.codes2 = L.up_c;
+  g.scales2 = L.up_s;
+  g.codes_stride = L.gc_bytes;
+  g.scales_stride = L.gs_elems;
+  g.nb = nbh;
+  g.ncols = L.I;
+  g.tiles = tiles;
+  g.ntiles = ntiles;
+  g.perm = perm;
+  g.k = L.k;
+  g.act = L.act;
+  g.hact = hact;
+  dim3 gg((unsigned)w.max_tiles, (unsigned)((L.I + TN - 1) / TN));
+  if (L.dtype == Q8_0)
+    HALE_STEP(K_GROUPED_GATE_UP, (k_grouped<Q8_0, true><<<gg, 256, 0, st>>>(g), hipGetLastError()));
+  else
+    HALE_STEP(K_GROUPED_GATE_UP, (k_grouped<Q4_0, true><<<gg, 256, 0, st>>>(g), hipGetLastError()));
+  // 4. grouped down
+  GroupedArgs d{};
+  d.codes = L.down_c;
+  d.scales = L.down_s;
+  d.codes_stride = L.dc_bytes;
+  d.scales_stride = L.ds_elems;
+  d.nb = nbi;
+  d.ncols = L.H;
+  d.tiles = tiles;
+  d.ntiles = ntiles;
+  d.perm = perm;
+  d.k = L.k;
+  d.act = hact;
+  d.y = y;
+  dim3 gd((unsigned)w.max_tiles, (unsigned)((L.H + TN - 1) / TN));
+  if (L.dtype == Q8_0)
+    HALE_STEP(K_GROUPED_DOWN, (k_grouped<Q8_0, false><<<gd, 256, 0, st>>>(d), hipGetLastError()));
+  else
+    HALE_STEP(K_GROUPED_DOWN, (k_grouped<Q4_0, false><<<gd, 256, 0, st>>>(d), hipGetLastError()));
+  // 5. route-order combine
+  dim3 gc((unsigned)((L.H + 255) / 256), (unsigned)T);
+  HALE_STEP(K_COMBINE, (k_combine<<<gc, 256, 0, st>>>(y, pos_of, L.route_w, L.k, L.H, out),
+                        hipGetLastError()));
+#undef HALE_STEP
+  return hipSuccess;
 }
 
 void prefill_free(PrefillWorkspace& ws) {
