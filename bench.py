@@ -35,6 +35,13 @@ HBM_PEAK_GBS = 8000.0
 
 E, HID, INTER, TOPK = 128, 2048, 768, 8
 DTYPE = H.Q4_0
+INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA
+
+# prefill workloads: (name, dtype, hidden, inter, experts, top_k, tokens)
+PREFILL = [
+    ("qwen3-30b-a3b prefill 512 tok q8_0", H.Q8_0, 2048, 768, 128, 8, 512),
+    ("qwen3-235b-a22b prefill 2048 tok q4_0", H.Q4_0, 4096, 1536, 128, 8, 2048),
+]
 
 
 def log(msg):
@@ -45,31 +52,90 @@ def expert_bytes(dtype, hidden, inter):
     return 2 * inter * H.row_bytes(dtype, hidden) + hidden * H.row_bytes(dtype, inter)
 
 
-def build_layers(ctx, nlayers, seed=1234):
+def build_layers(ctx, nlayers, seed=1234, dtype=DTYPE, hid=HID, inter=INTER, experts=E,
+                 topk=TOPK, router=True):
     """nlayers MoE layers with N(0, 0.02^2) weights quantized on the GPU."""
-    ng = INTER * H.row_bytes(DTYPE, HID)
-    nd = HID * H.row_bytes(DTYPE, INTER)
-    vals = ctx.malloc(E * INTER * HID * 4)
-    aos = [ctx.malloc(E * ng), ctx.malloc(E * ng), ctx.malloc(E * nd)]
-    rbuf = ctx.malloc(E * HID * 4)
+    ng = inter * H.row_bytes(dtype, hid)
+    nd = hid * H.row_bytes(dtype, inter)
+    chunk = min(experts, 32)  # experts generated per pass (bounds the f32 staging)
+    vals = ctx.malloc(chunk * inter * hid * 4)
+    aos = [ctx.malloc(chunk * ng), ctx.malloc(chunk * ng), ctx.malloc(chunk * nd)]
+    rbuf = ctx.malloc(experts * hid * 4) if router else None
     layers = []
     for l in range(nlayers):
-        rbuf.fill_normal(seed + 7919 * l, E * HID, 0.0, 0.02)
-        rmat = H._vp()
-        ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, H.F32, E, HID, H._vp(rbuf.address),
-                                                    E * HID * 4, H.C.byref(rmat)), "router")
-        router = H.WeightMatrix(ctx, rmat, E, HID, H.F32)
-        moe = H.MoeLayer(ctx, l, E, HID, INTER, DTYPE, TOPK, True, router)
-        for j, (rows, cols) in enumerate(((INTER, HID), (INTER, HID), (HID, INTER))):
-            vals.fill_normal(seed + 7919 * l + 101 * (j + 1), E * rows * cols, 0.0, 0.02)
-            ctx.check(H.lib().hale_encode_rows_device(ctx.handle, DTYPE, E * rows, cols,
-                                                      H._vp(vals.address), H._vp(aos[j].address)),
-                      "encode")
-        moe.set_experts_device(0, E, aos[0].address, aos[1].address, aos[2].address)
+        rm = None
+        if router:
+            rbuf.fill_normal(seed + 7919 * l, experts * hid, 0.0, 0.02)
+            rmat = H._vp()
+            ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, H.F32, experts, hid,
+                                                        H._vp(rbuf.address), experts * hid * 4,
+                                                        H.C.byref(rmat)), "router")
+            rm = H.WeightMatrix(ctx, rmat, experts, hid, H.F32)
+        moe = H.MoeLayer(ctx, l, experts, hid, inter, dtype, topk, True, rm)
+        for e0 in range(0, experts, chunk):
+            n = min(chunk, experts - e0)
+            for j, (rows, cols) in enumerate(((inter, hid), (inter, hid), (hid, inter))):
+                vals.fill_normal(seed + 7919 * l + 101 * (j + 1) + 1000003 * e0, n * rows * cols, 0.0, 0.02)
+                ctx.check(H.lib().hale_encode_rows_device(ctx.handle, dtype, n * rows, cols,
+                                                          H._vp(vals.address), H._vp(aos[j].address)),
+                          "encode")
+            moe.set_experts_device(e0, n, aos[0].address, aos[1].address, aos[2].address)
         layers.append(moe)
     for b in (vals, rbuf, *aos):
-        b.free()
+        if b is not None:
+            b.free()
     return layers
+
+
+def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps):
+    """One MoE layer forward over `tokens` tokens with Zipf-skewed routing."""
+    from hale_moe.synth import zipf_logits
+
+    ctx = H.Context(0)
+    moe = build_layers(ctx, 1, seed=4321, dtype=dtype, hid=hid, inter=inter, experts=experts,
+                       topk=topk, router=False)[0]
+    logits = zipf_logits(tokens, experts, 1.1, seed=7)
+    dl = ctx.malloc(logits.nbytes)
+    dl.upload(logits)
+    dx = ctx.malloc(tokens * hid * 4)
+    dx.fill_normal(17, tokens * hid, 0.0, 1.0)
+    dout = ctx.malloc(tokens * hid * 4)
+    didx = ctx.malloc(tokens * topk * 4)
+    for _ in range(2):
+        moe.forward_device(tokens, dx.address, dout.address, dl.address, didx.address)
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        moe.forward_device(tokens, dx.address, dout.address, dl.address)
+    ms = ctx.timer_stop() / reps
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(reps):
+        moe.forward_device(tokens, dx.address, dout.address, dl.address)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    idx = didx.download(np.int32, tokens * topk)
+    touched = len(np.unique(idx))
+    groups = np.bincount(idx, minlength=experts)
+    ops = 2.0 * tokens * topk * 3 * hid * inter
+    wbytes = touched * expert_bytes(dtype, hid, inter)
+    sec = ms / 1000.0
+    res = {
+        "workload": name, "tokens": tokens, "ms": round(ms, 4),
+        "tokens_per_s": round(tokens / sec, 1),
+        "tops": round(ops / sec / 1e12, 2),
+        "pct_int8_mfma_peak": round(100 * ops / sec / INT8_PEAK_OPS, 2),
+        "weight_bytes": wbytes, "pct_hbm_peak": round(100 * wbytes / sec / 1e9 / HBM_PEAK_GBS, 2),
+        "experts_touched": touched, "group_sizes": {"max": int(groups.max()),
+                                                      "median": float(np.median(groups)),
+                                                      "min": int(groups.min())},
+        "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()},
+    }
+    for b in (dl, dx, dout, didx):
+        b.free()
+    moe.close()
+    ctx.close()
+    return res
 
 
 def gpu_decode(args):
@@ -141,6 +207,7 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -165,6 +232,13 @@ def main():
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
                 "traffic": None, "bytes_per_launch": launch_bytes.get(dom)}
+
+    prefill = []
+    if not args.no_prefill:
+        for (name, dt, hid, inter, ex, k, tok) in PREFILL:
+            prefill.append(gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=10))
+            log(f"prefill {name}: {prefill[-1]['ms']} ms, {prefill[-1]['tokens_per_s']} tok/s, "
+                f"{prefill[-1]['pct_int8_mfma_peak']}% int8 MFMA")
 
     cpu = None
     if not args.no_cpu:
@@ -201,6 +275,7 @@ def main():
         "moe_layer_tokens_per_s": round(steps / sec, 1),
         "roofline": roofline,
         "kernels": kernels,
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

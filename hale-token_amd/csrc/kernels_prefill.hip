@@ -26,6 +26,7 @@ namespace hale {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int TM = 32;          // assignments (rows) per tile
 constexpr int TN = 128;         // output columns per work-group (4 waves x 32)
@@ -171,24 +172,27 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
 // (q4_0: the low nibbles are K 0-15, the high nibbles K 16-31).  Result
 // element j of lane l is row (j%4) + 4*(l/32) + 8*(j/4), column l%32.
 
-// 16 signed weight codes of K half `h` of (column, block)
+// The 16-byte chunk holding K half `h` of (column, block): q8_0 keeps the
+// halves in two chunks, q4_0 keeps both in one (low nibbles K 0-15, high
+// nibbles K 16-31).
 template <int DT>
-__device__ __forceinline__ v4i weight_half(const uint8_t* chunk0, int h) {
-  if constexpr (DT == Q8_0) {
-    u32x4 v = __builtin_nontemporal_load((const u32x4*)(chunk0 + h * TILE * 16));
-    v4i r;
-    __builtin_memcpy(&r, &v, 16);
-    return r;
-  } else {
-    u32x4 v = __builtin_nontemporal_load((const u32x4*)chunk0);
-    // nibble n -> signed code n - 8: (n | 0x80) - 8 keeps each byte apart,
-    // then ^ 0x80 maps n + 120 to n - 8 (mod 256)
-    u32x4 n = h ? ((v >> 4) & 0x0f0f0f0fu) : (v & 0x0f0f0f0fu);
-    n = ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-    v4i r;
-    __builtin_memcpy(&r, &n, 16);
-    return r;
-  }
+__device__ __forceinline__ u32x4 weight_chunk(const uint8_t* chunk0, int h) {
+  if constexpr (DT == Q8_0)
+    return __builtin_nontemporal_load((const u32x4*)(chunk0 + h * TILE * 16));
+  else
+    return __builtin_nontemporal_load((const u32x4*)chunk0);
+}
+
+// B operand from a loaded chunk.  q8_0: the signed codes as they are.  q4_0:
+// the unsigned nibbles n (0..15) of half h; the MFMA's accumulator then starts
+// at -8 * sum(x) of the row so that it ends at sum((n - 8) * x), the same
+// integer as with signed codes.
+template <int DT>
+__device__ __forceinline__ v4i weight_operand(u32x4 v, int h) {
+  if constexpr (DT == Q4_0) v = (v >> (u32x4)(4 * h)) & 0x0f0f0f0fu;
+  v4i r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
 }
 
 struct GroupedArgs {
@@ -212,7 +216,6 @@ struct GroupedArgs {
 template <int DT, bool GATE_UP>
 __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   constexpr int CH = Layout<DT>::CH;
-  __shared__ float s_dx[4][2][TM];  // per wave, double buffer: row scales of a block
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int ti = blockIdx.x;
@@ -244,58 +247,58 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
     su = a.scales2 + e * a.scales_stride + tile_n * nb * TILE + rn;
   }
 
-  float accg[16], accu[16];
-#pragma unroll
-  for (int j = 0; j < 16; j++) {
-    accg[j] = 0.0f;
-    accu[j] = 0.0f;
-  }
+  // accumulators start at +0.0 like the reference's `let mut total = 0.0`,
+  // so no sum can become -0.0: the sign of a zero scale product never shows
+  v16f accg = {}, accu = {};
 
-  // software pipeline: the operands of block b+1 load while block b computes
-  v4i xa, wg, wu = {0, 0, 0, 0};
+  // software pipeline: the raw operands of block b+1 load while block b
+  // computes; nothing reads them before the next iteration
+  u32x4 xr, wgr, wur = {0, 0, 0, 0};
   uint16_t dg, du = 0;
   float dxl;
   auto load = [&](int b) {
     const ActBlock* ab = arow_act + b;
-    u32x4 q = *(const u32x4*)(ab->q + 16 * h);
-    __builtin_memcpy(&xa, &q, 16);
+    xr = *(const u32x4*)(ab->q + 16 * h);
     dxl = ab->scale;
-    wg = weight_half<DT>(cg + (size_t)b * CH * TILE * 16, h);
+    wgr = weight_chunk<DT>(cg + (size_t)b * CH * TILE * 16, h);
     dg = sg[(size_t)b * TILE];
     if constexpr (GATE_UP) {
-      wu = weight_half<DT>(cu + (size_t)b * CH * TILE * 16, h);
+      wur = weight_chunk<DT>(cu + (size_t)b * CH * TILE * 16, h);
       du = su[(size_t)b * TILE];
     }
   };
+  // q4_0 offset term: B = -8 in every byte makes the product -8 * sum(x) of
+  // the row, broadcast over the columns
+  const v4i minus8 = {(int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u};
   load(0);
   for (int b = 0; b < nb; b++) {
-    const v4i cxa = xa, cwg = wg, cwu = wu;
+    const u32x4 cxr = xr, cwgr = wgr, cwur = wur;
     const uint16_t cdg = dg, cdu = du;
-    float* sdx = s_dx[wave][b & 1];
-    if (lane < 32) sdx[lane] = dxl;  // row lane's d_x for this block
+    const float cdx = dxl;
     if (b + 1 < nb) load(b + 1);
-    v16i ig = {};
-    ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(cxa, cwg, ig, 0, 0, 0);
+    v4i xa;
+    __builtin_memcpy(&xa, &cxr, 16);
+    v16i c0 = {};
+    if constexpr (DT == Q4_0) c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, minus8, c0, 0, 0, 0);
+    const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(cwgr, h), c0, 0, 0, 0);
     v16i iu = {};
-    if constexpr (GATE_UP) iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(cxa, cwu, iu, 0, 0, 0);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const float wgf = h2f(cdg);
-    const float wuf = h2f(cdu);
+    if constexpr (GATE_UP)
+      iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(cwur, h), c0, 0, 0, 0);
+    // scale products d_w[col] * d_x[row] of the whole 32x32 tile as a K=2
+    // f32 outer product whose second K column is zero: lanes 0-31 hold
+    // A[row][0] = d_x and B[0][col] = d_w.  The matrix core rounds each
+    // product exactly like a VALU multiply (only the sign of a zero product
+    // can differ, and that cannot reach an accumulator that starts at +0).
+    const float ax = lane < 32 ? cdx : 0.0f;
+    v16f pg = {};
+    pg = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(cdg) : 0.0f, pg, 0, 0, 0);
+    v16f pu = {};
+    if constexpr (GATE_UP)
+      pu = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(cdu) : 0.0f, pu, 0, 0, 0);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const f32x4 dx4 = *(const f32x4*)(sdx + 8 * q + 4 * h);  // rows 8q+4h .. +3
-#pragma unroll
-      for (int z = 0; z < 4; z++) {
-        const int j = 4 * q + z;
-        const float d = wgf * dx4[z];
-        accg[j] = accg[j] + d * (float)ig[j];
-        if constexpr (GATE_UP) {
-          const float du_ = wuf * dx4[z];
-          accu[j] = accu[j] + du_ * (float)iu[j];
-        }
-      }
+    for (int j = 0; j < 16; j++) {
+      accg[j] = accg[j] + pg[j] * (float)ig[j];
+      if constexpr (GATE_UP) accu[j] = accu[j] + pu[j] * (float)iu[j];
     }
   }
 
