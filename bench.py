@@ -12,10 +12,17 @@ value: algorithmic bytes per step (8 routed experts x 2,654,208 B + the
 1,048,576 B router) x steps / time, in GB/s.  roofline: the dominant
 kernel's algorithmic bytes per launch / its average duration, timed with
 HIP events on the library's stream during a second (eager) pass.
+roofline.traffic: HBM bytes per launch of that kernel from the FETCH_SIZE and
+WRITE_SIZE counter passes, each scaled by what the counter reads for the
+plain copy kernel, as committed in profiles/traffic_decode_q4_qwen3_30b.txt.
 cpu_baseline: the oracle (C restatement of the reference CPU algorithm)
 on one layer of the same shape, on this host's cores.
+prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
+2048 tokens q4_0 H 4096 I 1536; 128 experts, top-8, Zipf-skewed routing)
+with tokens/s, TOPS and the fraction of the int8 MFMA peak.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--no-prefill] [--decode-eager] [--copy-calibration BYTES]
 """
 import argparse
 import json
@@ -138,6 +145,62 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps):
     return res
 
 
+def copy_calibration(nbytes, reps=5):
+    """The library's plain copy kernel over nbytes, reps times: the yardstick
+    for the FETCH_SIZE / WRITE_SIZE counters (each launch reads and writes
+    nbytes)."""
+    ctx = H.Context(0)
+    a, b = ctx.malloc(nbytes), ctx.malloc(nbytes)
+    a.fill_normal(1, nbytes // 4)
+    b.copy_from(a, nbytes)
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        b.copy_from(a, nbytes)
+    ms = ctx.timer_stop() / reps
+    a.free()
+    b.free()
+    ctx.close()
+    return {"copy_bytes": nbytes, "launches": reps + 1, "ms": round(ms, 4),
+            "GB_per_s": round(2 * nbytes / ms / 1e6, 1)}
+
+
+def decode_eager(args):
+    """Two eager passes over the resident layers (no graph): the run the
+    per-dispatch counter passes profile."""
+    ctx = H.Context(0)
+    layers = build_layers(ctx, args.layers)
+    xs = ctx.malloc(64 * HID * 4)
+    xs.fill_normal(99, 64 * HID, 0.0, 1.0)
+    out = ctx.malloc(HID * 4)
+    L = len(layers)
+    for s in range(2 * L):
+        layers[s % L].forward_device(1, xs.offset((s % 64) * HID * 4), out.address)
+    ctx.synchronize()
+    for m in layers:
+        m.close()
+    ctx.close()
+    return 2 * L
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode_q4_qwen3_30b.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch by kernel, from the committed counter summary
+    (lines `traffic <kernel> <bytes>`), or {} when it is absent."""
+    out = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                p = line.split()
+                if len(p) == 3 and p[0] == "traffic":
+                    out[p[1]] = int(p[2])
+    except OSError:
+        pass
+    return out
+
+
 def gpu_decode(args):
     ctx = H.Context(0)
     t0 = time.time()
@@ -208,11 +271,21 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="only two eager decode passes over the layers (for counter runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only time the plain copy kernel over BYTES (counter yardstick)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        print(json.dumps(copy_calibration(args.copy_calibration)), flush=True)
+        return
+    if args.decode_eager:
+        print(json.dumps({"decode_eager_steps": decode_eager(args)}), flush=True)
+        return
 
     bytes_step = TOPK * expert_bytes(DTYPE, HID, INTER) + E * HID * 4
     steps, ms, prof = gpu_decode(args)
@@ -231,7 +304,7 @@ def main():
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1) if achieved else None,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-                "traffic": None, "bytes_per_launch": launch_bytes.get(dom)}
+                "traffic": measured_traffic().get(dom), "bytes_per_launch": launch_bytes.get(dom)}
 
     prefill = []
     if not args.no_prefill:

@@ -1,11 +1,50 @@
 // kernels.h -- launch interface between the host runtime and the kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
+#include <tuple>
+
 namespace hale {
+
+// Timing bracket of the per-kernel profiler.  While `stop` is set, launch()
+// hands the events to the runtime so that they take the kernels' own start
+// and end times: `start` at the first kernel of the bracket, `stop` at the
+// end of each kernel (the last one stands).  Per thread; the runtime opens
+// and closes brackets around its launchers.
+struct ProfEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+  bool started = false;
+};
+ProfEvents& prof_events();
+
+// kernel<<<grid, block, shmem, st>>>(args...), or the same launch with the
+// open bracket's events.  Arguments are converted to the kernel's parameter
+// types before their addresses are taken.
+template <typename... P, typename... A>
+hipError_t launch(void (*kernel)(P...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t st,
+                  A... args) {
+  static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+  ProfEvents& pe = prof_events();
+  if (!pe.stop) {
+    kernel<<<grid, block, shmem, st>>>(args...);
+    return hipGetLastError();
+  }
+  std::tuple<P...> typed{static_cast<P>(args)...};
+  void* ptrs[sizeof...(P) ? sizeof...(P) : 1];
+  std::apply([&](auto&... v) {
+    int i = 0;
+    ((ptrs[i++] = (void*)&v), ...);
+  }, typed);
+  hipError_t e = hipExtLaunchKernel((const void*)kernel, grid, block, ptrs, shmem, st,
+                                    pe.started ? nullptr : pe.start, pe.stop, 0);
+  pe.started = true;
+  return e;
+}
 
 struct ActBlock;
 
@@ -79,6 +118,7 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
 hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,
                              size_t cols, int32_t* isums, hipStream_t st);
 hipError_t launch_fill(float* p, size_t n, float v, hipStream_t st);
+hipError_t launch_copy(void* dst, const void* src, size_t n16, hipStream_t st);
 hipError_t launch_fill_normal(float* p, size_t n, uint64_t seed, float mean, float std,
                               hipStream_t st);
 
@@ -96,6 +136,7 @@ enum KernelKind : int {
   K_GROUPED_GATE_UP,
   K_GROUPED_DOWN,
   K_COMBINE,
+  K_COPY,
   K_KINDS
 };
 

@@ -788,6 +788,15 @@ __global__ void k_fill(float* __restrict__ p, size_t n, float v) {
   if (i < n) p[i] = v;
 }
 
+// dst[i] = src[i] for n16 16-byte units: one read and one write of every
+// byte, the yardstick for the HBM traffic counters
+__global__ __launch_bounds__(256) void k_copy(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
+                                              size_t n16) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+    __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 // ===========================================================================
 // Launchers
 // ===========================================================================
@@ -800,11 +809,8 @@ hipError_t launch_repack(int dtype, const uint8_t* aos, size_t rows, size_t cols
   size_t prow = padded_rows(rows);
   size_t n = prow * nb;
   if (n == 0) return hipSuccess;
-  if (dtype == Q8_0)
-    k_repack<Q8_0><<<blocks_for(n, 256), 256, 0, st>>>(aos, rows, nb, prow, codes, scales);
-  else
-    k_repack<Q4_0><<<blocks_for(n, 256), 256, 0, st>>>(aos, rows, nb, prow, codes, scales);
-  return hipGetLastError();
+  if (dtype == Q8_0) return launch(k_repack<Q8_0>, blocks_for(n, 256), 256, 0, st, aos, rows, nb, prow, codes, scales);
+  return launch(k_repack<Q4_0>, blocks_for(n, 256), 256, 0, st, aos, rows, nb, prow, codes, scales);
 }
 
 hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales, size_t rows,
@@ -812,43 +818,34 @@ hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales
   int nb = (int)(cols / QK);
   size_t n = rows * nb;
   if (n == 0) return hipSuccess;
-  if (dtype == Q8_0)
-    k_unpack<Q8_0><<<blocks_for(n, 256), 256, 0, st>>>(codes, scales, rows, nb, aos);
-  else
-    k_unpack<Q4_0><<<blocks_for(n, 256), 256, 0, st>>>(codes, scales, rows, nb, aos);
-  return hipGetLastError();
+  if (dtype == Q8_0) return launch(k_unpack<Q8_0>, blocks_for(n, 256), 256, 0, st, codes, scales, rows, nb, aos);
+  return launch(k_unpack<Q4_0>, blocks_for(n, 256), 256, 0, st, codes, scales, rows, nb, aos);
 }
 
 hipError_t launch_encode(int dtype, const float* values, size_t nblocks, uint8_t* out,
                          hipStream_t st) {
   if (nblocks == 0) return hipSuccess;
-  if (dtype == Q8_0)
-    k_encode<Q8_0><<<blocks_for(nblocks, 256), 256, 0, st>>>(values, nblocks, out);
-  else
-    k_encode<Q4_0><<<blocks_for(nblocks, 256), 256, 0, st>>>(values, nblocks, out);
-  return hipGetLastError();
+  if (dtype == Q8_0) return launch(k_encode<Q8_0>, blocks_for(nblocks, 256), 256, 0, st, values, nblocks, out);
+  return launch(k_encode<Q4_0>, blocks_for(nblocks, 256), 256, 0, st, values, nblocks, out);
 }
 
 hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipStream_t st) {
   if (nblocks == 0) return hipSuccess;
-  k_act_quant<<<blocks_for(nblocks * 32, 256), 256, 0, st>>>(x, nblocks, act);
-  return hipGetLastError();
+  return launch(k_act_quant, blocks_for(nblocks * 32, 256), 256, 0, st, x, nblocks, act);
 }
 
 hipError_t launch_route_logits(const float* router, const float* x, int H, int E, int T,
                                ActBlock* act, float* logits, hipStream_t st) {
   if (H > ROUTE_MAX_H || E > ROUTE_MAX_E || H % QK || E < 1 || T < 1) return hipErrorInvalidValue;
   dim3 grid(E, T);
-  k_route_logits<<<grid, 64, 0, st>>>(router, x, H, E, act, logits);
-  return hipGetLastError();
+  return launch(k_route_logits, grid, 64, 0, st, router, x, H, E, act, logits);
 }
 
 hipError_t launch_route_select(const float* logits, int E, int k, int normalize, int T,
                                int* route_idx, float* route_w, unsigned long long* stats,
                                hipStream_t st) {
   if (E > ROUTE_MAX_E || k > 64 || k > E || k < 1 || T < 1) return hipErrorInvalidValue;
-  k_route_select<<<T, 64, 0, st>>>(logits, E, k, normalize, route_idx, route_w, stats);
-  return hipGetLastError();
+  return launch(k_route_select, T, 64, 0, st, logits, E, k, normalize, route_idx, route_w, stats);
 }
 
 hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int slots,
@@ -860,8 +857,7 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   dim3 grid(groups, slots);
 #define HALE_GEMV_CASE(D, E)                                  \
   if (dtype == D && epi == E) {                               \
-    k_gemv<D, E><<<grid, 256, 0, st>>>(a);                    \
-    return hipGetLastError();                                 \
+    return launch(k_gemv<D, E>, grid, 256, 0, st, a);         \
   }
   HALE_GEMV_CASE(Q8_0, EPI_PLAIN)
   HALE_GEMV_CASE(Q8_0, EPI_GATE_UP)
@@ -876,13 +872,9 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
 hipError_t launch_down_combine(int dtype, const DownArgs& a, int groups, hipStream_t st) {
   if (groups == 0) return hipSuccess;
   if (a.nb < 1 || a.slots < 1 || a.slots > 64) return hipErrorInvalidValue;
-  if (dtype == Q8_0)
-    k_down_combine<Q8_0><<<groups, 64 * DOWN_WAVES, 0, st>>>(a);
-  else if (dtype == Q4_0)
-    k_down_combine<Q4_0><<<groups, 64 * DOWN_WAVES, 0, st>>>(a);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (dtype == Q8_0) return launch(k_down_combine<Q8_0>, groups, 64 * DOWN_WAVES, 0, st, a);
+  if (dtype == Q4_0) return launch(k_down_combine<Q4_0>, groups, 64 * DOWN_WAVES, 0, st, a);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,
@@ -890,24 +882,25 @@ hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* ac
   int nb = (int)(cols / QK);
   size_t n = rows * nb;
   if (n == 0) return hipSuccess;
-  if (dtype == Q8_0)
-    k_block_sums<Q8_0><<<blocks_for(n, 256), 256, 0, st>>>(codes, act, rows, nb, isums);
-  else
-    k_block_sums<Q4_0><<<blocks_for(n, 256), 256, 0, st>>>(codes, act, rows, nb, isums);
-  return hipGetLastError();
+  if (dtype == Q8_0) return launch(k_block_sums<Q8_0>, blocks_for(n, 256), 256, 0, st, codes, act, rows, nb, isums);
+  return launch(k_block_sums<Q4_0>, blocks_for(n, 256), 256, 0, st, codes, act, rows, nb, isums);
 }
 
 hipError_t launch_fill_normal(float* p, size_t n, uint64_t seed, float mean, float std,
                               hipStream_t st) {
   if (n == 0) return hipSuccess;
-  k_fill_normal<<<blocks_for((n + 1) / 2, 256), 256, 0, st>>>(p, n, seed, mean, std);
-  return hipGetLastError();
+  return launch(k_fill_normal, blocks_for((n + 1) / 2, 256), 256, 0, st, p, n, seed, mean, std);
 }
 
 hipError_t launch_fill(float* p, size_t n, float v, hipStream_t st) {
   if (n == 0) return hipSuccess;
-  k_fill<<<blocks_for(n, 256), 256, 0, st>>>(p, n, v);
-  return hipGetLastError();
+  return launch(k_fill, blocks_for(n, 256), 256, 0, st, p, n, v);
+}
+
+hipError_t launch_copy(void* dst, const void* src, size_t n16, hipStream_t st) {
+  if (!n16) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<size_t>(blocks_for(n16, 256), 256 * 64);
+  return launch(k_copy, grid, 256, 0, st, (u32x4*)dst, (const u32x4*)src, n16);
 }
 
 }  // namespace hale

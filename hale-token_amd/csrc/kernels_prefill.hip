@@ -428,9 +428,8 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   HALE_STEP(K_ROUTE, launch_route_select(logits, L.E, L.k, L.normalize, (int)T, L.route_idx,
                                          L.route_w, L.stats, st));
   // 2. group assignments by expert
-  HALE_STEP(K_GROUP, (k_group<<<1, 64 * GROUP_WAVES, 0, st>>>(L.route_idx, (int)A, L.E, perm,
-                                                               pos_of, tiles, ntiles),
-                      hipGetLastError()));
+  HALE_STEP(K_GROUP, launch(k_group, 1, 64 * GROUP_WAVES, 0, st, L.route_idx, (int)A, L.E, perm,
+                            pos_of, tiles, ntiles));
   // 3. grouped gate/up with SiLU and requantization
   GroupedArgs g{};
   g.codes = L.gate_c;
@@ -449,9 +448,9 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   g.hact = hact;
   dim3 gg((unsigned)w.max_tiles, (unsigned)((L.I + TN - 1) / TN));
   if (L.dtype == Q8_0)
-    HALE_STEP(K_GROUPED_GATE_UP, (k_grouped<Q8_0, true><<<gg, 256, 0, st>>>(g), hipGetLastError()));
+    HALE_STEP(K_GROUPED_GATE_UP, (launch(k_grouped<Q8_0, true>, gg, 256, 0, st, g)));
   else
-    HALE_STEP(K_GROUPED_GATE_UP, (k_grouped<Q4_0, true><<<gg, 256, 0, st>>>(g), hipGetLastError()));
+    HALE_STEP(K_GROUPED_GATE_UP, (launch(k_grouped<Q4_0, true>, gg, 256, 0, st, g)));
   // 4. grouped down
   GroupedArgs d{};
   d.codes = L.down_c;
@@ -468,13 +467,12 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   d.y = y;
   dim3 gd((unsigned)w.max_tiles, (unsigned)((L.H + TN - 1) / TN));
   if (L.dtype == Q8_0)
-    HALE_STEP(K_GROUPED_DOWN, (k_grouped<Q8_0, false><<<gd, 256, 0, st>>>(d), hipGetLastError()));
+    HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q8_0, false>, gd, 256, 0, st, d)));
   else
-    HALE_STEP(K_GROUPED_DOWN, (k_grouped<Q4_0, false><<<gd, 256, 0, st>>>(d), hipGetLastError()));
+    HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q4_0, false>, gd, 256, 0, st, d)));
   // 5. route-order combine
   dim3 gc((unsigned)((L.H + 255) / 256), (unsigned)T);
-  HALE_STEP(K_COMBINE, (k_combine<<<gc, 256, 0, st>>>(y, pos_of, L.route_w, L.k, L.H, out),
-                        hipGetLastError()));
+  HALE_STEP(K_COMBINE, launch(k_combine, gc, 256, 0, st, y, pos_of, L.route_w, L.k, L.H, out));
 #undef HALE_STEP
   return hipSuccess;
 }

@@ -45,8 +45,8 @@ struct hale_ctx {
   bool prof_on = false;
   std::vector<hipEvent_t> ev_pool;
   std::vector<ProfRecord> recs;
-  hipEvent_t open_start = nullptr;
   int open_kind = -1;
+  bool prof_saved = false;  // prof_on while a capture runs (profiling is off then)
   double prof_ms[K_KINDS] = {};
   uint64_t prof_n[K_KINDS] = {};
 };
@@ -207,22 +207,37 @@ static hipEvent_t prof_event(hale_ctx* c) {
   return e;
 }
 
+ProfEvents& hale::prof_events() {
+  static thread_local ProfEvents pe;
+  return pe;
+}
+
+// Opens a bracket: the kernels launched until prof_end record its events.
 static void prof_begin(hale_ctx* c, int kind) {
   if (!c->prof_on) return;
-  hipEvent_t e = prof_event(c);
-  if (!e) return;
-  (void)hipEventRecord(e, c->stream);
-  c->open_start = e;
+  hipEvent_t a = prof_event(c), b = prof_event(c);
+  if (!a || !b) {
+    if (a) c->ev_pool.push_back(a);
+    if (b) c->ev_pool.push_back(b);
+    return;
+  }
+  ProfEvents& pe = prof_events();
+  pe.start = a;
+  pe.stop = b;
+  pe.started = false;
   c->open_kind = kind;
 }
 
 static void prof_end(hale_ctx* c) {
-  if (!c->prof_on || !c->open_start) return;
-  hipEvent_t e = prof_event(c);
-  if (!e) return;
-  (void)hipEventRecord(e, c->stream);
-  c->recs.push_back({c->open_kind, c->open_start, e});
-  c->open_start = nullptr;
+  ProfEvents& pe = prof_events();
+  if (!pe.stop) return;
+  if (pe.started) {
+    c->recs.push_back({c->open_kind, pe.start, pe.stop});
+  } else {  // no kernel ran
+    c->ev_pool.push_back(pe.start);
+    c->ev_pool.push_back(pe.stop);
+  }
+  pe = ProfEvents{};
 }
 
 static void hook_begin(void* self, int kind) { prof_begin((hale_ctx*)self, kind); }
@@ -1044,6 +1059,16 @@ extern "C" int hale_fill_normal_device(hale_ctx* c, uint64_t seed, float mean, f
   return HALE_OK;
 }
 
+extern "C" int hale_copy_device(hale_ctx* c, void* d_dst, const void* d_src, size_t n) {
+  if (!c || (n && (!d_dst || !d_src))) return fail(c, HALE_EINVAL, "copy_device: NULL argument");
+  if (n % 16 || (uintptr_t)d_dst % 16 || (uintptr_t)d_src % 16)
+    return fail(c, HALE_EINVAL, "copy_device: size and addresses must be multiples of 16");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  LAUNCH(c, K_COPY, launch_copy(d_dst, d_src, n / 16, c->stream));
+  return HALE_OK;
+}
+
 extern "C" int hale_timer_start(hale_ctx* c) {
   if (!c) return HALE_EINVAL;
   std::lock_guard<std::recursive_mutex> g(c->mu);
@@ -1119,7 +1144,7 @@ extern "C" int hale_kernel_kinds(void) { return K_KINDS; }
 extern "C" const char* hale_kernel_name(int kind) {
   static const char* names[K_KINDS] = {"route", "gate_up", "down", "act_quant", "gemv", "encode",
                                        "repack", "fill", "group", "grouped_gate_up",
-                                       "grouped_down", "combine"};
+                                       "grouped_down", "combine", "copy"};
   return kind >= 0 && kind < K_KINDS ? names[kind] : "";
 }
 
@@ -1132,6 +1157,8 @@ extern "C" int hale_graph_begin(hale_ctx* c) {
     c->mu.unlock();
     return fail(c, HALE_EHIP, "begin capture: %s", hipGetErrorString(e));
   }
+  c->prof_saved = c->prof_on;  // profiler events are not captured into graphs
+  c->prof_on = false;
   return HALE_OK;
 }
 
@@ -1140,6 +1167,7 @@ extern "C" int hale_graph_end(hale_ctx* c, hale_graph** out) {
   *out = nullptr;
   hipGraph_t graph = nullptr;
   hipError_t e = hipStreamEndCapture(c->stream, &graph);
+  c->prof_on = c->prof_saved;
   c->mu.unlock();
   if (e != hipSuccess) return fail(c, HALE_EHIP, "end capture: %s", hipGetErrorString(e));
   hale_graph* g = new (std::nothrow) hale_graph;

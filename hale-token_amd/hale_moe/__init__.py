@@ -82,6 +82,7 @@ SIGNATURES = {
     "hale_memcpy_htod": (C.c_int, [_vp, _vp, _vp, _sz]),
     "hale_memcpy_dtoh": (C.c_int, [_vp, _vp, _vp, _sz]),
     "hale_fill_normal_device": (C.c_int, [_vp, C.c_uint64, C.c_float, C.c_float, _vp, _sz]),
+    "hale_copy_device": (C.c_int, [_vp, _vp, _vp, _sz]),
     "hale_timer_start": (C.c_int, [_vp]),
     "hale_timer_stop": (C.c_int, [_vp, C.POINTER(C.c_double)]),
     "hale_profile_enable": (C.c_int, [_vp, C.c_int]),
@@ -277,6 +278,13 @@ class DeviceBuffer:
         self.ctx.check(lib().hale_fill_normal_device(self.ctx.handle, seed, mean, std,
                                                      _vp(self.address + offset), count),
                        "fill_normal")
+
+    def copy_from(self, src: "DeviceBuffer", nbytes: int):
+        """self[0, nbytes) = src[0, nbytes) with the library's copy kernel."""
+        if nbytes > min(self.nbytes, src.nbytes):
+            raise ValueError("copy past the end of a buffer")
+        self.ctx.check(lib().hale_copy_device(self.ctx.handle, _vp(self.address), _vp(src.address),
+                                              nbytes), "copy")
 
     def free(self):
         if self.ptr and self.ctx.alive:

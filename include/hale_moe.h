@@ -216,6 +216,10 @@ int hale_memcpy_dtoh(hale_ctx *ctx, void *dst, const void *src, size_t n);
  * generator, enqueued on the context's stream). */
 int hale_fill_normal_device(hale_ctx *ctx, uint64_t seed, float mean,
                             float std, float *d_out, size_t n);
+/* d_dst[0, n) = d_src[0, n) by a plain streaming kernel (n and both
+ * addresses multiples of 16), enqueued on the context's stream: one read and
+ * one write per byte, the calibration for HBM traffic counters. */
+int hale_copy_device(hale_ctx *ctx, void *d_dst, const void *d_src, size_t n);
 
 /* Wall time of the work enqueued between start and stop, from HIP events
  * recorded on the context's stream; stop waits for that work. */

@@ -226,3 +226,30 @@ def test_moe_top_k_clamped_and_unnormalised(ctx):
     assert len(idx) == 4 and list(idx) == list(o_idx)
     assert same_bits(w, o_w)
     assert_parity(out, o_out)
+
+
+def test_moe_decode_mixtral_q4_bit_exact(ctx):
+    """Mixtral-8x7B-shaped layer: 8 q4_0 experts, H 4096, I 14336 (gate/up
+    rows of 2304 B, down rows of 448 blocks), f32 router [8 x 4096], top-2."""
+    L = O.OracleMoe.synthetic(O.Q4_0, 4096, 14336, 8, 2, normalize_topk=True, seed=202)
+    moe = make_layer(ctx, L)
+    for seed in range(3):
+        x = O.normal(4000 + seed, 4096)
+        out, idx, w = moe.forward(x, return_routes=True)
+        o_out, o_idx, o_w = L.forward(x, nthreads=8)
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+    moe.close()
+
+
+def test_copy_device(ctx):
+    n = 3 * 1024 * 1024 + 48
+    a, b = ctx.malloc(n), ctx.malloc(n)
+    a.fill_normal(7, n // 4)
+    b.copy_from(a, n)
+    assert (b.download(np.uint8, n) == a.download(np.uint8, n)).all()
+    with pytest.raises(ValueError):
+        b.copy_from(a, n - 8)
+    a.free()
+    b.free()
