@@ -104,18 +104,24 @@ __device__ __forceinline__ int total_key(float v) {
 // ---- wave helpers ---------------------------------------------------------
 
 // Reductions over a full wave (all 64 lanes active): DPP within 16-lane rows
-// (xor 1, xor 2, half mirror, mirror), ds_swizzle across the two rows of a
-// 32-lane half, readlane across the halves.  The result is wave-uniform.
+// (xor 1, xor 2, half mirror, mirror), then v_permlane16_swap (lane ^ 16)
+// and v_permlane32_swap (lane ^ 32), all on the VALU.  Every lane ends with
+// the result, returned wave-uniform.
+__device__ __forceinline__ unsigned xor16(unsigned x) {
+  auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);  // {row 2j, row 2j+1}
+  return (threadIdx.x & 16) ? p[0] : p[1];
+}
 template <typename Op>
 __device__ __forceinline__ unsigned wave_reduce_u32(unsigned x, Op op) {
   x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));   // xor 1
   x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));   // xor 2
   x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false));  // half mirror
   x = op(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false));  // mirror
-  x = op(x, (unsigned)__builtin_amdgcn_ds_swizzle((int)x, 0x401F));                     // xor 16
-  unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)x, 0);
-  unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)x, 32);
-  return op(lo, hi);
+  auto p16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = op(p16[0], p16[1]);
+  auto p32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  x = op(p32[0], p32[1]);
+  return (unsigned)__builtin_amdgcn_readfirstlane((int)x);
 }
 
 struct OpMaxU { __device__ unsigned operator()(unsigned a, unsigned b) const { return a > b ? a : b; } };
@@ -128,28 +134,7 @@ struct OpMaxF {
   }
 };
 
-// Maximum of a u64 over the full wave (all lanes active), wave-uniform.
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
-  auto step = [&](unsigned lo, unsigned hi) {
-    const unsigned long long y = ((unsigned long long)hi << 32) | lo;
-    x = y > x ? y : x;
-  };
-#define HALE_DPP_MAX64(ctrl)                                                              \
-  step((unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)x, ctrl, 0xF, 0xF, false), \
-       (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(x >> 32), ctrl, 0xF, 0xF, false))
-  HALE_DPP_MAX64(0xB1);   // xor 1
-  HALE_DPP_MAX64(0x4E);   // xor 2
-  HALE_DPP_MAX64(0x141);  // half mirror
-  HALE_DPP_MAX64(0x140);  // mirror
-#undef HALE_DPP_MAX64
-  step((unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)x, 0x401F),
-       (unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)(x >> 32), 0x401F));  // xor 16
-  const unsigned long long a = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(x >> 32), 0) << 32) |
-                               (unsigned)__builtin_amdgcn_readlane((int)(unsigned)x, 0);
-  const unsigned long long b = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(x >> 32), 32) << 32) |
-                               (unsigned)__builtin_amdgcn_readlane((int)(unsigned)x, 32);
-  return a > b ? a : b;
-}
+__device__ __forceinline__ unsigned wave_max_u32(unsigned x) { return wave_reduce_u32(x, OpMaxU()); }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
   return __uint_as_float(wave_reduce_u32(__float_as_uint(v), OpMaxF()));
@@ -159,9 +144,10 @@ __device__ __forceinline__ float lane_value(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// Reductions within each 32-lane half of a wave (all lanes active): DPP
-// inside 16-lane rows, ds_swizzle across the two rows of a half.  Every lane
-// of a half gets its half's result.
+// Reductions within each 32-lane half of a wave (the half's lanes active;
+// the other half may be inactive): DPP inside 16-lane rows, then
+// v_permlane16_swap between the two rows of the half.  Every lane of a half
+// gets its half's result.
 #define HALE_DPP_F32(x, ctrl) \
   __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false))
 __device__ __forceinline__ float half_wave_max(float v) {
@@ -169,7 +155,7 @@ __device__ __forceinline__ float half_wave_max(float v) {
   v = fmaxf(v, HALE_DPP_F32(v, 0x4E));
   v = fmaxf(v, HALE_DPP_F32(v, 0x141));
   v = fmaxf(v, HALE_DPP_F32(v, 0x140));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+  v = fmaxf(v, __uint_as_float(xor16(__float_as_uint(v))));
   return v;
 }
 
@@ -178,8 +164,41 @@ __device__ __forceinline__ int half_wave_sum(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
-  v += __builtin_amdgcn_ds_swizzle(v, 0x401F);
+  v += (int)xor16((unsigned)v);
   return v;
+}
+
+// acc + p[0] + p[1] + ... + p[n-1], strictly left to right, from 16-byte
+// aligned LDS: 16 values per batch in two alternating register buffers, so
+// the reads of batch c+1 are in flight while batch c is added.
+__device__ __forceinline__ float lds_sum_in_order(const float* p, int n, float acc) {
+  const f32x4* p4 = (const f32x4*)p;
+  const int nb = n / 16;
+  f32x4 A[4], B[4];
+  auto ld = [&](f32x4* d, int c) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) d[q] = p4[4 * c + q];
+  };
+  auto add = [&](const f32x4* d) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      acc = acc + d[q].x;
+      acc = acc + d[q].y;
+      acc = acc + d[q].z;
+      acc = acc + d[q].w;
+    }
+  };
+  if (nb > 0) ld(A, 0);
+  int c = 0;
+  for (; c + 1 < nb; c += 2) {
+    ld(B, c + 1);
+    add(A);
+    if (c + 2 < nb) ld(A, c + 2);
+    add(B);
+  }
+  if (c < nb) add(A);
+  for (int i = 16 * nb; i < n; i++) acc = acc + p[i];
+  return acc;
 }
 
 // Quantizes one 32-element block held one value per lane of a 32-lane

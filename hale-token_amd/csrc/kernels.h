@@ -48,7 +48,9 @@ hipError_t launch(void (*kernel)(P...), dim3 grid, dim3 block, uint32_t shmem, h
 
 struct ActBlock;
 
-enum Epilogue : int { EPI_PLAIN = 0, EPI_GATE_UP = 1, EPI_COMBINE = 2 };
+enum Epilogue : int { EPI_PLAIN = 0, EPI_GATE_UP = 1 };
+
+constexpr int DOWN_ROWS = 8;  // output rows per work-group of k_down_combine
 
 // Arguments of the exact tile GEMV (kernels_decode.hip).  Expert e's planes
 // start at codes + e * codes_stride / scales + e * scales_stride; the
@@ -65,10 +67,7 @@ struct GemvArgs {
   const ActBlock* act;     // [slot][act_stride] activation blocks
   int act_stride;          // 0: one activation shared by all slots
   const int* route_idx;    // [slots]
-  const float* route_w;    // [slots] (EPI_COMBINE)
   float* out;              // [rows]
-  float* ytmp;             // [slots][padded rows] (EPI_COMBINE)
-  unsigned* counters;      // [row groups], zero between launches (EPI_COMBINE)
   ActBlock* hact;          // [slots][hact_stride] (EPI_GATE_UP)
   int hact_stride;
   int slots;
@@ -99,7 +98,7 @@ struct DownArgs {
   float* out;              // [rows]
 };
 
-hipError_t launch_down_combine(int dtype, const DownArgs& a, int groups, hipStream_t st);
+hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st);
 
 hipError_t launch_repack(int dtype, const uint8_t* aos, size_t rows, size_t cols, uint8_t* codes,
                          uint16_t* scales, hipStream_t st);

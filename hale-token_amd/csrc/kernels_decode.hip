@@ -172,20 +172,38 @@ constexpr int ROUTE_MAX_H = 8192;
 constexpr int ROUTE_MAX_E = 1024;
 constexpr int GEMV_MAX_NB = 512;  // blocks per row the GEMV stages in LDS
 
-__global__ __launch_bounds__(64) void k_route_logits(const float* __restrict__ router,
-                                                     const float* __restrict__ x, int H, int E,
-                                                     ActBlock* __restrict__ act,
-                                                     float* __restrict__ logits) {
+constexpr int ROUTE_THREADS = 256;
+constexpr int ROUTE_VPT = ROUTE_MAX_H / 4 / ROUTE_THREADS;  // float4 of w (and of x) per thread
+
+__global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __restrict__ router,
+                                                                const float* __restrict__ x, int H,
+                                                                int E, ActBlock* __restrict__ act,
+                                                                float* __restrict__ logits) {
   __shared__ __attribute__((aligned(16))) float prod[ROUTE_MAX_H + 32];  // chain-major
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const int t = blockIdx.y;
   const int gx = gridDim.x;
   const int e = blockIdx.x;
   const float* xt = x + (size_t)t * H;
   const int nb = H / QK;
+  const float* w = router + (size_t)e * H;
+  const int steps = H / 8;
+  const int nvec = steps * 2;  // float4 chunks covering the 8-lane part
 
-  // activation quantization share: half-wave h takes block 2*(e + gx*i) + h
-  for (int bb = 2 * e + (lane >> 5); bb < nb; bb += 2 * gx) {
+  // every load of the row and of x first
+  f32x4 wv[ROUTE_VPT], xv[ROUTE_VPT];
+#pragma unroll
+  for (int j = 0; j < ROUTE_VPT; j++) {
+    const int c = tid + j * ROUTE_THREADS;
+    if (c < nvec) {
+      wv[j] = *(const f32x4*)(w + 4 * c);
+      xv[j] = *(const f32x4*)(xt + 4 * c);
+    }
+  }
+
+  // activation quantization share: half-wave hw takes blocks hw + 8 (e + gx i)
+  for (int bb = (tid >> 5) + 8 * e; bb < nb; bb += 8 * gx) {
     float v = xt[bb * QK + (lane & 31)];
     float scale;
     int qsum;
@@ -197,39 +215,26 @@ __global__ __launch_bounds__(64) void k_route_logits(const float* __restrict__ r
       ab->qsum = qsum;
     }
   }
-  if (e >= E) return;
 
   // products w[i]*x[i] (each one rounding, order free) into chain-major LDS:
   // chain l holds i = 8s + l at prod[l * stride + s]
-  const float* w = router + (size_t)e * H;
-  const int steps = H / 8;
   const int stride = steps + 4;  // 16 B aligned rows, chains on distinct banks
-  const int nvec = steps * 2;    // float4 chunks covering the 8-lane part
-  for (int c = lane; c < nvec; c += 64) {
-    f32x4 wv = *(const f32x4*)(w + 4 * c);
-    f32x4 xv = *(const f32x4*)(xt + 4 * c);
-    const int sidx = c >> 1, l0 = (c & 1) * 4;
-    prod[(l0 + 0) * stride + sidx] = wv.x * xv.x;
-    prod[(l0 + 1) * stride + sidx] = wv.y * xv.y;
-    prod[(l0 + 2) * stride + sidx] = wv.z * xv.z;
-    prod[(l0 + 3) * stride + sidx] = wv.w * xv.w;
+#pragma unroll
+  for (int j = 0; j < ROUTE_VPT; j++) {
+    const int c = tid + j * ROUTE_THREADS;
+    if (c < nvec) {
+      const int sidx = c >> 1, l0 = (c & 1) * 4;
+      prod[(l0 + 0) * stride + sidx] = wv[j].x * xv[j].x;
+      prod[(l0 + 1) * stride + sidx] = wv[j].y * xv[j].y;
+      prod[(l0 + 2) * stride + sidx] = wv[j].z * xv[j].z;
+      prod[(l0 + 3) * stride + sidx] = wv[j].w * xv[j].w;
+    }
   }
   __syncthreads();
-  // acc[l] += w[8i+l]*x[8i+l] in order of i, 16 values per batch of reads
+  if (tid >= 64) return;
+  // acc[l] += w[8i+l]*x[8i+l] in order of i
   float acc = 0.0f;
-  if (lane < 8) {
-    const float* p = prod + lane * stride;
-    int s0 = 0;
-    for (; s0 + 16 <= steps; s0 += 16) {
-      f32x4 q0 = *(const f32x4*)(p + s0), q1 = *(const f32x4*)(p + s0 + 4);
-      f32x4 q2 = *(const f32x4*)(p + s0 + 8), q3 = *(const f32x4*)(p + s0 + 12);
-      acc = acc + q0.x; acc = acc + q0.y; acc = acc + q0.z; acc = acc + q0.w;
-      acc = acc + q1.x; acc = acc + q1.y; acc = acc + q1.z; acc = acc + q1.w;
-      acc = acc + q2.x; acc = acc + q2.y; acc = acc + q2.z; acc = acc + q2.w;
-      acc = acc + q3.x; acc = acc + q3.y; acc = acc + q3.z; acc = acc + q3.w;
-    }
-    for (; s0 < steps; s0++) acc = acc + p[s0];
-  }
+  if (lane < 8) acc = lds_sum_in_order(prod + lane * stride, steps, acc);
   float a0 = __shfl(acc, 0), a1 = __shfl(acc, 1), a2 = __shfl(acc, 2), a3 = __shfl(acc, 3);
   float a4 = __shfl(acc, 4), a5 = __shfl(acc, 5), a6 = __shfl(acc, 6), a7 = __shfl(acc, 7);
   if (lane == 0) {
@@ -244,13 +249,15 @@ __global__ __launch_bounds__(64) void k_route_logits(const float* __restrict__ r
 // softmax_in_place (src/ops/activation.rs:11-21), top_k (src/ops/topk.rs:
 // 44-61) and the renormalisation of MoeLayer::route, run by one whole wave
 // (all 64 lanes active).  Element i lives in lane i % 64, slot i / 64.
-//   - the sum of exp(l_i - max) is taken strictly in index order by one lane
-//     reading LDS in batches;
-//   - top-k: each probability gets the unique key (total_cmp key, then the
-//     complement of its index) so that larger key = better; k rounds of a
-//     wave-wide maximum pick the experts best first.
+//   - the sum of exp(l_i - max) is taken strictly in index order by lane 0,
+//     reading the next 16 values from LDS while it adds the current 16;
+//   - top-k: each probability gets its total_cmp key as an order-preserving
+//     u32; in each of k rounds the wave's largest untaken key is found and
+//     the lowest untaken index holding it wins (ties go to the lower index,
+//     as in the reference), so the experts come out best first;
+//   - norm = sum of the chosen probabilities in that order, then w = p / norm.
 // The k chosen experts and renormalised weights go to sel_idx / sel_w
-// (LDS), best first.  rs is LDS scratch of ROUTE_MAX_E + 3*64 words.
+// (LDS), best first.  rs is LDS scratch of ROUTE_MAX_E + 4*64 words.
 constexpr int RS_SCRATCH = ROUTE_MAX_E + 4 * 64;
 
 template <int PER>  // elements per lane: E <= 64 * PER
@@ -258,7 +265,7 @@ __device__ __forceinline__ void route_select_t(const float* lg, int E, int k, in
                                                int* sel_idx, float* sel_w, const ExpTable& tab,
                                                float* rs) {
   const int lane = threadIdx.x & 63;
-  float* e_lds = rs;  // [E]
+  float* e_lds = rs;
   float v[PER];
   float mx = -__builtin_huge_valf();
 #pragma unroll
@@ -278,58 +285,55 @@ __device__ __forceinline__ void route_select_t(const float* lg, int E, int k, in
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float sum = 0.0f;  // sum += exp(v - max), index order
-  if (lane == 0) {
-    int i = 0;
-    for (; i + 16 <= E; i += 16) {
-      f32x4 a = *(const f32x4*)(e_lds + i), b = *(const f32x4*)(e_lds + i + 4);
-      f32x4 c = *(const f32x4*)(e_lds + i + 8), d = *(const f32x4*)(e_lds + i + 12);
-      sum = sum + a.x; sum = sum + a.y; sum = sum + a.z; sum = sum + a.w;
-      sum = sum + b.x; sum = sum + b.y; sum = sum + b.z; sum = sum + b.w;
-      sum = sum + c.x; sum = sum + c.y; sum = sum + c.z; sum = sum + c.w;
-      sum = sum + d.x; sum = sum + d.y; sum = sum + d.z; sum = sum + d.w;
-    }
-    for (; i < E; i++) sum = sum + e_lds[i];
-  }
+  if (lane == 0) sum = lds_sum_in_order(e_lds, E, sum);
   sum = lane_value(sum, 0);
-  unsigned long long key[PER];
+  unsigned key[PER];
+  unsigned live = 0;  // bit m: element lane + 64 m exists and is not taken
 #pragma unroll
   for (int m = 0; m < PER; m++) {
     const int i = lane + 64 * m;
-    key[m] = 0ull;  // below every real key
+    key[m] = 0u;
     if (i < E) {
-      v[m] = v[m] / sum;
-      const unsigned k32 = (unsigned)total_key(v[m]) ^ 0x80000000u;  // order-preserving
-      key[m] = ((unsigned long long)k32 << 32) | (0xffffffffu - (unsigned)i);
+      key[m] = (unsigned)total_key(v[m] / sum) ^ 0x80000000u;  // order-preserving
+      live |= 1u << m;
     }
   }
-  // k rounds: the wave's largest untaken key is the next best expert; its
-  // probability is decoded from the key's high word
+  // taken keys are set to 0, which is no larger than any real key, so the
+  // wave maximum is the largest untaken key; the live mask keeps a real key
+  // of 0 apart from a taken one
+  int my_idx = 0;
+  float my_p = 0.0f;
+  float norm = normalize ? -0.0f : 1.0f;  // Iterator::sum in best-first order
   for (int r = 0; r < k; r++) {
-    unsigned long long best = 0ull;
+    unsigned loc = key[0];
 #pragma unroll
-    for (int m = 0; m < PER; m++) best = key[m] > best ? key[m] : best;
-    best = wave_max_u64(best);
+    for (int m = 1; m < PER; m++) loc = key[m] > loc ? key[m] : loc;
+    const unsigned best = wave_max_u32(loc);
+    int widx = -1;
 #pragma unroll
-    for (int m = 0; m < PER; m++)
-      if (key[m] == best) key[m] = 0ull;  // unique keys: only the winner matches
-    if (lane == 0) {
-      const int bits = (int)((unsigned)(best >> 32) ^ 0x80000000u);
-      sel_idx[r] = (int)(0xffffffffu - (unsigned)best);
-      sel_w[r] = __int_as_float(bits ^ (int)(((unsigned)(bits >> 31)) >> 1));  // inverse of total_key
+    for (int m = 0; m < PER; m++) {
+      const unsigned long long msk = __ballot(((live >> m) & 1u) && key[m] == best);
+      if (widx < 0 && msk) widx = 64 * m + (int)__builtin_ctzll(msk);
+    }
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+      if (64 * m + lane == widx) {
+        key[m] = 0u;
+        live &= ~(1u << m);
+      }
+    }
+    const int bits = (int)(best ^ 0x80000000u);
+    const float pw = __int_as_float(bits ^ (int)(((unsigned)(bits >> 31)) >> 1));  // inverse of total_key
+    if (normalize) norm = norm + pw;
+    if (lane == r) {
+      my_idx = widx;
+      my_p = pw;
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float norm = 1.0f;
-  if (normalize) {
-    norm = -0.0f;  // Iterator::sum in best-first order
-    for (int r = 0; r < k; r++) norm = norm + sel_w[r];
+  if (lane < k) {
+    sel_idx[lane] = my_idx;
+    sel_w[lane] = my_p / norm;
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane < k) sel_w[lane] = sel_w[lane] / norm;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -393,9 +397,6 @@ __global__ __launch_bounds__(64) void k_route_select(const float* __restrict__ l
 //                quantized to its q8 block for the down projection
 //                (Expert::forward, src/expert/mod.rs:95-102).  With router
 //                logits given, the prologue selects the slot's expert.
-//   EPI_COMBINE  per-slot results to ytmp; the last slot's work-group of the
-//                row group adds them in route order: out = 0, then
-//                out = out + w_s * y_s (MoeLayer::forward, moe.rs:63-68)
 
 template <int DT>
 __device__ __forceinline__ float block_term(const u32x4* c, uint16_t sc, const ActBlock* ab) {
@@ -587,21 +588,6 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         hb->qsum = qsum;
       }
     }
-  } else {  // EPI_COMBINE
-    const size_t prow = padded_rows((size_t)a.rows);
-    const size_t row = tile * TILE + r;
-    a.ytmp[(size_t)slot * prow + row] = total;
-    __threadfence();
-    unsigned old = 0;
-    if (lane == 0) old = atomicAdd(&a.counters[g], 1u);
-    old = __shfl(old, 0);
-    if (old != (unsigned)(a.slots - 1)) return;
-    __threadfence();
-    if (lane == 0) a.counters[g] = 0u;
-    float acc = 0.0f;
-    for (int s = 0; s < a.slots; s++)
-      acc = acc + a.route_w[s] * __builtin_nontemporal_load(a.ytmp + (size_t)s * prow + row);
-    if (row < (size_t)a.rows) a.out[row] = acc;
   }
 }
 
@@ -611,29 +597,43 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 //
 // MoeLayer::forward (src/model/moe.rs:63-68) for one token: out = 0, then
 // for each route in best-first order out = out + w_s * down_s(h_s).  A
-// work-group owns DR = 16 output rows for every slot, so the combine needs
-// no other work-group.  Its units are the (slot, block) pairs in slot-major
-// order.  A wave covers 16 rows x 4 units per load (4 x 256 B); a chunk of
-// CB units loads at once (weights and activation blocks), terms go to LDS,
-// and lanes 0-15 of wave 0 fold them in unit order: a row's sum for slot s
-// is complete at the slot's last block, where it is scaled by w_s and added
-// to the output.
+// work-group owns DR = 8 output rows for every slot, so the combine needs no
+// other work-group, and the launch has H / 8 work-groups (256 at H = 2048).
+// Its units are the (slot, block) pairs in slot-major order.  One wave-load
+// covers 8 units x 8 rows: 8 segments of 128 B, each one cache line of the
+// tile layout.  A chunk of CB units is loaded at once (UPW loads in flight
+// per lane) together with its activation blocks; terms go to LDS.  The fold
+// runs on 64 lanes, one per (row, slot): each adds its slot's block terms in
+// block order, which is the reference's per-expert dot product, and the
+// combine then takes the slots in route order.
 
-constexpr int DR = 16;          // rows per work-group of k_down_combine
+// u / n for 0 <= u < 2^20 from a float reciprocal, corrected to the exact
+// quotient (below 2^20 the float estimate is off by at most one)
+__device__ __forceinline__ int div_small(int u, int n, float inv_n) {
+  int q = (int)((float)u * inv_n);
+  if (q * n > u) q--;
+  else if ((q + 1) * n <= u) q++;
+  return q;
+}
+
+constexpr int DR = DOWN_ROWS;   // rows per work-group of k_down_combine
 constexpr int DOWN_WAVES = 4;   // waves per work-group of k_down_combine
+constexpr int DOWN_MAX_SLOTS = 64;
 
 template <int DT>
 __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
   constexpr int NW = DOWN_WAVES;
-  constexpr int J = 64 / DR;        // units side by side in one wave
-  constexpr int UPW = 16 / CH;      // 16 loads of 16 B in flight per lane
-  constexpr int CB = NW * J * UPW;  // units per chunk: 256 (q4_0), 128 (q8_0)
+  constexpr int J = 64 / DR;        // units side by side in one wave-load
+  constexpr int UPW = 16 / CH;      // loads of 16 B in flight per lane
+  constexpr int CB = NW * J * UPW;  // units per chunk: 512 (q4_0), 256 (q8_0)
   constexpr int AQ = (CB * 3 + 64 * NW - 1) / (64 * NW);
-  __shared__ float terms[2][CB][DR];
-  __shared__ ActBlock s_act[2][CB];
-  __shared__ int s_exp[64];
-  __shared__ float s_w[64];
+  constexpr int SPL = DOWN_MAX_SLOTS / 8;  // slots per fold lane
+  __shared__ float terms[CB][DR];
+  __shared__ ActBlock s_act[CB];
+  __shared__ float s_tot[DOWN_MAX_SLOTS][DR];
+  __shared__ int s_exp[DOWN_MAX_SLOTS];
+  __shared__ float s_w[DOWN_MAX_SLOTS];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -641,14 +641,14 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
   const int nb = a.nb;
   const int slots = a.slots;
   const int nunits = slots * nb;
+  const float inv_nb = 1.0f / (float)nb;
   if (threadIdx.x < slots) {
     s_exp[threadIdx.x] = a.route_idx[threadIdx.x];
     s_w[threadIdx.x] = a.route_w[threadIdx.x];
   }
-  __syncthreads();
 
   const int r = lane % DR;          // row within the group
-  const int jl = lane / DR;         // unit lane
+  const int jl = lane / DR;         // unit within the wave-load
   const size_t row0 = (size_t)g * DR;
   const size_t tile = row0 / TILE;
   const int rt = (int)(row0 % TILE) + r;  // row within its 32-row tile
@@ -658,14 +658,14 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
   u32x4 cw[UPW][CH];
   uint16_t sw[UPW];
   u32x4 av[AQ];
-  // units past the end are clamped to the last unit (loaded, never stored)
-  auto unit_of = [&](int u0, int s) { return min(u0 + (wave + NW * s) * J + jl, nunits - 1); };
-  auto load_chunk = [&](int ch) {
-    const int u0 = ch * CB;
+  // unit of load s in the chunk at u0 (past the end: clamped to the last
+  // unit, loaded and never stored)
+  auto unit_of = [&](int u0, int s) { return min(u0 + (s * NW + wave) * J + jl, nunits - 1); };
+  auto load_chunk = [&](int u0) {
 #pragma unroll
     for (int s = 0; s < UPW; s++) {
       const int u = unit_of(u0, s);
-      const int sl = u / nb, b = u - sl * nb;
+      const int sl = div_small(u, nb, inv_nb), b = u - sl * nb;
       const size_t e = (size_t)s_exp[sl];
       const uint8_t* c0 = a.codes + e * a.codes_stride + row_off;
 #pragma unroll
@@ -678,63 +678,73 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
       const int i = threadIdx.x + q * 64 * NW;
       const int u = u0 + i / 3;
       if (i < CB * 3 && u < nunits) {
-        const int sl = u / nb, b = u - sl * nb;
+        const int sl = div_small(u, nb, inv_nb), b = u - sl * nb;
         av[q] = ((const u32x4*)(a.hact + (size_t)sl * a.hact_stride + b))[i % 3];
       }
     }
   };
 
-  float total = 0.0f, acc = 0.0f;
-  int fs = 0, fb = 0;  // slot and block of the next unit the fold takes
-  const int nchunks = (nunits + CB - 1) / CB;
-  load_chunk(0);
-  for (int ch = 0; ch < nchunks; ch++) {
-    const int u0 = ch * CB;
-    const int uend = min(nunits, u0 + CB);
-    ActBlock* sa = s_act[ch & 1];
+  // fold lane (row r, slot group jl): slots jl, jl + 8, ...; running sums of
+  // the current slot are kept per slot because a chunk may end mid-slot
+  float tot[SPL];
+#pragma unroll
+  for (int i = 0; i < SPL; i++) tot[i] = 0.0f;
+
+  __syncthreads();  // s_exp / s_w
+  for (int u0 = 0; u0 < nunits; u0 += CB) {
+    load_chunk(u0);
 #pragma unroll
     for (int q = 0; q < AQ; q++) {
       const int i = threadIdx.x + q * 64 * NW;
-      if (i < CB * 3 && u0 + i / 3 < nunits) ((u32x4*)sa)[i] = av[q];
+      if (i < CB * 3 && u0 + i / 3 < nunits) ((u32x4*)s_act)[i] = av[q];
     }
     __syncthreads();
     float tv[UPW];
 #pragma unroll
-    for (int s = 0; s < UPW; s++) tv[s] = block_term<DT>(cw[s], sw[s], sa + (unit_of(u0, s) - u0));
-    if (ch + 1 < nchunks) load_chunk(ch + 1);
-    float(*tb)[DR] = terms[ch & 1];
+    for (int s = 0; s < UPW; s++) tv[s] = block_term<DT>(cw[s], sw[s], s_act + (unit_of(u0, s) - u0));
 #pragma unroll
     for (int s = 0; s < UPW; s++) {
-      const int u = u0 + (wave + NW * s) * J + jl;
-      if (u < uend) tb[u - u0][r] = tv[s];
+      const int u = u0 + (s * NW + wave) * J + jl;
+      if (u < nunits && u - u0 < CB) terms[u - u0][r] = tv[s];
     }
     __syncthreads();
-    if (wave == 0 && lane < DR) {
-      int j = 0;
-      const int n = uend - u0;
-      while (j < n) {
-        const int run = min(n - j, nb - fb);  // units left in this slot and chunk
-        int q = 0;
-        for (; q + 8 <= run; q += 8) {
-          float v[8];
+    if (wave == 0) {
+      const int uend = min(nunits, u0 + CB);
 #pragma unroll
-          for (int z = 0; z < 8; z++) v[z] = tb[j + q + z][lane];
-#pragma unroll
-          for (int z = 0; z < 8; z++) total = total + v[z];
-        }
-        for (; q < run; q++) total = total + tb[j + q][lane];
-        j += run;
-        fb += run;
-        if (fb == nb) {
-          acc = acc + s_w[fs] * total;
-          total = 0.0f;
-          fb = 0;
-          fs++;
+      for (int i = 0; i < SPL; i++) {
+        const int sl = jl + 8 * i;
+        if (sl < slots) {
+          // this slot's units inside the chunk, in block order
+          const int ua = max(u0, sl * nb), ub = min(uend, (sl + 1) * nb);
+          float t = tot[i];
+          int u = ua;
+          for (; u + 4 <= ub; u += 4) {
+            const float v0 = terms[u - u0][r], v1 = terms[u + 1 - u0][r];
+            const float v2 = terms[u + 2 - u0][r], v3 = terms[u + 3 - u0][r];
+            t = t + v0;
+            t = t + v1;
+            t = t + v2;
+            t = t + v3;
+          }
+          for (; u < ub; u++) t = t + terms[u - u0][r];
+          tot[i] = t;
         }
       }
     }
+    __syncthreads();  // terms and s_act are rewritten by the next chunk
   }
-  if (wave == 0 && lane < DR) {
+  if (wave != 0) return;
+#pragma unroll
+  for (int i = 0; i < SPL; i++) {
+    const int sl = jl + 8 * i;
+    if (sl < slots) s_tot[sl][r] = tot[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < DR) {
+    float acc = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
+    for (int sl = 0; sl < slots; sl++) acc = acc + s_w[sl] * s_tot[sl][lane];
     const size_t row = row0 + lane;
     if (row < (size_t)a.rows) a.out[row] = acc;
   }
@@ -838,7 +848,7 @@ hipError_t launch_route_logits(const float* router, const float* x, int H, int E
                                ActBlock* act, float* logits, hipStream_t st) {
   if (H > ROUTE_MAX_H || E > ROUTE_MAX_E || H % QK || E < 1 || T < 1) return hipErrorInvalidValue;
   dim3 grid(E, T);
-  return launch(k_route_logits, grid, 64, 0, st, router, x, H, E, act, logits);
+  return launch(k_route_logits, grid, ROUTE_THREADS, 0, st, router, x, H, E, act, logits);
 }
 
 hipError_t launch_route_select(const float* logits, int E, int k, int normalize, int T,
@@ -861,17 +871,16 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   }
   HALE_GEMV_CASE(Q8_0, EPI_PLAIN)
   HALE_GEMV_CASE(Q8_0, EPI_GATE_UP)
-  HALE_GEMV_CASE(Q8_0, EPI_COMBINE)
   HALE_GEMV_CASE(Q4_0, EPI_PLAIN)
   HALE_GEMV_CASE(Q4_0, EPI_GATE_UP)
-  HALE_GEMV_CASE(Q4_0, EPI_COMBINE)
 #undef HALE_GEMV_CASE
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_down_combine(int dtype, const DownArgs& a, int groups, hipStream_t st) {
+hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
+  const unsigned groups = (unsigned)(padded_rows((size_t)a.rows) / DR);
   if (groups == 0) return hipSuccess;
-  if (a.nb < 1 || a.slots < 1 || a.slots > 64) return hipErrorInvalidValue;
+  if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS) return hipErrorInvalidValue;
   if (dtype == Q8_0) return launch(k_down_combine<Q8_0>, groups, 64 * DOWN_WAVES, 0, st, a);
   if (dtype == Q4_0) return launch(k_down_combine<Q4_0>, groups, 64 * DOWN_WAVES, 0, st, a);
   return hipErrorInvalidValue;

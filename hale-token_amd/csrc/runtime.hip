@@ -86,8 +86,6 @@ struct hale_moe {
   int* route_idx = nullptr;  // [cap_tok][k]
   float* route_w = nullptr;  // [cap_tok][k]
   ActBlock* hact = nullptr;  // [k][I/32]
-  float* ytmp = nullptr;     // [k][padded H]
-  unsigned* grp_counters = nullptr;  // [padded H / 64]
   size_t cap_tok = 0;
   // grouped prefill workspace
   PrefillWorkspace pw;
@@ -675,7 +673,6 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   m->dc_bytes = code_plane_bytes(dtype, H, I);
   m->ds_elems = scale_plane_bytes(H, I) / 2;
   m->present.assign(E, 0);
-  size_t hp = padded_rows(H);
   hipError_t e = hipSuccess;
 #define ALLOC(p, n) \
   if (e == hipSuccess) e = hipMalloc(&(p), (n))
@@ -687,12 +684,9 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   ALLOC(m->down_s, E * m->ds_elems * 2);
   ALLOC(m->stats, E * 8);
   ALLOC(m->hact, std::max<size_t>(m->k, 1) * (I / HALE_QK) * sizeof(ActBlock));
-  ALLOC(m->ytmp, std::max<size_t>(m->k, 1) * hp * 4);
-  ALLOC(m->grp_counters, (hp / 64) * 4);
   if (router) ALLOC(m->router, E * H * 4);
 #undef ALLOC
   if (e == hipSuccess) e = hipMemsetAsync(m->stats, 0, E * 8, c->stream);
-  if (e == hipSuccess) e = hipMemsetAsync(m->grp_counters, 0, (hp / 64) * 4, c->stream);
   if (e == hipSuccess && router)
     e = hipMemcpyAsync(m->router, router->f32, E * H * 4, hipMemcpyDeviceToDevice, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -720,8 +714,6 @@ extern "C" void hale_moe_destroy(hale_moe* m) {
   (void)hipFree(m->down_s);
   (void)hipFree(m->stats);
   (void)hipFree(m->hact);
-  (void)hipFree(m->ytmp);
-  (void)hipFree(m->grp_counters);
   (void)hipFree(m->router);
   delete m;
 }
@@ -855,7 +847,7 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     d.route_w = m->route_w + t * k;
     d.slots = k;
     d.out = out_t;
-    LAUNCH(c, K_DOWN, launch_down_combine(m->dtype, d, (int)(padded_rows(m->H) / 16), c->stream));
+    LAUNCH(c, K_DOWN, launch_down_combine(m->dtype, d, c->stream));
   }
   return HALE_OK;
 }
