@@ -101,6 +101,14 @@ __device__ __forceinline__ int total_key(float v) {
   return b ^ (int)(((unsigned)(b >> 31)) >> 1);
 }
 
+// total_cmp order as an unsigned key (larger key = later in total order),
+// and back
+__device__ __forceinline__ unsigned order_key(float v) { return (unsigned)total_key(v) ^ 0x80000000u; }
+__device__ __forceinline__ float key_value(unsigned key) {
+  const int bits = (int)(key ^ 0x80000000u);
+  return __int_as_float(bits ^ (int)(((unsigned)(bits >> 31)) >> 1));
+}
+
 // ---- wave helpers ---------------------------------------------------------
 
 // Reductions over a full wave (all 64 lanes active): DPP within 16-lane rows

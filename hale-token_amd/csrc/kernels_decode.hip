@@ -258,7 +258,48 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
 //   - norm = sum of the chosen probabilities in that order, then w = p / norm.
 // The k chosen experts and renormalised weights go to sel_idx / sel_w
 // (LDS), best first.  rs is LDS scratch of ROUTE_MAX_E + 4*64 words.
-constexpr int RS_SCRATCH = ROUTE_MAX_E + 4 * 64;
+// k rounds over order-preserving u32 keys (element lane + 64 m in key[m],
+// present where bit m of live is set): the wave's largest untaken key is
+// the next best and the lowest untaken index holding it wins, so lane r
+// ends with the r-th best index and its probability (decoded from the key)
+// for r < k.  Taken keys are set to 0, no larger than any real key, so the
+// wave maximum is the largest untaken key; the live mask keeps a real key of
+// 0 apart from a taken one.  norm: the chosen probabilities summed best
+// first from -0.0 (Iterator::sum), or 1 without renormalisation.
+template <int PER>
+__device__ __forceinline__ void topk_rounds(unsigned* key, unsigned& live, int k, int normalize,
+                                            int* my_idx, float* my_p, float* norm_out) {
+  const int lane = threadIdx.x & 63;
+  float norm = normalize ? -0.0f : 1.0f;
+  for (int r = 0; r < k; r++) {
+    unsigned loc = key[0];
+#pragma unroll
+    for (int m = 1; m < PER; m++) loc = key[m] > loc ? key[m] : loc;
+    const unsigned best = wave_max_u32(loc);
+    int widx = -1;
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+      const unsigned long long msk = __ballot(((live >> m) & 1u) && key[m] == best);
+      if (widx < 0 && msk) widx = 64 * m + (int)__builtin_ctzll(msk);
+    }
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+      if (64 * m + lane == widx) {
+        key[m] = 0u;
+        live &= ~(1u << m);
+      }
+    }
+    const float pw = key_value(best);
+    if (normalize) norm = norm + pw;
+    if (lane == r) {
+      *my_idx = widx;
+      *my_p = pw;
+    }
+  }
+  *norm_out = norm;
+}
+
+constexpr int RS_SCRATCH = 2 * ROUTE_MAX_E + 4 * 64;
 
 template <int PER>  // elements per lane: E <= 64 * PER
 __device__ __forceinline__ void route_select_t(const float* lg, int E, int k, int normalize,
@@ -294,42 +335,13 @@ __device__ __forceinline__ void route_select_t(const float* lg, int E, int k, in
     const int i = lane + 64 * m;
     key[m] = 0u;
     if (i < E) {
-      key[m] = (unsigned)total_key(v[m] / sum) ^ 0x80000000u;  // order-preserving
+      key[m] = order_key(v[m] / sum);
       live |= 1u << m;
     }
   }
-  // taken keys are set to 0, which is no larger than any real key, so the
-  // wave maximum is the largest untaken key; the live mask keeps a real key
-  // of 0 apart from a taken one
   int my_idx = 0;
-  float my_p = 0.0f;
-  float norm = normalize ? -0.0f : 1.0f;  // Iterator::sum in best-first order
-  for (int r = 0; r < k; r++) {
-    unsigned loc = key[0];
-#pragma unroll
-    for (int m = 1; m < PER; m++) loc = key[m] > loc ? key[m] : loc;
-    const unsigned best = wave_max_u32(loc);
-    int widx = -1;
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-      const unsigned long long msk = __ballot(((live >> m) & 1u) && key[m] == best);
-      if (widx < 0 && msk) widx = 64 * m + (int)__builtin_ctzll(msk);
-    }
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-      if (64 * m + lane == widx) {
-        key[m] = 0u;
-        live &= ~(1u << m);
-      }
-    }
-    const int bits = (int)(best ^ 0x80000000u);
-    const float pw = __int_as_float(bits ^ (int)(((unsigned)(bits >> 31)) >> 1));  // inverse of total_key
-    if (normalize) norm = norm + pw;
-    if (lane == r) {
-      my_idx = widx;
-      my_p = pw;
-    }
-  }
+  float my_p = 0.0f, norm = 0.0f;
+  topk_rounds<PER>(key, live, k, normalize, &my_idx, &my_p, &norm);
   if (lane < k) {
     sel_idx[lane] = my_idx;
     sel_w[lane] = my_p / norm;
@@ -352,6 +364,125 @@ __device__ __forceinline__ void route_select(const float* lg, int E, int k, int 
     route_select_t<8>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
   else
     route_select_t<16>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
+}
+
+// The same selection split over waves 0 and 1 of a work-group, for the
+// gate/up prologue (every wave of the work-group passes the two barriers
+// inside).  Ranking by logit gives the reference's order unless rounding
+// makes two
+// probabilities equal (the map logit -> exp(logit - max) -> probability is
+// non-decreasing).  Wave 0 ranks by logit while wave 1 takes the max, the
+// exp values, the in-order sum and the probability keys; then wave 0 checks
+// the ranking against the probabilities: each chosen pair, and the last
+// chosen against every unchosen element, must be in (probability desc,
+// index asc) order.  If a check fails it ranks again by probability.
+// Either way the result is the reference's.  rs: RS_SCRATCH words of LDS.
+template <int PER>
+__device__ __forceinline__ void route_select_pair_t(const float* lg, int E, int k, int normalize,
+                                                    int* sel_idx, float* sel_w, const ExpTable& tab,
+                                                    float* rs, int wave) {
+  const int lane = threadIdx.x & 63;
+  float* e_lds = rs;                                  // [E] exp values
+  unsigned* pkey = (unsigned*)(rs + ROUTE_MAX_E);     // [E] probability keys
+  float v[PER];
+  unsigned key[PER];
+  unsigned live = 0;
+  int my_idx = 0;
+  if (wave <= 1) {
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+      const int i = lane + 64 * m;
+      v[m] = (i < E) ? lg[i] : -__builtin_huge_valf();
+    }
+    if (wave == 1) {
+      float mx = v[0];
+#pragma unroll
+      for (int m = 1; m < PER; m++) mx = fmaxf(mx, v[m]);
+      mx = wave_max_f32(mx);
+#pragma unroll
+      for (int m = 0; m < PER; m++) v[m] = wave_expf(v[m] - mx, tab);
+#pragma unroll
+      for (int m = 0; m < PER; m++)
+        if (lane + 64 * m < E) e_lds[lane + 64 * m] = v[m];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float sum = 0.0f;  // sum += exp(v - max), index order
+      if (lane == 0) sum = lds_sum_in_order(e_lds, E, sum);
+      sum = lane_value(sum, 0);
+#pragma unroll
+      for (int m = 0; m < PER; m++)
+        if (lane + 64 * m < E) pkey[lane + 64 * m] = order_key(v[m] / sum);
+    } else {
+#pragma unroll
+      for (int m = 0; m < PER; m++) {
+        key[m] = 0u;
+        if (lane + 64 * m < E) {
+          key[m] = order_key(v[m]);
+          live |= 1u << m;
+        }
+      }
+      float unused_p, unused_norm;
+      topk_rounds<PER>(key, live, k, 0, &my_idx, &unused_p, &unused_norm);
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // lane r < k checks chosen r against chosen r + 1.  Every unchosen
+    // element ranks after the last chosen by logit, hence normally no higher
+    // by probability; the ranking fails if one has a larger probability key,
+    // or an equal one at a lower index.  live: unchosen existing elements of
+    // this lane.
+    const int next = __shfl(my_idx, lane + 1);
+    const int last = __shfl(my_idx, k - 1);
+    const unsigned klast = pkey[last];
+    bool bad = false;
+    if (lane + 1 < k) {
+      const unsigned ka = pkey[my_idx], kb = pkey[next];
+      bad = !(ka > kb || (ka == kb && my_idx < next));
+    }
+    unsigned pk[PER];
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+      const int i = lane + 64 * m;
+      pk[m] = (i < E) ? pkey[i] : 0u;
+      if ((live >> m) & 1u) bad = bad || pk[m] > klast || (pk[m] == klast && i < last);
+    }
+    float my_p = 0.0f, norm = 1.0f;
+    if (__ballot(bad) == 0ull) {
+      my_p = lane < k ? key_value(pkey[my_idx]) : 0.0f;
+      if (normalize) {
+        norm = -0.0f;  // Iterator::sum in best-first order
+        for (int r = 0; r < k; r++) norm = norm + lane_value(my_p, r);
+      }
+    } else {  // a tie the exp values did not show: rank by probability
+      unsigned live2 = 0;
+#pragma unroll
+      for (int m = 0; m < PER; m++)
+        if (lane + 64 * m < E) live2 |= 1u << m;
+      topk_rounds<PER>(pk, live2, k, normalize, &my_idx, &my_p, &norm);
+    }
+    if (lane < k) {
+      sel_idx[lane] = my_idx;
+      sel_w[lane] = my_p / norm;
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void route_select_pair(const float* lg, int E, int k, int normalize,
+                                                  int* sel_idx, float* sel_w, const ExpTable& tab,
+                                                  float* rs, int wave) {
+  if (E <= 64)
+    route_select_pair_t<1>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
+  else if (E <= 128)
+    route_select_pair_t<2>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
+  else if (E <= 256)
+    route_select_pair_t<4>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
+  else if (E <= 512)
+    route_select_pair_t<8>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
+  else
+    route_select_pair_t<16>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
 }
 
 // Standalone routing (MoeLayer::route without the experts, and the grouped
@@ -465,30 +596,44 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   const int slot = blockIdx.y;
   const int nb = a.nb;
 
-  // the activation blocks of this slot: loads issued first, stored to LDS
-  // once the weight loads are in flight
-  constexpr int APER = (GEMV_MAX_NB * 3 + 64 * NW - 1) / (64 * NW);
+  // The activation blocks of this slot go to LDS.  With routing in the
+  // prologue, wave 0 selects the experts from the first instruction on while
+  // waves 1-3 stage the activations; otherwise every wave stages and the
+  // weight loads are issued before the staging stores.
+  const bool routing = EPI == EPI_GATE_UP && a.logits != nullptr;
+  const int nstage = routing ? 64 * (NW - 1) : 64 * NW;  // staging threads
+  const int stid = routing ? (int)threadIdx.x - 64 : (int)threadIdx.x;
+  constexpr int APER = (GEMV_MAX_NB * 3 + 64 * (NW - 1) - 1) / (64 * (NW - 1));
   u32x4 av[APER];
-  {
+  if (stid >= 0) {
     const u32x4* src = (const u32x4*)(a.act + (size_t)slot * a.act_stride);
 #pragma unroll
     for (int j = 0; j < APER; j++) {
-      const int i = threadIdx.x + j * 64 * NW;
+      const int i = stid + j * nstage;
       if (i < nb * 3) av[j] = src[i];
     }
   }
+  auto stage_act = [&]() {
+    if (stid < 0) return;
+    u32x4* dst = (u32x4*)s_act;
+#pragma unroll
+    for (int j = 0; j < APER; j++) {
+      const int i = stid + j * nstage;
+      if (i < nb * 3) dst[i] = av[j];
+    }
+  };
   ExpTable tab;
   if constexpr (EPI == EPI_GATE_UP) tab.load();
   int expert = a.route_idx ? a.route_idx[slot] : 0;
   if constexpr (EPI == EPI_GATE_UP) {
-    if (a.logits) {  // choose this token's experts from the router logits
-      if (wave == 0) {
-        route_select(a.logits, a.E, a.slots, a.normalize, sel_idx, sel_w, tab, rs);
-        if (g == 0 && lane == 0) {  // one work-group per slot publishes it
-          a.route_out_idx[slot] = sel_idx[slot];
-          a.route_out_w[slot] = sel_w[slot];
-          if (a.stats) atomicAdd(&a.stats[sel_idx[slot]], 1ull);
-        }
+    if (routing) {  // choose this token's experts from the router logits
+      if (wave >= 2) stage_act();
+      route_select_pair(a.logits, a.E, a.slots, a.normalize, sel_idx, sel_w, tab, rs, wave);
+      if (wave == 1) stage_act();
+      if (g == 0 && threadIdx.x == 0) {  // one work-group per slot publishes it
+        a.route_out_idx[slot] = sel_idx[slot];
+        a.route_out_w[slot] = sel_w[slot];
+        if (a.stats) atomicAdd(&a.stats[sel_idx[slot]], 1ull);
       }
       __syncthreads();
       expert = sel_idx[slot];
@@ -533,15 +678,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   float total = 0.0f;
   const int nchunks = (nb + CB - 1) / CB;
   load_chunk(0);
-  {
-    u32x4* dst = (u32x4*)s_act;
-#pragma unroll
-    for (int j = 0; j < APER; j++) {
-      const int i = threadIdx.x + j * 64 * NW;
-      if (i < nb * 3) dst[i] = av[j];
-    }
+  if (!routing) {
+    stage_act();
+    __syncthreads();
   }
-  __syncthreads();
   for (int ch = 0; ch < nchunks; ch++) {
     const int b0 = ch * CB;
     const int bend = min(nb, b0 + CB);

@@ -253,3 +253,28 @@ def test_copy_device(ctx):
         b.copy_from(a, n - 8)
     a.free()
     b.free()
+
+
+from routing_cases import TIE_LOGITS  # noqa: E402
+
+
+@pytest.mark.parametrize("k", [2, 3])
+def test_moe_probability_tie_hidden_in_exp_values(ctx, k):
+    L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 8, k, normalize_topk=True, seed=9, with_router=False)
+    moe = make_layer(ctx, L)
+    lgs = np.array([t[0] for t in TIE_LOGITS], np.float32)
+    xs = O.normal(31, len(TIE_LOGITS) * 64).reshape(-1, 64)
+    for t in range(len(TIE_LOGITS)):  # decode path, one token at a time
+        out, idx, w = moe.forward(xs[t], logits=lgs[t], return_routes=True)
+        o_out, o_idx, o_w = L.forward(xs[t], logits=lgs[t])
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+    xs8 = np.repeat(xs, 4, axis=0)  # 8 tokens: the grouped path
+    lg8 = np.repeat(lgs, 4, axis=0)
+    out, idx, w = moe.forward(xs8, logits=lg8, return_routes=True)
+    o_out, o_idx, o_w = L.prefill(xs8, logits=lg8)
+    assert (idx == o_idx).all()
+    assert same_bits(w, o_w)
+    assert_parity(out, o_out)
+    moe.close()

@@ -479,3 +479,20 @@ def test_values_helper_matches_reference_definition():
 def test_normals_have_the_requested_moments():
     v = O.normal(1, 200000, 0.0, 0.02)
     assert abs(float(v.mean())) < 2e-4 and abs(float(v.std()) - 0.02) < 2e-4
+
+
+def test_probability_ties_hidden_in_exp_values():
+    """The GPU decode test's tie logits: the two named experts have exp values
+    one ulp apart but equal probabilities, so ranking by exp value puts the
+    higher index first while the reference order puts the lower index first."""
+    from routing_cases import TIE_LOGITS
+
+    for lg, (a, b) in TIE_LOGITS:
+        lg = np.array(lg, np.float32)
+        mx = lg.max()
+        e = [O.expf(float(np.float32(v - mx))) for v in lg]
+        p = O.softmax(lg)
+        assert e[a] > e[b] and a > b
+        assert p[a] == p[b]
+        idx, _ = O.top_k(p, 2)
+        assert list(idx) == [b, a]
