@@ -22,7 +22,8 @@ prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
 with tokens/s, TOPS and the fraction of the int8 MFMA peak.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--no-prefill] [--decode-eager] [--copy-calibration BYTES]
+                       [--no-prefill] [--prefill-only] [--decode-eager]
+                       [--copy-calibration BYTES]
 """
 import argparse
 import json
@@ -271,6 +272,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill workloads (for counter runs)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="only two eager decode passes over the layers (for counter runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -285,6 +288,11 @@ def main():
         return
     if args.decode_eager:
         print(json.dumps({"decode_eager_steps": decode_eager(args)}), flush=True)
+        return
+    if args.prefill_only:
+        res = [gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=3)
+               for (name, dt, hid, inter, ex, k, tok) in PREFILL]
+        print(json.dumps({"prefill": res}), flush=True)
         return
 
     bytes_step = TOPK * expert_bytes(DTYPE, HID, INTER) + E * HID * 4

@@ -213,94 +213,117 @@ struct GroupedArgs {
   float* y;               // down output: [A][ncols] by sorted position
 };
 
+// Work items are (tile, 128-column group) pairs, ordered by blocks of CGB
+// column groups, then tile, then column group within the block.  The XCDs
+// take work-groups in turn (linear id % 8), so work-group L runs item
+// (L % 8) * per + L / 8: each XCD works through a contiguous run of items,
+// where neighbouring items share a tile's activation rows (same tile, next
+// column group) or an expert's weights (next tile of the same expert, same
+// column groups), and both stay in that XCD's L2.
+constexpr int CGB = 3;
+
 template <int DT, bool GATE_UP>
 __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   constexpr int CH = Layout<DT>::CH;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int ti = blockIdx.x;
-  if (ti >= *a.ntiles) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nt = *a.ntiles;
+  const int ncg = (a.ncols + TN - 1) / TN;
+  const int total = nt * ncg;
+  const int per = (total + 7) >> 3;
+  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= per || item >= total) return;
+  const int ncb = min(CGB, ncg - (item / (nt * CGB)) * CGB);  // column groups in this block
+  const int cb = item / (nt * CGB);
+  const int rem = item - cb * nt * CGB;
+  const int ti = rem / ncb;
+  const int colg = cb * CGB + rem % ncb;
   const Tile tl = a.tiles[ti];
-  const int n0 = blockIdx.y * TN + wave * 32;
+  const int n0 = colg * TN + wave * 32;
   if (n0 >= a.ncols) return;
   const int h = lane >> 5;
-  const int n = n0 + (lane & 31);  // this lane's output column (weight row)
   const int nb = a.nb;
 
-  // activation row of A operand lane (row lane % 32, clamped into the tile)
+  // Addresses are wave-uniform bases (expert, 32-column tile, block) plus a
+  // 32-bit per-lane byte offset, so the block loop advances only scalars.
+  // Activation row of A operand lane: row lane % 32, clamped into the tile.
   const int arow = tl.row0 + min(lane & 31, tl.rows - 1);
-  const ActBlock* arow_act;
-  if constexpr (GATE_UP)
-    arow_act = a.act + (size_t)(a.perm[arow] / a.k) * nb;
-  else
-    arow_act = a.act + (size_t)arow * nb;
-
-  const size_t tile_n = (size_t)n / TILE;
-  const int rn = n % TILE;
+  const int aidx = GATE_UP ? a.perm[arow] / a.k : arow;  // token (gate/up) or sorted row (down)
+  const unsigned aoff = (unsigned)aidx * (unsigned)nb * (unsigned)sizeof(ActBlock);
+  const int tile_n = n0 / TILE;
+  const int rn = lane & 31;  // column within the tile
   const size_t e = (size_t)tl.expert;
-  const uint8_t* cg = a.codes + e * a.codes_stride + (tile_n * nb * CH * TILE + rn) * 16;
-  const uint16_t* sg = a.scales + e * a.scales_stride + tile_n * nb * TILE + rn;
-  const uint8_t* cu = nullptr;
-  const uint16_t* su = nullptr;
-  if constexpr (GATE_UP) {
-    cu = a.codes2 + e * a.codes_stride + (tile_n * nb * CH * TILE + rn) * 16;
-    su = a.scales2 + e * a.scales_stride + tile_n * nb * TILE + rn;
-  }
+  const size_t cplane = (size_t)tile_n * nb * CH * TILE * 16, splane = (size_t)tile_n * nb * TILE;
+  const uint8_t* cg = a.codes + e * a.codes_stride + cplane;
+  const uint16_t* sg = a.scales + e * a.scales_stride + splane;
+  const uint8_t* cu = GATE_UP ? a.codes2 + e * a.codes_stride + cplane : nullptr;
+  const uint16_t* su = GATE_UP ? a.scales2 + e * a.scales_stride + splane : nullptr;
+  const unsigned coff = (unsigned)rn * 16 + (DT == Q8_0 ? (unsigned)h * TILE * 16 : 0u);
+  const unsigned soff = (unsigned)rn * 2;
+  const char* actb = (const char*)a.act;
 
   // accumulators start at +0.0 like the reference's `let mut total = 0.0`,
   // so no sum can become -0.0: the sign of a zero scale product never shows
   v16f accg = {}, accu = {};
 
-  // software pipeline: the raw operands of block b+1 load while block b
-  // computes; nothing reads them before the next iteration
-  u32x4 xr, wgr, wur = {0, 0, 0, 0};
-  uint16_t dg, du = 0;
-  float dxl;
-  auto load = [&](int b) {
-    const ActBlock* ab = arow_act + b;
-    xr = *(const u32x4*)(ab->q + 16 * h);
-    dxl = ab->scale;
-    wgr = weight_chunk<DT>(cg + (size_t)b * CH * TILE * 16, h);
-    dg = sg[(size_t)b * TILE];
+  // Operands of one block.  Two sets alternate (the loop is unrolled by
+  // two), so block b+1 loads while block b computes without register copies.
+  struct Ops {
+    u32x4 xr, wg, wu;
+    float dx;
+    uint16_t dg, du;
+  };
+  auto load = [&](Ops& o, int b) {
+    const char* ab = actb + (size_t)b * sizeof(ActBlock);
+    o.xr = *(const u32x4*)(ab + aoff + 16 * h);
+    o.dx = *(const float*)(ab + aoff + 32);
+    const size_t cb = (size_t)b * CH * TILE * 16;
+    o.wg = __builtin_nontemporal_load((const u32x4*)(cg + cb + coff));
+    o.dg = *(const uint16_t*)((const char*)(sg + (size_t)b * TILE) + soff);
     if constexpr (GATE_UP) {
-      wur = weight_chunk<DT>(cu + (size_t)b * CH * TILE * 16, h);
-      du = su[(size_t)b * TILE];
+      o.wu = __builtin_nontemporal_load((const u32x4*)(cu + cb + coff));
+      o.du = *(const uint16_t*)((const char*)(su + (size_t)b * TILE) + soff);
     }
   };
   // q4_0 offset term: B = -8 in every byte makes the product -8 * sum(x) of
   // the row, broadcast over the columns
   const v4i minus8 = {(int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u};
-  load(0);
-  for (int b = 0; b < nb; b++) {
-    const u32x4 cxr = xr, cwgr = wgr, cwur = wur;
-    const uint16_t cdg = dg, cdu = du;
-    const float cdx = dxl;
-    if (b + 1 < nb) load(b + 1);
+  auto compute = [&](const Ops& o) {
     v4i xa;
-    __builtin_memcpy(&xa, &cxr, 16);
+    __builtin_memcpy(&xa, &o.xr, 16);
     v16i c0 = {};
     if constexpr (DT == Q4_0) c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, minus8, c0, 0, 0, 0);
-    const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(cwgr, h), c0, 0, 0, 0);
+    const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(o.wg, h), c0, 0, 0, 0);
     v16i iu = {};
     if constexpr (GATE_UP)
-      iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(cwur, h), c0, 0, 0, 0);
+      iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(o.wu, h), c0, 0, 0, 0);
     // scale products d_w[col] * d_x[row] of the whole 32x32 tile as a K=2
     // f32 outer product whose second K column is zero: lanes 0-31 hold
     // A[row][0] = d_x and B[0][col] = d_w.  The matrix core rounds each
     // product exactly like a VALU multiply (only the sign of a zero product
     // can differ, and that cannot reach an accumulator that starts at +0).
-    const float ax = lane < 32 ? cdx : 0.0f;
+    const float ax = lane < 32 ? o.dx : 0.0f;
     v16f pg = {};
-    pg = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(cdg) : 0.0f, pg, 0, 0, 0);
+    pg = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(o.dg) : 0.0f, pg, 0, 0, 0);
     v16f pu = {};
     if constexpr (GATE_UP)
-      pu = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(cdu) : 0.0f, pu, 0, 0, 0);
+      pu = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(o.du) : 0.0f, pu, 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       accg[j] = accg[j] + pg[j] * (float)ig[j];
       if constexpr (GATE_UP) accu[j] = accu[j] + pu[j] * (float)iu[j];
     }
+  };
+  Ops A, B;
+  load(A, 0);
+  int b = 0;
+  for (; b + 1 < nb; b += 2) {
+    load(B, b + 1);
+    compute(A);
+    if (b + 2 < nb) load(A, b + 2);
+    compute(B);
   }
+  if (b < nb) compute(A);
 
   if constexpr (GATE_UP) {
     // h = silu(g) * u, quantized per (row, 32-column block): the 32 columns
@@ -329,7 +352,7 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       const int row = (j % 4) + 4 * h + 8 * (j / 4);
-      if (row < tl.rows) a.y[(size_t)(tl.row0 + row) * a.ncols + n] = accg[j];
+      if (row < tl.rows) a.y[(size_t)(tl.row0 + row) * a.ncols + n0 + rn] = accg[j];
     }
   }
 }
@@ -446,7 +469,7 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   g.k = L.k;
   g.act = L.act;
   g.hact = hact;
-  dim3 gg((unsigned)w.max_tiles, (unsigned)((L.I + TN - 1) / TN));
+  const unsigned gg = (unsigned)((w.max_tiles * ((L.I + TN - 1) / TN) + 7) / 8 * 8);
   if (L.dtype == Q8_0)
     HALE_STEP(K_GROUPED_GATE_UP, (launch(k_grouped<Q8_0, true>, gg, 256, 0, st, g)));
   else
@@ -465,7 +488,7 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   d.k = L.k;
   d.act = hact;
   d.y = y;
-  dim3 gd((unsigned)w.max_tiles, (unsigned)((L.H + TN - 1) / TN));
+  const unsigned gd = (unsigned)((w.max_tiles * ((L.H + TN - 1) / TN) + 7) / 8 * 8);
   if (L.dtype == Q8_0)
     HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q8_0, false>, gd, 256, 0, st, d)));
   else
