@@ -45,6 +45,12 @@ E, HID, INTER, TOPK = 128, 2048, 768, 8
 DTYPE = H.Q4_0
 INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA
 
+# further decode workloads: (name, dtype, hidden, inter, experts, top_k, layers)
+DECODE_MORE = [
+    ("mixtral-8x7b decode q4_0", H.Q4_0, 4096, 14336, 8, 2, 4),
+    ("qwen3-235b-a22b decode q4_0", H.Q4_0, 4096, 1536, 128, 8, 6),
+]
+
 # prefill workloads: (name, dtype, hidden, inter, experts, top_k, tokens)
 PREFILL = [
     ("qwen3-30b-a3b prefill 512 tok q8_0", H.Q8_0, 2048, 768, 128, 8, 512),
@@ -202,6 +208,50 @@ def measured_traffic():
     return out
 
 
+def gpu_decode_more(name, dtype, hid, inter, experts, topk, nlayers, reps=20):
+    """One-token MoE layer decode over nlayers resident layers visited in
+    turn (cold weights), replayed from a graph; GB/s of routed expert bytes
+    plus router bytes."""
+    ctx = H.Context(0)
+    layers = build_layers(ctx, nlayers, seed=555, dtype=dtype, hid=hid, inter=inter,
+                          experts=experts, topk=topk)
+    xs = ctx.malloc(16 * hid * 4)
+    xs.fill_normal(7, 16 * hid, 0.0, 1.0)
+    out = ctx.malloc(hid * 4)
+
+    def step(s):
+        layers[s % nlayers].forward_device(1, xs.offset((s % 16) * hid * 4), out.address)
+
+    for s in range(2 * nlayers):
+        step(s)
+    ctx.synchronize()
+    graph = ctx.capture(lambda: [step(s) for s in range(nlayers)])
+    graph.launch()
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        graph.launch()
+    ms = ctx.timer_stop()
+    steps = reps * nlayers
+    ctx.profile(True)
+    ctx.profile_reset()
+    for s in range(2 * nlayers):
+        step(s)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    graph.close()
+    for m in layers:
+        m.close()
+    ctx.close()
+    bytes_step = topk * expert_bytes(dtype, hid, inter) + experts * hid * 4
+    us = 1000 * ms / steps
+    return {"workload": name, "bytes_per_step": bytes_step, "us_per_step": round(us, 2),
+            "GB_per_s": round(bytes_step / us / 1e3, 1),
+            "pct_hbm_peak": round(100 * bytes_step / us / 1e3 / HBM_PEAK_GBS, 2),
+            "layers_resident": nlayers,
+            "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
+
+
 def gpu_decode(args):
     ctx = H.Context(0)
     t0 = time.time()
@@ -314,6 +364,12 @@ def main():
                 "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
                 "traffic": measured_traffic().get(dom), "bytes_per_launch": launch_bytes.get(dom)}
 
+    more = []
+    if not args.no_prefill:
+        for (name, dt, hid, inter, ex, k, nl) in DECODE_MORE:
+            more.append(gpu_decode_more(name, dt, hid, inter, ex, k, nl))
+            log(f"decode {name}: {more[-1]['us_per_step']} us/step, {more[-1]['GB_per_s']} GB/s")
+
     prefill = []
     if not args.no_prefill:
         for (name, dt, hid, inter, ex, k, tok) in PREFILL:
@@ -356,6 +412,7 @@ def main():
         "moe_layer_tokens_per_s": round(steps / sec, 1),
         "roofline": roofline,
         "kernels": kernels,
+        "decode_more": more,
         "prefill": prefill,
         "cpu_baseline": cpu,
     }

@@ -176,10 +176,16 @@ __device__ __forceinline__ int half_wave_sum(int v) {
   return v;
 }
 
-// acc + p[0] + p[1] + ... + p[n-1], strictly left to right, from 16-byte
-// aligned LDS: 16 values per batch in two alternating register buffers, so
-// the reads of batch c+1 are in flight while batch c is added.
+// acc + p[0] + p[1] + ... + p[n-1], strictly left to right, from LDS: the
+// values before the first 16-byte boundary one by one, then 16 per batch
+// in two alternating register buffers, so the reads of batch c+1 are in
+// flight while batch c is added.
 __device__ __forceinline__ float lds_sum_in_order(const float* p, int n, float acc) {
+  int head = (int)((16 - ((uintptr_t)p & 15)) & 15) / 4;
+  if (head > n) head = n;
+  for (int i = 0; i < head; i++) acc = acc + p[i];
+  p += head;
+  n -= head;
   const f32x4* p4 = (const f32x4*)p;
   const int nb = n / 16;
   f32x4 A[4], B[4];

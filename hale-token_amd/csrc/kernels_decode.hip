@@ -789,7 +789,15 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
 
   const int r = lane % DR;          // row within the group
   const int jl = lane / DR;         // unit within the wave-load
-  const size_t row0 = (size_t)g * DR;
+  // The four 8-row groups of a 32-row tile share its scale lines; work-group
+  // g runs on XCD g % 8, so when the grid is a multiple of 32 the groups of
+  // one tile get ids of one residue class: XCD x takes tiles x, x + 8, ...
+  // (all four groups of each), a permutation of the row groups.
+  size_t row0 = (size_t)g * DR;
+  if ((gridDim.x & 31) == 0) {
+    const int gx = g & 7, gj = g >> 3;
+    row0 = (size_t)(gx + 8 * (gj >> 2)) * TILE + (size_t)(gj & 3) * DR;
+  }
   const size_t tile = row0 / TILE;
   const int rt = (int)(row0 % TILE) + r;  // row within its 32-row tile
   const size_t row_off = (tile * nb * CH * TILE + rt) * 16;
