@@ -215,6 +215,34 @@ __device__ __forceinline__ float lds_sum_in_order(const float* p, int n, float a
   return acc;
 }
 
+// acc + p[0] + p[S] + ... + p[(n-1)·S], strictly left to right, from LDS:
+// batches of 8 in two alternating register buffers, so the reads of batch
+// c+1 are in flight while batch c is added.
+template <int S>
+__device__ __forceinline__ float lds_sum_strided(const float* p, int n, float acc) {
+  const int nb = n / 8;
+  float A[8], B[8];
+  auto ld = [&](float* d, int c) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) d[q] = p[(8 * c + q) * S];
+  };
+  auto add = [&](const float* d) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) acc = acc + d[q];
+  };
+  if (nb > 0) ld(A, 0);
+  int c = 0;
+  for (; c + 1 < nb; c += 2) {
+    ld(B, c + 1);
+    add(A);
+    if (c + 2 < nb) ld(A, c + 2);
+    add(B);
+  }
+  if (c < nb) add(A);
+  for (int i = 8 * nb; i < n; i++) acc = acc + p[i * S];
+  return acc;
+}
+
 // Quantizes one 32-element block held one value per lane of a 32-lane
 // group (Q8Activations::quantize, src/tensor/quant.rs:85-91).  The max is
 // order independent; the scale stays f32.  Returns the code of this lane.

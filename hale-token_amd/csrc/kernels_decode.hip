@@ -663,16 +663,16 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   // Blocks past the end of the row are clamped to the last block (an
   // in-bounds load whose term is never stored), so the chunk loop has no
   // branches and all of its loads are in flight together.
+  auto load_block = [&](int ch, int s) {
+    const int b = min(ch * CB + wave + NW * s, nb - 1);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+      cw[s][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
+    sw[s] = srow[(size_t)b * TILE];
+  };
   auto load_chunk = [&](int ch) {
-    const int b0 = ch * CB;
 #pragma unroll
-    for (int s = 0; s < UPW; s++) {
-      const int b = min(b0 + wave + NW * s, nb - 1);
-#pragma unroll
-      for (int c = 0; c < CH; c++)
-        cw[s][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
-      sw[s] = srow[(size_t)b * TILE];
-    }
+    for (int s = 0; s < UPW; s++) load_block(ch, s);
   };
 
   float total = 0.0f;
@@ -686,28 +686,34 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     const int b0 = ch * CB;
     const int bend = min(nb, b0 + CB);
     float(*tb)[GROUP] = terms[ch & 1];
+    // Terms in groups of four blocks; each group's registers take the next
+    // chunk's loads as soon as its terms are done.  The scheduling barriers
+    // keep the activation reads of one group live at a time, so the kernel
+    // stays within 256 VGPRs (two work-groups per CU).
     float tv[UPW];
+    const bool more = ch + 1 < nchunks;
 #pragma unroll
-    for (int s = 0; s < UPW; s++) tv[s] = block_term<DT>(cw[s], sw[s], act + min(b0 + wave + NW * s, nb - 1));
-    if (ch + 1 < nchunks) load_chunk(ch + 1);
+    for (int s0 = 0; s0 < UPW; s0 += 4) {
 #pragma unroll
-    for (int s = 0; s < UPW; s++) {
-      const int b = b0 + wave + NW * s;
-      if (b < bend) tb[b - b0][lane] = tv[s];
-    }
-    __syncthreads();
-    if (wave == 0) {
-      const int n = bend - b0;
-      int b = 0;
-      for (; b + 8 <= n; b += 8) {
-        float v[8];
+      for (int s = s0; s < s0 + 4; s++)
+        tv[s] = block_term<DT>(cw[s], sw[s], act + min(b0 + wave + NW * s, nb - 1));
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = tb[b + u][lane];
+      for (int s = s0; s < s0 + 4; s++) asm volatile("" : "+v"(tv[s]));  // computed here, not at the store
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) total = total + v[u];
+        for (int s = s0; s < s0 + 4; s++) load_block(ch + 1, s);
       }
-      for (; b < n; b++) total = total + tb[b][lane];
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // Rows past the end of the row's blocks take the clamped terms and are
+    // never folded; an unconditional store keeps each term's computation
+    // where it is written (a conditional one would be sunk into the store's
+    // branch, keeping every input live until then).
+#pragma unroll
+    for (int s = 0; s < UPW; s++) tb[wave + NW * s][lane] = tv[s];
+    __syncthreads();
+    if (wave == 0) total = lds_sum_strided<GROUP>(&tb[0][lane], bend - b0, total);
   }
   if (wave != 0) return;
 
@@ -769,7 +775,10 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
   constexpr int CB = NW * J * UPW;  // units per chunk: 512 (q4_0), 256 (q8_0)
   constexpr int AQ = (CB * 3 + 64 * NW - 1) / (64 * NW);
   constexpr int SPL = DOWN_MAX_SLOTS / 8;  // slots per fold lane
-  __shared__ float terms[CB][DR];
+  // terms of row r at [r][unit]: a fold lane reads its slot's terms from
+  // consecutive addresses (16-byte reads, several in flight); the row pitch
+  // CB + 8 puts the 64 lanes of a term store in distinct banks
+  __shared__ __attribute__((aligned(16))) float terms[DR][CB + 8];
   __shared__ ActBlock s_act[CB];
   __shared__ float s_tot[DOWN_MAX_SLOTS][DR];
   __shared__ int s_exp[DOWN_MAX_SLOTS];
@@ -809,18 +818,28 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
   // unit of load s in the chunk at u0 (past the end: clamped to the last
   // unit, loaded and never stored)
   auto unit_of = [&](int u0, int s) { return min(u0 + (s * NW + wave) * J + jl, nunits - 1); };
-  auto load_chunk = [&](int u0) {
+  // wave-load s of the chunk at u0 holds at least one unit (wave-uniform)
+  auto live = [&](int u0, int s) { return (s * NW + wave) * J < nunits - u0; };
+  // The expert of each lane's unit comes from LDS; the lookups of a batch of
+  // wave-loads are issued together (and pinned there) before its loads.
+  int ex[UPW];
+  auto lookup = [&](int u0, int s0, int n) {
 #pragma unroll
-    for (int s = 0; s < UPW; s++) {
-      const int u = unit_of(u0, s);
-      const int sl = div_small(u, nb, inv_nb), b = u - sl * nb;
-      const size_t e = (size_t)s_exp[sl];
-      const uint8_t* c0 = a.codes + e * a.codes_stride + row_off;
+    for (int s = s0; s < s0 + n; s++) ex[s] = s_exp[div_small(unit_of(u0, s), nb, inv_nb)];
 #pragma unroll
-      for (int c = 0; c < CH; c++)
-        cw[s][c] = __builtin_nontemporal_load((const u32x4*)(c0 + ((size_t)b * CH + c) * TILE * 16));
-      sw[s] = a.scales[e * a.scales_stride + srow_off + (size_t)b * TILE];
-    }
+    for (int s = s0; s < s0 + n; s++) asm volatile("" : "+v"(ex[s]));
+  };
+  auto load_unit = [&](int u0, int s) {
+    const int u = unit_of(u0, s);
+    const int sl = div_small(u, nb, inv_nb), b = u - sl * nb;
+    const size_t e = (size_t)ex[s];
+    const uint8_t* c0 = a.codes + e * a.codes_stride + row_off;
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+      cw[s][c] = __builtin_nontemporal_load((const u32x4*)(c0 + ((size_t)b * CH + c) * TILE * 16));
+    sw[s] = a.scales[e * a.scales_stride + srow_off + (size_t)b * TILE];
+  };
+  auto load_act = [&](int u0) {
 #pragma unroll
     for (int q = 0; q < AQ; q++) {
       const int i = threadIdx.x + q * 64 * NW;
@@ -838,23 +857,47 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
 #pragma unroll
   for (int i = 0; i < SPL; i++) tot[i] = 0.0f;
 
+  load_act(0);      // the activation blocks do not depend on the routes
   __syncthreads();  // s_exp / s_w
+  lookup(0, 0, UPW);
+#pragma unroll
+  for (int s = 0; s < UPW; s++)
+    if (live(0, s)) load_unit(0, s);
   for (int u0 = 0; u0 < nunits; u0 += CB) {
-    load_chunk(u0);
 #pragma unroll
     for (int q = 0; q < AQ; q++) {
       const int i = threadIdx.x + q * 64 * NW;
       if (i < CB * 3 && u0 + i / 3 < nunits) ((u32x4*)s_act)[i] = av[q];
     }
     __syncthreads();
+    // Terms in groups of four wave-loads; each group's registers take the
+    // next chunk's loads as soon as its terms are done (the asm statements
+    // and scheduling barriers keep that order and the register count low).
+    const bool more = u0 + CB < nunits;
     float tv[UPW];
 #pragma unroll
-    for (int s = 0; s < UPW; s++) tv[s] = block_term<DT>(cw[s], sw[s], s_act + (unit_of(u0, s) - u0));
+    for (int s0 = 0; s0 < UPW; s0 += 4) {
 #pragma unroll
-    for (int s = 0; s < UPW; s++) {
-      const int u = u0 + (s * NW + wave) * J + jl;
-      if (u < nunits && u - u0 < CB) terms[u - u0][r] = tv[s];
+      for (int s = s0; s < s0 + 4; s++)
+        if (live(u0, s)) tv[s] = block_term<DT>(cw[s], sw[s], s_act + (unit_of(u0, s) - u0));
+#pragma unroll
+      for (int s = s0; s < s0 + 4; s++)
+        if (live(u0, s)) asm volatile("" : "+v"(tv[s]));
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) {
+        lookup(u0 + CB, s0, 4);
+#pragma unroll
+        for (int s = s0; s < s0 + 4; s++)
+          if (live(u0 + CB, s)) load_unit(u0 + CB, s);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if (more) load_act(u0 + CB);
+    // (s * NW + wave) * J + jl < CB: every store is in the chunk; units past
+    // the end of a live wave-load hold clamped terms that the fold never reads
+#pragma unroll
+    for (int s = 0; s < UPW; s++)
+      if (live(u0, s)) terms[r][(s * NW + wave) * J + jl] = tv[s];
     __syncthreads();
     if (wave == 0) {
       const int uend = min(nunits, u0 + CB);
@@ -864,18 +907,7 @@ __global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
         if (sl < slots) {
           // this slot's units inside the chunk, in block order
           const int ua = max(u0, sl * nb), ub = min(uend, (sl + 1) * nb);
-          float t = tot[i];
-          int u = ua;
-          for (; u + 4 <= ub; u += 4) {
-            const float v0 = terms[u - u0][r], v1 = terms[u + 1 - u0][r];
-            const float v2 = terms[u + 2 - u0][r], v3 = terms[u + 3 - u0][r];
-            t = t + v0;
-            t = t + v1;
-            t = t + v2;
-            t = t + v3;
-          }
-          for (; u < ub; u++) t = t + terms[u - u0][r];
-          tot[i] = t;
+          if (ub > ua) tot[i] = lds_sum_in_order(&terms[r][ua - u0], ub - ua, tot[i]);
         }
       }
     }

@@ -172,17 +172,6 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
 // (q4_0: the low nibbles are K 0-15, the high nibbles K 16-31).  Result
 // element j of lane l is row (j%4) + 4*(l/32) + 8*(j/4), column l%32.
 
-// The 16-byte chunk holding K half `h` of (column, block): q8_0 keeps the
-// halves in two chunks, q4_0 keeps both in one (low nibbles K 0-15, high
-// nibbles K 16-31).
-template <int DT>
-__device__ __forceinline__ u32x4 weight_chunk(const uint8_t* chunk0, int h) {
-  if constexpr (DT == Q8_0)
-    return __builtin_nontemporal_load((const u32x4*)(chunk0 + h * TILE * 16));
-  else
-    return __builtin_nontemporal_load((const u32x4*)chunk0);
-}
-
 // B operand from a loaded chunk.  q8_0: the signed codes as they are.  q4_0:
 // the unsigned nibbles n (0..15) of half h; the MFMA's accumulator then starts
 // at -8 * sum(x) of the row so that it ends at sum((n - 8) * x), the same
@@ -266,29 +255,33 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   // so no sum can become -0.0: the sign of a zero scale product never shows
   v16f accg = {}, accu = {};
 
-  // Operands of one block.  Two sets alternate (the loop is unrolled by
-  // two), so block b+1 loads while block b computes without register copies.
+  // Operands of one block.
   struct Ops {
     u32x4 xr, wg, wu;
     float dx;
     uint16_t dg, du;
   };
+  // Weights use ordinary (cached) loads: every tile of an expert reads the
+  // same column group, and neighbouring items run on one XCD, so the later
+  // tiles find the lines in L2.
   auto load = [&](Ops& o, int b) {
     const char* ab = actb + (size_t)b * sizeof(ActBlock);
     o.xr = *(const u32x4*)(ab + aoff + 16 * h);
     o.dx = *(const float*)(ab + aoff + 32);
     const size_t cb = (size_t)b * CH * TILE * 16;
-    o.wg = __builtin_nontemporal_load((const u32x4*)(cg + cb + coff));
+    o.wg = *(const u32x4*)(cg + cb + coff);
     o.dg = *(const uint16_t*)((const char*)(sg + (size_t)b * TILE) + soff);
     if constexpr (GATE_UP) {
-      o.wu = __builtin_nontemporal_load((const u32x4*)(cu + cb + coff));
+      o.wu = *(const u32x4*)(cu + cb + coff);
       o.du = *(const uint16_t*)((const char*)(su + (size_t)b * TILE) + soff);
     }
   };
   // q4_0 offset term: B = -8 in every byte makes the product -8 * sum(x) of
   // the row, broadcast over the columns
   const v4i minus8 = {(int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u};
-  auto compute = [&](const Ops& o) {
+  // `valid` is false for the clamped blocks past the end: their scale
+  // products are zero, so they add +0 or -0, which leaves every sum as it is
+  auto compute = [&](const Ops& o, bool valid) {
     v4i xa;
     __builtin_memcpy(&xa, &o.xr, 16);
     v16i c0 = {};
@@ -302,28 +295,36 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
     // A[row][0] = d_x and B[0][col] = d_w.  The matrix core rounds each
     // product exactly like a VALU multiply (only the sign of a zero product
     // can differ, and that cannot reach an accumulator that starts at +0).
-    const float ax = lane < 32 ? o.dx : 0.0f;
+    const bool use = lane < 32 && valid;
+    const float ax = use ? o.dx : 0.0f;
     v16f pg = {};
-    pg = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(o.dg) : 0.0f, pg, 0, 0, 0);
+    pg = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, use ? h2f(o.dg) : 0.0f, pg, 0, 0, 0);
     v16f pu = {};
     if constexpr (GATE_UP)
-      pu = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, lane < 32 ? h2f(o.du) : 0.0f, pu, 0, 0, 0);
+      pu = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, use ? h2f(o.du) : 0.0f, pu, 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       accg[j] = accg[j] + pg[j] * (float)ig[j];
       if constexpr (GATE_UP) accu[j] = accu[j] + pu[j] * (float)iu[j];
     }
   };
-  Ops A, B;
-  load(A, 0);
-  int b = 0;
-  for (; b + 1 < nb; b += 2) {
-    load(B, b + 1);
-    compute(A);
-    if (b + 2 < nb) load(A, b + 2);
-    compute(B);
+  // NS operand sets in a ring: block b + NS - 1 loads while block b
+  // computes (four sets for the down projection; two for gate/up, whose
+  // sets are larger and which is bound by its VALU work, not by latency).
+  // The loop body has no branches (so the load counters are tracked across
+  // iterations): blocks past the end are loaded clamped to the last block
+  // and computed with zero scales.
+  constexpr int NS = GATE_UP ? 2 : 4;
+  Ops S[NS];
+#pragma unroll
+  for (int j = 0; j < NS - 1; j++) load(S[j], min(j, nb - 1));
+  for (int b = 0; b < nb; b += NS) {
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+      load(S[(j + NS - 1) % NS], min(b + j + NS - 1, nb - 1));
+      compute(S[j], b + j < nb);
+    }
   }
-  if (b < nb) compute(A);
 
   if constexpr (GATE_UP) {
     // h = silu(g) * u, quantized per (row, 32-column block): the 32 columns
