@@ -1,0 +1,79 @@
+// pack.h -- the Hale expert pack (src/expert/pack.rs), host side: header
+// parsing, positioned reads, and the loader that streams a layer's records
+// into a MoE layer's HBM planes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <memory>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/hale_moe.h"
+
+namespace hale {
+
+// PackHeader (src/expert/pack.rs:55-73)
+struct PackHeader {
+  uint32_t version = 0;
+  int dtype = -1;
+  size_t hidden = 0, inter = 0, num_experts = 0;
+  std::vector<size_t> moe_layers;
+  size_t record_bytes = 0, record_stride = 0, data_offset = 0;
+  // PackHeader::file_size (:96-99)
+  size_t file_size() const { return data_offset + moe_layers.size() * num_experts * record_stride; }
+};
+
+// Parses the JSON header; false (with a message) on malformed input or a
+// missing field.
+bool parse_pack_header(const char* json, size_t len, PackHeader* h, std::string* err);
+
+// Records a failure on a context (hale_last_error) and returns `code`.
+int ctx_fail(hale_ctx* c, int code, const char* fmt, ...);
+
+// One load of a layer's experts from a pack: the loader thread and its
+// result.  Shared by the pack (its current load) and the layer (its pending
+// load); whichever needs the result first joins the thread.
+struct PackLoad {
+  std::thread th;
+  int rc = HALE_OK;  // written by the thread before it ends
+  std::string err;
+  void join() {
+    if (th.joinable()) th.join();
+  }
+};
+
+}  // namespace hale
+
+// One open pack.  The loader thread, its stream and its staging buffers
+// belong to the pack, so one load runs per pack at a time.
+struct hale_pack {
+  hale_ctx* ctx = nullptr;  // bound by the first load into a layer
+  int device = 0;
+  int fd = -1;
+  std::string path;
+  hale::PackHeader h;
+  hipStream_t stream = nullptr;  // uploads and repacks (default priority)
+  // staging: two slots of `slot_bytes`, pinned host and device
+  size_t slot_bytes = 0;
+  void* pinned[2] = {nullptr, nullptr};
+  void* dstage[2] = {nullptr, nullptr};
+  hipEvent_t copied[2] = {nullptr, nullptr};  // slot's host->device copy done
+  std::shared_ptr<hale::PackLoad> load;  // the running (or last) load
+};
+
+namespace hale {
+
+// Positioned read of `n` bytes at `off` (retries short reads); false with a
+// message on failure or end of file.
+bool pack_pread(const hale_pack* p, void* dst, size_t n, uint64_t off, std::string* err);
+
+// Record offset of (layer, expert); false with a message when the key is
+// not in the pack (PackHeader::offset_of, src/expert/pack.rs:104-123).
+bool pack_offset_of(const PackHeader& h, uint32_t layer, uint32_t expert, uint64_t* off,
+                    std::string* err);
+
+}  // namespace hale

@@ -5,11 +5,13 @@
 // kernels of kernels_decode.hip / kernels_prefill.hip.  Reference items are
 // cited per entry point in the public header.
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
@@ -18,6 +20,7 @@
 #include "../../include/hale_moe.h"
 #include "hale_device.h"
 #include "kernels.h"
+#include "pack.h"
 #include "prefill.h"
 
 using namespace hale;
@@ -89,6 +92,11 @@ struct hale_moe {
   size_t cap_tok = 0;
   // grouped prefill workspace
   PrefillWorkspace pw;
+  // load from an expert pack: pending until the layer's next use waits for
+  // it (joins the loader thread, then orders the context's stream after
+  // `loaded`, recorded on the pack's stream after the last upload)
+  std::shared_ptr<hale::PackLoad> load;
+  hipEvent_t loaded = nullptr;
 };
 
 // ---------------------------------------------------------------------------
@@ -117,7 +125,19 @@ static int fail(hale_ctx* c, int code, const char* fmt, ...) {
       return fail((ctx), HALE_EHIP, "%s failed: %s", #call, hipGetErrorString(e_));        \
   } while (0)
 
+int hale::ctx_fail(hale_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (!c) return fail(nullptr, code, "%s", buf);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  return fail(c, code, "%s", buf);
+}
+
 static bool quantized(int dtype) { return dtype == HALE_Q8_0 || dtype == HALE_Q4_0; }
+static int moe_wait_load(hale_moe* m);
 
 // ---------------------------------------------------------------------------
 // context
@@ -703,7 +723,9 @@ extern "C" void hale_moe_destroy(hale_moe* m) {
   hale_ctx* c = m->ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   (void)hipSetDevice(c->device);
+  (void)moe_wait_load(m);
   (void)hipStreamSynchronize(c->stream);
+  if (m->loaded) (void)hipEventDestroy(m->loaded);
   moe_free_scratch(m);
   prefill_free(m->pw);
   (void)hipFree(m->gate_c);
@@ -730,6 +752,8 @@ static int set_expert(hale_moe* m, uint32_t e, const void* gate, const void* up,
                 need_g, nd, need_d);
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
+  int rc0 = moe_wait_load(m);
+  if (rc0) return rc0;
   const uint8_t *sg = (const uint8_t*)gate, *su = (const uint8_t*)up, *sd = (const uint8_t*)down;
   if (!on_device) {
     void* s;
@@ -773,6 +797,8 @@ extern "C" int hale_moe_set_expert_matrices(hale_moe* m, uint32_t e, const hale_
     return fail(c, HALE_EINVAL, "expert shapes do not match the layer");
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_wait_load(m);
+  if (rc) return rc;
   // identical padded geometry, so the planes copy as they are
   HIPCHK(c, hipMemcpyAsync(m->gate_c + e * m->gc_bytes, gate->codes, m->gc_bytes, hipMemcpyDeviceToDevice, c->stream));
   HIPCHK(c, hipMemcpyAsync(m->up_c + e * m->gc_bytes, up->codes, m->gc_bytes, hipMemcpyDeviceToDevice, c->stream));
@@ -782,6 +808,19 @@ extern "C" int hale_moe_set_expert_matrices(hale_moe* m, uint32_t e, const hale_
   HIPCHK(c, hipMemcpyAsync(m->down_s + e * m->ds_elems, down->scales, m->ds_elems * 2, hipMemcpyDeviceToDevice, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   m->present[e] = 1;
+  return HALE_OK;
+}
+
+// Waits for this layer's pending pack load: joins the loader thread, then
+// orders the context's stream after the uploads.
+static int moe_wait_load(hale_moe* m) {
+  if (!m->load) return HALE_OK;
+  hale_ctx* c = m->ctx;
+  std::shared_ptr<hale::PackLoad> L = std::move(m->load);
+  L->join();
+  if (L->rc != HALE_OK) return fail(c, L->rc, "%s", L->err.c_str());
+  HIPCHK(c, hipStreamWaitEvent(c->stream, m->loaded, 0));
+  std::fill(m->present.begin(), m->present.end(), (char)1);
   return HALE_OK;
 }
 
@@ -882,7 +921,9 @@ static PrefillLayer prefill_layer(hale_moe* m) {
 
 static int moe_forward_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
                                float* dout) {
-  int rc = check_all_present(m);
+  int rc = moe_wait_load(m);
+  if (rc) return rc;
+  rc = check_all_present(m);
   if (rc) return rc;
   rc = moe_reserve(m, ntok);
   if (rc) return rc;
@@ -988,6 +1029,8 @@ extern "C" int hale_moe_set_experts_device(hale_moe* m, uint32_t first, uint32_t
   size_t nd = m->H * (size_t)hale_row_bytes(m->dtype, m->I);
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_wait_load(m);
+  if (rc) return rc;
   for (uint32_t i = 0; i < count; i++) {
     size_t e = first + i;
     LAUNCH(c, K_REPACK, launch_repack(m->dtype, (const uint8_t*)d_gate + i * ng, m->I, m->H,
@@ -1000,6 +1043,148 @@ extern "C" int hale_moe_set_experts_device(hale_moe* m, uint32_t first, uint32_t
   HIPCHK(c, hipStreamSynchronize(c->stream));
   for (uint32_t i = 0; i < count; i++) m->present[first + i] = 1;
   return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// expert pack -> HBM (the file tier under the resident tier)
+// ---------------------------------------------------------------------------
+
+// Loader thread of one layer: the layer's records are contiguous in the
+// file, so each batch is one positioned read into a pinned slot, one copy to
+// the matching device slot and a repack per matrix, on the pack's stream.
+// A slot is refilled only after its previous copy has finished.
+static void pack_loader(hale_pack* p, hale_moe* m, hale::PackLoad* L, uint64_t off0, size_t batch) {
+  const size_t stride = p->h.record_stride, rbytes = p->h.record_bytes;
+  const size_t proj = m->I * (size_t)hale_row_bytes(m->dtype, m->H);
+  auto hip = [&](hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    L->rc = HALE_EHIP;
+    L->err = std::string("pack load: ") + what + ": " + hipGetErrorString(e);
+    return false;
+  };
+  if (!hip(hipSetDevice(p->device), "hipSetDevice")) return;
+  for (size_t e0 = 0, it = 0; e0 < m->E; e0 += batch, it++) {
+    const int s = (int)(it & 1);
+    const size_t n = std::min(batch, m->E - e0);
+    const size_t bytes = (n - 1) * stride + rbytes;
+    if (!hip(hipEventSynchronize(p->copied[s]), "hipEventSynchronize")) return;
+    std::string err;
+    if (!hale::pack_pread(p, p->pinned[s], bytes, off0 + e0 * stride, &err)) {
+      L->rc = HALE_EIO;
+      L->err = err;
+      return;
+    }
+    if (!hip(hipMemcpyAsync(p->dstage[s], p->pinned[s], bytes, hipMemcpyHostToDevice, p->stream),
+             "upload"))
+      return;
+    if (!hip(hipEventRecord(p->copied[s], p->stream), "hipEventRecord")) return;
+    for (size_t i = 0; i < n; i++) {
+      const size_t e = e0 + i;
+      const uint8_t* rec = (const uint8_t*)p->dstage[s] + i * stride;
+      hipError_t r = launch_repack(m->dtype, rec, m->I, m->H, m->gate_c + e * m->gc_bytes,
+                                   m->gate_s + e * m->gs_elems, p->stream);
+      if (r == hipSuccess)
+        r = launch_repack(m->dtype, rec + proj, m->I, m->H, m->up_c + e * m->gc_bytes,
+                          m->up_s + e * m->gs_elems, p->stream);
+      if (r == hipSuccess)
+        r = launch_repack(m->dtype, rec + 2 * proj, m->H, m->I, m->down_c + e * m->dc_bytes,
+                          m->down_s + e * m->ds_elems, p->stream);
+      if (!hip(r, "repack")) return;
+    }
+  }
+  hip(hipEventRecord(m->loaded, p->stream), "hipEventRecord");
+}
+
+static void pack_free_staging(hale_pack* p) {
+  for (int s = 0; s < 2; s++) {
+    if (p->pinned[s]) (void)hipHostFree(p->pinned[s]);
+    if (p->dstage[s]) (void)hipFree(p->dstage[s]);
+    p->pinned[s] = p->dstage[s] = nullptr;
+  }
+  p->slot_bytes = 0;
+}
+
+extern "C" int hale_moe_prefetch_pack(hale_moe* m, hale_pack* p) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !p) return fail(c, HALE_EINVAL, "prefetch_pack: NULL argument");
+  if (p->ctx && p->ctx != c)
+    return fail(c, HALE_EINVAL, "the pack already loads into another context's layers");
+  const hale::PackHeader& h = p->h;
+  if (h.dtype != m->dtype || h.hidden != m->H || h.inter != m->I || h.num_experts != m->E)
+    return fail(c, HALE_EINVAL,
+                "pack (dtype %d, hidden %zu, inter %zu, %zu experts) does not match the layer "
+                "(dtype %d, hidden %zu, inter %zu, %zu experts)",
+                h.dtype, h.hidden, h.inter, h.num_experts, m->dtype, m->H, m->I, m->E);
+  const size_t need = 2 * m->I * (size_t)hale_row_bytes(m->dtype, m->H) +
+                      m->H * (size_t)hale_row_bytes(m->dtype, m->I);
+  if (h.record_bytes != need)
+    return fail(c, HALE_EPACK, "record is %zu bytes, expected %zu", h.record_bytes, need);
+  uint64_t off0 = 0;
+  std::string err;
+  if (!hale::pack_offset_of(h, m->layer, 0, &off0, &err)) return fail(c, HALE_EPACK, "%s", err.c_str());
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  if (!p->ctx) {  // first load: bind the pack to this context's device
+    HIPCHK(c, hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking));
+    for (int s = 0; s < 2; s++) HIPCHK(c, hipEventCreateWithFlags(&p->copied[s], hipEventDisableTiming));
+    p->ctx = c;
+    p->device = c->device;
+  }
+  int rc = moe_wait_load(m);  // this layer's previous load
+  if (rc) return rc;
+  if (p->load) p->load->join();  // the pack's previous load (its layer keeps the result)
+  // batches of about 64 MiB of records
+  const size_t batch = std::max<size_t>(1, std::min<size_t>(m->E, (size_t(64) << 20) / h.record_stride));
+  const size_t slot = batch * h.record_stride;
+  if (p->slot_bytes < slot) {
+    HIPCHK(c, hipStreamSynchronize(p->stream));
+    pack_free_staging(p);
+    for (int s = 0; s < 2; s++)
+      if (hipHostMalloc(&p->pinned[s], slot, hipHostMallocDefault) != hipSuccess ||
+          hipMalloc(&p->dstage[s], slot) != hipSuccess) {
+        pack_free_staging(p);
+        return fail(c, HALE_ENOMEM, "pack staging: 2 x %zu bytes", slot);
+      }
+    p->slot_bytes = slot;
+  }
+  if (!m->loaded) HIPCHK(c, hipEventCreateWithFlags(&m->loaded, hipEventDisableTiming));
+  auto L = std::make_shared<hale::PackLoad>();
+  try {
+    L->th = std::thread(pack_loader, p, m, L.get(), off0, batch);
+  } catch (...) {
+    return fail(c, HALE_ENOMEM, "cannot start the pack loader thread");
+  }
+  p->load = L;
+  m->load = L;
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_load_pack(hale_moe* m, hale_pack* p) {
+  int rc = hale_moe_prefetch_pack(m, p);
+  if (rc) return rc;
+  hale_ctx* c = m->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  rc = moe_wait_load(m);
+  if (rc) return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" void hale_pack_close(hale_pack* p) {
+  if (!p) return;
+  if (hale_ctx* c = p->ctx) {
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    if (p->load) p->load->join();
+    p->load.reset();
+    (void)hipSetDevice(p->device);
+    (void)hipStreamSynchronize(p->stream);
+    pack_free_staging(p);
+    for (int s = 0; s < 2; s++)
+      if (p->copied[s]) (void)hipEventDestroy(p->copied[s]);
+    (void)hipStreamDestroy(p->stream);
+  }
+  if (p->fd >= 0) ::close(p->fd);
+  delete p;
 }
 
 // ---------------------------------------------------------------------------

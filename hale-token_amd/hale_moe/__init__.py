@@ -35,7 +35,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libhale_moe.so")
 F32, F16, BF16, Q8_0, Q4_0 = 0, 1, 2, 3, 4
 QK = 32
 _NAMES = {"f32": F32, "f16": F16, "bf16": BF16, "q8_0": Q8_0, "q8": Q8_0, "q4_0": Q4_0, "q4": Q4_0}
-OK, EINVAL, EHIP, ENOMEM, ENOTFOUND = 0, 1, 2, 3, 4
+OK, EINVAL, EHIP, ENOMEM, ENOTFOUND, EIO, EPACK = 0, 1, 2, 3, 4, 5, 6
 
 _vp = C.c_void_p
 _fp = C.POINTER(C.c_float)
@@ -77,6 +77,16 @@ SIGNATURES = {
     "hale_moe_forward_device": (C.c_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "hale_moe_set_experts_device": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _vp, _vp, _vp]),
     "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
+    "hale_pack_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "hale_pack_close": (None, [_vp]),
+    "hale_pack_info": (C.c_int, [_vp, C.POINTER(C.c_int), C.POINTER(_sz), C.POINTER(_sz),
+                                 C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz),
+                                 C.POINTER(_sz)]),
+    "hale_pack_moe_layer": (C.c_int, [_vp, _sz, _u32p]),
+    "hale_pack_offset_of": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _u64p]),
+    "hale_pack_read_expert": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _vp, _sz]),
+    "hale_moe_load_pack": (C.c_int, [_vp, _vp]),
+    "hale_moe_prefetch_pack": (C.c_int, [_vp, _vp]),
     "hale_device_malloc": (C.c_int, [_vp, _sz, C.POINTER(_vp)]),
     "hale_device_free": (C.c_int, [_vp, _vp]),
     "hale_memcpy_htod": (C.c_int, [_vp, _vp, _vp, _sz]),
@@ -101,6 +111,25 @@ _LIB = None
 
 class HaleError(RuntimeError):
     """A runtime failure reported by the library (HaleError in the reference)."""
+
+
+class InvalidArgument(HaleError):
+    """HaleError::InvalidArgument / Json (src/error.rs): a file that is not a
+    valid expert pack, or a key outside it."""
+
+
+def _raise(rc: int, msg: str):
+    if rc == EINVAL:
+        raise ValueError(msg)
+    if rc == ENOTFOUND:
+        raise KeyError(msg)
+    if rc == ENOMEM:
+        raise MemoryError(msg)
+    if rc == EIO:
+        raise OSError(msg)
+    if rc == EPACK:
+        raise InvalidArgument(msg)
+    raise HaleError(msg)
 
 
 def lib():
@@ -168,13 +197,7 @@ class Context:
         msg = lib().hale_last_error(self.handle).decode()
         if what:
             msg = f"{what}: {msg}"
-        if rc == EINVAL:
-            raise ValueError(msg)
-        if rc == ENOTFOUND:
-            raise KeyError(msg)
-        if rc == ENOMEM:
-            raise MemoryError(msg)
-        raise HaleError(msg)
+        _raise(rc, msg)
 
     @property
     def stream(self) -> int:
@@ -512,6 +535,103 @@ class HbmExpertProvider:
         return {ExpertKey(self._layer.layer, e): int(v) for e, v in enumerate(c) if v}
 
 
+@dataclass(frozen=True)
+class PackHeader:
+    """PackHeader (src/expert/pack.rs:55-73)."""
+
+    version: int
+    dtype: int
+    hidden_size: int
+    intermediate_size: int
+    num_experts: int
+    moe_layers: tuple
+    record_bytes: int
+    record_stride: int
+    data_offset: int
+
+    def file_size(self) -> int:
+        """PackHeader::file_size (src/expert/pack.rs:96-99)."""
+        return self.data_offset + len(self.moe_layers) * self.num_experts * self.record_stride
+
+
+def _check_free(rc: int, what: str):
+    """Status of a context-free call (message from hale_last_error(NULL))."""
+    if rc != OK:
+        _raise(rc, f"{what}: {lib().hale_last_error(None).decode()}")
+
+
+class PackExpertSource:
+    """Reads experts from a Hale expert pack (src/expert/pack.rs:200-275):
+    the file tier under the HBM tier.  MoeLayer.load_pack / prefetch_pack
+    make a whole layer resident from it."""
+
+    def __init__(self, handle, path: str):
+        self.handle, self.path = handle, path
+        dt, h, i, e, nl, rb, rs, do = (C.c_int(), _sz(), _sz(), _sz(), _sz(), _sz(), _sz(), _sz())
+        _check_free(lib().hale_pack_info(handle, C.byref(dt), C.byref(h), C.byref(i), C.byref(e),
+                                         C.byref(nl), C.byref(rb), C.byref(rs), C.byref(do)),
+                    "pack header")
+        layers = []
+        for o in range(nl.value):
+            v = C.c_uint32()
+            _check_free(lib().hale_pack_moe_layer(handle, o, C.byref(v)), "pack header")
+            layers.append(int(v.value))
+        self.header = PackHeader(1, dt.value, h.value, i.value, e.value, tuple(layers), rb.value,
+                                 rs.value, do.value)
+
+    @classmethod
+    def open(cls, path) -> "PackExpertSource":
+        """PackExpertSource::open (src/expert/pack.rs:207-249): InvalidArgument
+        for a file that is not a pack, OSError when it cannot be read."""
+        h = _vp()
+        _check_free(lib().hale_pack_open(os.fsencode(str(path)), C.byref(h)), "open pack")
+        return cls(h, str(path))
+
+    def offset_of(self, key: "ExpertKey") -> int:
+        """PackHeader::offset_of (src/expert/pack.rs:104-123)."""
+        off = C.c_uint64()
+        _check_free(lib().hale_pack_offset_of(self.handle, key.layer, key.expert, C.byref(off)),
+                    "offset_of")
+        return int(off.value)
+
+    def read_record(self, key: "ExpertKey"):
+        """The record of `key` as (gate, up, down) byte arrays in the pack
+        dtype (ExpertSource::load before decode_record)."""
+        h = self.header
+        buf = np.zeros(h.record_bytes, dtype=np.uint8)
+        _check_free(lib().hale_pack_read_expert(self.handle, key.layer, key.expert,
+                                                buf.ctypes.data_as(_vp), buf.size), "load")
+        proj = h.intermediate_size * row_bytes(h.dtype, h.hidden_size)
+        return buf[:proj], buf[proj:2 * proj], buf[2 * proj:]
+
+    def load(self, ctx: "Context", key: "ExpertKey") -> "Expert":
+        """ExpertSource::load (src/expert/pack.rs:252-260): the expert's three
+        matrices, uploaded to the context's device."""
+        h = self.header
+        g, u, d = self.read_record(key)
+        I, H = h.intermediate_size, h.hidden_size
+        return Expert(WeightMatrix.new(ctx, I, H, h.dtype, g), WeightMatrix.new(ctx, I, H, h.dtype, u),
+                      WeightMatrix.new(ctx, H, I, h.dtype, d))
+
+    def expert_bytes(self) -> int:
+        return self.header.record_bytes
+
+    def describe(self) -> str:
+        names = {v: k for k, v in _NAMES.items() if k not in ("q8", "q4")}
+        return f"SSD pack {self.path} ({names.get(self.header.dtype, self.header.dtype)})"
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().hale_pack_close(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class MoeLayer:
     """Router plus HBM-resident experts (src/model/moe.rs:25-70)."""
 
@@ -560,6 +680,20 @@ class MoeLayer:
                                                          _vp(d_up), _vp(d_down)), "set_experts")
         for e in range(first, first + count):
             self._present[e] = True
+
+    def load_pack(self, pack: PackExpertSource):
+        """Makes every expert of this layer resident from the pack (all
+        records of the layer, read and uploaded before returning)."""
+        self.ctx.adopt(pack)  # a bound pack closes before its context
+        self.ctx.check(lib().hale_moe_load_pack(self.handle, pack.handle), "load_pack")
+        self._present = [True] * self.num_experts
+
+    def prefetch_pack(self, pack: PackExpertSource):
+        """Starts loading this layer's experts from the pack and returns; the
+        layer's next use waits for the load (and raises its error)."""
+        self.ctx.adopt(pack)
+        self.ctx.check(lib().hale_moe_prefetch_pack(self.handle, pack.handle), "prefetch_pack")
+        self._present = [True] * self.num_experts
 
     def forward_device(self, ntok: int, d_x: int, d_out: int, d_logits: int = 0,
                        d_index: int = 0, d_weight: int = 0):

@@ -43,7 +43,11 @@ typedef enum {
   HALE_EINVAL = 1,   /* bad shape, dtype, length or argument            */
   HALE_EHIP = 2,     /* HIP runtime error (message in hale_last_error)  */
   HALE_ENOMEM = 3,   /* device or host allocation failed                */
-  HALE_ENOTFOUND = 4 /* expert not registered (ExpertProvider::fetch)   */
+  HALE_ENOTFOUND = 4, /* expert not registered (ExpertProvider::fetch)  */
+  HALE_EIO = 5,       /* file I/O failed (HaleError::Io)                 */
+  HALE_EPACK = 6      /* not a valid expert pack, or a key outside it
+                         (HaleError::InvalidArgument / Json from
+                         src/expert/pack.rs)                              */
 } hale_status;
 
 /* Element formats.  Ref: DType (src/tensor/dtype.rs:15-25), same order. */
@@ -60,6 +64,7 @@ typedef enum {
 typedef struct hale_ctx hale_ctx;       /* device + stream + scratch      */
 typedef struct hale_matrix hale_matrix; /* Ref: WeightMatrix              */
 typedef struct hale_moe hale_moe;       /* Ref: MoeLayer + its provider   */
+typedef struct hale_pack hale_pack;     /* Ref: PackExpertSource          */
 
 /* ---- context --------------------------------------------------------- */
 
@@ -69,7 +74,8 @@ int hale_ctx_create(int device, hale_ctx **out);
  * must be destroyed first. */
 void hale_ctx_destroy(hale_ctx *ctx);
 /* Message of the last failed call on ctx ("" if none).  NULL ctx gives the
- * message of the last failed hale_ctx_create in this thread. */
+ * message of the last failed hale_ctx_create or hale_pack_* call in this
+ * thread. */
 const char *hale_last_error(const hale_ctx *ctx);
 /* The hipStream_t the context enqueues on (for the _device entry points). */
 void *hale_ctx_stream(hale_ctx *ctx);
@@ -202,6 +208,56 @@ int hale_moe_set_experts_device(hale_moe *moe, uint32_t first, uint32_t count,
  * RoutingStats::count (src/expert/stats.rs:53-55): selections per expert
  * of this layer since creation.  counts[num_experts]. */
 int hale_moe_routing_counts(hale_moe *moe, uint64_t *counts);
+
+/* ---- expert pack: the file tier under the HBM tier ------------------ */
+
+/* Opens a Hale expert pack ("HALEPACK" magic, u64 LE header length, JSON
+ * PackHeader, records gate|up|down at a fixed stride from data_offset).
+ * Rejects, with HALE_EPACK, what PackExpertSource::open rejects: a wrong
+ * magic, a header longer than 64 x 16 KiB, unparsable JSON, a version other
+ * than 1, a file shorter than data_offset + layers x experts x stride.
+ * Ref: PackExpertSource::open (src/expert/pack.rs:207-249), PackHeader
+ * (:55-73).  The hale_pack_* calls take no context: their failures are
+ * reported by hale_last_error(NULL) in the calling thread.  The first load
+ * into a layer binds the pack to that layer's context, on whose device it
+ * then uploads through its own HIP stream. */
+int hale_pack_open(const char *path, hale_pack **out);
+/* Waits for a load in progress, then closes the file. */
+void hale_pack_close(hale_pack *pack);
+/* PackHeader fields (any output may be NULL). */
+int hale_pack_info(const hale_pack *pack, int *dtype, size_t *hidden,
+                   size_t *inter, size_t *num_experts, size_t *num_moe_layers,
+                   size_t *record_bytes, size_t *record_stride,
+                   size_t *data_offset);
+/* Model layer index of the pack's `ordinal`-th MoE layer (file order). */
+int hale_pack_moe_layer(const hale_pack *pack, size_t ordinal,
+                        uint32_t *layer);
+/* Byte offset of (layer, expert)'s record; HALE_EPACK for a layer without
+ * experts in the pack or an expert out of range.  Ref: PackHeader::offset_of
+ * (src/expert/pack.rs:104-123). */
+int hale_pack_offset_of(const hale_pack *pack, uint32_t layer,
+                        uint32_t expert, uint64_t *offset);
+/* Reads one record (record_bytes: gate | up | down in the pack dtype) into
+ * host memory with a positioned read.  Ref: ExpertSource::load for
+ * PackExpertSource (src/expert/pack.rs:252-260). */
+int hale_pack_read_expert(hale_pack *pack, uint32_t layer, uint32_t expert,
+                          void *buf, size_t nbytes);
+
+/* HBM tier from the pack: makes every expert of moe's layer resident.  The
+ * pack's dtype and shapes must match the layer (HALE_EINVAL otherwise; a
+ * layer missing from the pack is HALE_EPACK).  hale_moe_prefetch_pack
+ * returns at once: a loader thread reads the layer's records (one large
+ * sequential read per batch into pinned host buffers) and uploads and
+ * repacks them on the pack's stream, so the layer's experts arrive while
+ * other layers compute.  The layer's next use (forward, set_expert, load
+ * or destroy) waits for the load and reports its error.  One load per
+ * pack at a time: a second prefetch on the same pack waits for the first
+ * load's reads.  hale_moe_load_pack is the synchronous form.  Ref: the
+ * ExpertCache miss path (src/expert/cache.rs:124-194) over
+ * PackExpertSource, and roadmap item 2 (prefetch the next layer's
+ * experts, docs/roadmap.md:13-16). */
+int hale_moe_load_pack(hale_moe *moe, hale_pack *pack);
+int hale_moe_prefetch_pack(hale_moe *moe, hale_pack *pack);
 
 /* ---- support entry points -------------------------------------------
  * No counterpart in the reference: device memory, timing and graph capture
