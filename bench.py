@@ -17,6 +17,9 @@ WRITE_SIZE counter passes, each scaled by what the counter reads for the
 plain copy kernel, as committed in profiles/traffic_decode_q4_qwen3_30b.txt.
 cpu_baseline: the oracle (C restatement of the reference CPU algorithm)
 on one layer of the same shape, on this host's cores.
+decode_more: Mixtral-8x7B- and Qwen3-235B-shaped decode layers, same timing.
+float_matvec: WeightMatrix::matvec over float weights (a bf16 vocabulary
+projection and a dense f32 matrix), GB/s of weight bytes.
 prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
 2048 tokens q4_0 H 4096 I 1536; 128 experts, top-8, Zipf-skewed routing)
 with tokens/s, TOPS and the fraction of the int8 MFMA peak.
@@ -252,6 +255,70 @@ def gpu_decode_more(name, dtype, hid, inter, experts, topk, nlayers, reps=20):
             "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
 
 
+# (workload, dtype, rows, cols, distinct copies rotated so the weights stay cold)
+FLOAT_MATVEC = [
+    ("lm_head bf16 [151936 x 2048] (Qwen3 vocabulary)", H.BF16, 151936, 2048, 2),
+    ("dense f32 [4096 x 4096]", H.F32, 4096, 4096, 8),
+]
+
+
+def gpu_float_matvec(name, dtype, rows, cols, copies, reps=20):
+    """WeightMatrix::matvec over float weights, the 8-lane dot of the
+    reference; GB/s of weight bytes, graph-replayed over `copies` distinct
+    matrices visited in turn."""
+    ctx = H.Context(0)
+    nbytes = rows * H.row_bytes(dtype, cols)
+    vals = ctx.malloc(rows * cols * 4)
+    enc = ctx.malloc(nbytes)
+    mats = []
+    for c in range(copies):
+        vals.fill_normal(900 + c, rows * cols, 0.0, 0.02)
+        ctx.check(H.lib().hale_encode_rows_device(ctx.handle, dtype, rows, cols, H._vp(vals.address),
+                                                  H._vp(enc.address)), "encode")
+        h = H._vp()
+        ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, dtype, rows, cols, H._vp(enc.address),
+                                                    nbytes, H.C.byref(h)), "upload")
+        mats.append(H.WeightMatrix(ctx, h, rows, cols, dtype))
+    enc.free()
+    vals.free()
+    x = ctx.malloc(cols * 4)
+    x.fill_normal(5, cols, 0.0, 1.0)
+    out = ctx.malloc(rows * 4)
+
+    def step(s):
+        ctx.check(H.lib().hale_matvec_device(ctx.handle, mats[s % copies].handle, H._vp(x.address),
+                                             H._vp(out.address)), "matvec")
+
+    for s in range(2 * copies):
+        step(s)
+    ctx.synchronize()
+    graph = ctx.capture(lambda: [step(s) for s in range(copies)])
+    graph.launch()
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        graph.launch()
+    ms = ctx.timer_stop()
+    ctx.profile(True)
+    ctx.profile_reset()
+    for s in range(2 * copies):
+        step(s)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    graph.close()
+    for m in mats:
+        m.close()
+    ctx.close()
+    us = 1000 * ms / (reps * copies)
+    k = prof.get("gemv")
+    kus = 1000 * k[0] / k[1] if k else None
+    return {"workload": name, "bytes_per_call": nbytes, "us_per_call": round(us, 2),
+            "GB_per_s": round(nbytes / us / 1e3, 1),
+            "pct_hbm_peak": round(100 * nbytes / us / 1e3 / HBM_PEAK_GBS, 2),
+            "kernel_avg_us": round(kus, 2) if kus else None,
+            "kernel_GB_per_s": round(nbytes / kus / 1e3, 1) if kus else None}
+
+
 def gpu_decode(args):
     ctx = H.Context(0)
     t0 = time.time()
@@ -370,6 +437,12 @@ def main():
             more.append(gpu_decode_more(name, dt, hid, inter, ex, k, nl))
             log(f"decode {name}: {more[-1]['us_per_step']} us/step, {more[-1]['GB_per_s']} GB/s")
 
+    fmv = []
+    if not args.no_prefill:
+        for (name, dt, rows, cols, copies) in FLOAT_MATVEC:
+            fmv.append(gpu_float_matvec(name, dt, rows, cols, copies))
+            log(f"matvec {name}: {fmv[-1]['us_per_call']} us, {fmv[-1]['GB_per_s']} GB/s")
+
     prefill = []
     if not args.no_prefill:
         for (name, dt, hid, inter, ex, k, tok) in PREFILL:
@@ -413,6 +486,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "decode_more": more,
+        "float_matvec": fmv,
         "prefill": prefill,
         "cpu_baseline": cpu,
     }

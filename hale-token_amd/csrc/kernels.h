@@ -118,6 +118,12 @@ hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* ac
                              size_t cols, int32_t* isums, hipStream_t st);
 hipError_t launch_fill(float* p, size_t n, float v, hipStream_t st);
 hipError_t launch_copy(void* dst, const void* src, size_t n16, hipStream_t st);
+// out[rows] = W x for row-major f32 / f16 / bf16 W [rows][cols] (x 16-byte
+// aligned), in the reference's 8-lane dot order.
+hipError_t launch_gemv_float(int dtype, const void* w, const float* x, size_t rows, size_t cols,
+                             float* out, hipStream_t st);
+// values[n] -> f16 / bf16 bits (half's from_f32)
+hipError_t launch_encode_half(int dtype, const float* values, size_t n, void* out, hipStream_t st);
 hipError_t launch_fill_normal(float* p, size_t n, uint64_t seed, float mean, float std,
                               hipStream_t st);
 

@@ -66,7 +66,7 @@ struct hale_matrix {
   size_t rows = 0, cols = 0;
   uint8_t* codes = nullptr;    // quantized: tile planes
   uint16_t* scales = nullptr;
-  float* f32 = nullptr;        // F32: row-major copy
+  uint8_t* raw = nullptr;      // f32 / f16 / bf16: the row-major bytes as given
 };
 
 struct hale_moe {
@@ -309,8 +309,8 @@ static int matrix_create(hale_ctx* c, int dtype, size_t rows, size_t cols, const
                          size_t nbytes, bool on_device, hale_matrix** out) {
   if (!c || !out) return fail(c, HALE_EINVAL, "matrix upload: NULL argument");
   *out = nullptr;
-  if (dtype != HALE_F32 && !quantized(dtype))
-    return fail(c, HALE_EINVAL, "matrix upload: dtype %d not supported (q8_0, q4_0, f32)", dtype);
+  if (dtype < HALE_F32 || dtype > HALE_Q4_0)
+    return fail(c, HALE_EINVAL, "matrix upload: unknown dtype %d", dtype);
   long long rb = hale_row_bytes(dtype, cols);
   if (rb < 0) return fail(c, HALE_EINVAL, "dtype %d needs row length divisible by 32, got %zu", dtype, cols);
   if (nbytes != rows * (size_t)rb)
@@ -327,15 +327,15 @@ static int matrix_create(hale_ctx* c, int dtype, size_t rows, size_t cols, const
   m->rows = rows;
   m->cols = cols;
   hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-  if (dtype == HALE_F32) {
-    if (hipMalloc(&m->f32, nbytes) != hipSuccess) {
+  if (!quantized(dtype)) {
+    if (hipMalloc(&m->raw, nbytes) != hipSuccess) {
       delete m;
       return fail(c, HALE_ENOMEM, "device allocation of %zu bytes", nbytes);
     }
-    hipError_t e = hipMemcpyAsync(m->f32, bytes, nbytes, kind, c->stream);
+    hipError_t e = hipMemcpyAsync(m->raw, bytes, nbytes, kind, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
-      (void)hipFree(m->f32);
+      (void)hipFree(m->raw);
       delete m;
       return fail(c, HALE_EHIP, "upload: %s", hipGetErrorString(e));
     }
@@ -389,7 +389,7 @@ extern "C" void hale_matrix_destroy(hale_matrix* m) {
   (void)hipStreamSynchronize(m->ctx->stream);
   (void)hipFree(m->codes);
   (void)hipFree(m->scales);
-  (void)hipFree(m->f32);
+  (void)hipFree(m->raw);
   delete m;
 }
 
@@ -407,8 +407,8 @@ extern "C" int hale_matrix_download(hale_ctx* c, const hale_matrix* m, void* byt
   if (nbytes != need) return fail(c, HALE_EINVAL, "matrix download needs %zu bytes, got %zu", need, nbytes);
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
-  if (m->dtype == HALE_F32) {
-    HIPCHK(c, hipMemcpyAsync(bytes, m->f32, nbytes, hipMemcpyDeviceToHost, c->stream));
+  if (!quantized(m->dtype)) {
+    HIPCHK(c, hipMemcpyAsync(bytes, m->raw, nbytes, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return HALE_OK;
   }
@@ -452,9 +452,23 @@ extern "C" int hale_quantize_q8_act(hale_ctx* c, const float* x, size_t n, float
 }
 
 static int encode_check(hale_ctx* c, int dtype, size_t rows, size_t cols) {
-  if (!quantized(dtype)) return fail(c, HALE_EINVAL, "encode: dtype %d is not q8_0/q4_0", dtype);
-  if (cols % HALE_QK) return fail(c, HALE_EINVAL, "encode: row length %zu not a multiple of 32", cols);
+  if (dtype < HALE_F32 || dtype > HALE_Q4_0) return fail(c, HALE_EINVAL, "encode: unknown dtype %d", dtype);
+  if (quantized(dtype) && cols % HALE_QK)
+    return fail(c, HALE_EINVAL, "encode: row length %zu not a multiple of 32", cols);
   (void)rows;
+  return HALE_OK;
+}
+
+// Enqueues encode_row over rows x cols device values into d_bytes.
+static int encode_enqueue(hale_ctx* c, int dtype, size_t rows, size_t cols, const float* dv,
+                          void* db) {
+  if (dtype == HALE_F32) {
+    if (rows * cols) HIPCHK(c, hipMemcpyAsync(db, dv, rows * cols * 4, hipMemcpyDeviceToDevice, c->stream));
+  } else if (!quantized(dtype)) {
+    LAUNCH(c, K_ENCODE, launch_encode_half(dtype, dv, rows * cols, db, c->stream));
+  } else {
+    LAUNCH(c, K_ENCODE, launch_encode(dtype, dv, rows * (cols / HALE_QK), (uint8_t*)db, c->stream));
+  }
   return HALE_OK;
 }
 
@@ -465,8 +479,7 @@ extern "C" int hale_encode_rows_device(hale_ctx* c, int dtype, size_t rows, size
   if (rc) return rc;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
-  LAUNCH(c, K_ENCODE, launch_encode(dtype, d_values, rows * (cols / HALE_QK), (uint8_t*)d_bytes, c->stream));
-  return HALE_OK;
+  return encode_enqueue(c, dtype, rows, cols, d_values, d_bytes);
 }
 
 extern "C" int hale_encode_rows(hale_ctx* c, int dtype, size_t rows, size_t cols,
@@ -484,7 +497,8 @@ extern "C" int hale_encode_rows(hale_ctx* c, int dtype, size_t rows, size_t cols
   float* dv = (float*)s;
   uint8_t* db = (uint8_t*)s + align_up(nin, 256);
   HIPCHK(c, hipMemcpyAsync(dv, values, nin, hipMemcpyHostToDevice, c->stream));
-  LAUNCH(c, K_ENCODE, launch_encode(dtype, dv, rows * (cols / HALE_QK), db, c->stream));
+  rc = encode_enqueue(c, dtype, rows, cols, dv, db);
+  if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync(bytes, db, nout, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   return HALE_OK;
@@ -506,12 +520,16 @@ static GemvArgs plain_args(const hale_matrix* m, const ActBlock* act, float* out
   return a;
 }
 
-// Enqueues out = m x for device x/out.  F32 matrices use the router kernel's
-// 8-lane dot (one work-group per row, logits-only mode is not needed here).
+// Enqueues out = m x for device x/out: float matrices through the 8-lane
+// float GEMV, quantized ones through activation quantization and the tile
+// GEMV.
 static int matvec_enqueue(hale_ctx* c, const hale_matrix* m, const float* dx, float* dout,
                           ActBlock* act) {
-  if (m->dtype == HALE_F32)
-    return fail(c, HALE_EINVAL, "matvec on f32 matrices is not part of the quantized path");
+  if (!quantized(m->dtype)) {
+    if ((uintptr_t)dx % 16) return fail(c, HALE_EINVAL, "matvec: x must be 16-byte aligned");
+    LAUNCH(c, K_GEMV, launch_gemv_float(m->dtype, m->raw, dx, m->rows, m->cols, dout, c->stream));
+    return HALE_OK;
+  }
   size_t nb = m->cols / HALE_QK;
   LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nb, act, c->stream));
   GemvArgs a = plain_args(m, act, dout);
@@ -708,7 +726,7 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
 #undef ALLOC
   if (e == hipSuccess) e = hipMemsetAsync(m->stats, 0, E * 8, c->stream);
   if (e == hipSuccess && router)
-    e = hipMemcpyAsync(m->router, router->f32, E * H * 4, hipMemcpyDeviceToDevice, c->stream);
+    e = hipMemcpyAsync(m->router, router->raw, E * H * 4, hipMemcpyDeviceToDevice, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) {
     hale_moe_destroy(m);

@@ -92,8 +92,10 @@ size_t hale_block_bytes(int dtype);
 /* ---- weight matrices ------------------------------------------------- */
 
 /* Ref: WeightMatrix::new (src/tensor/matrix.rs:19-47).  `bytes` holds
- * rows x row_bytes(cols) bytes in the reference layout (host memory).
- * Supported dtypes: Q8_0, Q4_0 (expert weights) and F32 (router). */
+ * rows x row_bytes(cols) bytes in the reference layout (host memory), in
+ * any dtype: Q8_0 / Q4_0 are repacked into the tile layout, F32 / F16 /
+ * BF16 stay row-major as given (dense weights such as attention
+ * projections, the lm_head, the router). */
 int hale_matrix_upload(hale_ctx *ctx, int dtype, size_t rows, size_t cols,
                        const void *bytes, size_t nbytes, hale_matrix **out);
 /* Same, with the reference-layout bytes already in device memory (for
@@ -116,9 +118,11 @@ int hale_matrix_download(hale_ctx *ctx, const hale_matrix *m, void *bytes,
  * scales[n/32] (f32, not rounded to f16), quants[n]. */
 int hale_quantize_q8_act(hale_ctx *ctx, const float *x, size_t n,
                          float *scales, int8_t *quants);
-/* Ref: encode_row for Q8_0 / Q4_0 (src/tensor/quant.rs:274-321), applied to
- * each row of a row-major rows x cols f32 matrix (WeightMatrix::from_f32,
- * src/tensor/matrix.rs:48-61).  Host buffers; bytes gets rows*row_bytes. */
+/* Ref: encode_row (src/tensor/quant.rs:274-321), applied to each row of a
+ * row-major rows x cols f32 matrix (WeightMatrix::from_f32,
+ * src/tensor/matrix.rs:48-61): Q8_0 / Q4_0 blocks, F16 / BF16 rounded to
+ * nearest even (half's from_f32), F32 copied.  Host buffers; bytes gets
+ * rows*row_bytes. */
 int hale_encode_rows(hale_ctx *ctx, int dtype, size_t rows, size_t cols,
                      const float *values, void *bytes);
 int hale_encode_rows_device(hale_ctx *ctx, int dtype, size_t rows,
@@ -129,9 +133,14 @@ int hale_encode_rows_device(hale_ctx *ctx, int dtype, size_t rows,
 
 /* Ref: WeightMatrix::matvec (src/tensor/matrix.rs:115-126) and
  * matvec_serial (:130-143), which return identical bits.  xlen must equal
- * cols and outlen rows (the reference asserts both). */
+ * cols and outlen rows (the reference asserts both).  Quantized matrices:
+ * x is quantized once, then dot_q8_0 / dot_q4_0 per row (quant.rs:
+ * 115-144).  Float matrices: dot_f32 / dot_decoded per row (quant.rs:
+ * 146-233: eight lane accumulators, the fixed reduce, then the tail). */
 int hale_matvec(hale_ctx *ctx, const hale_matrix *m, const float *x,
                 size_t xlen, float *out, size_t outlen);
+/* Same on device buffers (d_x 16-byte aligned for float matrices),
+ * enqueued on the context's stream. */
 int hale_matvec_device(hale_ctx *ctx, const hale_matrix *m, const float *d_x,
                        float *d_out);
 /* The per-block i32 sums of dot_q8_0 / dot_q4_0 (src/tensor/quant.rs:
