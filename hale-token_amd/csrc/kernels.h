@@ -122,6 +122,34 @@ hipError_t launch_copy(void* dst, const void* src, size_t n16, hipStream_t st);
 // aligned), in the reference's 8-lane dot order.
 hipError_t launch_gemv_float(int dtype, const void* w, const float* x, size_t rows, size_t cols,
                              float* out, hipStream_t st);
+// out[r] = rms_norm(x[r] (+ delta[r], stored back into x), w) for each of
+// `rows` rows of n values (n <= 8192)
+hipError_t launch_rms_norm(float* x, const float* delta, const float* w, size_t rows, size_t n,
+                           float eps, float* out, hipStream_t st);
+
+// One token of grouped-query attention after the q/k/v projections: QK-norm
+// and RoPE of q and k, k/v pushed to the cache at row seq - 1, scores,
+// softmax and the context.  keys/values are [ld][nkv*hd] f32, scores
+// [nh][ld], ctx [nh*hd].
+struct AttnArgs {
+  float* q;            // [nh*hd], normalised and rotated in place
+  const float* k;      // [nkv*hd] projection output
+  const float* v;      // [nkv*hd]
+  int nh, nkv, hd;
+  const float* q_norm;  // [hd] or null
+  const float* k_norm;  // [hd] or null
+  float eps;
+  const float* cos;     // [hd/2]
+  const float* sin;
+  float* keys;
+  float* values;
+  int seq;              // positions after the push (position + 1)
+  int ld;               // cache capacity (rows of keys/values, row stride of scores)
+  float* scores;
+  float* ctx;
+};
+hipError_t launch_attention_core(const AttnArgs& a, hipStream_t st);
+
 // values[n] -> f16 / bf16 bits (half's from_f32)
 hipError_t launch_encode_half(int dtype, const float* values, size_t n, void* out, hipStream_t st);
 hipError_t launch_fill_normal(float* p, size_t n, uint64_t seed, float mean, float std,
@@ -142,6 +170,8 @@ enum KernelKind : int {
   K_GROUPED_DOWN,
   K_COMBINE,
   K_COPY,
+  K_NORM,
+  K_ATTENTION,
   K_KINDS
 };
 

@@ -1206,6 +1206,201 @@ extern "C" void hale_pack_close(hale_pack* p) {
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm and attention (the steps on either side of the MoE block)
+// ---------------------------------------------------------------------------
+
+extern "C" int hale_rms_norm_device(hale_ctx* c, float* d_x, const float* d_delta,
+                                    const float* d_weight, size_t rows, size_t n, float eps,
+                                    float* d_out) {
+  if (!c || !d_x || !d_weight || !d_out) return fail(c, HALE_EINVAL, "rms_norm: NULL argument");
+  if (n == 0 || n > 8192) return fail(c, HALE_EINVAL, "rms_norm: length %zu outside 1..8192", n);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  LAUNCH(c, K_NORM, launch_rms_norm(d_x, d_delta, d_weight, rows, n, eps, d_out, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_rms_norm(hale_ctx* c, const float* x, const float* weight, size_t n, float eps,
+                             float* out) {
+  if (!c || !x || !weight || !out) return fail(c, HALE_EINVAL, "rms_norm: NULL argument");
+  if (n == 0 || n > 8192) return fail(c, HALE_EINVAL, "rms_norm: length %zu outside 1..8192", n);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t b = align_up(n * 4, 256);
+  void* s;
+  int rc = ctx_scratch(c, 3 * b, &s);
+  if (rc) return rc;
+  float* dx = (float*)s;
+  float* dw = (float*)((char*)s + b);
+  float* dout = (float*)((char*)s + 2 * b);
+  HIPCHK(c, hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(dw, weight, n * 4, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_NORM, launch_rms_norm(dx, nullptr, dw, 1, n, eps, dout, c->stream));
+  HIPCHK(c, hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+struct hale_attention {
+  hale_ctx* ctx = nullptr;
+  const hale_matrix *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+  size_t H = 0, nh = 0, nkv = 0, hd = 0, max_len = 0, len = 0;
+  float eps = 0.0f;
+  float *q_norm = nullptr, *k_norm = nullptr;  // [hd] device copies, or null
+  float *keys = nullptr, *values = nullptr;    // the layer cache, [max_len][nkv*hd]
+  // per-call buffers: q, k, v, context, scores [nh][max_len], x/cos/sin/out
+  // staging of the host entry point, q8 activation blocks
+  float *dq = nullptr, *dk = nullptr, *dv = nullptr, *dctx = nullptr, *scores = nullptr;
+  float *hx = nullptr, *hcos = nullptr, *hsin = nullptr, *hout = nullptr;
+  ActBlock* act = nullptr;
+};
+
+extern "C" void hale_attention_destroy(hale_attention* a) {
+  if (!a) return;
+  hale_ctx* c = a->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (void* p : {(void*)a->q_norm, (void*)a->k_norm, (void*)a->keys, (void*)a->values, (void*)a->dq,
+                  (void*)a->dk, (void*)a->dv, (void*)a->dctx, (void*)a->scores, (void*)a->hx,
+                  (void*)a->hcos, (void*)a->hsin, (void*)a->hout, (void*)a->act})
+    (void)hipFree(p);
+  delete a;
+}
+
+extern "C" int hale_attention_create(hale_ctx* c, const hale_matrix* q, const hale_matrix* k,
+                                     const hale_matrix* v, const hale_matrix* o,
+                                     const float* q_norm, const float* k_norm, size_t num_heads,
+                                     size_t num_kv_heads, size_t head_dim, float norm_eps,
+                                     size_t max_len, hale_attention** out) {
+  if (!c || !q || !k || !v || !o || !out) return fail(c, HALE_EINVAL, "attention_create: NULL argument");
+  *out = nullptr;
+  const size_t nh = num_heads, nkv = num_kv_heads, hd = head_dim, H = q->cols;
+  if (nh == 0 || nkv == 0 || nh % nkv)
+    return fail(c, HALE_EINVAL, "num_heads %zu must be a positive multiple of num_kv_heads %zu", nh, nkv);
+  if (hd < 4 || hd > 1024 || hd % 4)
+    return fail(c, HALE_EINVAL, "head_dim %zu must be a multiple of 4 in 4..1024", hd);
+  if (max_len == 0 || max_len > (1u << 24)) return fail(c, HALE_EINVAL, "max_len %zu outside 1..2^24", max_len);
+  if (q->rows != nh * hd || k->rows != nkv * hd || v->rows != nkv * hd || k->cols != H ||
+      v->cols != H || o->rows != H || o->cols != nh * hd)
+    return fail(c, HALE_EINVAL, "projection shapes do not match %zu heads x %zu, %zu kv heads, hidden %zu",
+                nh, hd, nkv, H);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  hale_attention* a = new (std::nothrow) hale_attention;
+  if (!a) return fail(c, HALE_ENOMEM, "out of host memory");
+  a->ctx = c;
+  a->q = q;
+  a->k = k;
+  a->v = v;
+  a->o = o;
+  a->H = H;
+  a->nh = nh;
+  a->nkv = nkv;
+  a->hd = hd;
+  a->eps = norm_eps;
+  a->max_len = max_len;
+  const size_t kv_dim = nkv * hd, wide = std::max(H, nh * hd);
+  hipError_t e = hipSuccess;
+#define ALLOC(p, n) \
+  if (e == hipSuccess) e = hipMalloc(&(p), (n))
+  if (q_norm) ALLOC(a->q_norm, hd * 4);
+  if (k_norm) ALLOC(a->k_norm, hd * 4);
+  ALLOC(a->keys, max_len * kv_dim * 4);
+  ALLOC(a->values, max_len * kv_dim * 4);
+  ALLOC(a->dq, nh * hd * 4);
+  ALLOC(a->dk, kv_dim * 4);
+  ALLOC(a->dv, kv_dim * 4);
+  ALLOC(a->dctx, nh * hd * 4);
+  ALLOC(a->scores, nh * max_len * 4);
+  ALLOC(a->hx, H * 4);
+  ALLOC(a->hcos, hd * 2);
+  ALLOC(a->hsin, hd * 2);
+  ALLOC(a->hout, H * 4);
+  ALLOC(a->act, (wide / HALE_QK + 1) * sizeof(ActBlock));
+#undef ALLOC
+  if (e == hipSuccess && q_norm) e = hipMemcpyAsync(a->q_norm, q_norm, hd * 4, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess && k_norm) e = hipMemcpyAsync(a->k_norm, k_norm, hd * 4, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    hale_attention_destroy(a);
+    return fail(c, HALE_ENOMEM, "attention allocation (%zu positions): %s", max_len, hipGetErrorString(e));
+  }
+  *out = a;
+  return HALE_OK;
+}
+
+extern "C" int hale_attention_reset(hale_attention* a) {
+  if (!a) return HALE_EINVAL;
+  std::lock_guard<std::recursive_mutex> g(a->ctx->mu);
+  a->len = 0;
+  return HALE_OK;
+}
+
+extern "C" int hale_attention_len(const hale_attention* a, size_t* len) {
+  if (!a || !len) return HALE_EINVAL;
+  *len = a->len;
+  return HALE_OK;
+}
+
+extern "C" int hale_attention_forward_device(hale_attention* a, const float* d_x, size_t position,
+                                             const float* d_cos, const float* d_sin, float* d_out) {
+  hale_ctx* c = a ? a->ctx : nullptr;
+  if (!a || !d_x || !d_cos || !d_sin || !d_out) return fail(c, HALE_EINVAL, "attention: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  if (position != a->len)
+    return fail(c, HALE_EINVAL, "attention at position %zu, but the cache holds %zu positions", position, a->len);
+  if (position >= a->max_len)
+    return fail(c, HALE_EINVAL, "context overflow: %zu positions needed, the cache holds %zu",
+                position + 1, a->max_len);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = matvec_enqueue(c, a->q, d_x, a->dq, a->act);
+  if (!rc) rc = matvec_enqueue(c, a->k, d_x, a->dk, a->act);
+  if (!rc) rc = matvec_enqueue(c, a->v, d_x, a->dv, a->act);
+  if (rc) return rc;
+  AttnArgs t{};
+  t.q = a->dq;
+  t.k = a->dk;
+  t.v = a->dv;
+  t.nh = (int)a->nh;
+  t.nkv = (int)a->nkv;
+  t.hd = (int)a->hd;
+  t.q_norm = a->q_norm;
+  t.k_norm = a->k_norm;
+  t.eps = a->eps;
+  t.cos = d_cos;
+  t.sin = d_sin;
+  t.keys = a->keys;
+  t.values = a->values;
+  t.seq = (int)position + 1;
+  t.ld = (int)a->max_len;
+  t.scores = a->scores;
+  t.ctx = a->dctx;
+  LAUNCH(c, K_ATTENTION, launch_attention_core(t, c->stream));
+  rc = matvec_enqueue(c, a->o, a->dctx, d_out, a->act);
+  if (rc) return rc;
+  a->len = position + 1;  // LayerCache::push
+  return HALE_OK;
+}
+
+extern "C" int hale_attention_forward(hale_attention* a, const float* x, size_t position,
+                                      const float* cos, const float* sin, float* out) {
+  hale_ctx* c = a ? a->ctx : nullptr;
+  if (!a || !x || !cos || !sin || !out) return fail(c, HALE_EINVAL, "attention: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t half = a->hd / 2;
+  HIPCHK(c, hipMemcpyAsync(a->hx, x, a->H * 4, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(a->hcos, cos, half * 4, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(a->hsin, sin, half * 4, hipMemcpyHostToDevice, c->stream));
+  int rc = hale_attention_forward_device(a, a->hx, position, a->hcos, a->hsin, a->hout);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync(out, a->hout, a->H * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
 // support entry points
 // ---------------------------------------------------------------------------
 
@@ -1339,7 +1534,8 @@ extern "C" int hale_kernel_kinds(void) { return K_KINDS; }
 extern "C" const char* hale_kernel_name(int kind) {
   static const char* names[K_KINDS] = {"route", "gate_up", "down", "act_quant", "gemv", "encode",
                                        "repack", "fill", "group", "grouped_gate_up",
-                                       "grouped_down", "combine", "copy"};
+                                       "grouped_down", "combine", "copy", "rms_norm",
+                                       "attention"};
   return kind >= 0 && kind < K_KINDS ? names[kind] : "";
 }
 

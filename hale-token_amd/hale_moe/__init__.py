@@ -87,6 +87,15 @@ SIGNATURES = {
     "hale_pack_read_expert": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _vp, _sz]),
     "hale_moe_load_pack": (C.c_int, [_vp, _vp]),
     "hale_moe_prefetch_pack": (C.c_int, [_vp, _vp]),
+    "hale_rms_norm": (C.c_int, [_vp, _fp, _fp, _sz, C.c_float, _fp]),
+    "hale_rms_norm_device": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_float, _vp]),
+    "hale_attention_create": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _fp, _fp, _sz, _sz, _sz, C.c_float,
+                                        _sz, C.POINTER(_vp)]),
+    "hale_attention_destroy": (None, [_vp]),
+    "hale_attention_reset": (C.c_int, [_vp]),
+    "hale_attention_len": (C.c_int, [_vp, C.POINTER(_sz)]),
+    "hale_attention_forward": (C.c_int, [_vp, _fp, _sz, _fp, _fp, _fp]),
+    "hale_attention_forward_device": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _vp]),
     "hale_device_malloc": (C.c_int, [_vp, _sz, C.POINTER(_vp)]),
     "hale_device_free": (C.c_int, [_vp, _vp]),
     "hale_memcpy_htod": (C.c_int, [_vp, _vp, _vp, _sz]),
@@ -533,6 +542,73 @@ class HbmExpertProvider:
         """RoutingStats counters of this layer as {ExpertKey: count}."""
         c = self.routing_counts()
         return {ExpertKey(self._layer.layer, e): int(v) for e, v in enumerate(c) if v}
+
+
+def rms_norm(ctx: "Context", x, weight, eps: float, out: np.ndarray | None = None) -> np.ndarray:
+    """rms_norm (src/ops/norm.rs:7-14) on the GPU."""
+    v, w = _f32(x), _f32(weight)
+    if v.size != w.size:
+        raise ValueError("rms_norm: x and weight lengths differ")
+    if out is None:
+        out = np.zeros_like(v)
+    ctx.check(lib().hale_rms_norm(ctx.handle, _p(v, _fp), _p(w, _fp), v.size, eps, _p(out, _fp)),
+              "rms_norm")
+    return out
+
+
+class Attention:
+    """Attention (src/model/attention.rs:11-86) with its layer's KV cache,
+    resident on the GPU.  forward(x, position, cos, sin) appends the token's
+    key and value and returns the block's output."""
+
+    def __init__(self, ctx: "Context", q_proj: "WeightMatrix", k_proj: "WeightMatrix",
+                 v_proj: "WeightMatrix", o_proj: "WeightMatrix", q_norm, k_norm,
+                 num_heads: int, num_kv_heads: int, head_dim: int, norm_eps: float,
+                 max_len: int = 4096):
+        self.ctx = ctx
+        self._mats = (q_proj, k_proj, v_proj, o_proj)  # borrowed by the native object
+        self.hidden = o_proj.rows()
+        self.head_dim = head_dim
+        qn = None if q_norm is None else _f32(q_norm)
+        kn = None if k_norm is None else _f32(k_norm)
+        h = _vp()
+        ctx.check(lib().hale_attention_create(ctx.handle, q_proj.handle, k_proj.handle, v_proj.handle,
+                                              o_proj.handle, None if qn is None else _p(qn, _fp),
+                                              None if kn is None else _p(kn, _fp), num_heads,
+                                              num_kv_heads, head_dim, norm_eps, max_len, C.byref(h)),
+                  "Attention")
+        self.handle = h
+        ctx.adopt(self)
+
+    def __len__(self) -> int:
+        n = _sz()
+        lib().hale_attention_len(self.handle, C.byref(n))
+        return int(n.value)
+
+    def reset(self):
+        self.ctx.check(lib().hale_attention_reset(self.handle), "reset")
+
+    def forward(self, x, position: int, cos, sin, out: np.ndarray | None = None) -> np.ndarray:
+        """Attention::forward (src/model/attention.rs:31-86)."""
+        v, c, s_ = _f32(x), _f32(cos), _f32(sin)
+        if v.size != self.hidden or c.size != self.head_dim // 2 or s_.size != self.head_dim // 2:
+            raise ValueError("attention input lengths")
+        if out is None:
+            out = np.zeros(self.hidden, dtype=np.float32)
+        self.ctx.check(lib().hale_attention_forward(self.handle, _p(v, _fp), position, _p(c, _fp),
+                                                    _p(s_, _fp), _p(out, _fp)), "Attention::forward")
+        return out
+
+    def close(self):
+        if getattr(self, "handle", None) and self.ctx.alive:
+            lib().hale_attention_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 @dataclass(frozen=True)

@@ -268,6 +268,53 @@ int hale_pack_read_expert(hale_pack *pack, uint32_t layer, uint32_t expert,
 int hale_moe_load_pack(hale_moe *moe, hale_pack *pack);
 int hale_moe_prefetch_pack(hale_moe *moe, hale_pack *pack);
 
+/* ---- the steps on either side of the MoE block ------------------------ */
+
+typedef struct hale_attention hale_attention; /* Ref: Attention + LayerCache */
+
+/* Ref: rms_norm (src/ops/norm.rs:7-14): out = x * scale * w with
+ * scale = 1 / sqrt(sum(x^2) / n + eps), the squares summed in order.
+ * n <= 8192. */
+int hale_rms_norm(hale_ctx *ctx, const float *x, const float *weight, size_t n,
+                  float eps, float *out);
+/* Device form over `rows` rows of n values.  With d_delta non-NULL, each row
+ * first becomes x = x + delta, stored back into d_x (add_in_place,
+ * src/model/transformer.rs:197-203, the residual before the next norm).
+ * d_out may equal d_x. */
+int hale_rms_norm_device(hale_ctx *ctx, float *d_x, const float *d_delta,
+                         const float *d_weight, size_t rows, size_t n,
+                         float eps, float *d_out);
+
+/* Ref: Attention (src/model/attention.rs:11-24) with its layer's KV cache
+ * (src/model/kv_cache.rs:9-32), room for max_len positions.  q [heads*hd][H],
+ * k / v [kv_heads*hd][H], o [H][heads*hd] are uploaded matrices of any
+ * dtype, borrowed (they must outlive the attention).  q_norm / k_norm:
+ * QK-norm weights [head_dim] (host memory, copied) or NULL (Mixtral).
+ * head_dim a multiple of 4 up to 1024; heads a multiple of kv_heads. */
+int hale_attention_create(hale_ctx *ctx, const hale_matrix *q_proj,
+                          const hale_matrix *k_proj, const hale_matrix *v_proj,
+                          const hale_matrix *o_proj, const float *q_norm,
+                          const float *k_norm, size_t num_heads,
+                          size_t num_kv_heads, size_t head_dim, float norm_eps,
+                          size_t max_len, hale_attention **out);
+void hale_attention_destroy(hale_attention *attn);
+/* Empties the cache (a new sequence). */
+int hale_attention_reset(hale_attention *attn);
+/* Positions in the cache (the position of the next token). */
+int hale_attention_len(const hale_attention *attn, size_t *len);
+/* Ref: Attention::forward (src/model/attention.rs:31-86) for the token at
+ * `position`, which must equal the cache length: q/k/v projections,
+ * QK-norm and RoPE (rotate-half, cos/sin [head_dim/2] from Rope::angles),
+ * the cache push, scores in order, softmax_in_place, the context in
+ * position order, o projection.  x, out [H].  HALE_EINVAL on a position
+ * other than the cache length or past max_len (ContextOverflow). */
+int hale_attention_forward(hale_attention *attn, const float *x, size_t position,
+                           const float *cos, const float *sin, float *out);
+/* Same on device buffers (d_x 16-byte aligned), enqueued on the stream. */
+int hale_attention_forward_device(hale_attention *attn, const float *d_x,
+                                  size_t position, const float *d_cos,
+                                  const float *d_sin, float *d_out);
+
 /* ---- support entry points -------------------------------------------
  * No counterpart in the reference: device memory, timing and graph capture
  * for benchmarks and tests, so that a caller needs no second HIP runtime. */

@@ -524,6 +524,90 @@ size_t orc_top_k(const float *scores, size_t n, size_t k, uint32_t *index,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Norms, RoPE and attention: src/ops/norm.rs, src/ops/rope.rs,              */
+/* src/model/attention.rs                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* inverse_rms, src/ops/norm.rs:25-28: the squares summed in order
+ * (Iterator::sum, from -0.0), divided by n as f32, then 1 / sqrt(. + eps). */
+static float inverse_rms(const float *x, size_t n, float eps) {
+  float s = -0.0f;
+  for (size_t i = 0; i < n; i++) s = s + x[i] * x[i];
+  const float mean_sq = s / (float)n;
+  return 1.0f / sqrtf(mean_sq + eps);
+}
+
+/* rms_norm, src/ops/norm.rs:7-14: `v * scale * w` associates left. */
+void orc_rms_norm(const float *x, const float *w, size_t n, float eps, float *out) {
+  const float scale = inverse_rms(x, n, eps);
+  for (size_t i = 0; i < n; i++) out[i] = x[i] * scale * w[i];
+}
+
+/* rms_norm_in_place, src/ops/norm.rs:17-23: `*v *= scale * w`. */
+void orc_rms_norm_in_place(float *x, const float *w, size_t n, float eps) {
+  const float scale = inverse_rms(x, n, eps);
+  for (size_t i = 0; i < n; i++) x[i] = x[i] * (scale * w[i]);
+}
+
+/* Rope::apply, src/ops/rope.rs:36-44 */
+void orc_rope_apply(float *head, size_t hd, const float *cos, const float *sin) {
+  const size_t half = hd / 2;
+  for (size_t i = 0; i < half; i++) {
+    const float a = head[i], b = head[half + i];
+    head[i] = a * cos[i] - b * sin[i];
+    head[half + i] = b * cos[i] + a * sin[i];
+  }
+}
+
+/* Attention::forward, src/model/attention.rs:31-86 */
+void orc_attention_forward(const orc_attention *a, const float *x, size_t position,
+                           const float *cos, const float *sin, float *keys,
+                           float *values, float *out) {
+  const size_t hd = a->head_dim, nh = a->num_heads, nkv = a->num_kv_heads;
+  const size_t kv_dim = nkv * hd;
+  float *q = (float *)calloc(nh * hd, 4);
+  float *k = keys + position * kv_dim;   /* cache.push(&k, &v) */
+  float *v = values + position * kv_dim;
+  orc_matvec(a->dtype, nh * hd, a->hidden, a->q_proj, x, q, 1);
+  orc_matvec(a->dtype, kv_dim, a->hidden, a->k_proj, x, k, 1);
+  orc_matvec(a->dtype, kv_dim, a->hidden, a->v_proj, x, v, 1);
+  for (size_t h = 0; h < nh; h++) {  /* QK-norm, then RoPE, per head */
+    if (a->q_norm) orc_rms_norm_in_place(q + h * hd, a->q_norm, hd, a->norm_eps);
+    orc_rope_apply(q + h * hd, hd, cos, sin);
+  }
+  for (size_t h = 0; h < nkv; h++) {
+    if (a->k_norm) orc_rms_norm_in_place(k + h * hd, a->k_norm, hd, a->norm_eps);
+    orc_rope_apply(k + h * hd, hd, cos, sin);
+  }
+  const size_t seq_len = position + 1;
+  const size_t group = nh / nkv;
+  const float scale = 1.0f / sqrtf((float)hd);
+  float *context = (float *)calloc(nh * hd, 4);
+  float *scores = (float *)malloc(seq_len * 4);
+  for (size_t h = 0; h < nh; h++) {
+    const size_t kv_offset = (h / group) * hd;
+    const float *qh = q + h * hd;
+    for (size_t t = 0; t < seq_len; t++) {
+      const float *key = keys + t * kv_dim + kv_offset;
+      float s = -0.0f;  /* Iterator::sum */
+      for (size_t j = 0; j < hd; j++) s = s + qh[j] * key[j];
+      scores[t] = s * scale;
+    }
+    orc_softmax_in_place(scores, seq_len);
+    float *ctx = context + h * hd;
+    for (size_t t = 0; t < seq_len; t++) {
+      const float p = scores[t];
+      const float *val = values + t * kv_dim + kv_offset;
+      for (size_t c = 0; c < hd; c++) ctx[c] = ctx[c] + p * val[c];
+    }
+  }
+  orc_matvec(a->dtype, a->hidden, nh * hd, a->o_proj, context, out, 1);
+  free(q);
+  free(context);
+  free(scores);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Expert and MoE layer                                                     */
 /* ------------------------------------------------------------------------ */
 

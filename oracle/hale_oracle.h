@@ -119,6 +119,39 @@ int orc_moe_prefill(const orc_moe_layer *layer, size_t tokens,
                     const float *x, const float *logits, float *out,
                     uint32_t *index, float *weight, int nthreads);
 
+/* ---- around the MoE block: src/ops/norm.rs, src/ops/rope.rs,
+ * src/model/attention.rs ---- */
+/* rms_norm (norm.rs:7-14): out[i] = x[i] * scale * w[i] with
+ * scale = 1 / sqrt(sum(x^2) / n + eps), the sum taken in order. */
+void orc_rms_norm(const float *x, const float *w, size_t n, float eps, float *out);
+/* rms_norm_in_place (norm.rs:17-23): x[i] = x[i] * (scale * w[i]). */
+void orc_rms_norm_in_place(float *x, const float *w, size_t n, float eps);
+/* Rope::apply (rope.rs:36-44): rotate-half over one head of hd values. */
+void orc_rope_apply(float *head, size_t hd, const float *cos, const float *sin);
+
+typedef struct {
+  int dtype;               /* dtype of the four projections             */
+  size_t hidden;           /* H                                          */
+  size_t num_heads;        /* query heads                                */
+  size_t num_kv_heads;     /* key/value heads (GQA)                      */
+  size_t head_dim;         /* hd (even)                                  */
+  float norm_eps;          /* eps of the per-head QK-norm                */
+  const uint8_t *q_proj;   /* [num_heads*hd][H] encoded rows             */
+  const uint8_t *k_proj;   /* [num_kv_heads*hd][H]                       */
+  const uint8_t *v_proj;   /* [num_kv_heads*hd][H]                       */
+  const uint8_t *o_proj;   /* [H][num_heads*hd]                          */
+  const float *q_norm;     /* [hd] QK-norm weights, or NULL              */
+  const float *k_norm;     /* [hd], or NULL                              */
+} orc_attention;
+
+/* Attention::forward (attention.rs:31-86) for the token at `position`.
+ * keys / values are the layer's cache, [position + 1][kv_dim] f32: rows
+ * 0 .. position-1 hold earlier tokens, row `position` receives this token's
+ * key (after QK-norm and RoPE) and value.  cos / sin: [hd/2]. */
+void orc_attention_forward(const orc_attention *a, const float *x, size_t position,
+                           const float *cos, const float *sin, float *keys,
+                           float *values, float *out);
+
 /* ---- seeded synthetic inputs ----
  * xorshift64* as in src/generate/sampler.rs:128-146 (shifts 12/25/27,
  * multiplier 0x2545F4914F6CDD1D, seed max(1)); normals by Box-Muller in

@@ -45,6 +45,25 @@ class MoeLayerDesc(C.Structure):
     ]
 
 
+class AttentionDesc(C.Structure):
+    """orc_attention: the fields of Attention (src/model/attention.rs:11-24)."""
+
+    _fields_ = [
+        ("dtype", C.c_int),
+        ("hidden", C.c_size_t),
+        ("num_heads", C.c_size_t),
+        ("num_kv_heads", C.c_size_t),
+        ("head_dim", C.c_size_t),
+        ("norm_eps", C.c_float),
+        ("q_proj", _u8p),
+        ("k_proj", _u8p),
+        ("v_proj", _u8p),
+        ("o_proj", _u8p),
+        ("q_norm", _fp),
+        ("k_norm", _fp),
+    ]
+
+
 def _load(variant: str = ""):
     path = os.path.join(_HERE, f"libhale_oracle{variant}.so")
     if not os.path.exists(path):
@@ -78,6 +97,11 @@ def _load(variant: str = ""):
         "orc_moe_route": (C.c_size_t, [C.POINTER(MoeLayerDesc), _fp, _fp, _u32p, _fp]),
         "orc_moe_forward": (C.c_int, [C.POINTER(MoeLayerDesc), _fp, _fp, _fp, _u32p, _fp, C.c_int]),
         "orc_moe_prefill": (C.c_int, [C.POINTER(MoeLayerDesc), C.c_size_t, _fp, _fp, _fp, _u32p, _fp, C.c_int]),
+        "orc_rms_norm": (None, [_fp, _fp, C.c_size_t, C.c_float, _fp]),
+        "orc_rms_norm_in_place": (None, [_fp, _fp, C.c_size_t, C.c_float]),
+        "orc_rope_apply": (None, [_fp, C.c_size_t, _fp, _fp]),
+        "orc_attention_forward": (None, [C.POINTER(AttentionDesc), _fp, C.c_size_t, _fp, _fp, _fp,
+                                         _fp, _fp]),
         "orc_xorshift64star": (C.c_uint64, [C.POINTER(C.c_uint64)]),
         "orc_fill_normal": (None, [C.c_uint64, C.c_float, C.c_float, _fp, C.c_size_t]),
         "orc_test_values": (None, [C.c_size_t, C.c_uint32, _fp]),
@@ -332,6 +356,70 @@ class OracleMoe:
         if rc:
             raise ValueError("moe_prefill")
         return out, idx[:, :self.k_eff], w[:, :self.k_eff]
+
+
+# ---- norms, RoPE, attention ----------------------------------------------
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """rms_norm (src/ops/norm.rs:7-14)."""
+    v, wv = f32(x), f32(w)
+    out = np.zeros_like(v)
+    lib().orc_rms_norm(_p(v, _fp), _p(wv, _fp), v.size, eps, _p(out, _fp))
+    return out
+
+
+def rms_norm_in_place(x, w, eps: float) -> np.ndarray:
+    """rms_norm_in_place (src/ops/norm.rs:17-23), on a copy."""
+    v, wv = f32(x).copy(), f32(w)
+    lib().orc_rms_norm_in_place(_p(v, _fp), _p(wv, _fp), v.size, eps)
+    return v
+
+
+def rope_apply(head, cos, sin) -> np.ndarray:
+    """Rope::apply (src/ops/rope.rs:36-44), on a copy."""
+    v, c, s_ = f32(head).copy(), f32(cos), f32(sin)
+    lib().orc_rope_apply(_p(v, _fp), v.size, _p(c, _fp), _p(s_, _fp))
+    return v
+
+
+class OracleAttention:
+    """An attention block in host memory plus its layer KV cache
+    (src/model/attention.rs, src/model/kv_cache.rs:9-32)."""
+
+    def __init__(self, dtype, hidden, num_heads, num_kv_heads, head_dim, norm_eps,
+                 q_proj, k_proj, v_proj, o_proj, q_norm=None, k_norm=None, max_len=4096):
+        self.dtype, self.hidden = dtype, hidden
+        self.num_heads, self.num_kv_heads, self.head_dim = num_heads, num_kv_heads, head_dim
+        self.kv_dim = num_kv_heads * head_dim
+        self.mats = [np.ascontiguousarray(m, dtype=np.uint8) for m in (q_proj, k_proj, v_proj, o_proj)]
+        self.q_norm = None if q_norm is None else f32(q_norm)
+        self.k_norm = None if k_norm is None else f32(k_norm)
+        self.desc = AttentionDesc(dtype, hidden, num_heads, num_kv_heads, head_dim, norm_eps,
+                                  *[_p(m, _u8p) for m in self.mats],
+                                  None if self.q_norm is None else _p(self.q_norm, _fp),
+                                  None if self.k_norm is None else _p(self.k_norm, _fp))
+        self.keys = np.zeros((max_len, self.kv_dim), dtype=np.float32)
+        self.values = np.zeros((max_len, self.kv_dim), dtype=np.float32)
+        self.len = 0
+
+    def forward(self, x, cos, sin) -> np.ndarray:
+        """Attention::forward at position = the cache length; appends k/v."""
+        v, c, s_ = f32(x), f32(cos), f32(sin)
+        out = np.zeros(self.hidden, dtype=np.float32)
+        lib().orc_attention_forward(C.byref(self.desc), _p(v, _fp), self.len, _p(c, _fp), _p(s_, _fp),
+                                    _p(self.keys, _fp), _p(self.values, _fp), _p(out, _fp))
+        self.len += 1
+        return out
+
+
+def rope_angles(head_dim: int, theta: float, position: int):
+    """Rope::new + Rope::angles (src/ops/rope.rs:14-33) in numpy float32
+    (the caller supplies cos/sin to attention, as the reference's
+    Transformer does; these are inputs, not a parity target)."""
+    half = head_dim // 2
+    i = np.arange(half, dtype=np.float32)
+    inv = (np.float32(1.0) / np.power(np.float32(theta), (2 * i) / np.float32(head_dim))).astype(np.float32)
+    ang = (np.float32(position) * inv).astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
 
 
 # ---- seeded inputs -------------------------------------------------------

@@ -496,3 +496,132 @@ def test_probability_ties_hidden_in_exp_values():
         assert p[a] == p[b]
         idx, _ = O.top_k(p, 2)
         assert list(idx) == [b, a]
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm, RoPE and attention (src/ops/norm.rs, src/ops/rope.rs,
+# src/model/attention.rs)
+# ---------------------------------------------------------------------------
+
+def test_rms_norm_reference_case():
+    # src/ops/norm.rs:34-48
+    x = np.array([3.0, -4.0, 0.0, 5.0], dtype=np.float32)
+    out = O.rms_norm(x, np.ones(4, np.float32), 0.0)
+    assert abs(np.sqrt(np.mean(out.astype(np.float64) ** 2)) - 1.0) < 1e-6
+    y = O.rms_norm_in_place(x, np.full(4, 2.0, np.float32), 0.0)
+    assert np.max(np.abs(y - 2.0 * out)) < 1e-6
+
+
+def test_rms_norm_sums_squares_in_order():
+    # squares [2^24, 1, 1]: in order (2^24 + 1) + 1 = 2^24 (two ties to even);
+    # summed pairwise the total would be 2^24 + 2, giving another scale
+    x = np.array([4096.0, 1.0, 1.0], dtype=np.float32)
+    got = O.rms_norm(x, np.ones(3, np.float32), 0.0)
+    in_order = np.float32(1.0) / np.sqrt(np.float32(16777216.0) / np.float32(3.0))
+    pairwise = np.float32(1.0) / np.sqrt(np.float32(16777218.0) / np.float32(3.0))
+    assert in_order != pairwise
+    assert got[1] == in_order
+
+
+def test_rms_norm_and_in_place_associate_differently():
+    # rms_norm is (x * scale) * w; rms_norm_in_place is x * (scale * w).  The
+    # scale is read back from a unit-weight norm of a row whose first value
+    # is 1 (1 * scale * 1 = scale), then both associations are checked on
+    # rows where they round differently.
+    rng = np.random.default_rng(3)
+    differ = 0
+    for _ in range(200):
+        x = rng.standard_normal(8).astype(np.float32)
+        x[0] = 1.0
+        w = rng.standard_normal(8).astype(np.float32)
+        scale = O.rms_norm(x, np.ones(8, np.float32), 1e-6)[0]
+        a, b = O.rms_norm(x, w, 1e-6), O.rms_norm_in_place(x, w, 1e-6)
+        assert np.array_equal(a, (x * scale) * w)
+        assert np.array_equal(b, x * (scale * w))
+        differ += int(not np.array_equal(a, b))
+    assert differ > 0
+
+
+def test_rope_reference_case_and_quarter_turn():
+    # src/ops/rope.rs:52-69: position 0 is the identity, a rotation keeps the norm
+    h = np.arange(1, 9, dtype=np.float32)
+    c0, s0 = O.rope_angles(8, 10000.0, 0)
+    assert np.array_equal(O.rope_apply(h, c0, s0), h)
+    c, s = O.rope_angles(8, 10000.0, 17)
+    r = O.rope_apply(h, c, s)
+    assert abs(float(np.sum(r * r)) - float(np.sum(h * h))) < 1e-3 and not np.array_equal(r, h)
+    # cos 0, sin 1: (a, b) -> (-b, a) exactly (rotate-half pairs i and i + d/2)
+    q = O.rope_apply(h, np.zeros(4, np.float32), np.ones(4, np.float32))
+    assert np.array_equal(q, np.concatenate([-h[4:], h[:4]]))
+
+
+def _attention(dtype, H, nh, nkv, hd, seed, qk_norm=True, identity_o=False, std=0.05):
+    mats = []
+    for j, (r, c) in enumerate(((nh * hd, H), (nkv * hd, H), (nkv * hd, H), (H, nh * hd))):
+        if j == 3 and identity_o:
+            mats.append(O.encode_matrix(dtype, np.eye(r, c, dtype=np.float32)))
+        else:
+            mats.append(O.encode_matrix(dtype, O.normal(seed + j, r * c, 0.0, std).reshape(r, c)))
+    qn = kn = None
+    if qk_norm:
+        qn, kn = O.normal(seed + 10, hd, 1.0, 0.1), O.normal(seed + 11, hd, 1.0, 0.1)
+    return O.OracleAttention(dtype, H, nh, nkv, hd, 1e-6, *mats, q_norm=qn, k_norm=kn, max_len=64), mats
+
+
+def test_attention_first_position_returns_the_value_heads():
+    # seq_len 1: softmax gives p = 1, so the context is each head's value head
+    # (GQA: query heads h share value head h // group); with an identity
+    # o_proj the output is the context itself
+    H, nh, nkv, hd = 64, 4, 2, 16
+    A, mats = _attention(O.F32, H, nh, nkv, hd, seed=5, identity_o=True)
+    x = O.normal(9, H)
+    c, s = O.rope_angles(hd, 1e6, 0)
+    out = A.forward(x, c, s)
+    v = O.matvec(O.F32, nkv * hd, H, mats[2], x)
+    want = np.concatenate([v[(h // (nh // nkv)) * hd:(h // (nh // nkv) + 1) * hd] for h in range(nh)])
+    assert np.array_equal(out, want)
+
+
+def test_attention_equal_keys_average_the_values():
+    # the same token twice: equal keys, p = 0.5 each, context 0.5 v + 0.5 v = v
+    H, nh, nkv, hd = 64, 4, 4, 16
+    A, mats = _attention(O.F32, H, nh, nkv, hd, seed=6, identity_o=True, qk_norm=False)
+    x = O.normal(10, H)
+    c, s = np.ones(hd // 2, np.float32), np.zeros(hd // 2, np.float32)
+    first = A.forward(x, c, s)
+    second = A.forward(x, c, s)
+    assert np.array_equal(first, second)
+
+
+def test_attention_close_to_float64_model():
+    H, nh, nkv, hd = 64, 4, 2, 16
+    A, mats = _attention(O.F32, H, nh, nkv, hd, seed=7, qk_norm=True)
+    W = [O.decode_row(O.F32, m, m.size // 4).astype(np.float64) for m in mats]
+    Wq, Wk, Wv = W[0].reshape(nh * hd, H), W[1].reshape(nkv * hd, H), W[2].reshape(nkv * hd, H)
+    Wo = W[3].reshape(H, nh * hd)
+    qn, kn = A.q_norm.astype(np.float64), A.k_norm.astype(np.float64)
+    Ks, Vs = [], []
+
+    def norm_rope(hv, w, c, s):
+        hv = hv / np.sqrt(np.mean(hv * hv) + 1e-6) * w
+        a, b = hv[:hd // 2], hv[hd // 2:]
+        return np.concatenate([a * c - b * s, b * c + a * s])
+
+    for pos in range(6):
+        x = O.normal(20 + pos, H).astype(np.float64)
+        c, s = (v.astype(np.float64) for v in O.rope_angles(hd, 1e6, pos))
+        got = A.forward(x.astype(np.float32), c.astype(np.float32), s.astype(np.float32))
+        q, k, v = Wq @ x, Wk @ x, Wv @ x
+        q = np.concatenate([norm_rope(q[h * hd:(h + 1) * hd], qn, c, s) for h in range(nh)])
+        k = np.concatenate([norm_rope(k[h * hd:(h + 1) * hd], kn, c, s) for h in range(nkv)])
+        Ks.append(k)
+        Vs.append(v)
+        ctx = []
+        for h in range(nh):
+            g = h // (nh // nkv)
+            sc = np.array([q[h * hd:(h + 1) * hd] @ K[g * hd:(g + 1) * hd] for K in Ks]) / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            p /= p.sum()
+            ctx.append(sum(pi * V[g * hd:(g + 1) * hd] for pi, V in zip(p, Vs)))
+        want = Wo @ np.concatenate(ctx)
+        assert np.max(np.abs(got - want)) < 1e-4 * max(1.0, np.max(np.abs(want)))
