@@ -20,6 +20,8 @@ on one layer of the same shape, on this host's cores.
 decode_more: Mixtral-8x7B- and Qwen3-235B-shaped decode layers, same timing.
 float_matvec: WeightMatrix::matvec over float weights (a bf16 vocabulary
 projection and a dense f32 matrix), GB/s of weight bytes.
+attention: RMSNorm + Attention::forward of one token with 4096 cached
+positions (Qwen3-30B-A3B shape, bf16 projections), per-kernel times.
 prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
 2048 tokens q4_0 H 4096 I 1536; 128 experts, top-8, Zipf-skewed routing)
 with tokens/s, TOPS and the fraction of the int8 MFMA peak.
@@ -319,6 +321,75 @@ def gpu_float_matvec(name, dtype, rows, cols, copies, reps=20):
             "kernel_GB_per_s": round(nbytes / kus / 1e3, 1) if kus else None}
 
 
+# (workload, projection dtype, hidden, heads, kv heads, head dim, QK-norm, cached positions)
+ATTENTION = [
+    ("qwen3-30b-a3b attention decode bf16, 4096 cached positions", H.BF16, 2048, 32, 4, 128, True, 4096),
+]
+
+
+def gpu_attention(name, dtype, hid, nh, nkv, hd, qk, positions, timed=64):
+    """Attention::forward for one token after `positions - timed` cached
+    positions, timed over the last `timed` positions (each appends its k/v),
+    plus the RMSNorm before it.  Bytes per call: the four projections plus the
+    keys and values read."""
+    ctx = H.Context(0)
+    shapes = ((nh * hd, hid), (nkv * hd, hid), (nkv * hd, hid), (hid, nh * hd))
+    vals = ctx.malloc(max(r * c for r, c in shapes) * 4)
+    enc = ctx.malloc(max(r * H.row_bytes(dtype, c) for r, c in shapes))
+    mats = []
+    for j, (r, c) in enumerate(shapes):
+        vals.fill_normal(700 + j, r * c, 0.0, 0.02)
+        ctx.check(H.lib().hale_encode_rows_device(ctx.handle, dtype, r, c, H._vp(vals.address),
+                                                  H._vp(enc.address)), "encode")
+        h = H._vp()
+        ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, dtype, r, c, H._vp(enc.address),
+                                                    r * H.row_bytes(dtype, c), H.C.byref(h)), "upload")
+        mats.append(H.WeightMatrix(ctx, h, r, c, dtype))
+    enc.free()
+    vals.free()
+    norm_w = np.ones(hd, np.float32) if qk else None
+    att = H.Attention(ctx, *mats, norm_w, norm_w, nh, nkv, hd, 1e-6, max_len=positions)
+    x = ctx.malloc(hid * 4)
+    x.fill_normal(3, hid, 0.0, 1.0)
+    w = ctx.malloc(hid * 4)
+    w.fill_normal(4, hid, 1.0, 0.1)
+    xn = ctx.malloc(hid * 4)
+    out = ctx.malloc(hid * 4)
+    cs = ctx.malloc(hd * 4)
+    cs.fill_normal(5, hd, 0.0, 0.5)
+
+    def call(pos):
+        ctx.check(H.lib().hale_rms_norm_device(ctx.handle, H._vp(x.address), None, H._vp(w.address), 1,
+                                               hid, np.float32(1e-6), H._vp(xn.address)), "rms_norm")
+        ctx.check(H.lib().hale_attention_forward_device(att.handle, H._vp(xn.address), pos,
+                                                        H._vp(cs.address), H._vp(cs.address + hd * 2),
+                                                        H._vp(out.address)), "attention")
+
+    for pos in range(positions - timed):
+        call(pos)
+    ctx.synchronize()
+    ctx.profile(True)
+    ctx.profile_reset()
+    ctx.timer_start()
+    for pos in range(positions - timed, positions):
+        call(pos)
+    ms = ctx.timer_stop()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    att.close()
+    for m in mats:
+        m.close()
+    for b in (x, w, xn, out, cs):
+        b.free()
+    ctx.close()
+    wbytes = sum(r * H.row_bytes(dtype, c) for r, c in shapes)
+    kv = 2 * (positions - timed // 2) * nkv * hd * 4
+    us = 1000 * ms / timed
+    return {"workload": name, "us_per_token": round(us, 2), "weight_bytes": wbytes,
+            "kv_bytes": kv, "GB_per_s": round((wbytes + kv) / us / 1e3, 1),
+            "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
+
+
 def gpu_decode(args):
     ctx = H.Context(0)
     t0 = time.time()
@@ -443,6 +514,12 @@ def main():
             fmv.append(gpu_float_matvec(name, dt, rows, cols, copies))
             log(f"matvec {name}: {fmv[-1]['us_per_call']} us, {fmv[-1]['GB_per_s']} GB/s")
 
+    attn = []
+    if not args.no_prefill:
+        for (name, dt, hid, nh, nkv, hd, qk, npos) in ATTENTION:
+            attn.append(gpu_attention(name, dt, hid, nh, nkv, hd, qk, npos))
+            log(f"attention {name}: {attn[-1]['us_per_token']} us/token, {attn[-1]['GB_per_s']} GB/s")
+
     prefill = []
     if not args.no_prefill:
         for (name, dt, hid, inter, ex, k, tok) in PREFILL:
@@ -487,6 +564,7 @@ def main():
         "kernels": kernels,
         "decode_more": more,
         "float_matvec": fmv,
+        "attention": attn,
         "prefill": prefill,
         "cpu_baseline": cpu,
     }

@@ -22,7 +22,6 @@ namespace hale {
 
 constexpr int NORM_MAX = 8192;     // elements one RMSNorm work-group holds in LDS
 constexpr int HEAD_MAX = 1024;     // largest head_dim
-constexpr int PCHUNK = 1024;       // probabilities staged in LDS per context pass
 
 // inverse_rms (src/ops/norm.rs:25-28) of n values whose squares are in
 // sq[0, n) of LDS; every thread gets the scale.
@@ -115,28 +114,54 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
   if (t >= seq) return;
   const f32x4* key = (const f32x4*)(keys + (size_t)t * kv_dim + kvo);
   float s = -0.0f;  // Iterator::sum
-  for (int j = 0; j < hd / 4; j++) {
-    const f32x4 kv = key[j];
-    s = s + qh[4 * j] * kv.x;
-    s = s + qh[4 * j + 1] * kv.y;
-    s = s + qh[4 * j + 2] * kv.z;
-    s = s + qh[4 * j + 3] * kv.w;
+  // 32 key values per batch in two alternating register sets: the loads of
+  // batch b + 1 are in flight while batch b is added (hd is a multiple of 16)
+  const int nb = hd / 32;
+  f32x4 A[8], B[8];
+  auto ld8 = [&](f32x4* d, int b) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) d[u] = key[8 * b + u];
+  };
+  auto add8 = [&](const f32x4* d, int b) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int j = 32 * b + 4 * u;
+      s = s + qh[j] * d[u].x;
+      s = s + qh[j + 1] * d[u].y;
+      s = s + qh[j + 2] * d[u].z;
+      s = s + qh[j + 3] * d[u].w;
+    }
+  };
+  if (nb > 0) ld8(A, 0);
+  int b = 0;
+  for (; b + 1 < nb; b += 2) {
+    ld8(B, b + 1);
+    add8(A, b);
+    if (b + 2 < nb) ld8(A, b + 2);
+    add8(B, b + 1);
+  }
+  if (b < nb) add8(A, b);
+  for (int j = 32 * nb; j < hd; j += 4) {  // a 16-value remainder
+    const f32x4 kv = key[j / 4];
+    s = s + qh[j] * kv.x;
+    s = s + qh[j + 1] * kv.y;
+    s = s + qh[j + 2] * kv.z;
+    s = s + qh[j + 3] * kv.w;
   }
   scores[(size_t)h * ld + t] = s * scale;
 }
 
-// softmax_in_place over the head's scores, then the context
-// ctx[c] = 0 + p_0 v_0[c] + p_1 v_1[c] + ... (one thread per c).
-__global__ __launch_bounds__(256) void k_attn_softmax_ctx(float* __restrict__ scores,
-                                                          const float* __restrict__ values, int hd,
-                                                          int kv_dim, int group, int seq, int ld,
-                                                          float* __restrict__ ctx) {
-  __shared__ __attribute__((aligned(16))) float pbuf[PCHUNK];
+// softmax_in_place over each head's scores (one work-group per head): the
+// max in any order, the exponentials in parallel, their sum in order by one
+// thread (through LDS in chunks, several reads in flight), then one division
+// per score.  The probabilities replace the scores.
+constexpr int SM_CHUNK = 12288;  // exponentials per LDS chunk (48 KB)
+
+__global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ scores, int seq, int ld) {
+  __shared__ __attribute__((aligned(16))) float buf[SM_CHUNK];
   __shared__ float red[4];
   __shared__ float bcast[1];
-  const int h = blockIdx.x;
-  const int kvo = (h / group) * hd;
-  float* sc = scores + (size_t)h * ld;
+  float* sc = scores + (size_t)blockIdx.x * ld;
   const int tid = threadIdx.x;
   // max: fold(-inf, f32::max); order-free (a NaN is skipped either way)
   float m = -INFINITY;
@@ -145,42 +170,102 @@ __global__ __launch_bounds__(256) void k_attn_softmax_ctx(float* __restrict__ sc
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (int t = tid; t < seq; t += 256) sc[t] = hale_expf(sc[t] - m);
-  __syncthreads();
-  if (tid == 0) {  // sum += v, in order from 0.0
-    float sum = 0.0f;
-    for (int t = 0; t < seq; t++) sum = sum + sc[t];
-    bcast[0] = sum;
-  }
-  __syncthreads();
-  const float sum = bcast[0];
-  for (int t = tid; t < seq; t += 256) sc[t] = sc[t] / sum;
-  __syncthreads();
-  // context, PCHUNK probabilities at a time through LDS
-  float acc[HEAD_MAX / 256];
-#pragma unroll
-  for (int i = 0; i < HEAD_MAX / 256; i++) acc[i] = 0.0f;
-  for (int t0 = 0; t0 < seq; t0 += PCHUNK) {
-    const int n = min(PCHUNK, seq - t0);
-    for (int t = tid; t < n; t += 256) pbuf[t] = sc[t0 + t];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < HEAD_MAX / 256; i++) {
-      const int c = tid + 256 * i;
-      if (c < hd) {
-        const float* vc = values + (size_t)t0 * kv_dim + kvo + c;
-        float a = acc[i];
-        for (int t = 0; t < n; t++) a = a + pbuf[t] * vc[(size_t)t * kv_dim];
-        acc[i] = a;
-      }
+  float sum = 0.0f;  // sum += v from 0.0, carried by thread 0
+  for (int c0 = 0; c0 < seq; c0 += SM_CHUNK) {
+    const int n = min(SM_CHUNK, seq - c0);
+    for (int t = tid; t < n; t += 256) {
+      const float e = hale_expf(sc[c0 + t] - m);
+      sc[c0 + t] = e;
+      buf[t] = e;
     }
     __syncthreads();
+    if (tid == 0) sum = lds_sum_in_order(buf, n, sum);
+    __syncthreads();
   }
+  if (tid == 0) bcast[0] = sum;
+  __syncthreads();
+  sum = bcast[0];
+  for (int t = tid; t < seq; t += 256) sc[t] = sc[t] / sum;
+}
+
+// The context ctx[h][c] = 0 + p_0 v_0[c] + p_1 v_1[c] + ... in position
+// order.  A work-group takes one key/value head and 16 of its columns for
+// every query head of its group (thread (query head, column) < group x 16
+// folds one chain; all 256 threads load), so each value is read once.  Values and
+// probabilities stream through two LDS tiles of T positions, staged through
+// registers: tile i + 1 loads while the chains add tile i.
+constexpr int CTX_COLS = 16;
+constexpr int CTX_LDS = 6144;  // floats per tile (values T x 16 + probabilities group x T)
+
+__global__ __launch_bounds__(256) void k_attn_ctx(const float* __restrict__ probs,
+                                                  const float* __restrict__ values, int hd,
+                                                  int kv_dim, int group, int seq, int ld,
+                                                  float* __restrict__ ctx) {
+  __shared__ __attribute__((aligned(16))) float tile[2][CTX_LDS];
+  const int g = blockIdx.x;                 // key/value head
+  const int c0 = blockIdx.y * CTX_COLS;     // first column
+  constexpr int nthr = 256;
+  const int tid = threadIdx.x;
+  const bool chain = tid < group * CTX_COLS;
+  const int hq = tid / CTX_COLS, c = tid % CTX_COLS;
+  // positions per tile: a multiple of 4 with T * (16 + group) <= CTX_LDS
+  const int T = CTX_LDS / (CTX_COLS + group) / 4 * 4;
+  const int nv4 = T * (CTX_COLS / 4);       // float4 of values per tile
+  const int np4 = group * (T / 4);          // float4 of probabilities per tile
+  const int ntiles = (seq + T - 1) / T;
+  constexpr int MAXL = CTX_LDS / 4 / nthr;  // float4 loads per thread
+  f32x4 r[MAXL];
+  const float* vbase = values + (size_t)g * hd + c0;
+  const float* pbase = probs + (size_t)g * group * ld;
+  auto load = [&](int ti) {
+    const int t0 = ti * T, n = min(T, seq - t0);
 #pragma unroll
-  for (int i = 0; i < HEAD_MAX / 256; i++) {
-    const int c = tid + 256 * i;
-    if (c < hd) ctx[(size_t)h * hd + c] = acc[i];
+    for (int j = 0; j < MAXL; j++) {
+      const int i = tid + nthr * j;
+      if (i < nv4) {
+        const int t = i / (CTX_COLS / 4), q = i % (CTX_COLS / 4);
+        if (t < n) r[j] = *(const f32x4*)(vbase + (size_t)(t0 + t) * kv_dim + 4 * q);
+      } else if (i < nv4 + np4) {
+        const int k = i - nv4, hh = k / (T / 4), t = 4 * (k % (T / 4));
+        if (t < n) r[j] = *(const f32x4*)(pbase + (size_t)hh * ld + t0 + t);
+      }
+    }
+  };
+  auto store = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < MAXL; j++) {
+      const int i = tid + nthr * j;
+      if (i < nv4 + np4) *(f32x4*)&tile[b][4 * i] = r[j];
+    }
+  };
+  float acc = 0.0f;
+  if (ntiles > 0) {
+    load(0);
+    store(0);
   }
+  __syncthreads();
+  for (int ti = 0; ti < ntiles; ti++) {
+    const int b = ti & 1;
+    if (ti + 1 < ntiles) load(ti + 1);
+    const int n = min(T, seq - ti * T);
+    const float* vt = tile[b];
+    const float* pt = tile[b] + T * CTX_COLS + hq * T;
+    if (chain) {
+      // eight products from LDS at a time, then their in-order adds
+      int t = 0;
+      for (; t + 8 <= n; t += 8) {
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pv[u] = pt[t + u] * vt[(t + u) * CTX_COLS + c];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = acc + pv[u];
+      }
+      for (; t < n; t++) acc = acc + pt[t] * vt[t * CTX_COLS + c];
+    }
+    if (ti + 1 < ntiles) store(b ^ 1);
+    __syncthreads();
+  }
+  if (chain) ctx[(size_t)(g * group + hq) * hd + c0 + c] = acc;
 }
 
 hipError_t launch_rms_norm(float* x, const float* delta, const float* w, size_t rows, size_t n,
@@ -191,8 +276,10 @@ hipError_t launch_rms_norm(float* x, const float* delta, const float* w, size_t 
 }
 
 hipError_t launch_attention_core(const AttnArgs& a, hipStream_t st) {
-  if (a.hd < 4 || a.hd > HEAD_MAX || a.hd % 4 || a.nh < 1 || a.nkv < 1 || a.nh % a.nkv || a.seq < 1 ||
-      a.seq > a.ld)
+  // head_dim a multiple of 16 (context column blocks), GQA group <= 16
+  // (work-groups of group x 16 threads), score rows 16-byte aligned
+  if (a.hd < 16 || a.hd > HEAD_MAX || a.hd % CTX_COLS || a.nh < 1 || a.nkv < 1 || a.nh % a.nkv ||
+      a.nh / a.nkv > 16 || a.seq < 1 || a.seq > a.ld || a.ld % 4)
     return hipErrorInvalidValue;
   const int kv_dim = a.nkv * a.hd;
   hipError_t e = launch(k_qk_norm_rope, (unsigned)(a.nh + a.nkv), 64, 0, st, a.q, a.k, a.v, a.nh, a.hd,
@@ -204,8 +291,11 @@ hipError_t launch_attention_core(const AttnArgs& a, hipStream_t st) {
   e = launch(k_attn_scores, gs, 256, 0, st, (const float*)a.q, (const float*)a.keys, a.hd, kv_dim,
              a.nh / a.nkv, a.seq, a.ld, scale, a.scores);
   if (e != hipSuccess) return e;
-  return launch(k_attn_softmax_ctx, (unsigned)a.nh, 256, 0, st, a.scores, (const float*)a.values, a.hd,
-                kv_dim, a.nh / a.nkv, a.seq, a.ld, a.ctx);
+  e = launch(k_attn_softmax, (unsigned)a.nh, 256, 0, st, a.scores, a.seq, a.ld);
+  if (e != hipSuccess) return e;
+  dim3 gc((unsigned)a.nkv, (unsigned)(a.hd / CTX_COLS));
+  return launch(k_attn_ctx, gc, 256, 0, st, (const float*)a.scores,
+                (const float*)a.values, a.hd, kv_dim, a.nh / a.nkv, a.seq, a.ld, a.ctx);
 }
 
 }  // namespace hale

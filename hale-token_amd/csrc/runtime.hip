@@ -1278,8 +1278,9 @@ extern "C" int hale_attention_create(hale_ctx* c, const hale_matrix* q, const ha
   const size_t nh = num_heads, nkv = num_kv_heads, hd = head_dim, H = q->cols;
   if (nh == 0 || nkv == 0 || nh % nkv)
     return fail(c, HALE_EINVAL, "num_heads %zu must be a positive multiple of num_kv_heads %zu", nh, nkv);
-  if (hd < 4 || hd > 1024 || hd % 4)
-    return fail(c, HALE_EINVAL, "head_dim %zu must be a multiple of 4 in 4..1024", hd);
+  if (hd < 16 || hd > 1024 || hd % 16)
+    return fail(c, HALE_EINVAL, "head_dim %zu must be a multiple of 16 in 16..1024", hd);
+  if (nh / nkv > 16) return fail(c, HALE_EINVAL, "GQA group %zu above 16", nh / nkv);
   if (max_len == 0 || max_len > (1u << 24)) return fail(c, HALE_EINVAL, "max_len %zu outside 1..2^24", max_len);
   if (q->rows != nh * hd || k->rows != nkv * hd || v->rows != nkv * hd || k->cols != H ||
       v->cols != H || o->rows != H || o->cols != nh * hd)
@@ -1312,7 +1313,7 @@ extern "C" int hale_attention_create(hale_ctx* c, const hale_matrix* q, const ha
   ALLOC(a->dk, kv_dim * 4);
   ALLOC(a->dv, kv_dim * 4);
   ALLOC(a->dctx, nh * hd * 4);
-  ALLOC(a->scores, nh * max_len * 4);
+  ALLOC(a->scores, nh * ((max_len + 3) / 4 * 4) * 4);
   ALLOC(a->hx, H * 4);
   ALLOC(a->hcos, hd * 2);
   ALLOC(a->hsin, hd * 2);
@@ -1373,7 +1374,7 @@ extern "C" int hale_attention_forward_device(hale_attention* a, const float* d_x
   t.keys = a->keys;
   t.values = a->values;
   t.seq = (int)position + 1;
-  t.ld = (int)a->max_len;
+  t.ld = (int)((a->max_len + 3) / 4 * 4);  // score rows 16-byte aligned
   t.scores = a->scores;
   t.ctx = a->dctx;
   LAUNCH(c, K_ATTENTION, launch_attention_core(t, c->stream));

@@ -290,7 +290,8 @@ int hale_rms_norm_device(hale_ctx *ctx, float *d_x, const float *d_delta,
  * k / v [kv_heads*hd][H], o [H][heads*hd] are uploaded matrices of any
  * dtype, borrowed (they must outlive the attention).  q_norm / k_norm:
  * QK-norm weights [head_dim] (host memory, copied) or NULL (Mixtral).
- * head_dim a multiple of 4 up to 1024; heads a multiple of kv_heads. */
+ * head_dim a multiple of 16 up to 1024; heads a multiple of kv_heads, at
+ * most 16 query heads per key/value head. */
 int hale_attention_create(hale_ctx *ctx, const hale_matrix *q_proj,
                           const hale_matrix *k_proj, const hale_matrix *v_proj,
                           const hale_matrix *o_proj, const float *q_norm,
