@@ -279,7 +279,7 @@ int hale_rms_norm(hale_ctx *ctx, const float *x, const float *weight, size_t n,
                   float eps, float *out);
 /* Device form over `rows` rows of n values.  With d_delta non-NULL, each row
  * first becomes x = x + delta, stored back into d_x (add_in_place,
- * src/model/transformer.rs:197-203, the residual before the next norm).
+ * src/model/transformer.rs:203-205,242-246, the residual before the next norm).
  * d_out may equal d_x. */
 int hale_rms_norm_device(hale_ctx *ctx, float *d_x, const float *d_delta,
                          const float *d_weight, size_t rows, size_t n,
