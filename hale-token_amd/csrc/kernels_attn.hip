@@ -164,12 +164,27 @@ __global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ scores
   float* sc = scores + (size_t)blockIdx.x * ld;
   const int tid = threadIdx.x;
   // max: fold(-inf, f32::max); order-free (a NaN is skipped either way)
+  // up to SM_CHUNK scores stay in LDS from the first read to the division
+  const bool resident = seq <= SM_CHUNK;
   float m = -INFINITY;
-  for (int t = tid; t < seq; t += 256) m = fmaxf(m, sc[t]);
+  for (int t = tid; t < seq; t += 256) {
+    const float v = sc[t];
+    m = fmaxf(m, v);
+    if (resident) buf[t] = v;
+  }
   m = wave_max_f32(m);
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  if (resident) {
+    for (int t = tid; t < seq; t += 256) buf[t] = hale_expf(buf[t] - m);
+    __syncthreads();
+    if (tid == 0) bcast[0] = lds_sum_in_order(buf, seq, 0.0f);
+    __syncthreads();
+    const float sum = bcast[0];
+    for (int t = tid; t < seq; t += 256) sc[t] = buf[t] / sum;
+    return;
+  }
   float sum = 0.0f;  // sum += v from 0.0, carried by thread 0
   for (int c0 = 0; c0 < seq; c0 += SM_CHUNK) {
     const int n = min(SM_CHUNK, seq - c0);
@@ -208,62 +223,93 @@ __global__ __launch_bounds__(256) void k_attn_ctx(const float* __restrict__ prob
   const int tid = threadIdx.x;
   const bool chain = tid < group * CTX_COLS;
   const int hq = tid / CTX_COLS, c = tid % CTX_COLS;
-  // positions per tile: a multiple of 4 with T * (16 + group) <= CTX_LDS
-  const int T = CTX_LDS / (CTX_COLS + group) / 4 * 4;
+  // positions per tile: a multiple of 4 with T * 16 + group * (T + 4) <=
+  // CTX_LDS; probability rows are T + 4 floats apart, so the query heads of
+  // a wave read distinct banks
+  const int T = (CTX_LDS - 4 * group) / (CTX_COLS + group) / 4 * 4;
+  const int PP = T + 4;                     // probability row pitch
   const int nv4 = T * (CTX_COLS / 4);       // float4 of values per tile
   const int np4 = group * (T / 4);          // float4 of probabilities per tile
   const int ntiles = (seq + T - 1) / T;
   constexpr int MAXL = CTX_LDS / 4 / nthr;  // float4 loads per thread
-  f32x4 r[MAXL];
   const float* vbase = values + (size_t)g * hd + c0;
   const float* pbase = probs + (size_t)g * group * ld;
-  auto load = [&](int ti) {
+  // NST register stages: tiles ti + 2 .. ti + NST are in flight while tile
+  // ti is added from LDS and tile ti + 1 waits in the other LDS buffer
+  constexpr int NST = 4;
+  f32x4 r[NST][MAXL];
+  auto load = [&](f32x4* R, int ti) {
+    if (ti >= ntiles) return;
     const int t0 = ti * T, n = min(T, seq - t0);
 #pragma unroll
     for (int j = 0; j < MAXL; j++) {
       const int i = tid + nthr * j;
       if (i < nv4) {
         const int t = i / (CTX_COLS / 4), q = i % (CTX_COLS / 4);
-        if (t < n) r[j] = *(const f32x4*)(vbase + (size_t)(t0 + t) * kv_dim + 4 * q);
+        if (t < n) R[j] = *(const f32x4*)(vbase + (size_t)(t0 + t) * kv_dim + 4 * q);
       } else if (i < nv4 + np4) {
         const int k = i - nv4, hh = k / (T / 4), t = 4 * (k % (T / 4));
-        if (t < n) r[j] = *(const f32x4*)(pbase + (size_t)hh * ld + t0 + t);
+        if (t < n) R[j] = *(const f32x4*)(pbase + (size_t)hh * ld + t0 + t);
       }
     }
   };
-  auto store = [&](int b) {
+  auto store = [&](const f32x4* R, int b) {
 #pragma unroll
     for (int j = 0; j < MAXL; j++) {
       const int i = tid + nthr * j;
-      if (i < nv4 + np4) *(f32x4*)&tile[b][4 * i] = r[j];
+      if (i < nv4) {
+        *(f32x4*)&tile[b][4 * i] = R[j];
+      } else if (i < nv4 + np4) {
+        const int k = i - nv4, hh = k / (T / 4), t = 4 * (k % (T / 4));
+        *(f32x4*)&tile[b][T * CTX_COLS + hh * PP + t] = R[j];
+      }
     }
   };
   float acc = 0.0f;
-  if (ntiles > 0) {
-    load(0);
-    store(0);
-  }
-  __syncthreads();
-  for (int ti = 0; ti < ntiles; ti++) {
-    const int b = ti & 1;
-    if (ti + 1 < ntiles) load(ti + 1);
+  auto fold = [&](int ti) {
     const int n = min(T, seq - ti * T);
-    const float* vt = tile[b];
-    const float* pt = tile[b] + T * CTX_COLS + hq * T;
-    if (chain) {
-      // eight products from LDS at a time, then their in-order adds
-      int t = 0;
-      for (; t + 8 <= n; t += 8) {
-        float pv[8];
+    const float* vt = tile[ti & 1];
+    const float* pt = tile[ti & 1] + T * CTX_COLS + hq * PP;
+    // products of FB positions at a time in two alternating register sets:
+    // batch k + 1's LDS reads are in flight while batch k is added (FB adds
+    // overlap the next batch's reads)
+    constexpr int FB = 8;
+    float PA[FB], PB[FB];
+    auto prod = [&](float* d, int t) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) pv[u] = pt[t + u] * vt[(t + u) * CTX_COLS + c];
+      for (int u = 0; u < FB; u++) d[u] = pt[t + u] * vt[(t + u) * CTX_COLS + c];
+    };
+    auto add = [&](const float* d) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) acc = acc + pv[u];
-      }
-      for (; t < n; t++) acc = acc + pt[t] * vt[t * CTX_COLS + c];
+      for (int u = 0; u < FB; u++) acc = acc + d[u];
+    };
+    const int nbk = n / FB;
+    if (nbk > 0) prod(PA, 0);
+    int k = 0;
+    for (; k + 1 < nbk; k += 2) {
+      prod(PB, FB * (k + 1));
+      add(PA);
+      if (k + 2 < nbk) prod(PA, FB * (k + 2));
+      add(PB);
     }
-    if (ti + 1 < ntiles) store(b ^ 1);
-    __syncthreads();
+    if (k < nbk) add(PA);
+    for (int t = FB * nbk; t < n; t++) acc = acc + pt[t] * vt[t * CTX_COLS + c];
+  };
+#pragma unroll
+  for (int j = 0; j < NST; j++) load(r[j], j);
+  if (ntiles > 0) store(r[0], 0);
+  __syncthreads();
+  for (int ti0 = 0; ti0 < ntiles; ti0 += NST) {
+#pragma unroll
+    for (int j = 0; j < NST; j++) {
+      const int ti = ti0 + j;  // stage j holds tile ti (stored), stage j + 1 tile ti + 1
+      if (ti < ntiles) {
+        if (chain) fold(ti);
+        if (ti + 1 < ntiles) store(r[(j + 1) % NST], (ti + 1) & 1);
+        load(r[(j + 1) % NST], ti + 1 + NST);  // the stage just stored takes tile ti + 1 + NST
+        __syncthreads();
+      }
+    }
   }
   if (chain) ctx[(size_t)(g * group + hq) * hd + c0 + c] = acc;
 }
