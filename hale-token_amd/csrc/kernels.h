@@ -172,6 +172,7 @@ enum KernelKind : int {
   K_COPY,
   K_NORM,
   K_ATTENTION,
+  K_GATHER,
   K_KINDS
 };
 

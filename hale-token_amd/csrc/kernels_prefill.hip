@@ -32,6 +32,14 @@ constexpr int TM = 32;          // assignments (rows) per tile
 constexpr int TN = 128;         // output columns per work-group (4 waves x 32)
 constexpr int GROUP_WAVES = 16;  // waves of the grouping kernel
 constexpr int GROUP_MAX_E = 1024;
+// Activations of the grouped kernels, tile-major: per (tile, 32-column
+// block) the codes as the MFMA's A operand wants them, [K half][32 rows]
+// [16 B], then the 32 rows' f32 scales, so one wave's operand of a block is
+// 1 KB contiguous and its scales one line.  The gate/up input is gathered
+// into this layout from the token-major blocks; the requantized SiLU output
+// is written in it by the gate/up kernel for the down kernel.
+constexpr int TACT_CODES = 2 * TM * 16;
+constexpr int TACT_BLOCK = TACT_CODES + TM * 4;
 
 struct Tile {
   int expert;
@@ -195,10 +203,8 @@ struct GroupedArgs {
   int ncols;     // N (I for gate/up, H for down)
   const Tile* tiles;
   const int* ntiles;
-  const int* perm;        // sorted position -> assignment
-  int k;                  // slots per token
-  const ActBlock* act;    // gate/up: [T][nb] by token; down: [A][nb] by sorted position
-  ActBlock* hact;         // gate/up output: [A][ncols/32] by sorted position
+  const uint8_t* tin;     // input: [tile][nb] TACT_BLOCK
+  uint8_t* tout;          // gate/up output: [tile][ncols/32] TACT_BLOCK
   float* y;               // down output: [A][ncols] by sorted position
 };
 
@@ -235,10 +241,7 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
 
   // Addresses are wave-uniform bases (expert, 32-column tile, block) plus a
   // 32-bit per-lane byte offset, so the block loop advances only scalars.
-  // Activation row of A operand lane: row lane % 32, clamped into the tile.
-  const int arow = tl.row0 + min(lane & 31, tl.rows - 1);
-  const int aidx = GATE_UP ? a.perm[arow] / a.k : arow;  // token (gate/up) or sorted row (down)
-  const unsigned aoff = (unsigned)aidx * (unsigned)nb * (unsigned)sizeof(ActBlock);
+  const uint8_t* tblk = a.tin + (size_t)ti * nb * TACT_BLOCK;
   const int tile_n = n0 / TILE;
   const int rn = lane & 31;  // column within the tile
   const size_t e = (size_t)tl.expert;
@@ -249,7 +252,6 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   const uint16_t* su = GATE_UP ? a.scales2 + e * a.scales_stride + splane : nullptr;
   const unsigned coff = (unsigned)rn * 16 + (DT == Q8_0 ? (unsigned)h * TILE * 16 : 0u);
   const unsigned soff = (unsigned)rn * 2;
-  const char* actb = (const char*)a.act;
 
   // accumulators start at +0.0 like the reference's `let mut total = 0.0`,
   // so no sum can become -0.0: the sign of a zero scale product never shows
@@ -265,9 +267,9 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   // same column group, and neighbouring items run on one XCD, so the later
   // tiles find the lines in L2.
   auto load = [&](Ops& o, int b) {
-    const char* ab = actb + (size_t)b * sizeof(ActBlock);
-    o.xr = *(const u32x4*)(ab + aoff + 16 * h);
-    o.dx = *(const float*)(ab + aoff + 32);
+    const uint8_t* tb = tblk + (size_t)b * TACT_BLOCK;
+    o.xr = *(const u32x4*)(tb + h * (TM * 16) + rn * 16);
+    o.dx = *(const float*)(tb + TACT_CODES + rn * 4);
     const size_t cb = (size_t)b * CH * TILE * 16;
     o.wg = *(const u32x4*)(cg + cb + coff);
     o.dg = *(const uint16_t*)((const char*)(sg + (size_t)b * TILE) + soff);
@@ -313,7 +315,10 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   // sets are larger and which is bound by its VALU work, not by latency).
   // The loop body has no branches (so the load counters are tracked across
   // iterations): blocks past the end are loaded clamped to the last block
-  // and computed with zero scales.
+  // and computed with zero scales.  The scheduling barriers keep each
+  // block's loads where they are issued; left free, the scheduler sinks
+  // some of them next to their use to save registers, and the wave then
+  // waits out a whole L2 round trip.
   constexpr int NS = GATE_UP ? 2 : 4;
   Ops S[NS];
 #pragma unroll
@@ -322,17 +327,21 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
 #pragma unroll
     for (int j = 0; j < NS; j++) {
       load(S[(j + NS - 1) % NS], min(b + j + NS - 1, nb - 1));
+      __builtin_amdgcn_sched_barrier(0);
       compute(S[j], b + j < nb);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
   if constexpr (GATE_UP) {
     // h = silu(g) * u, quantized per (row, 32-column block): the 32 columns
-    // of a row sit in the 32 lanes of one half
+    // of a row sit in the 32 lanes of one half.  All 32 rows of the tile are
+    // written; rows past tl.rows repeat the last row's values and only ever
+    // feed result rows that the down kernel does not store.
     ExpTable tab;
     tab.load();
-    const int nblk = n0 / QK;
     const int nbo = a.ncols / QK;
+    uint8_t* tb = a.tout + ((size_t)ti * nbo + n0 / QK) * TACT_BLOCK;
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       const int row = (j % 4) + 4 * h + 8 * (j / 4);
@@ -340,14 +349,8 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
       float scale;
       int qsum;
       const int qv = quant_block_lane(hv, &scale, &qsum);
-      if (row < tl.rows) {
-        ActBlock* hb = a.hact + (size_t)(tl.row0 + row) * nbo + nblk;
-        hb->q[lane & 31] = (int8_t)qv;
-        if ((lane & 31) == 0) {
-          hb->scale = scale;
-          hb->qsum = qsum;
-        }
-      }
+      tb[(rn >> 4) * (TM * 16) + row * 16 + (rn & 15)] = (uint8_t)(int8_t)qv;
+      if (rn == 0) *(float*)(tb + TACT_CODES + row * 4) = scale;
     }
   } else {
 #pragma unroll
@@ -356,6 +359,31 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
       if (row < tl.rows) a.y[(size_t)(tl.row0 + row) * a.ncols + n0 + rn] = accg[j];
     }
   }
+}
+
+// Gather of the gate/up input into the tile layout: work-group (tile, 8
+// blocks), thread (block, row): row r of tile ti is token perm[row0 + r] / k
+// (rows past the tile's end repeat its last row).  Grid: max_tiles x
+// ceil(nb / 8); work-groups past the live tile count exit.
+__global__ __launch_bounds__(256) void k_gather_tiles(const ActBlock* __restrict__ act, int nb,
+                                                      const Tile* __restrict__ tiles,
+                                                      const int* __restrict__ ntiles,
+                                                      const int* __restrict__ perm, int k,
+                                                      uint8_t* __restrict__ tin) {
+  const int ti = blockIdx.x;
+  if (ti >= *ntiles) return;
+  const int r = threadIdx.x & 31;
+  const int b = blockIdx.y * 8 + (threadIdx.x >> 5);
+  if (b >= nb) return;
+  const Tile tl = tiles[ti];
+  const int tok = perm[tl.row0 + min(r, tl.rows - 1)] / k;
+  const ActBlock* src = act + (size_t)tok * nb + b;
+  const u32x4 lo = *(const u32x4*)src->q;
+  const u32x4 hi = *(const u32x4*)(src->q + 16);
+  uint8_t* dst = tin + ((size_t)ti * nb + b) * TACT_BLOCK;
+  *(u32x4*)(dst + r * 16) = lo;
+  *(u32x4*)(dst + TM * 16 + r * 16) = hi;
+  *(float*)(dst + TACT_CODES + r * 4) = src->scale;
 }
 
 // out[t] = 0, then out[t] = out[t] + w[t][s] * y[pos(t, s)] for s in route
@@ -382,7 +410,7 @@ size_t prefill_min_tokens(size_t) { return 8; }
 static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 struct WsLayout {
-  size_t perm, pos_of, tiles, ntiles, hact, y, total;
+  size_t perm, pos_of, tiles, ntiles, tin, tact, y, total;
   size_t max_tiles;
 };
 
@@ -399,8 +427,10 @@ static WsLayout ws_layout(const PrefillLayer& L, size_t T) {
   o += align256(w.max_tiles * sizeof(Tile));
   w.ntiles = o;
   o += 256;
-  w.hact = o;
-  o += align256(A * (size_t)(L.I / QK) * sizeof(ActBlock));
+  w.tin = o;
+  o += align256(w.max_tiles * (size_t)(L.H / QK) * TACT_BLOCK);
+  w.tact = o;
+  o += align256(w.max_tiles * (size_t)(L.I / QK) * TACT_BLOCK);
   w.y = o;
   o += align256(A * (size_t)L.H * 4);
   w.total = o;
@@ -429,7 +459,8 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   int* pos_of = (int*)(b + w.pos_of);
   Tile* tiles = (Tile*)(b + w.tiles);
   int* ntiles = (int*)(b + w.ntiles);
-  ActBlock* hact = (ActBlock*)(b + w.hact);
+  uint8_t* tin = (uint8_t*)(b + w.tin);
+  uint8_t* tact = (uint8_t*)(b + w.tact);
   float* y = (float*)(b + w.y);
   const int nbh = L.H / QK, nbi = L.I / QK;
   const size_t A = T * (size_t)L.k;
@@ -454,7 +485,11 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   // 2. group assignments by expert
   HALE_STEP(K_GROUP, launch(k_group, 1, 64 * GROUP_WAVES, 0, st, L.route_idx, (int)A, L.E, perm,
                             pos_of, tiles, ntiles));
-  // 3. grouped gate/up with SiLU and requantization
+  // 3. gather the activations into tiles, then the grouped gate/up with SiLU
+  // and requantization
+  HALE_STEP(K_GATHER, launch(k_gather_tiles, dim3((unsigned)w.max_tiles, (unsigned)((nbh + 7) / 8)),
+                             256, 0, st, (const ActBlock*)L.act, nbh, tiles, ntiles, perm, L.k,
+                             tin));
   GroupedArgs g{};
   g.codes = L.gate_c;
   g.scales = L.gate_s;
@@ -466,10 +501,8 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   g.ncols = L.I;
   g.tiles = tiles;
   g.ntiles = ntiles;
-  g.perm = perm;
-  g.k = L.k;
-  g.act = L.act;
-  g.hact = hact;
+  g.tin = tin;
+  g.tout = tact;
   const unsigned gg = (unsigned)((w.max_tiles * ((L.I + TN - 1) / TN) + 7) / 8 * 8);
   if (L.dtype == Q8_0)
     HALE_STEP(K_GROUPED_GATE_UP, (launch(k_grouped<Q8_0, true>, gg, 256, 0, st, g)));
@@ -485,9 +518,7 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   d.ncols = L.H;
   d.tiles = tiles;
   d.ntiles = ntiles;
-  d.perm = perm;
-  d.k = L.k;
-  d.act = hact;
+  d.tin = tact;
   d.y = y;
   const unsigned gd = (unsigned)((w.max_tiles * ((L.H + TN - 1) / TN) + 7) / 8 * 8);
   if (L.dtype == Q8_0)

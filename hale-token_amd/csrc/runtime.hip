@@ -1536,7 +1536,7 @@ extern "C" const char* hale_kernel_name(int kind) {
   static const char* names[K_KINDS] = {"route", "gate_up", "down", "act_quant", "gemv", "encode",
                                        "repack", "fill", "group", "grouped_gate_up",
                                        "grouped_down", "combine", "copy", "rms_norm",
-                                       "attention"};
+                                       "attention", "gather"};
   return kind >= 0 && kind < K_KINDS ? names[kind] : "";
 }
 
