@@ -35,6 +35,17 @@ struct alignas(16) ActBlock {
 };
 static_assert(sizeof(ActBlock) == 48, "ActBlock is 48 bytes");
 
+// ---- buffer resources ------------------------------------------------------
+//
+// A raw buffer of `bytes` bytes at p (base and size wave-uniform).  Loads
+// through it take a per-lane 32-bit offset and a wave-uniform offset, so a
+// loop that walks the buffer advances only a scalar; reads past `bytes`
+// return zero.  Word 3 0x00020000 is the raw (unswizzled, 32-bit data
+// format) setting of the CDNA buffer descriptor.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // ---- scalar conversions -------------------------------------------------
 
 __device__ __forceinline__ float h2f(uint16_t h) {

@@ -239,19 +239,22 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   const int h = lane >> 5;
   const int nb = a.nb;
 
-  // Addresses are wave-uniform bases (expert, 32-column tile, block) plus a
-  // 32-bit per-lane byte offset, so the block loop advances only scalars.
-  const uint8_t* tblk = a.tin + (size_t)ti * nb * TACT_BLOCK;
-  const int tile_n = n0 / TILE;
+  // Operands are read through buffer resources over wave-uniform planes
+  // (the tile's activations; the expert's 32-column weight tile) with a
+  // per-lane offset, so the block loop advances only scalar offsets.
   const int rn = lane & 31;  // column within the tile
-  const size_t e = (size_t)tl.expert;
+  const int tile_n = n0 / TILE;
+  const size_t e = (size_t)__builtin_amdgcn_readfirstlane(tl.expert);
   const size_t cplane = (size_t)tile_n * nb * CH * TILE * 16, splane = (size_t)tile_n * nb * TILE;
-  const uint8_t* cg = a.codes + e * a.codes_stride + cplane;
-  const uint16_t* sg = a.scales + e * a.scales_stride + splane;
-  const uint8_t* cu = GATE_UP ? a.codes2 + e * a.codes_stride + cplane : nullptr;
-  const uint16_t* su = GATE_UP ? a.scales2 + e * a.scales_stride + splane : nullptr;
-  const unsigned coff = (unsigned)rn * 16 + (DT == Q8_0 ? (unsigned)h * TILE * 16 : 0u);
-  const unsigned soff = (unsigned)rn * 2;
+  const unsigned cbytes = (unsigned)(nb * CH * TILE * 16), sbytes = (unsigned)(nb * TILE * 2);
+  const auto ra = buffer_rsrc(a.tin + (size_t)ti * nb * TACT_BLOCK, (unsigned)(nb * TACT_BLOCK));
+  const auto rg = buffer_rsrc(a.codes + e * a.codes_stride + cplane, cbytes);
+  const auto rsg = buffer_rsrc(a.scales + e * a.scales_stride + splane, sbytes);
+  const auto ru = buffer_rsrc(GATE_UP ? a.codes2 + e * a.codes_stride + cplane : a.codes, cbytes);
+  const auto rsu = buffer_rsrc(GATE_UP ? a.scales2 + e * a.scales_stride + splane : a.scales, sbytes);
+  const int xoff = h * (TM * 16) + rn * 16, dxoff = TACT_CODES + rn * 4;
+  const int coff = rn * 16 + (DT == Q8_0 ? h * TILE * 16 : 0);
+  const int soff = rn * 2;
 
   // accumulators start at +0.0 like the reference's `let mut total = 0.0`,
   // so no sum can become -0.0: the sign of a zero scale product never shows
@@ -267,15 +270,14 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
   // same column group, and neighbouring items run on one XCD, so the later
   // tiles find the lines in L2.
   auto load = [&](Ops& o, int b) {
-    const uint8_t* tb = tblk + (size_t)b * TACT_BLOCK;
-    o.xr = *(const u32x4*)(tb + h * (TM * 16) + rn * 16);
-    o.dx = *(const float*)(tb + TACT_CODES + rn * 4);
-    const size_t cb = (size_t)b * CH * TILE * 16;
-    o.wg = *(const u32x4*)(cg + cb + coff);
-    o.dg = *(const uint16_t*)((const char*)(sg + (size_t)b * TILE) + soff);
+    const int ab = b * TACT_BLOCK, cb = b * (CH * TILE * 16), sb = b * (TILE * 2);
+    o.xr = __builtin_amdgcn_raw_buffer_load_b128(ra, xoff, ab, 0);
+    o.dx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, dxoff, ab, 0));
+    o.wg = __builtin_amdgcn_raw_buffer_load_b128(rg, coff, cb, 0);
+    o.dg = __builtin_amdgcn_raw_buffer_load_b16(rsg, soff, sb, 0);
     if constexpr (GATE_UP) {
-      o.wu = *(const u32x4*)(cu + cb + coff);
-      o.du = *(const uint16_t*)((const char*)(su + (size_t)b * TILE) + soff);
+      o.wu = __builtin_amdgcn_raw_buffer_load_b128(ru, coff, cb, 0);
+      o.du = __builtin_amdgcn_raw_buffer_load_b16(rsu, soff, sb, 0);
     }
   };
   // q4_0 offset term: B = -8 in every byte makes the product -8 * sum(x) of
