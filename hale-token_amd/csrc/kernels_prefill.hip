@@ -27,6 +27,7 @@ namespace hale {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int TM = 32;          // assignments (rows) per tile
 constexpr int TN = 128;         // output columns per work-group (4 waves x 32)
@@ -217,8 +218,12 @@ struct GroupedArgs {
 // column groups), and both stay in that XCD's L2.
 constexpr int CGB = 3;
 
+// At most 128 VGPRs (four waves per SIMD): the kernel is bound by its VALU
+// work, and a fourth wave hides more of the matrix-core latency than the
+// registers above 128 would save.
 template <int DT, bool GATE_UP>
-__global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_grouped(
+    GroupedArgs a) {
   constexpr int CH = Layout<DT>::CH;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -294,18 +299,30 @@ __global__ __launch_bounds__(256) void k_grouped(GroupedArgs a) {
     v16i iu = {};
     if constexpr (GATE_UP)
       iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(o.wu, h), c0, 0, 0, 0);
-    // scale products d_w[col] * d_x[row] of the whole 32x32 tile as a K=2
-    // f32 outer product whose second K column is zero: lanes 0-31 hold
-    // A[row][0] = d_x and B[0][col] = d_w.  The matrix core rounds each
-    // product exactly like a VALU multiply (only the sign of a zero product
-    // can differ, and that cannot reach an accumulator that starts at +0).
-    const bool use = lane < 32 && valid;
-    const float ax = use ? o.dx : 0.0f;
-    v16f pg = {};
-    pg = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, use ? h2f(o.dg) : 0.0f, pg, 0, 0, 0);
-    v16f pu = {};
-    if constexpr (GATE_UP)
-      pu = __builtin_amdgcn_mfma_f32_32x32x2f32(ax, use ? h2f(o.du) : 0.0f, pu, 0, 0, 0);
+    // Scale products d_w[col] * d_x[row] of the whole 32x32 tile on the
+    // matrix core, which rounds each product exactly like a VALU multiply
+    // (only the sign of a zero product can differ, and that cannot reach an
+    // accumulator that starts at +0).  gate/up: one two-block K=1 outer
+    // product, A[row] = d_x in both halves of the wave and B[col] = the gate
+    // scale in lanes 0-31 (block 0, results 0-15), the up scale in lanes
+    // 32-63 (block 1, results 16-31).  down: a K=2 outer product whose
+    // second K column is zero: lanes 0-31 hold A[row][0] = d_x and
+    // B[0][col] = d_w.
+    v16f pg, pu;
+    if constexpr (GATE_UP) {
+      const float ax = valid ? o.dx : 0.0f;
+      const v32f p2 = __builtin_amdgcn_mfma_f32_32x32x1f32(ax, h2f(lane < 32 ? o.dg : o.du),
+                                                            v32f{}, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        pg[j] = p2[j];
+        pu[j] = p2[16 + j];
+      }
+    } else {
+      const bool use = lane < 32 && valid;
+      pg = __builtin_amdgcn_mfma_f32_32x32x2f32(use ? o.dx : 0.0f, use ? h2f(o.dg) : 0.0f, v16f{},
+                                                0, 0, 0);
+    }
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       accg[j] = accg[j] + pg[j] * (float)ig[j];
@@ -389,18 +406,32 @@ __global__ __launch_bounds__(256) void k_gather_tiles(const ActBlock* __restrict
 }
 
 // out[t] = 0, then out[t] = out[t] + w[t][s] * y[pos(t, s)] for s in route
-// order (MoeLayer::forward's combine, src/model/moe.rs:63-68).
+// order (MoeLayer::forward's combine, src/model/moe.rs:63-68).  Thread i of
+// work-group (c, t) owns columns 4i..4i+3 of column chunk c; the rows of 8
+// slots are loaded together before they are added in slot order.
+constexpr int COMBINE_COLS = 1024;
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y,
                                                  const int* __restrict__ pos_of,
                                                  const float* __restrict__ route_w, int k, int H,
                                                  float* __restrict__ out) {
   const int t = blockIdx.y;
-  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.x * COMBINE_COLS + 4 * (int)threadIdx.x;
   if (i >= H) return;
-  float acc = 0.0f;
-  for (int s = 0; s < k; s++)
-    acc = acc + route_w[(size_t)t * k + s] * y[(size_t)pos_of[(size_t)t * k + s] * H + i];
-  out[(size_t)t * H + i] = acc;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < k; s0 += 8) {
+    f32x4 v[8];
+    float w[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int s = min(s0 + j, k - 1);
+      w[j] = route_w[(size_t)t * k + s];
+      v[j] = *(const f32x4*)(y + (size_t)pos_of[(size_t)t * k + s] * H + i);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (s0 + j < k) acc = acc + w[j] * v[j];
+  }
+  *(f32x4*)(out + (size_t)t * H + i) = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -528,7 +559,7 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   else
     HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q4_0, false>, gd, 256, 0, st, d)));
   // 5. route-order combine
-  dim3 gc((unsigned)((L.H + 255) / 256), (unsigned)T);
+  dim3 gc((unsigned)((L.H + COMBINE_COLS - 1) / COMBINE_COLS), (unsigned)T);
   HALE_STEP(K_COMBINE, launch(k_combine, gc, 256, 0, st, y, pos_of, L.route_w, L.k, L.H, out));
 #undef HALE_STEP
   return hipSuccess;
