@@ -140,9 +140,10 @@ __global__ __launch_bounds__(256) void k_encode(const float* __restrict__ values
 // Activation quantization: Q8Activations::quantize (quant.rs:77-93)
 // ===========================================================================
 
-// x [ntok][n] -> act [ntok][n/32]; each 32-lane group quantizes one block.
-__global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, size_t nblocks,
-                                                   ActBlock* __restrict__ act) {
+// x [ntok][n] -> act [ntok][n/32], any alignment of x: each 32-lane group
+// quantizes one block.
+__global__ __launch_bounds__(256) void k_act_quant_any(const float* __restrict__ x, size_t nblocks,
+                                                       ActBlock* __restrict__ act) {
   size_t blk = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) / 32;
   int j = threadIdx.x & 31;
   if (blk >= nblocks) return;  // uniform across the 32-lane group
@@ -154,6 +155,36 @@ __global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, 
   if (j == 0) {
     act[blk].scale = scale;
     act[blk].qsum = qsum;
+  }
+}
+
+// The same for 16-byte aligned x; each 8-lane group quantizes one block
+// from one 16-byte load per lane.  The block maximum and the code sum are
+// order-free (max and integer sums), and scale, reciprocal and codes are
+// the expressions of quant_block_lane.
+__global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, size_t nblocks,
+                                                   ActBlock* __restrict__ act) {
+  const size_t blk = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) / 8;
+  const int j = threadIdx.x & 7;
+  if (blk >= nblocks) return;  // uniform across the 8-lane group
+  const f32x4 v = *(const f32x4*)(x + blk * QK + 4 * j);
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = fmaxf(amax, HALE_DPP_F32(amax, 0xB1));   // lane ^ 1
+  amax = fmaxf(amax, HALE_DPP_F32(amax, 0x4E));   // lane ^ 2
+  amax = fmaxf(amax, HALE_DPP_F32(amax, 0x141));  // mirror within 8 lanes
+  const float scale = amax / 127.0f;
+  const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  const int q0 = sat_i8(roundf(v.x * inv)), q1 = sat_i8(roundf(v.y * inv));
+  const int q2 = sat_i8(roundf(v.z * inv)), q3 = sat_i8(roundf(v.w * inv));
+  int qs = q0 + q1 + q2 + q3;
+  qs += __builtin_amdgcn_update_dpp(0, qs, 0xB1, 0xF, 0xF, false);
+  qs += __builtin_amdgcn_update_dpp(0, qs, 0x4E, 0xF, 0xF, false);
+  qs += __builtin_amdgcn_update_dpp(0, qs, 0x141, 0xF, 0xF, false);
+  *(unsigned*)(act[blk].q + 4 * j) = (unsigned)(q0 & 0xff) | (unsigned)(q1 & 0xff) << 8 |
+                                     (unsigned)(q2 & 0xff) << 16 | (unsigned)(q3 & 0xff) << 24;
+  if (j == 0) {
+    act[blk].scale = scale;
+    act[blk].qsum = qs;
   }
 }
 
@@ -1021,7 +1052,9 @@ hipError_t launch_encode(int dtype, const float* values, size_t nblocks, uint8_t
 
 hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipStream_t st) {
   if (nblocks == 0) return hipSuccess;
-  return launch(k_act_quant, blocks_for(nblocks * 32, 256), 256, 0, st, x, nblocks, act);
+  if ((uintptr_t)x % 16)
+    return launch(k_act_quant_any, blocks_for(nblocks * 32, 256), 256, 0, st, x, nblocks, act);
+  return launch(k_act_quant, blocks_for(nblocks * 8, 256), 256, 0, st, x, nblocks, act);
 }
 
 hipError_t launch_route_logits(const float* router, const float* x, int H, int E, int T,

@@ -58,7 +58,9 @@ struct Tile {
 // (earlier assignments to the same expert), so each expert's group keeps
 // token order.  Wave w owns a contiguous slice of the assignments; lanes
 // with equal experts in a 64-wide chunk are found with ballots over the
-// expert's bits.
+// expert's bits.  The layer's routing counts (stats, optional) grow by each
+// expert's group size here rather than by one atomic per assignment, which
+// would serialize on the popular experts' counters.
 
 __device__ __forceinline__ unsigned long long match_mask(int e, int nbits, bool valid) {
   unsigned long long m = __ballot(valid);
@@ -73,7 +75,8 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
                                                             int E, int* __restrict__ perm,
                                                             int* __restrict__ pos_of,
                                                             Tile* __restrict__ tiles,
-                                                            int* __restrict__ ntiles) {
+                                                            int* __restrict__ ntiles,
+                                                            unsigned long long* __restrict__ stats) {
   __shared__ int cnt[GROUP_WAVES][GROUP_MAX_E];
   __shared__ int scan_a[GROUP_MAX_E];
   __shared__ int scan_t[GROUP_MAX_E];
@@ -129,6 +132,7 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
     const int total = cnt[0][e];
     int base = e ? scan_a[e - 1] : 0;
     const int tot_e = scan_a[e] - base;
+    if (stats) stats[e] += (unsigned long long)tot_e;  // routing counts, one add per expert
     int run = base;
     for (int q = 0; q < GROUP_WAVES; q++) {
       const int c = q ? cnt[q][e] : total;
@@ -514,10 +518,10 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
     logits = L.logits;
   }
   HALE_STEP(K_ROUTE, launch_route_select(logits, L.E, L.k, L.normalize, (int)T, L.route_idx,
-                                         L.route_w, L.stats, st));
+                                         L.route_w, nullptr, st));
   // 2. group assignments by expert
   HALE_STEP(K_GROUP, launch(k_group, 1, 64 * GROUP_WAVES, 0, st, L.route_idx, (int)A, L.E, perm,
-                            pos_of, tiles, ntiles));
+                            pos_of, tiles, ntiles, L.stats));
   // 3. gather the activations into tiles, then the grouped gate/up with SiLU
   // and requantization
   HALE_STEP(K_GATHER, launch(k_gather_tiles, dim3((unsigned)w.max_tiles, (unsigned)((nbh + 7) / 8)),

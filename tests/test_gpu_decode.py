@@ -95,6 +95,26 @@ def test_matvec_bit_exact(ctx, dtype, rows, cols):
         assert (m.block_sums(x) == O.matvec_block_sums(dtype, rows, cols, w, x)).all()
 
 
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+@pytest.mark.parametrize("shift", [0, 4, 8, 12])
+def test_matvec_device_any_x_alignment(ctx, dtype, shift):
+    # the activation quantizer reads x 16 bytes at a time when x is 16-byte
+    # aligned and value by value otherwise; both give the oracle's bits
+    rows, cols = 256, 1024
+    w = O.encode_matrix(dtype, O.normal(rows, rows * cols, 0, 0.02).reshape(rows, cols))
+    x = O.normal(8, cols)
+    x[:32] = 0.0
+    m = H.WeightMatrix.new(ctx, rows, cols, dtype, w)
+    bx, bo = ctx.malloc(cols * 4 + 16), ctx.malloc(rows * 4)
+    bx.upload(x, offset=shift)
+    ctx.check(H.lib().hale_matvec_device(ctx.handle, m.handle, H._vp(bx.address + shift),
+                                         H._vp(bo.address)), "matvec_device")
+    got = bo.download(np.float32, rows)
+    assert same_bits(got, O.matvec(dtype, rows, cols, w, x))
+    bx.free()
+    bo.free()
+
+
 def test_matvec_rejects_wrong_lengths(ctx):
     w = O.encode_matrix(H.Q8_0, O.normal(1, 64 * 64).reshape(64, 64))
     m = H.WeightMatrix.new(ctx, 64, 64, H.Q8_0, w)

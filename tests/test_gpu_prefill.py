@@ -96,7 +96,12 @@ def test_grouped_qwen30b_prefill_512_q8(ctx):
     logits = zipf_logits(T, E, 1.1, seed=3)
     rng = np.random.default_rng(0)
     sample = sorted(set(rng.choice(T, 48, replace=False).tolist()) | {0, T - 1})
-    check(moe, L, xs, logits, sample=sample)
+    _, idx = check(moe, L, xs, logits, sample=sample)
+    # routing counts (added once per expert by the grouping kernel) equal
+    # the selections, over two forwards
+    moe.forward(xs, logits=logits)
+    counts = moe.experts.routing_counts()
+    assert (counts == 2 * np.bincount(idx.ravel(), minlength=E)).all()
 
 
 def test_grouped_qwen235b_prefill_2048_q4_sampled(ctx):
