@@ -204,46 +204,56 @@ __global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ scores
 }
 
 // The context ctx[h][c] = 0 + p_0 v_0[c] + p_1 v_1[c] + ... in position
-// order.  A work-group takes one key/value head and 16 of its columns for
-// every query head of its group (thread (query head, column) < group x 16
-// folds one chain; all 256 threads load), so each value is read once.  Values and
-// probabilities stream through two LDS tiles of T positions, staged through
-// registers: tile i + 1 loads while the chains add tile i.
+// order.  A work-group takes one key/value head, 16 of its columns and up
+// to CTX_HEADS query heads of its group: thread (query head, column) of the
+// first wave carries one chain.  A dependent f32 add costs about 10 cycles
+// on one wave and an independent multiply or LDS read can issue in its
+// shadow, so the chain wave only reads and adds: the values sit transposed
+// in LDS (a column's positions contiguous), the chain reads 4 positions of
+// its probabilities and of its column per 16-byte read, and it multiplies
+// batch k + 1 while it adds batch k.  The other three waves stream values
+// and probabilities through registers into two LDS tiles of T positions:
+// tile i + 1 is stored while tile i is added, and the NST register stages
+// keep about 60 KB per work-group in flight, which covers the latency of
+// the value stream from HBM.
 constexpr int CTX_COLS = 16;
-constexpr int CTX_LDS = 6144;  // floats per tile (values T x 16 + probabilities group x T)
+constexpr int CTX_HEADS = 4;   // query heads per work-group (64 chains: one wave)
+constexpr int CTX_LDS = 7168;  // floats per LDS tile: values [16][T + 4], probabilities [heads][T + 4]
+constexpr int CTX_MAXL = 8;    // float4 loads per loading thread per tile
 
 __global__ __launch_bounds__(256) void k_attn_ctx(const float* __restrict__ probs,
                                                   const float* __restrict__ values, int hd,
                                                   int kv_dim, int group, int seq, int ld,
                                                   float* __restrict__ ctx) {
   __shared__ __attribute__((aligned(16))) float tile[2][CTX_LDS];
-  const int g = blockIdx.x;                 // key/value head
-  const int c0 = blockIdx.y * CTX_COLS;     // first column
-  constexpr int nthr = 256;
+  const int g = blockIdx.x;               // key/value head
+  const int c0 = blockIdx.y * CTX_COLS;   // first column
+  const int h0 = blockIdx.z * CTX_HEADS;  // first query head within the group
+  const int nh = min(CTX_HEADS, group - h0);
   const int tid = threadIdx.x;
-  const bool chain = tid < group * CTX_COLS;
+  const bool chain = tid < nh * CTX_COLS;
   const int hq = tid / CTX_COLS, c = tid % CTX_COLS;
-  // positions per tile: a multiple of 4 with T * 16 + group * (T + 4) <=
-  // CTX_LDS; probability rows are T + 4 floats apart, so the query heads of
-  // a wave read distinct banks
-  const int T = (CTX_LDS - 4 * group) / (CTX_COLS + group) / 4 * 4;
-  const int PP = T + 4;                     // probability row pitch
-  const int nv4 = T * (CTX_COLS / 4);       // float4 of values per tile
-  const int np4 = group * (T / 4);          // float4 of probabilities per tile
+  constexpr int nload = 256 - 64;  // loading threads: waves 1-3
+  const int lt = tid - 64;
+  // T: a multiple of 64 that fits the LDS tile and CTX_MAXL loads per
+  // loading thread; rows are T + 4 floats apart, 4 banks apart modulo 64
+  const int t_lds = (CTX_LDS / (CTX_COLS + nh) - 4) / 64 * 64;
+  const int t_reg = CTX_MAXL * nload / (CTX_COLS / 4 + 1) / 64 * 64;
+  const int T = min(t_lds, t_reg);
+  const int RP = T + 4;
+  const int nv4 = T * (CTX_COLS / 4);  // float4 of values per tile
+  const int np4 = nh * (T / 4);        // float4 of probabilities per tile
   const int ntiles = (seq + T - 1) / T;
-  constexpr int MAXL = CTX_LDS / 4 / nthr;  // float4 loads per thread
   const float* vbase = values + (size_t)g * hd + c0;
-  const float* pbase = probs + (size_t)g * group * ld;
-  // NST register stages: tiles ti + 2 .. ti + NST are in flight while tile
-  // ti is added from LDS and tile ti + 1 waits in the other LDS buffer
-  constexpr int NST = 4;
-  f32x4 r[NST][MAXL];
+  const float* pbase = probs + ((size_t)g * group + h0) * ld;
+  constexpr int NST = 3;
+  f32x4 r[NST][CTX_MAXL];
   auto load = [&](f32x4* R, int ti) {
-    if (ti >= ntiles) return;
+    if (ti >= ntiles || lt < 0) return;
     const int t0 = ti * T, n = min(T, seq - t0);
 #pragma unroll
-    for (int j = 0; j < MAXL; j++) {
-      const int i = tid + nthr * j;
+    for (int j = 0; j < CTX_MAXL; j++) {
+      const int i = lt + nload * j;
       if (i < nv4) {
         const int t = i / (CTX_COLS / 4), q = i % (CTX_COLS / 4);
         if (t < n) R[j] = *(const f32x4*)(vbase + (size_t)(t0 + t) * kv_dim + 4 * q);
@@ -254,64 +264,99 @@ __global__ __launch_bounds__(256) void k_attn_ctx(const float* __restrict__ prob
     }
   };
   auto store = [&](const f32x4* R, int b) {
+    if (lt < 0) return;
 #pragma unroll
-    for (int j = 0; j < MAXL; j++) {
-      const int i = tid + nthr * j;
+    for (int j = 0; j < CTX_MAXL; j++) {
+      const int i = lt + nload * j;
       if (i < nv4) {
-        *(f32x4*)&tile[b][4 * i] = R[j];
+        const int t = i / (CTX_COLS / 4), q = i % (CTX_COLS / 4);
+        float* col = &tile[b][4 * q * RP + t];  // value (t, 4q + k) at row 4q + k
+        col[0] = R[j].x;
+        col[RP] = R[j].y;
+        col[2 * RP] = R[j].z;
+        col[3 * RP] = R[j].w;
       } else if (i < nv4 + np4) {
         const int k = i - nv4, hh = k / (T / 4), t = 4 * (k % (T / 4));
-        *(f32x4*)&tile[b][T * CTX_COLS + hh * PP + t] = R[j];
+        *(f32x4*)&tile[b][(CTX_COLS + hh) * RP + t] = R[j];
       }
     }
   };
   float acc = 0.0f;
-  auto fold = [&](int ti) {
-    const int n = min(T, seq - ti * T);
-    const float* vt = tile[ti & 1];
-    const float* pt = tile[ti & 1] + T * CTX_COLS + hq * PP;
-    // products of FB positions at a time in two alternating register sets:
-    // batch k + 1's LDS reads are in flight while batch k is added (FB adds
-    // overlap the next batch's reads)
-    constexpr int FB = 8;
-    float PA[FB], PB[FB];
-    auto prod = [&](float* d, int t) {
-#pragma unroll
-      for (int u = 0; u < FB; u++) d[u] = pt[t + u] * vt[(t + u) * CTX_COLS + c];
-    };
-    auto add = [&](const float* d) {
-#pragma unroll
-      for (int u = 0; u < FB; u++) acc = acc + d[u];
-    };
-    const int nbk = n / FB;
-    if (nbk > 0) prod(PA, 0);
-    int k = 0;
-    for (; k + 1 < nbk; k += 2) {
-      prod(PB, FB * (k + 1));
-      add(PA);
-      if (k + 2 < nbk) prod(PA, FB * (k + 2));
-      add(PB);
-    }
-    if (k < nbk) add(PA);
-    for (int t = FB * nbk; t < n; t++) acc = acc + pt[t] * vt[t * CTX_COLS + c];
+  struct B8 {
+    f32x4 a, b;
   };
+  // 8 consecutive floats of a row from t (reads past the tile's positions
+  // stay inside the row: t is clamped to T - 8, and those products are
+  // never added)
+  auto ld8 = [&](const float* row, int t) {
+    t = min(t, T - 8);
+    B8 x;
+    x.a = *(const f32x4*)(row + t);
+    x.b = *(const f32x4*)(row + t + 4);
+    return x;
+  };
+  // add the 8 products of D in order while the next batch's products form:
+  // one asm block fixes the alternation (the compiler's schedule would put
+  // the adds back to back, each waiting out the previous one's latency)
+  auto step = [&](const B8& D, const B8& P, const B8& V, B8& E) {
+    asm volatile(
+        "v_add_f32 %0, %0, %9\n\tv_mul_f32 %1, %17, %25\n\t"
+        "v_add_f32 %0, %0, %10\n\tv_mul_f32 %2, %18, %26\n\t"
+        "v_add_f32 %0, %0, %11\n\tv_mul_f32 %3, %19, %27\n\t"
+        "v_add_f32 %0, %0, %12\n\tv_mul_f32 %4, %20, %28\n\t"
+        "v_add_f32 %0, %0, %13\n\tv_mul_f32 %5, %21, %29\n\t"
+        "v_add_f32 %0, %0, %14\n\tv_mul_f32 %6, %22, %30\n\t"
+        "v_add_f32 %0, %0, %15\n\tv_mul_f32 %7, %23, %31\n\t"
+        "v_add_f32 %0, %0, %16\n\tv_mul_f32 %8, %24, %32"
+        : "+v"(acc), "=&v"(E.a.x), "=&v"(E.a.y), "=&v"(E.a.z), "=&v"(E.a.w), "=&v"(E.b.x),
+          "=&v"(E.b.y), "=&v"(E.b.z), "=&v"(E.b.w)
+        : "v"(D.a.x), "v"(D.a.y), "v"(D.a.z), "v"(D.a.w), "v"(D.b.x), "v"(D.b.y), "v"(D.b.z),
+          "v"(D.b.w), "v"(P.a.x), "v"(P.a.y), "v"(P.a.z), "v"(P.a.w), "v"(P.b.x), "v"(P.b.y),
+          "v"(P.b.z), "v"(P.b.w), "v"(V.a.x), "v"(V.a.y), "v"(V.a.z), "v"(V.a.w), "v"(V.b.x),
+          "v"(V.b.y), "v"(V.b.z), "v"(V.b.w));
+  };
+  auto fold = [&](int b, int n) {
+    const float* pr = &tile[b][(CTX_COLS + hq) * RP];
+    const float* vr = &tile[b][c * RP];
+    const int n8 = n & ~7;
+    if (n8 > 0) {
+      B8 P = ld8(pr, 0), V = ld8(vr, 0), D, E;
+      D.a = P.a * V.a;
+      D.b = P.b * V.b;
+      P = ld8(pr, 8);
+      V = ld8(vr, 8);
+      int t = 0;
+      for (; t + 16 <= n8; t += 16) {  // D: products of batch t, P/V: operands of t + 8
+        const B8 P2 = ld8(pr, t + 16), V2 = ld8(vr, t + 16);
+        step(D, P, V, E);
+        P = ld8(pr, t + 24);
+        V = ld8(vr, t + 24);
+        step(E, P2, V2, D);
+      }
+      if (t < n8) step(D, P, V, E);
+    }
+    for (int t = n8; t < n; t++) acc = acc + pr[t] * vr[t];
+  };
+  // stage s holds the tiles ti with ti % NST == s: tiles 0 .. NST - 1 load
+  // first, tile 0 goes to LDS and its stage takes tile NST
 #pragma unroll
   for (int j = 0; j < NST; j++) load(r[j], j);
   if (ntiles > 0) store(r[0], 0);
+  load(r[0], NST);
   __syncthreads();
   for (int ti0 = 0; ti0 < ntiles; ti0 += NST) {
 #pragma unroll
     for (int j = 0; j < NST; j++) {
       const int ti = ti0 + j;  // stage j holds tile ti (stored), stage j + 1 tile ti + 1
       if (ti < ntiles) {
-        if (chain) fold(ti);
+        if (chain) fold(ti & 1, min(T, seq - ti * T));
         if (ti + 1 < ntiles) store(r[(j + 1) % NST], (ti + 1) & 1);
         load(r[(j + 1) % NST], ti + 1 + NST);  // the stage just stored takes tile ti + 1 + NST
         __syncthreads();
       }
     }
   }
-  if (chain) ctx[(size_t)(g * group + hq) * hd + c0 + c] = acc;
+  if (chain) ctx[(size_t)(g * group + h0 + hq) * hd + c0 + c] = acc;
 }
 
 hipError_t launch_rms_norm(float* x, const float* delta, const float* w, size_t rows, size_t n,
@@ -339,7 +384,8 @@ hipError_t launch_attention_core(const AttnArgs& a, hipStream_t st) {
   if (e != hipSuccess) return e;
   e = launch(k_attn_softmax, (unsigned)a.nh, 256, 0, st, a.scores, a.seq, a.ld);
   if (e != hipSuccess) return e;
-  dim3 gc((unsigned)a.nkv, (unsigned)(a.hd / CTX_COLS));
+  const int group = a.nh / a.nkv;
+  dim3 gc((unsigned)a.nkv, (unsigned)(a.hd / CTX_COLS), (unsigned)((group + CTX_HEADS - 1) / CTX_HEADS));
   return launch(k_attn_ctx, gc, 256, 0, st, (const float*)a.scores,
                 (const float*)a.values, a.hd, kv_dim, a.nh / a.nkv, a.seq, a.ld, a.ctx);
 }

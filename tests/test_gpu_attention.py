@@ -104,13 +104,15 @@ def test_attention_decode_bit_exact(ctx, dtype, Hd, nh, nkv, hd, qk, steps):
     att.close()
 
 
-def test_attention_long_context(ctx):
-    # 1100 positions: several 256-position score blocks and context passes
-    # over more than one 1024-probability chunk
-    ref, att = build(ctx, O.BF16, 256, 8, 2, 32, seed=77, qk_norm=True, max_len=1100)
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 32), (16, 2, 16), (16, 1, 16)])
+def test_attention_long_context(ctx, nh, nkv, hd):
+    # 1100 positions with GQA groups of 4, 8 and 16: several 256-position
+    # score blocks, and context passes over 4 to 6 LDS tiles, so every
+    # register stage of the value stream is refilled more than once
+    ref, att = build(ctx, O.BF16, 256, nh, nkv, hd, seed=77, qk_norm=True, max_len=1100)
     for pos in range(1100):
         x = O.normal(5000 + pos, 256)
-        c, s = O.rope_angles(32, 1e6, pos)
+        c, s = O.rope_angles(hd, 1e6, pos)
         got = att.forward(x, pos, c, s)
         want = ref.forward(x, c, s)
         if pos % 100 == 99 or pos == 1099:
