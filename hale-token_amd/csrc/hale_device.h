@@ -187,16 +187,12 @@ __device__ __forceinline__ int half_wave_sum(int v) {
   return v;
 }
 
-// acc + p[0] + p[1] + ... + p[n-1], strictly left to right, from LDS: the
-// values before the first 16-byte boundary one by one, then 16 per batch
-// in two alternating register buffers, so the reads of batch c+1 are in
-// flight while batch c is added.
-__device__ __forceinline__ float lds_sum_in_order(const float* p, int n, float acc) {
-  int head = (int)((16 - ((uintptr_t)p & 15)) & 15) / 4;
-  if (head > n) head = n;
-  for (int i = 0; i < head; i++) acc = acc + p[i];
-  p += head;
-  n -= head;
+// acc + p[0] + p[1] + ... + p[n-1], strictly left to right, from LDS with
+// p 16-byte aligned: 16 values per batch in two alternating register
+// buffers, so the reads of batch c+1 are in flight while batch c is added,
+// then the n % 16 tail.  With a wave-uniform n the loop stays under scalar
+// control even when p differs between lanes.
+__device__ __forceinline__ float lds_sum_in_order_a16(const float* p, int n, float acc) {
   const f32x4* p4 = (const f32x4*)p;
   const int nb = n / 16;
   f32x4 A[4], B[4];
@@ -224,6 +220,16 @@ __device__ __forceinline__ float lds_sum_in_order(const float* p, int n, float a
   if (c < nb) add(A);
   for (int i = 16 * nb; i < n; i++) acc = acc + p[i];
   return acc;
+}
+
+// The same for any p: the values before the first 16-byte boundary one by
+// one, then the aligned sum.  (A p that differs between lanes makes the
+// head count, and with it the loop, divergent: use the aligned form there.)
+__device__ __forceinline__ float lds_sum_in_order(const float* p, int n, float acc) {
+  int head = (int)((16 - ((uintptr_t)p & 15)) & 15) / 4;
+  if (head > n) head = n;
+  for (int i = 0; i < head; i++) acc = acc + p[i];
+  return lds_sum_in_order_a16(p + head, n - head, acc);
 }
 
 // acc + p[0] + p[S] + ... + p[(n-1)·S], strictly left to right, from LDS:

@@ -205,158 +205,128 @@ __global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ scores
 
 // The context ctx[h][c] = 0 + p_0 v_0[c] + p_1 v_1[c] + ... in position
 // order.  A work-group takes one key/value head, 16 of its columns and up
-// to CTX_HEADS query heads of its group: thread (query head, column) of the
+// to CTX_HEADS query heads of its group; thread (query head, column) of the
 // first wave carries one chain.  A dependent f32 add costs about 10 cycles
-// on one wave and an independent multiply or LDS read can issue in its
-// shadow, so the chain wave only reads and adds: the values sit transposed
-// in LDS (a column's positions contiguous), the chain reads 4 positions of
-// its probabilities and of its column per 16-byte read, and it multiplies
-// batch k + 1 while it adds batch k.  The other three waves stream values
-// and probabilities through registers into two LDS tiles of T positions:
-// tile i + 1 is stored while tile i is added, and the NST register stages
-// keep about 60 KB per work-group in flight, which covers the latency of
-// the value stream from HBM.
+// on one wave, and one wave issues about one instruction per 6 cycles, so
+// the chains only read products and add them: one 16-byte LDS read per 4
+// positions from their own row of a product tile [head x 16 + column][T].
+// Waves 1-3 fill the product tile of tile i + 1 while the chains add tile
+// i.  Their items are 4 columns of one position's values (16 bytes, kept in
+// registers) and 4 positions of one head's probabilities (16 bytes), which
+// go to a small LDS tile one iteration before the products that use them,
+// so the probabilities that the softmax kernel has just written arrive in
+// few, wide loads.  NST register stages of items are in flight.
 constexpr int CTX_COLS = 16;
-constexpr int CTX_HEADS = 4;   // query heads per work-group (64 chains: one wave)
-constexpr int CTX_LDS = 7168;  // floats per LDS tile: values [16][T + 4], probabilities [heads][T + 4]
-constexpr int CTX_MAXL = 8;    // float4 loads per loading thread per tile
+constexpr int CTX_HEADS = 2;       // query heads per work-group (32 chains)
+constexpr int CTX_T = 256;         // positions per tile
+constexpr int CTX_RP = CTX_T + 4;  // row pitch: rows 4 banks apart modulo 64
+constexpr int CTX_ITEMS = (CTX_T * CTX_COLS / 4 + 191) / 192;  // value items per loading thread
+static_assert(CTX_HEADS * CTX_T / 4 <= 192, "one probability item per loading thread");
 
 __global__ __launch_bounds__(256) void k_attn_ctx(const float* __restrict__ probs,
                                                   const float* __restrict__ values, int hd,
                                                   int kv_dim, int group, int seq, int ld,
                                                   float* __restrict__ ctx) {
-  __shared__ __attribute__((aligned(16))) float tile[2][CTX_LDS];
+  constexpr int T = CTX_T, RP = CTX_RP;
+  __shared__ __attribute__((aligned(16))) float prod[2][CTX_HEADS * CTX_COLS * RP];
+  __shared__ __attribute__((aligned(16))) float pbuf[2][CTX_HEADS * T];
   const int g = blockIdx.x;               // key/value head
   const int c0 = blockIdx.y * CTX_COLS;   // first column
   const int h0 = blockIdx.z * CTX_HEADS;  // first query head within the group
   const int nh = min(CTX_HEADS, group - h0);
   const int tid = threadIdx.x;
-  const bool chain = tid < nh * CTX_COLS;
-  const int hq = tid / CTX_COLS, c = tid % CTX_COLS;
-  constexpr int nload = 256 - 64;  // loading threads: waves 1-3
-  const int lt = tid - 64;
-  // T: a multiple of 64 that fits the LDS tile and CTX_MAXL loads per
-  // loading thread; rows are T + 4 floats apart, 4 banks apart modulo 64
-  const int t_lds = (CTX_LDS / (CTX_COLS + nh) - 4) / 64 * 64;
-  const int t_reg = CTX_MAXL * nload / (CTX_COLS / 4 + 1) / 64 * 64;
-  const int T = min(t_lds, t_reg);
-  const int RP = T + 4;
-  const int nv4 = T * (CTX_COLS / 4);  // float4 of values per tile
-  const int np4 = nh * (T / 4);        // float4 of probabilities per tile
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ntiles = (seq + T - 1) / T;
+  auto tile_n = [&](int ti) { return min(T, seq - ti * T); };
+
+  if (wave == 0) {
+    // the chains: two barriers before the first tile, then one per tile
+    float acc = 0.0f;
+    __syncthreads();
+    __syncthreads();
+    for (int ti = 0; ti < ntiles; ti++) {
+      if (tid < nh * CTX_COLS) acc = lds_sum_in_order_a16(&prod[ti & 1][tid * RP], tile_n(ti), acc);
+      __syncthreads();
+    }
+    if (tid < nh * CTX_COLS)
+      ctx[(size_t)(g * group + h0 + tid / CTX_COLS) * hd + c0 + tid % CTX_COLS] = acc;
+    return;
+  }
+
+  // waves 1-3: value item i = lt + 192 j of a tile is position i / 4,
+  // columns 4q .. 4q + 3 with q = i % 4; probability item lt is head
+  // lt / (T / 4), positions 4 (lt % (T / 4)) .. + 3
+  constexpr int NLOAD = 192;
+  const int lt = tid - 64;
   const float* vbase = values + (size_t)g * hd + c0;
   const float* pbase = probs + ((size_t)g * group + h0) * ld;
-  constexpr int NST = 3;
-  f32x4 r[NST][CTX_MAXL];
-  auto load = [&](f32x4* R, int ti) {
-    if (ti >= ntiles || lt < 0) return;
-    const int t0 = ti * T, n = min(T, seq - t0);
+  const bool pitem = lt < nh * (T / 4);
+  const int ph = lt / (T / 4), pt = 4 * (lt % (T / 4));
+  struct Stage {
+    f32x4 v[CTX_ITEMS];
+    f32x4 p;
+  };
+  constexpr int NST = 4;
+  Stage r[NST];
+  auto load = [&](Stage& R, int ti) {
+    if (ti >= ntiles) return;
+    const int t0 = ti * T, n = tile_n(ti);
+    const float* vb = vbase + (size_t)t0 * kv_dim;
 #pragma unroll
-    for (int j = 0; j < CTX_MAXL; j++) {
-      const int i = lt + nload * j;
-      if (i < nv4) {
-        const int t = i / (CTX_COLS / 4), q = i % (CTX_COLS / 4);
-        if (t < n) R[j] = *(const f32x4*)(vbase + (size_t)(t0 + t) * kv_dim + 4 * q);
-      } else if (i < nv4 + np4) {
-        const int k = i - nv4, hh = k / (T / 4), t = 4 * (k % (T / 4));
-        if (t < n) R[j] = *(const f32x4*)(pbase + (size_t)hh * ld + t0 + t);
-      }
+    for (int j = 0; j < CTX_ITEMS; j++) {
+      const int i = lt + NLOAD * j, t = i / 4, q = i % 4;
+      if (i < T * 4 && t < n) R.v[j] = *(const f32x4*)(vb + (size_t)t * kv_dim + 4 * q);
     }
+    // reads up to 3 past n stay inside the row: ld is a multiple of 4
+    if (pitem && pt < n) R.p = *(const f32x4*)(pbase + (size_t)ph * ld + t0 + pt);
   };
-  auto store = [&](const f32x4* R, int b) {
-    if (lt < 0) return;
+  auto store_p = [&](const Stage& R, int b) {
+    if (pitem) *(f32x4*)&pbuf[b][ph * T + pt] = R.p;
+  };
+  // products of the items into product buffer b (positions past the tile's
+  // end are not written; the chains never read them)
+  auto multiply = [&](const Stage& R, int b, int n) {
 #pragma unroll
-    for (int j = 0; j < CTX_MAXL; j++) {
-      const int i = lt + nload * j;
-      if (i < nv4) {
-        const int t = i / (CTX_COLS / 4), q = i % (CTX_COLS / 4);
-        float* col = &tile[b][4 * q * RP + t];  // value (t, 4q + k) at row 4q + k
-        col[0] = R[j].x;
-        col[RP] = R[j].y;
-        col[2 * RP] = R[j].z;
-        col[3 * RP] = R[j].w;
-      } else if (i < nv4 + np4) {
-        const int k = i - nv4, hh = k / (T / 4), t = 4 * (k % (T / 4));
-        *(f32x4*)&tile[b][(CTX_COLS + hh) * RP + t] = R[j];
+    for (int j = 0; j < CTX_ITEMS; j++) {
+      const int i = lt + NLOAD * j, t = i / 4, q = i % 4;
+      if (i < T * 4 && t < n) {
+#pragma unroll
+        for (int hh = 0; hh < CTX_HEADS; hh++) {
+          if (hh < nh) {
+            const float p = pbuf[b][hh * T + t];
+            float* d = &prod[b][(hh * CTX_COLS + 4 * q) * RP + t];
+            d[0] = p * R.v[j].x;
+            d[RP] = p * R.v[j].y;
+            d[2 * RP] = p * R.v[j].z;
+            d[3 * RP] = p * R.v[j].w;
+          }
+        }
       }
     }
   };
-  float acc = 0.0f;
-  struct B8 {
-    f32x4 a, b;
-  };
-  // 8 consecutive floats of a row from t (reads past the tile's positions
-  // stay inside the row: t is clamped to T - 8, and those products are
-  // never added)
-  auto ld8 = [&](const float* row, int t) {
-    t = min(t, T - 8);
-    B8 x;
-    x.a = *(const f32x4*)(row + t);
-    x.b = *(const f32x4*)(row + t + 4);
-    return x;
-  };
-  // add the 8 products of D in order while the next batch's products form:
-  // one asm block fixes the alternation (the compiler's schedule would put
-  // the adds back to back, each waiting out the previous one's latency)
-  auto step = [&](const B8& D, const B8& P, const B8& V, B8& E) {
-    asm volatile(
-        "v_add_f32 %0, %0, %9\n\tv_mul_f32 %1, %17, %25\n\t"
-        "v_add_f32 %0, %0, %10\n\tv_mul_f32 %2, %18, %26\n\t"
-        "v_add_f32 %0, %0, %11\n\tv_mul_f32 %3, %19, %27\n\t"
-        "v_add_f32 %0, %0, %12\n\tv_mul_f32 %4, %20, %28\n\t"
-        "v_add_f32 %0, %0, %13\n\tv_mul_f32 %5, %21, %29\n\t"
-        "v_add_f32 %0, %0, %14\n\tv_mul_f32 %6, %22, %30\n\t"
-        "v_add_f32 %0, %0, %15\n\tv_mul_f32 %7, %23, %31\n\t"
-        "v_add_f32 %0, %0, %16\n\tv_mul_f32 %8, %24, %32"
-        : "+v"(acc), "=&v"(E.a.x), "=&v"(E.a.y), "=&v"(E.a.z), "=&v"(E.a.w), "=&v"(E.b.x),
-          "=&v"(E.b.y), "=&v"(E.b.z), "=&v"(E.b.w)
-        : "v"(D.a.x), "v"(D.a.y), "v"(D.a.z), "v"(D.a.w), "v"(D.b.x), "v"(D.b.y), "v"(D.b.z),
-          "v"(D.b.w), "v"(P.a.x), "v"(P.a.y), "v"(P.a.z), "v"(P.a.w), "v"(P.b.x), "v"(P.b.y),
-          "v"(P.b.z), "v"(P.b.w), "v"(V.a.x), "v"(V.a.y), "v"(V.a.z), "v"(V.a.w), "v"(V.b.x),
-          "v"(V.b.y), "v"(V.b.z), "v"(V.b.w));
-  };
-  auto fold = [&](int b, int n) {
-    const float* pr = &tile[b][(CTX_COLS + hq) * RP];
-    const float* vr = &tile[b][c * RP];
-    const int n8 = n & ~7;
-    if (n8 > 0) {
-      B8 P = ld8(pr, 0), V = ld8(vr, 0), D, E;
-      D.a = P.a * V.a;
-      D.b = P.b * V.b;
-      P = ld8(pr, 8);
-      V = ld8(vr, 8);
-      int t = 0;
-      for (; t + 16 <= n8; t += 16) {  // D: products of batch t, P/V: operands of t + 8
-        const B8 P2 = ld8(pr, t + 16), V2 = ld8(vr, t + 16);
-        step(D, P, V, E);
-        P = ld8(pr, t + 24);
-        V = ld8(vr, t + 24);
-        step(E, P2, V2, D);
-      }
-      if (t < n8) step(D, P, V, E);
-    }
-    for (int t = n8; t < n; t++) acc = acc + pr[t] * vr[t];
-  };
-  // stage s holds the tiles ti with ti % NST == s: tiles 0 .. NST - 1 load
-  // first, tile 0 goes to LDS and its stage takes tile NST
+  // Stage s holds the tiles ti with ti % NST == s.  Tile ti's probabilities
+  // go to LDS at iteration ti - 2, its products form at iteration ti - 1,
+  // and its stage is refilled at iteration ti (each step a barrier after
+  // the previous one, so no load waits for a store of the same registers).
 #pragma unroll
   for (int j = 0; j < NST; j++) load(r[j], j);
-  if (ntiles > 0) store(r[0], 0);
-  load(r[0], NST);
+  if (ntiles > 0) store_p(r[0], 0);
+  __syncthreads();
+  if (ntiles > 0) multiply(r[0], 0, tile_n(0));
+  if (ntiles > 1) store_p(r[1], 1);
   __syncthreads();
   for (int ti0 = 0; ti0 < ntiles; ti0 += NST) {
 #pragma unroll
     for (int j = 0; j < NST; j++) {
-      const int ti = ti0 + j;  // stage j holds tile ti (stored), stage j + 1 tile ti + 1
+      const int ti = ti0 + j;  // the chains add tile ti
       if (ti < ntiles) {
-        if (chain) fold(ti & 1, min(T, seq - ti * T));
-        if (ti + 1 < ntiles) store(r[(j + 1) % NST], (ti + 1) & 1);
-        load(r[(j + 1) % NST], ti + 1 + NST);  // the stage just stored takes tile ti + 1 + NST
+        if (ti + 1 < ntiles) multiply(r[(j + 1) % NST], (ti + 1) & 1, tile_n(ti + 1));
+        if (ti + 2 < ntiles) store_p(r[(j + 2) % NST], ti & 1);
+        load(r[j], ti + NST);
         __syncthreads();
       }
     }
   }
-  if (chain) ctx[(size_t)(g * group + h0 + hq) * hd + c0 + c] = acc;
 }
 
 hipError_t launch_rms_norm(float* x, const float* delta, const float* w, size_t rows, size_t n,

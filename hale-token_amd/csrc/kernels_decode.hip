@@ -265,7 +265,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
   if (tid >= 64) return;
   // acc[l] += w[8i+l]*x[8i+l] in order of i
   float acc = 0.0f;
-  if (lane < 8) acc = lds_sum_in_order(prod + lane * stride, steps, acc);
+  if (lane < 8) acc = lds_sum_in_order_a16(prod + lane * stride, steps, acc);
   float a0 = __shfl(acc, 0), a1 = __shfl(acc, 1), a2 = __shfl(acc, 2), a3 = __shfl(acc, 3);
   float a4 = __shfl(acc, 4), a5 = __shfl(acc, 5), a6 = __shfl(acc, 6), a7 = __shfl(acc, 7);
   if (lane == 0) {
