@@ -153,9 +153,14 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
 
 // softmax_in_place over each head's scores (one work-group per head): the
 // max in any order, the exponentials in parallel, their sum in order by one
-// thread (through LDS in chunks, several reads in flight), then one division
-// per score.  The probabilities replace the scores.
+// thread, then one division per score.  The probabilities replace the
+// scores.  Up to SM_CHUNK scores stay in LDS from the first read to the
+// division, and there the in-order sum (about 10 cycles per dependent add)
+// runs in lane 0 of wave 0 while waves 1-3 form the exponentials of the
+// next SM_PIPE positions.  Longer rows go through global memory in chunks
+// of SM_CHUNK.
 constexpr int SM_CHUNK = 12288;  // exponentials per LDS chunk (48 KB)
+constexpr int SM_PIPE = 512;     // positions per step of the pipelined sum
 
 __global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ scores, int seq, int ld) {
   __shared__ __attribute__((aligned(16))) float buf[SM_CHUNK];
@@ -164,24 +169,45 @@ __global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ scores
   float* sc = scores + (size_t)blockIdx.x * ld;
   const int tid = threadIdx.x;
   // max: fold(-inf, f32::max); order-free (a NaN is skipped either way)
-  // up to SM_CHUNK scores stay in LDS from the first read to the division
   const bool resident = seq <= SM_CHUNK;
+  // 16 loads per thread in flight before they are reduced
   float m = -INFINITY;
-  for (int t = tid; t < seq; t += 256) {
-    const float v = sc[t];
-    m = fmaxf(m, v);
-    if (resident) buf[t] = v;
+  for (int t0 = tid; t0 < seq; t0 += 256 * 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int t = t0 + 256 * j;
+      v[j] = t < seq ? sc[t] : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int t = t0 + 256 * j;
+      m = fmaxf(m, v[j]);
+      if (resident && t < seq) buf[t] = v[j];
+    }
   }
   m = wave_max_f32(m);
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   if (resident) {
-    for (int t = tid; t < seq; t += 256) buf[t] = hale_expf(buf[t] - m);
+    // step k: waves 1-3 exponentiate block k + 1 while lane 0 adds block k
+    const int nblk = (seq + SM_PIPE - 1) / SM_PIPE;
+    auto expo = [&](int k) {
+      const int e = min(seq, (k + 1) * SM_PIPE);
+      for (int t = k * SM_PIPE + tid - 64; t < e; t += 192) buf[t] = hale_expf(buf[t] - m);
+    };
+    float sum = 0.0f;  // sum += exp(v - max), index order
+    if (tid >= 64) expo(0);
     __syncthreads();
-    if (tid == 0) bcast[0] = lds_sum_in_order(buf, seq, 0.0f);
+    for (int k = 0; k < nblk; k++) {
+      if (tid == 0) sum = lds_sum_in_order_a16(buf + k * SM_PIPE, min(SM_PIPE, seq - k * SM_PIPE), sum);
+      else if (tid >= 64 && k + 1 < nblk) expo(k + 1);
+      __syncthreads();
+    }
+    if (tid == 0) bcast[0] = sum;
     __syncthreads();
-    const float sum = bcast[0];
+    sum = bcast[0];
     for (int t = tid; t < seq; t += 256) sc[t] = buf[t] / sum;
     return;
   }
