@@ -100,55 +100,79 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(float* __restrict__ q, cons
   }
 }
 
-// scores[h][t] = (q_h . key_t) * scale for t < seq, one thread per t.
+// scores[h][t] = (q_h . key_t) * scale for t < seq: the dot product in
+// index order from -0.0 (Iterator::sum), then one multiply.  A work-group
+// takes SC_POS positions of one key/value head for up to SC_HEADS query
+// heads of its group (thread (query head, position) carries one chain), so
+// every key row is read once per group.  Keys and the queries stream
+// through LDS in chunks of SC_W dimensions: coalesced 16-byte loads (four
+// lanes per 64-byte row piece), chunk c + 1 in registers while chunk c is
+// added, and each chain reads its 4 key and 4 query values per 16-byte read.
+constexpr int SC_POS = 32;
+constexpr int SC_HEADS = 8;
+constexpr int SC_W = 16;
+constexpr int SC_KP = SC_W + 4;  // key row pitch in LDS
+
 __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q,
                                                      const float* __restrict__ keys, int hd,
                                                      int kv_dim, int group, int seq, int ld,
                                                      float scale, float* __restrict__ scores) {
-  __shared__ __attribute__((aligned(16))) float qh[HEAD_MAX];
-  const int h = blockIdx.y;
-  const int kvo = (h / group) * hd;
-  for (int i = threadIdx.x; i < hd; i += 256) qh[i] = q[(size_t)h * hd + i];
-  __syncthreads();
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= seq) return;
-  const f32x4* key = (const f32x4*)(keys + (size_t)t * kv_dim + kvo);
+  __shared__ __attribute__((aligned(16))) float kt[2][SC_POS * SC_KP];
+  __shared__ __attribute__((aligned(16))) float qt[2][SC_HEADS * SC_W];
+  const int g = blockIdx.y;                // key/value head
+  const int h0 = blockIdx.z * SC_HEADS;    // first query head within the group
+  const int nhq = min(SC_HEADS, group - h0);
+  // work-group x runs on XCD x % 8: give each XCD a contiguous run of
+  // position blocks, so each score row is written in long runs per XCD
+  const int nbx = gridDim.x;
+  const int bx = nbx % 8 ? (int)blockIdx.x : (int)(blockIdx.x % 8) * (nbx / 8) + (int)blockIdx.x / 8;
+  const int t0 = bx * SC_POS;
+  const int tid = threadIdx.x;
+  const int hq = tid / SC_POS, tp = tid % SC_POS;
+  const bool chain = hq < nhq && t0 + tp < seq;
+  const int nc = hd / SC_W;
+  // loads of one chunk: threads 0-127 a float4 of the keys (row tid / 4,
+  // part tid % 4), threads 128 .. 128 + 4 nhq a float4 of the queries
+  const int kr = tid / 4, kq = tid % 4;
+  const bool kload = tid < SC_POS * 4 && t0 + kr < seq;
+  const int qi = tid - SC_POS * 4, qh = qi / 4, qq = qi % 4;
+  const bool qload = qi >= 0 && qh < nhq;
+  const float* krow = keys + (size_t)(t0 + kr) * kv_dim + g * hd + 4 * kq;
+  const float* qrow = q + (size_t)(g * group + h0 + qh) * hd + 4 * qq;
+  f32x4 reg = {};
+  auto load = [&](int c) {
+    if (kload) reg = *(const f32x4*)(krow + SC_W * c);
+    if (qload) reg = *(const f32x4*)(qrow + SC_W * c);
+  };
+  auto store = [&](int b) {
+    if (kload) *(f32x4*)&kt[b][kr * SC_KP + 4 * kq] = reg;
+    if (qload) *(f32x4*)&qt[b][qh * SC_W + 4 * qq] = reg;
+  };
   float s = -0.0f;  // Iterator::sum
-  // 32 key values per batch in two alternating register sets: the loads of
-  // batch b + 1 are in flight while batch b is added (hd is a multiple of 16)
-  const int nb = hd / 32;
-  f32x4 A[8], B[8];
-  auto ld8 = [&](f32x4* d, int b) {
+  load(0);
+  store(0);
+  if (nc > 1) load(1);
+  __syncthreads();
+  for (int c = 0; c < nc; c++) {
+    if (chain) {
+      const f32x4* kk = (const f32x4*)&kt[c & 1][tp * SC_KP];
+      const f32x4* qv = (const f32x4*)&qt[c & 1][hq * SC_W];
 #pragma unroll
-    for (int u = 0; u < 8; u++) d[u] = key[8 * b + u];
-  };
-  auto add8 = [&](const f32x4* d, int b) {
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int j = 32 * b + 4 * u;
-      s = s + qh[j] * d[u].x;
-      s = s + qh[j + 1] * d[u].y;
-      s = s + qh[j + 2] * d[u].z;
-      s = s + qh[j + 3] * d[u].w;
+      for (int u = 0; u < SC_W / 4; u++) {
+        const f32x4 a = qv[u], b = kk[u];
+        s = s + a.x * b.x;
+        s = s + a.y * b.y;
+        s = s + a.z * b.z;
+        s = s + a.w * b.w;
+      }
     }
-  };
-  if (nb > 0) ld8(A, 0);
-  int b = 0;
-  for (; b + 1 < nb; b += 2) {
-    ld8(B, b + 1);
-    add8(A, b);
-    if (b + 2 < nb) ld8(A, b + 2);
-    add8(B, b + 1);
+    if (c + 1 < nc) {
+      store((c + 1) & 1);  // that buffer was last read in iteration c - 1
+      if (c + 2 < nc) load(c + 2);
+    }
+    __syncthreads();
   }
-  if (b < nb) add8(A, b);
-  for (int j = 32 * nb; j < hd; j += 4) {  // a 16-value remainder
-    const f32x4 kv = key[j / 4];
-    s = s + qh[j] * kv.x;
-    s = s + qh[j + 1] * kv.y;
-    s = s + qh[j + 2] * kv.z;
-    s = s + qh[j + 3] * kv.w;
-  }
-  scores[(size_t)h * ld + t] = s * scale;
+  if (chain) scores[(size_t)(g * group + h0 + hq) * ld + t0 + tp] = s * scale;
 }
 
 // softmax_in_place over each head's scores (one work-group per head): the
@@ -374,13 +398,14 @@ hipError_t launch_attention_core(const AttnArgs& a, hipStream_t st) {
                         a.values + (size_t)(a.seq - 1) * kv_dim);
   if (e != hipSuccess) return e;
   const float scale = 1.0f / sqrtf((float)a.hd);
-  dim3 gs((unsigned)((a.seq + 255) / 256), (unsigned)a.nh);
+  const int group = a.nh / a.nkv;
+  dim3 gs((unsigned)((a.seq + SC_POS - 1) / SC_POS), (unsigned)a.nkv,
+          (unsigned)((group + SC_HEADS - 1) / SC_HEADS));
   e = launch(k_attn_scores, gs, 256, 0, st, (const float*)a.q, (const float*)a.keys, a.hd, kv_dim,
              a.nh / a.nkv, a.seq, a.ld, scale, a.scores);
   if (e != hipSuccess) return e;
   e = launch(k_attn_softmax, (unsigned)a.nh, 256, 0, st, a.scores, a.seq, a.ld);
   if (e != hipSuccess) return e;
-  const int group = a.nh / a.nkv;
   dim3 gc((unsigned)a.nkv, (unsigned)(a.hd / CTX_COLS), (unsigned)((group + CTX_HEADS - 1) / CTX_HEADS));
   return launch(k_attn_ctx, gc, 256, 0, st, (const float*)a.scores,
                 (const float*)a.values, a.hd, kv_dim, a.nh / a.nkv, a.seq, a.ld, a.ctx);
