@@ -35,8 +35,12 @@ __device__ __forceinline__ float block_inverse_rms(const float* sq, int n, float
 }
 
 // One work-group per row: out = rms_norm(x + delta, w) with x updated to
-// x + delta first when delta is given (add_in_place, then rms_norm).
-// (out may be x itself: each thread reads an element before writing it.)
+// x + delta first when delta is given (add_in_place, then rms_norm).  The
+// row and the weights are read once, all loads in flight together, and
+// stay in registers through the in-order sum of the squares.  (out may be x
+// itself: every element is read before any is written.)
+constexpr int NORM_PER = NORM_MAX / 256;  // elements per thread
+
 __global__ __launch_bounds__(256) void k_rms_norm(float* x, const float* __restrict__ delta,
                                                   const float* __restrict__ w, int n, float eps,
                                                   float* out) {
@@ -45,17 +49,38 @@ __global__ __launch_bounds__(256) void k_rms_norm(float* x, const float* __restr
   float* xr = x + (size_t)blockIdx.x * n;
   const float* dr = delta ? delta + (size_t)blockIdx.x * n : nullptr;
   float* orow = out + (size_t)blockIdx.x * n;
-  for (int i = threadIdx.x; i < n; i += 256) {
-    float v = xr[i];
-    if (dr) {
-      v = v + dr[i];
-      xr[i] = v;
+  const int tid = threadIdx.x;
+  float xv[NORM_PER], wv[NORM_PER];
+#pragma unroll
+  for (int j = 0; j < NORM_PER; j++) {
+    const int i = tid + 256 * j;
+    if (i < n) {
+      xv[j] = xr[i];
+      wv[j] = w[i];
     }
-    sq[i] = v * v;
+  }
+  if (dr) {
+#pragma unroll
+    for (int j = 0; j < NORM_PER; j++) {
+      const int i = tid + 256 * j;
+      if (i < n) {
+        xv[j] = xv[j] + dr[i];
+        xr[i] = xv[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NORM_PER; j++) {
+    const int i = tid + 256 * j;
+    if (i < n) sq[i] = xv[j] * xv[j];
   }
   __syncthreads();
   const float scale = block_inverse_rms(sq, n, eps, bcast);
-  for (int i = threadIdx.x; i < n; i += 256) orow[i] = xr[i] * scale * w[i];
+#pragma unroll
+  for (int j = 0; j < NORM_PER; j++) {
+    const int i = tid + 256 * j;
+    if (i < n) orow[i] = xv[j] * scale * wv[j];
+  }
 }
 
 // QK-norm and RoPE of every query and key head, then the cache push.
