@@ -106,9 +106,10 @@ def test_attention_decode_bit_exact(ctx, dtype, Hd, nh, nkv, hd, qk, steps):
 
 @pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 32), (16, 2, 16), (16, 1, 16)])
 def test_attention_long_context(ctx, nh, nkv, hd):
-    # 1100 positions with GQA groups of 4, 8 and 16: several 256-position
-    # score blocks, and context passes over 4 to 6 LDS tiles, so every
-    # register stage of the value stream is refilled more than once
+    # 1100 positions with GQA groups of 4, 8 and 16: 35 score blocks of 32
+    # positions, three softmax pipeline steps of 512, and context passes over
+    # five 256-position tiles, so a register stage of the value stream is
+    # refilled and both LDS buffers alternate
     ref, att = build(ctx, O.BF16, 256, nh, nkv, hd, seed=77, qk_norm=True, max_len=1100)
     for pos in range(1100):
         x = O.normal(5000 + pos, 256)
@@ -116,6 +117,20 @@ def test_attention_long_context(ctx, nh, nkv, hd):
         got = att.forward(x, pos, c, s)
         want = ref.forward(x, c, s)
         if pos % 100 == 99 or pos == 1099:
+            assert same_bits(got, want), pos
+    att.close()
+
+
+def test_attention_softmax_past_one_lds_chunk(ctx):
+    # a score row longer than the softmax keeps in LDS (12288) goes through
+    # global memory in chunks: positions on both sides of the limit
+    ref, att = build(ctx, O.F32, 64, 4, 2, 16, seed=91, qk_norm=False, max_len=12300)
+    for pos in range(12300):
+        x = O.normal(100 + pos, 64)
+        c, s = O.rope_angles(16, 1e6, pos)
+        got = att.forward(x, pos, c, s)
+        want = ref.forward(x, c, s)
+        if pos in (12286, 12287, 12288, 12299):
             assert same_bits(got, want), pos
     att.close()
 
