@@ -263,6 +263,24 @@ def test_moe_decode_mixtral_q4_bit_exact(ctx):
     moe.close()
 
 
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+@pytest.mark.parametrize("hidden,E,k", [(4096, 16, 3), (4096, 8, 8), (4160, 8, 2)])
+def test_moe_decode_wide_hidden(ctx, dtype, hidden, E, k):
+    # wide hidden sizes for both dtypes (H 4160: 520 row groups, not a
+    # multiple of 32, so the down kernel's XCD permutation of the row groups
+    # is off); 2, 3 and 8 slots per token
+    L = O.OracleMoe.synthetic(dtype, hidden, 256, E, k, normalize_topk=True, seed=hidden + E + k)
+    moe = make_layer(ctx, L)
+    for seed in range(2):
+        x = O.normal(7000 + seed, hidden)
+        out, idx, w = moe.forward(x, return_routes=True)
+        o_out, o_idx, o_w = L.forward(x, nthreads=8)
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+    moe.close()
+
+
 def test_copy_device(ctx):
     n = 3 * 1024 * 1024 + 48
     a, b = ctx.malloc(n), ctx.malloc(n)
