@@ -404,6 +404,154 @@ __global__ __launch_bounds__(256) void k_attn_ctx(const float* __restrict__ prob
   }
 }
 
+// softmax_in_place and the context in one kernel for score rows up to
+// SMC_MAX positions: work-group (key/value head, 16 columns, 2 query heads)
+// as in k_attn_ctx.  It reads its heads' scores into LDS, takes each head's
+// max, then lanes 0 and 1 of wave 0 carry the two heads' in-order sums of
+// the exp values while waves 1-3 form the exponentials SM_PIPE positions
+// ahead.  The context follows as in k_attn_ctx, except that a product's
+// probability is formed where it is used (exp value / sum, the reference's
+// division), and the first value tiles are loaded before the softmax
+// starts.  The eight work-groups of a head pair each repeat its softmax;
+// that work hides under the sum chain, and no probability goes back to
+// memory.
+constexpr int SMC_MAX = 8192;
+
+__global__ __launch_bounds__(256) void k_attn_softmax_ctx(const float* __restrict__ scores,
+                                                          const float* __restrict__ values, int hd,
+                                                          int kv_dim, int group, int seq, int ld,
+                                                          float* __restrict__ ctx) {
+  constexpr int T = CTX_T, RP = CTX_RP;
+  __shared__ __attribute__((aligned(16))) float ebuf[CTX_HEADS][SMC_MAX];
+  __shared__ __attribute__((aligned(16))) float prod[2][CTX_HEADS * CTX_COLS * RP];
+  __shared__ float red[CTX_HEADS][4];
+  __shared__ float s_sum[CTX_HEADS];
+  const int g = blockIdx.x;               // key/value head
+  const int c0 = blockIdx.y * CTX_COLS;   // first column
+  const int h0 = blockIdx.z * CTX_HEADS;  // first query head within the group
+  const int nh = min(CTX_HEADS, group - h0);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int ntiles = (seq + T - 1) / T;
+  auto tile_n = [&](int ti) { return min(T, seq - ti * T); };
+  const float* srow = scores + ((size_t)g * group + h0) * ld;
+
+  // value items of waves 1-3 (as in k_attn_ctx); the first NST tiles go out
+  // before the softmax
+  constexpr int NLOAD = 192;
+  const int lt = tid - 64;
+  const float* vbase = values + (size_t)g * hd + c0;
+  constexpr int NST = 4;
+  f32x4 r[NST][CTX_ITEMS];
+  auto load = [&](f32x4* R, int ti) {
+    if (ti >= ntiles || lt < 0) return;
+    const int t0 = ti * T, n = tile_n(ti);
+    const float* vb = vbase + (size_t)t0 * kv_dim;
+#pragma unroll
+    for (int j = 0; j < CTX_ITEMS; j++) {
+      const int i = lt + NLOAD * j, t = i / 4, q = i % 4;
+      if (i < T * 4 && t < n) R[j] = *(const f32x4*)(vb + (size_t)t * kv_dim + 4 * q);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < NST; j++) load(r[j], j);
+
+  // softmax: each head's max (order-free), exp values in place, in-order sum
+  float mx[CTX_HEADS];
+#pragma unroll
+  for (int hh = 0; hh < CTX_HEADS; hh++) {
+    float m = -INFINITY;
+    if (hh < nh) {
+      for (int t0 = tid; t0 < seq; t0 += 256 * 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const int t = t0 + 256 * j;
+          v[j] = t < seq ? srow[(size_t)hh * ld + t] : -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const int t = t0 + 256 * j;
+          m = fmaxf(m, v[j]);
+          if (t < seq) ebuf[hh][t] = v[j];
+        }
+      }
+    }
+    m = wave_max_f32(m);
+    if (lane == 0) red[hh][wave] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int hh = 0; hh < CTX_HEADS; hh++)
+    mx[hh] = fmaxf(fmaxf(red[hh][0], red[hh][1]), fmaxf(red[hh][2], red[hh][3]));
+  const int nblk = (seq + SM_PIPE - 1) / SM_PIPE;
+  auto expo = [&](int k) {  // waves 1-3: the exp values of block k of every head
+    const int b0 = k * SM_PIPE, len = min(SM_PIPE, seq - b0);
+    for (int i = lt; i < nh * len; i += NLOAD) {
+      const int hh = i / len, t = b0 + i % len;
+      ebuf[hh][t] = hale_expf(ebuf[hh][t] - (hh ? mx[1] : mx[0]));
+    }
+  };
+  float sum = 0.0f;  // lane hh of wave 0: sum += exp(v - max), index order
+  if (lt >= 0) expo(0);
+  __syncthreads();
+  for (int k = 0; k < nblk; k++) {
+    if (wave == 0) {
+      if (lane < nh)
+        sum = lds_sum_in_order_a16(&ebuf[lane][k * SM_PIPE], min(SM_PIPE, seq - k * SM_PIPE), sum);
+    } else if (k + 1 < nblk) {
+      expo(k + 1);
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && lane < nh) s_sum[lane] = sum;
+  __syncthreads();
+  float sm[CTX_HEADS];
+#pragma unroll
+  for (int hh = 0; hh < CTX_HEADS; hh++) sm[hh] = hh < nh ? s_sum[hh] : 1.0f;
+
+  // context: products p_t v_t[c] with p_t = e_t / sum, tile i + 1 formed
+  // while the chains add tile i
+  auto multiply = [&](const f32x4* R, int ti, int b) {
+    if (lt < 0) return;
+    const int t0 = ti * T, n = tile_n(ti);
+#pragma unroll
+    for (int j = 0; j < CTX_ITEMS; j++) {
+      const int i = lt + NLOAD * j, t = i / 4, q = i % 4;
+      if (i < T * 4 && t < n) {
+#pragma unroll
+        for (int hh = 0; hh < CTX_HEADS; hh++) {
+          if (hh < nh) {
+            const float pr = ebuf[hh][t0 + t] / sm[hh];
+            float* d = &prod[b][(hh * CTX_COLS + 4 * q) * RP + t];
+            d[0] = pr * R[j].x;
+            d[RP] = pr * R[j].y;
+            d[2 * RP] = pr * R[j].z;
+            d[3 * RP] = pr * R[j].w;
+          }
+        }
+      }
+    }
+  };
+  const bool chain = tid < nh * CTX_COLS;
+  float acc = 0.0f;
+  if (ntiles > 0) multiply(r[0], 0, 0);
+  __syncthreads();
+  for (int ti0 = 0; ti0 < ntiles; ti0 += NST) {
+#pragma unroll
+    for (int j = 0; j < NST; j++) {
+      const int ti = ti0 + j;  // the chains add tile ti
+      if (ti < ntiles) {
+        if (chain) acc = lds_sum_in_order_a16(&prod[ti & 1][tid * RP], tile_n(ti), acc);
+        if (ti + 1 < ntiles) multiply(r[(j + 1) % NST], ti + 1, (ti + 1) & 1);
+        load(r[j], ti + NST);  // its products went to LDS one iteration ago
+        __syncthreads();
+      }
+    }
+  }
+  if (chain) ctx[(size_t)(g * group + h0 + tid / CTX_COLS) * hd + c0 + tid % CTX_COLS] = acc;
+}
+
 hipError_t launch_rms_norm(float* x, const float* delta, const float* w, size_t rows, size_t n,
                            float eps, float* out, hipStream_t st) {
   if (rows == 0) return hipSuccess;
@@ -429,11 +577,14 @@ hipError_t launch_attention_core(const AttnArgs& a, hipStream_t st) {
   e = launch(k_attn_scores, gs, 256, 0, st, (const float*)a.q, (const float*)a.keys, a.hd, kv_dim,
              a.nh / a.nkv, a.seq, a.ld, scale, a.scores);
   if (e != hipSuccess) return e;
+  dim3 gc((unsigned)a.nkv, (unsigned)(a.hd / CTX_COLS), (unsigned)((group + CTX_HEADS - 1) / CTX_HEADS));
+  if (a.seq <= SMC_MAX)
+    return launch(k_attn_softmax_ctx, gc, 256, 0, st, (const float*)a.scores,
+                  (const float*)a.values, a.hd, kv_dim, group, a.seq, a.ld, a.ctx);
   e = launch(k_attn_softmax, (unsigned)a.nh, 256, 0, st, a.scores, a.seq, a.ld);
   if (e != hipSuccess) return e;
-  dim3 gc((unsigned)a.nkv, (unsigned)(a.hd / CTX_COLS), (unsigned)((group + CTX_HEADS - 1) / CTX_HEADS));
   return launch(k_attn_ctx, gc, 256, 0, st, (const float*)a.scores,
-                (const float*)a.values, a.hd, kv_dim, a.nh / a.nkv, a.seq, a.ld, a.ctx);
+                (const float*)a.values, a.hd, kv_dim, group, a.seq, a.ld, a.ctx);
 }
 
 }  // namespace hale
