@@ -456,37 +456,48 @@ __global__ __launch_bounds__(256) void k_attn_softmax_ctx(const float* __restric
 #pragma unroll
   for (int j = 0; j < NST; j++) load(r[j], j);
 
-  // softmax: each head's max (order-free), exp values in place, in-order sum
+  // softmax: each head's max (order-free; both heads' loads in flight
+  // together), exp values in place, in-order sum
   float mx[CTX_HEADS];
+  {
+    float m[CTX_HEADS];
 #pragma unroll
-  for (int hh = 0; hh < CTX_HEADS; hh++) {
-    float m = -INFINITY;
-    if (hh < nh) {
-      for (int t0 = tid; t0 < seq; t0 += 256 * 16) {
-        float v[16];
+    for (int hh = 0; hh < CTX_HEADS; hh++) m[hh] = -INFINITY;
+    for (int t0 = tid; t0 < seq; t0 += 256 * 16) {
+      float v[CTX_HEADS][16];
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-          const int t = t0 + 256 * j;
-          v[j] = t < seq ? srow[(size_t)hh * ld + t] : -INFINITY;
-        }
+      for (int hh = 0; hh < CTX_HEADS; hh++)
 #pragma unroll
         for (int j = 0; j < 16; j++) {
           const int t = t0 + 256 * j;
-          m = fmaxf(m, v[j]);
-          if (t < seq) ebuf[hh][t] = v[j];
+          v[hh][j] = hh < nh && t < seq ? srow[(size_t)hh * ld + t] : -INFINITY;
         }
-      }
+#pragma unroll
+      for (int hh = 0; hh < CTX_HEADS; hh++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const int t = t0 + 256 * j;
+          m[hh] = fmaxf(m[hh], v[hh][j]);
+          if (hh < nh && t < seq) ebuf[hh][t] = v[hh][j];
+        }
     }
-    m = wave_max_f32(m);
-    if (lane == 0) red[hh][wave] = m;
+#pragma unroll
+    for (int hh = 0; hh < CTX_HEADS; hh++) {
+      const float mw = wave_max_f32(m[hh]);
+      if (lane == 0) red[hh][wave] = mw;
+    }
   }
   __syncthreads();
 #pragma unroll
   for (int hh = 0; hh < CTX_HEADS; hh++)
     mx[hh] = fmaxf(fmaxf(red[hh][0], red[hh][1]), fmaxf(red[hh][2], red[hh][3]));
-  const int nblk = (seq + SM_PIPE - 1) / SM_PIPE;
+  // blocks of the sum: a short first block (the chains start sooner), then
+  // SM_PIPE positions each
+  constexpr int FIRST = 128;
+  auto bstart = [&](int k) { return k == 0 ? 0 : min(seq, FIRST + (k - 1) * SM_PIPE); };
+  const int nblk = 1 + (max(0, seq - FIRST) + SM_PIPE - 1) / SM_PIPE;
   auto expo = [&](int k) {  // waves 1-3: the exp values of block k of every head
-    const int b0 = k * SM_PIPE, len = min(SM_PIPE, seq - b0);
+    const int b0 = bstart(k), len = bstart(k + 1) - b0;
     for (int i = lt; i < nh * len; i += NLOAD) {
       const int hh = i / len, t = b0 + i % len;
       ebuf[hh][t] = hale_expf(ebuf[hh][t] - (hh ? mx[1] : mx[0]));
@@ -497,8 +508,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_ctx(const float* __restric
   __syncthreads();
   for (int k = 0; k < nblk; k++) {
     if (wave == 0) {
-      if (lane < nh)
-        sum = lds_sum_in_order_a16(&ebuf[lane][k * SM_PIPE], min(SM_PIPE, seq - k * SM_PIPE), sum);
+      if (lane < nh) sum = lds_sum_in_order_a16(&ebuf[lane][bstart(k)], bstart(k + 1) - bstart(k), sum);
     } else if (k + 1 < nblk) {
       expo(k + 1);
     }

@@ -104,12 +104,13 @@ def test_attention_decode_bit_exact(ctx, dtype, Hd, nh, nkv, hd, qk, steps):
     att.close()
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 32), (16, 2, 16), (16, 1, 16)])
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 32), (16, 2, 16), (16, 1, 16), (6, 2, 16), (4, 4, 16)])
 def test_attention_long_context(ctx, nh, nkv, hd):
-    # 1100 positions with GQA groups of 4, 8 and 16: 35 score blocks of 32
-    # positions, three softmax pipeline steps of 512, and context passes over
-    # five 256-position tiles, so a register stage of the value stream is
-    # refilled and both LDS buffers alternate
+    # 1100 positions with GQA groups of 4, 8, 16, 3 and 1: 35 score blocks of
+    # 32 positions, three softmax pipeline steps of 512, and context passes
+    # over five 256-position tiles, so a register stage of the value stream
+    # is refilled and both LDS buffers alternate; groups 3 and 1 leave a
+    # work-group of the softmax + context kernel with one query head
     ref, att = build(ctx, O.BF16, 256, nh, nkv, hd, seed=77, qk_norm=True, max_len=1100)
     for pos in range(1100):
         x = O.normal(5000 + pos, 256)
@@ -122,15 +123,17 @@ def test_attention_long_context(ctx, nh, nkv, hd):
 
 
 def test_attention_softmax_past_one_lds_chunk(ctx):
-    # a score row longer than the softmax keeps in LDS (12288) goes through
-    # global memory in chunks: positions on both sides of the limit
+    # rows up to 8192 positions run softmax and context in one kernel, longer
+    # ones in two; a score row longer than the softmax keeps in LDS (12288)
+    # goes through global memory in chunks: positions on both sides of both
+    # limits
     ref, att = build(ctx, O.F32, 64, 4, 2, 16, seed=91, qk_norm=False, max_len=12300)
     for pos in range(12300):
         x = O.normal(100 + pos, 64)
         c, s = O.rope_angles(16, 1e6, pos)
         got = att.forward(x, pos, c, s)
         want = ref.forward(x, c, s)
-        if pos in (12286, 12287, 12288, 12299):
+        if pos in (8190, 8191, 8192, 12286, 12287, 12288, 12299):
             assert same_bits(got, want), pos
     att.close()
 
