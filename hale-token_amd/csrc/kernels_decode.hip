@@ -609,12 +609,18 @@ __device__ __forceinline__ int block_isum(const u32x4* c, const ActBlock* ab) {
   return isum;
 }
 
+// Waves per work-group: eight for gate/up (the terms of a one-token layer
+// are spread over twice the waves, so they take half as long after the
+// loads land), four for plain rows.
+template <int EPI> constexpr int gemv_waves() { return EPI == EPI_GATE_UP ? 8 : 4; }
+
 template <int DT, int EPI>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(64 * gemv_waves<EPI>()) void k_gemv(GemvArgs a) {
   constexpr int CH = Layout<DT>::CH;
-  constexpr int NW = 4;             // waves per work-group
-  constexpr int UPW = 16 / CH;      // blocks per wave per chunk (16 loads in flight)
-  constexpr int CB = UPW * NW;      // blocks per chunk
+  constexpr int NW = gemv_waves<EPI>();  // waves per work-group
+  constexpr int UPW = 64 / NW / CH;      // blocks per wave per chunk (64 / NW loads in flight)
+  constexpr int CB = UPW * NW;           // blocks per chunk
+  static_assert(UPW % 4 == 0, "terms go in groups of four blocks");
   __shared__ float terms[2][CB][GROUP];
   __shared__ ActBlock s_act[GEMV_MAX_NB];
   __shared__ int sel_idx[64];
@@ -1080,7 +1086,7 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   dim3 grid(groups, slots);
 #define HALE_GEMV_CASE(D, E)                                  \
   if (dtype == D && epi == E) {                               \
-    return launch(k_gemv<D, E>, grid, 256, 0, st, a);         \
+    return launch(k_gemv<D, E>, grid, 64 * gemv_waves<E>(), 0, st, a); \
   }
   HALE_GEMV_CASE(Q8_0, EPI_PLAIN)
   HALE_GEMV_CASE(Q8_0, EPI_GATE_UP)
