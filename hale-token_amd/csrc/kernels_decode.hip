@@ -609,15 +609,14 @@ __device__ __forceinline__ int block_isum(const u32x4* c, const ActBlock* ab) {
   return isum;
 }
 
-// Waves per work-group: eight for gate/up (the terms of a one-token layer
-// are spread over twice the waves, so they take half as long after the
-// loads land), four for plain rows.
-template <int EPI> constexpr int gemv_waves() { return EPI == EPI_GATE_UP ? 8 : 4; }
-
-template <int DT, int EPI>
-__global__ __launch_bounds__(64 * gemv_waves<EPI>()) void k_gemv(GemvArgs a) {
+// NW waves per work-group: four for plain rows; eight for gate/up (the
+// terms of a one-token layer are spread over twice the waves, so they take
+// half as long after the loads land), sixteen for q4_0 gate/up rows that
+// fit one chunk (H <= 2048; with more chunks four loads in flight per lane
+// pipeline worse).
+template <int DT, int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   constexpr int CH = Layout<DT>::CH;
-  constexpr int NW = gemv_waves<EPI>();  // waves per work-group
   constexpr int UPW = 64 / NW / CH;      // blocks per wave per chunk (64 / NW loads in flight)
   constexpr int CB = UPW * NW;           // blocks per chunk
   static_assert(UPW % 4 == 0, "terms go in groups of four blocks");
@@ -1084,14 +1083,15 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   if (a.logits && (epi != EPI_GATE_UP || a.E > ROUTE_MAX_E || slots > 64 || slots > a.E))
     return hipErrorInvalidValue;
   dim3 grid(groups, slots);
-#define HALE_GEMV_CASE(D, E)                                  \
+#define HALE_GEMV_CASE(D, E, W)                               \
   if (dtype == D && epi == E) {                               \
-    return launch(k_gemv<D, E>, grid, 64 * gemv_waves<E>(), 0, st, a); \
+    return launch(k_gemv<D, E, W>, grid, 64 * W, 0, st, a);   \
   }
-  HALE_GEMV_CASE(Q8_0, EPI_PLAIN)
-  HALE_GEMV_CASE(Q8_0, EPI_GATE_UP)
-  HALE_GEMV_CASE(Q4_0, EPI_PLAIN)
-  HALE_GEMV_CASE(Q4_0, EPI_GATE_UP)
+  HALE_GEMV_CASE(Q8_0, EPI_PLAIN, 4)
+  HALE_GEMV_CASE(Q8_0, EPI_GATE_UP, 8)
+  HALE_GEMV_CASE(Q4_0, EPI_PLAIN, 4)
+  if (a.nb <= 64) HALE_GEMV_CASE(Q4_0, EPI_GATE_UP, 16)
+  HALE_GEMV_CASE(Q4_0, EPI_GATE_UP, 8)
 #undef HALE_GEMV_CASE
   return hipErrorInvalidValue;
 }
