@@ -799,16 +799,20 @@ __device__ __forceinline__ int div_small(int u, int n, float inv_n) {
 }
 
 constexpr int DR = DOWN_ROWS;   // rows per work-group of k_down_combine
-constexpr int DOWN_WAVES = 4;   // waves per work-group of k_down_combine
+// Waves per work-group of k_down_combine: 8 when the row groups fit the
+// CUs one work-group each (the terms after the loads land are spread over
+// twice the waves: 7.4 -> 6.2 us at H 2048), else 4, which keeps two
+// work-groups per CU (8 waves need 167 VGPRs: at H 4096, 512 row groups
+// would run in two rounds).
 constexpr int DOWN_MAX_SLOTS = 64;
 
-template <int DT>
-__global__ __launch_bounds__(64 * DOWN_WAVES) void k_down_combine(DownArgs a) {
+template <int DT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
-  constexpr int NW = DOWN_WAVES;
   constexpr int J = 64 / DR;        // units side by side in one wave-load
-  constexpr int UPW = 16 / CH;      // loads of 16 B in flight per lane
-  constexpr int CB = NW * J * UPW;  // units per chunk: 512 (q4_0), 256 (q8_0)
+  constexpr int UPW = 64 / NW / CH;  // loads of 16 B in flight per lane
+  constexpr int CB = NW * J * UPW;   // units per chunk: 512 (q4_0), 256 (q8_0)
+  static_assert(UPW % 4 == 0, "terms go in groups of four wave-loads");
   constexpr int AQ = (CB * 3 + 64 * NW - 1) / (64 * NW);
   constexpr int SPL = DOWN_MAX_SLOTS / 8;  // slots per fold lane
   // terms of row r at [r][unit]: a fold lane reads its slot's terms from
@@ -1100,8 +1104,16 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   const unsigned groups = (unsigned)(padded_rows((size_t)a.rows) / DR);
   if (groups == 0) return hipSuccess;
   if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS) return hipErrorInvalidValue;
-  if (dtype == Q8_0) return launch(k_down_combine<Q8_0>, groups, 64 * DOWN_WAVES, 0, st, a);
-  if (dtype == Q4_0) return launch(k_down_combine<Q4_0>, groups, 64 * DOWN_WAVES, 0, st, a);
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  if (groups <= (unsigned)cus) {
+    if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 8>, groups, 512, 0, st, a);
+    if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 8>, groups, 512, 0, st, a);
+  }
+  if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 4>, groups, 256, 0, st, a);
+  if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 4>, groups, 256, 0, st, a);
   return hipErrorInvalidValue;
 }
 
