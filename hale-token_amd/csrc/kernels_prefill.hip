@@ -91,13 +91,30 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
   const int a0 = w * slice, a1 = min(A, a0 + slice);
   const unsigned long long lt = (1ull << lane) - 1ull;
 
+  // The experts of GPRE chunks of 64 assignments are loaded together (one
+  // memory round trip per batch rather than per chunk).
+  constexpr int GPRE = 16;
+  auto load_batch = [&](int cb, int* ev) {
+#pragma unroll
+    for (int j = 0; j < GPRE; j++) {
+      const int a = cb + 64 * j + lane;
+      ev[j] = a < a1 ? route_idx[a] : 0;
+    }
+  };
+
   // pass 1: per-wave counts
-  for (int c = a0; c < a1; c += 64) {
-    const int a = c + lane;
-    const bool valid = a < a1;
-    const int e = valid ? route_idx[a] : 0;
-    const unsigned long long m = match_mask(e, nbits, valid);
-    if (valid && (m >> lane) == 1ull) cnt[w][e] += __popcll(m);  // highest lane of its group
+  for (int cb = a0; cb < a1; cb += 64 * GPRE) {
+    int ev[GPRE];
+    load_batch(cb, ev);
+#pragma unroll
+    for (int j = 0; j < GPRE; j++) {
+      const int a = cb + 64 * j + lane;
+      if (cb + 64 * j >= a1) break;  // wave-uniform
+      const bool valid = a < a1;
+      const int e = ev[j];
+      const unsigned long long m = match_mask(e, nbits, valid);
+      if (valid && (m >> lane) == 1ull) cnt[w][e] += __popcll(m);  // highest lane of its group
+    }
   }
   __syncthreads();
 
@@ -153,23 +170,29 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
   __syncthreads();
 
   // pass 2: stable positions
-  for (int c = a0; c < a1; c += 64) {
-    const int a = c + lane;
-    const bool valid = a < a1;
-    const int e = valid ? route_idx[a] : 0;
-    const unsigned long long m = match_mask(e, nbits, valid);
-    if (valid) {
-      const int pos = cnt[w][e] + __popcll(m & lt);
-      perm[pos] = a;
-      pos_of[a] = pos;
+  for (int cb = a0; cb < a1; cb += 64 * GPRE) {
+    int ev[GPRE];
+    load_batch(cb, ev);
+#pragma unroll
+    for (int j = 0; j < GPRE; j++) {
+      const int a = cb + 64 * j + lane;
+      if (cb + 64 * j >= a1) break;  // wave-uniform
+      const bool valid = a < a1;
+      const int e = ev[j];
+      const unsigned long long m = match_mask(e, nbits, valid);
+      if (valid) {
+        const int pos = cnt[w][e] + __popcll(m & lt);
+        perm[pos] = a;
+        pos_of[a] = pos;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (valid && (m >> lane) == 1ull) cnt[w][e] += __popcll(m);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (valid && (m >> lane) == 1ull) cnt[w][e] += __popcll(m);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
