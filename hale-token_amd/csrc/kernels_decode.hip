@@ -633,8 +633,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   const int nb = a.nb;
 
   // The activation blocks of this slot go to LDS.  With routing in the
-  // prologue, wave 0 selects the experts from the first instruction on while
-  // waves 1-3 stage the activations; otherwise every wave stages and the
+  // prologue, waves 0 and 1 select the experts from the first instruction on
+  // while the other waves stage the activations (wave 1 joins them after its
+  // part of the selection); otherwise every wave stages and the
   // weight loads are issued before the staging stores.
   const bool routing = EPI == EPI_GATE_UP && a.logits != nullptr;
   const int nstage = routing ? 64 * (NW - 1) : 64 * NW;  // staging threads
@@ -725,7 +726,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
     // Terms in groups of four blocks; each group's registers take the next
     // chunk's loads as soon as its terms are done.  The scheduling barriers
     // keep the activation reads of one group live at a time, so the kernel
-    // stays within 256 VGPRs (two work-groups per CU).
+    // keeps few VGPRs (83-134: two work-groups per CU).
     float tv[UPW];
     const bool more = ch + 1 < nchunks;
 #pragma unroll
