@@ -264,11 +264,14 @@ def test_moe_decode_mixtral_q4_bit_exact(ctx):
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-@pytest.mark.parametrize("hidden,E,k", [(4096, 16, 3), (4096, 8, 8), (4160, 8, 2)])
+@pytest.mark.parametrize("hidden,E,k", [(4096, 16, 3), (4096, 8, 8), (4160, 8, 2), (2048, 8, 8),
+                                        (2080, 8, 4)])
 def test_moe_decode_wide_hidden(ctx, dtype, hidden, E, k):
     # wide hidden sizes for both dtypes (H 4160: 520 row groups, not a
     # multiple of 32, so the down kernel's XCD permutation of the row groups
-    # is off); 2, 3 and 8 slots per token
+    # is off); 2, 3, 4 and 8 slots per token.  H 2048: one-chunk gate/up rows
+    # (16 waves for q4_0) and 256 down row groups (8 waves); H 2080: 65
+    # blocks (8 waves, two chunks) and 264 row groups (4 waves)
     L = O.OracleMoe.synthetic(dtype, hidden, 256, E, k, normalize_topk=True, seed=hidden + E + k)
     moe = make_layer(ctx, L)
     for seed in range(2):
