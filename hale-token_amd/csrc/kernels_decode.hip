@@ -9,6 +9,8 @@
 // order in one lane.
 #pragma clang fp contract(off)
 
+#include <atomic>
+
 #include "hale_device.h"
 #include "kernels.h"
 
@@ -1105,10 +1107,17 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   const unsigned groups = (unsigned)(padded_rows((size_t)a.rows) / DR);
   if (groups == 0) return hipSuccess;
   if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS) return hipErrorInvalidValue;
-  int dev = 0, cus = 0;
+  // CUs of the current device, looked up once per device
+  static std::atomic<int> cu_count[64];
+  int dev = 0;
   hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
+  int cus = dev < 64 ? cu_count[dev].load(std::memory_order_relaxed) : 0;
+  if (cus == 0) {
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    if (dev < 64) cu_count[dev].store(cus, std::memory_order_relaxed);
+  }
   if (groups <= (unsigned)cus) {
     if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 8>, groups, 512, 0, st, a);
     if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 8>, groups, 512, 0, st, a);
