@@ -499,22 +499,12 @@ static WsLayout ws_layout(const PrefillLayer& L, size_t T) {
 
 size_t prefill_workspace_bytes(const PrefillLayer& L, size_t T) { return ws_layout(L, T).total; }
 
-hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T, const float* x,
+hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const float* x,
                            const float* logits, float* out, hipStream_t st,
                            const LaunchHook& hook) {
-  if (L.E > GROUP_MAX_E || L.k < 1 || L.H % QK || L.I % QK) return hipErrorInvalidValue;
+  if (L.E > GROUP_MAX_E || L.k < 1 || L.H % QK || L.I % QK || !ws) return hipErrorInvalidValue;
   const WsLayout w = ws_layout(L, T);
-  if (ws.bytes < w.total) {
-    hipError_t e = hipStreamSynchronize(st);
-    if (e != hipSuccess) return e;
-    if (ws.base) (void)hipFree(ws.base);
-    ws.base = nullptr;
-    ws.bytes = 0;
-    e = hipMalloc(&ws.base, w.total);
-    if (e != hipSuccess) return e;
-    ws.bytes = w.total;
-  }
-  char* b = (char*)ws.base;
+  char* b = (char*)ws;
   int* perm = (int*)(b + w.perm);
   int* pos_of = (int*)(b + w.pos_of);
   Tile* tiles = (Tile*)(b + w.tiles);
@@ -590,12 +580,6 @@ hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T
   HALE_STEP(K_COMBINE, launch(k_combine, gc, 256, 0, st, y, pos_of, L.route_w, L.k, L.H, out));
 #undef HALE_STEP
   return hipSuccess;
-}
-
-void prefill_free(PrefillWorkspace& ws) {
-  if (ws.base) (void)hipFree(ws.base);
-  ws.base = nullptr;
-  ws.bytes = 0;
 }
 
 }  // namespace hale

@@ -9,7 +9,7 @@ namespace hale {
 
 struct ActBlock;
 
-// Device workspace of the grouped path, grown on demand.
+// Device workspace of the grouped path (the runtime grows it on demand).
 struct PrefillWorkspace {
   void* base = nullptr;
   size_t bytes = 0;
@@ -25,7 +25,6 @@ struct PrefillLayer {
   size_t gc_bytes, gs_elems, dc_bytes, ds_elems;  // per-expert plane sizes
   ActBlock* act;         // [T][H/32]
   float* logits;         // [T][E]
-  unsigned* tok_counters;  // [T], zero between launches
   int* route_idx;        // [T][k]
   float* route_w;        // [T][k]
   unsigned long long* stats;  // [E]
@@ -36,9 +35,10 @@ size_t prefill_min_tokens(size_t k);
 // Bytes of workspace for T tokens.
 size_t prefill_workspace_bytes(const PrefillLayer& L, size_t T);
 struct LaunchHook;
-hipError_t prefill_enqueue(const PrefillLayer& L, PrefillWorkspace& ws, size_t T, const float* x,
+// Enqueues the grouped forward of T tokens; ws holds at least
+// prefill_workspace_bytes(L, T) bytes of device memory (256-byte aligned).
+hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const float* x,
                            const float* logits, float* out, hipStream_t st,
                            const LaunchHook& hook);
-void prefill_free(PrefillWorkspace& ws);
 
 }  // namespace hale

@@ -52,6 +52,12 @@ struct hale_ctx {
   bool prof_saved = false;  // prof_on while a capture runs (profiling is off then)
   double prof_ms[K_KINDS] = {};
   uint64_t prof_n[K_KINDS] = {};
+  // Graphs keep the device addresses they were captured with.  While any
+  // graph of this context exists, scratch that a call outgrows is retired
+  // here instead of freed, so that replaying an older graph never touches
+  // freed memory; the last hale_graph_destroy frees it.
+  int live_graphs = 0;
+  std::vector<void*> retired;
 };
 
 struct hale_graph {
@@ -82,14 +88,10 @@ struct hale_moe {
   size_t gc_bytes = 0, gs_elems = 0, dc_bytes = 0, ds_elems = 0;
   std::vector<char> present;
   unsigned long long* stats = nullptr;  // [E] routing counts
-  // decode scratch
-  ActBlock* act = nullptr;  // [cap_tok][H/32]
-  float* logits = nullptr;  // [cap_tok][E]
-  unsigned* tok_counters = nullptr;  // [cap_tok]
-  int* route_idx = nullptr;  // [cap_tok][k]
-  float* route_w = nullptr;  // [cap_tok][k]
-  ActBlock* hact = nullptr;  // [k][I/32]
+  // per-token scratch (TokScratch, carved from one buffer) for cap_tok tokens
+  void* tok_base = nullptr;
   size_t cap_tok = 0;
+  ActBlock* hact = nullptr;  // [k][I/32], the decode path's requantized h
   // grouped prefill workspace
   PrefillWorkspace pw;
   // load from an expert pack: pending until the layer's next use waits for
@@ -168,6 +170,7 @@ extern "C" void hale_ctx_destroy(hale_ctx* c) {
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
+  for (void* p : c->retired) (void)hipFree(p);
   for (auto& r : c->recs) {
     (void)hipEventDestroy(r.start);
     (void)hipEventDestroy(r.stop);
@@ -193,11 +196,36 @@ extern "C" int hale_ctx_synchronize(hale_ctx* c) {
   return HALE_OK;
 }
 
+// Device memory a call has outgrown: freed at once, or kept until the last
+// graph of the context is destroyed when a graph may still use it.
+static void scratch_release(hale_ctx* c, void* p) {
+  if (!p) return;
+  if (c->live_graphs > 0)
+    c->retired.push_back(p);
+  else
+    (void)hipFree(p);
+}
+
+// Scratch may only grow outside graph capture: growing synchronizes the
+// stream and allocates, which a capture cannot record.
+static int growth_allowed(hale_ctx* c, const char* what, size_t bytes) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  HIPCHK(c, hipStreamIsCapturing(c->stream, &st));
+  if (st != hipStreamCaptureStatusNone)
+    return fail(c, HALE_EINVAL,
+                "%s must grow to %zu bytes while the stream is being captured; make the same "
+                "call once before the capture",
+                what, bytes);
+  return HALE_OK;
+}
+
 // Grows the context scratch to at least `bytes` (synchronous).
 static int ctx_scratch(hale_ctx* c, size_t bytes, void** p) {
   if (c->scratch_bytes < bytes) {
+    int rc = growth_allowed(c, "context scratch", bytes);
+    if (rc) return rc;
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    if (c->scratch) (void)hipFree(c->scratch);
+    scratch_release(c, c->scratch);
     c->scratch = nullptr;
     c->scratch_bytes = 0;
     if (hipMalloc(&c->scratch, bytes) != hipSuccess)
@@ -644,40 +672,72 @@ extern "C" int hale_expert_forward(hale_ctx* c, const hale_matrix* gate, const h
 // MoE layer
 // ---------------------------------------------------------------------------
 
-static void moe_free_scratch(hale_moe* m) {
-  (void)hipFree(m->act);
-  (void)hipFree(m->logits);
-  (void)hipFree(m->tok_counters);
-  (void)hipFree(m->route_idx);
-  (void)hipFree(m->route_w);
-  m->act = nullptr;
-  m->logits = nullptr;
-  m->tok_counters = nullptr;
-  m->route_idx = nullptr;
-  m->route_w = nullptr;
-  m->cap_tok = 0;
+// Per-token scratch of one forward over ntok tokens, carved from one
+// buffer: q8 activation blocks, router logits, the chosen experts and their
+// weights.  Nothing in it has to start at zero.
+struct TokScratch {
+  ActBlock* act;   // [ntok][H/32]
+  float* logits;   // [ntok][E]
+  int* route_idx;  // [ntok][k]
+  float* route_w;  // [ntok][k]
+};
+
+static size_t tok_scratch_bytes(const hale_moe* m, size_t ntok) {
+  return align_up(ntok * (m->H / HALE_QK) * sizeof(ActBlock), 256) + align_up(ntok * m->E * 4, 256) +
+         2 * align_up(ntok * std::max<size_t>(m->k, 1) * 4, 256);
 }
 
-// Per-token scratch for ntok tokens; counters are zeroed once here and the
-// kernels leave them zero.
-static int moe_reserve(hale_moe* m, size_t ntok) {
+static TokScratch tok_scratch_carve(const hale_moe* m, void* base, size_t ntok) {
+  char* p = (char*)base;
+  TokScratch s;
+  s.act = (ActBlock*)p;
+  p += align_up(ntok * (m->H / HALE_QK) * sizeof(ActBlock), 256);
+  s.logits = (float*)p;
+  p += align_up(ntok * m->E * 4, 256);
+  s.route_idx = (int*)p;
+  p += align_up(ntok * std::max<size_t>(m->k, 1) * 4, 256);
+  s.route_w = (float*)p;
+  return s;
+}
+
+// The layer's per-token scratch for at least ntok tokens.
+static int moe_reserve(hale_moe* m, size_t ntok, TokScratch* out) {
   hale_ctx* c = m->ctx;
-  if (m->cap_tok >= ntok) return HALE_OK;
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  moe_free_scratch(m);
-  size_t nbh = m->H / HALE_QK;
-  hipError_t e = hipMalloc(&m->act, ntok * nbh * sizeof(ActBlock));
-  if (e == hipSuccess) e = hipMalloc(&m->logits, ntok * m->E * 4);
-  if (e == hipSuccess) e = hipMalloc(&m->tok_counters, ntok * 4);
-  if (e == hipSuccess) e = hipMalloc(&m->route_idx, ntok * m->k * 4);
-  if (e == hipSuccess) e = hipMalloc(&m->route_w, ntok * m->k * 4);
-  if (e == hipSuccess) e = hipMemsetAsync(m->tok_counters, 0, ntok * 4, c->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-  if (e != hipSuccess) {
-    moe_free_scratch(m);
-    return fail(c, HALE_ENOMEM, "MoE scratch for %zu tokens: %s", ntok, hipGetErrorString(e));
+  if (m->cap_tok < ntok) {
+    const size_t bytes = tok_scratch_bytes(m, ntok);
+    int rc = growth_allowed(c, "MoE layer scratch", bytes);
+    if (rc) return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    scratch_release(c, m->tok_base);
+    m->tok_base = nullptr;
+    m->cap_tok = 0;
+    hipError_t e = hipMalloc(&m->tok_base, bytes);
+    if (e != hipSuccess) {
+      m->tok_base = nullptr;
+      return fail(c, HALE_ENOMEM, "MoE scratch for %zu tokens: %s", ntok, hipGetErrorString(e));
+    }
+    m->cap_tok = ntok;
   }
-  m->cap_tok = ntok;
+  *out = tok_scratch_carve(m, m->tok_base, m->cap_tok);
+  return HALE_OK;
+}
+
+// The layer's grouped-path workspace for at least T tokens.
+static int moe_prefill_ws(hale_moe* m, const PrefillLayer& L, size_t T, void** out) {
+  hale_ctx* c = m->ctx;
+  const size_t need = prefill_workspace_bytes(L, T);
+  if (m->pw.bytes < need) {
+    int rc = growth_allowed(c, "grouped prefill workspace", need);
+    if (rc) return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    scratch_release(c, m->pw.base);
+    m->pw.base = nullptr;
+    m->pw.bytes = 0;
+    if (hipMalloc(&m->pw.base, need) != hipSuccess)
+      return fail(c, HALE_ENOMEM, "grouped prefill workspace of %zu bytes", need);
+    m->pw.bytes = need;
+  }
+  *out = m->pw.base;
   return HALE_OK;
 }
 
@@ -724,7 +784,7 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   ALLOC(m->hact, std::max<size_t>(m->k, 1) * (I / HALE_QK) * sizeof(ActBlock));
   if (router) ALLOC(m->router, E * H * 4);
 #undef ALLOC
-  if (e == hipSuccess) e = hipMemsetAsync(m->stats, 0, E * 8, c->stream);
+  if (e == hipSuccess) e = launch_fill((float*)m->stats, 2 * E, 0.0f, c->stream);  // zero counts
   if (e == hipSuccess && router)
     e = hipMemcpyAsync(m->router, router->raw, E * H * 4, hipMemcpyDeviceToDevice, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -744,8 +804,8 @@ extern "C" void hale_moe_destroy(hale_moe* m) {
   (void)moe_wait_load(m);
   (void)hipStreamSynchronize(c->stream);
   if (m->loaded) (void)hipEventDestroy(m->loaded);
-  moe_free_scratch(m);
-  prefill_free(m->pw);
+  (void)hipFree(m->tok_base);
+  (void)hipFree(m->pw.base);
   (void)hipFree(m->gate_c);
   (void)hipFree(m->up_c);
   (void)hipFree(m->down_c);
@@ -852,23 +912,18 @@ static int check_all_present(hale_moe* m) {
 // Enqueues the decode path for ntok tokens (token t's route in slot range
 // [t*k, t*k+k)).  x/logits/out are device pointers.
 static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
-                              float* dout) {
+                              float* dout, const TokScratch& s) {
   hale_ctx* c = m->ctx;
   const int k = (int)m->k;
   const size_t nbh = m->H / HALE_QK, nbi = m->I / HALE_QK;
-  if (!m->router && !dlogits) return fail(c, HALE_EINVAL, "layer has no router: logits are required");
   if (dlogits)
-    LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, ntok * nbh, m->act, c->stream));
+    LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, ntok * nbh, s.act, c->stream));
   else
-    LAUNCH(c, K_ROUTE, launch_route_logits(m->router, dx, (int)m->H, (int)m->E, (int)ntok, m->act,
-                                           m->logits, c->stream));
-  const float* lg = dlogits ? dlogits : m->logits;
+    LAUNCH(c, K_ROUTE, launch_route_logits(m->router, dx, (int)m->H, (int)m->E, (int)ntok, s.act,
+                                           s.logits, c->stream));
+  const float* lg = dlogits ? dlogits : s.logits;
   for (size_t t = 0; t < ntok; t++) {
     float* out_t = dout + t * m->H;
-    if (k == 0) {
-      LAUNCH(c, K_FILL, launch_fill(out_t, m->H, 0.0f, c->stream));
-      continue;
-    }
     GemvArgs a{};
     a.codes = m->gate_c;
     a.scales = m->gate_s;
@@ -878,14 +933,14 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     a.scales_stride = m->gs_elems;
     a.nb = (int)nbh;
     a.rows = (int)m->I;
-    a.act = m->act + t * nbh;
+    a.act = s.act + t * nbh;
     a.act_stride = 0;
     a.route_idx = nullptr;  // the prologue selects the experts from the logits
     a.logits = lg + t * m->E;
     a.E = (int)m->E;
     a.normalize = m->normalize;
-    a.route_out_idx = m->route_idx + t * k;
-    a.route_out_w = m->route_w + t * k;
+    a.route_out_idx = s.route_idx + t * k;
+    a.route_out_w = s.route_w + t * k;
     a.stats = m->stats;
     a.hact = m->hact;
     a.hact_stride = (int)nbi;
@@ -900,8 +955,8 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     d.rows = (int)m->H;
     d.hact = m->hact;
     d.hact_stride = (int)nbi;
-    d.route_idx = m->route_idx + t * k;
-    d.route_w = m->route_w + t * k;
+    d.route_idx = s.route_idx + t * k;
+    d.route_w = s.route_w + t * k;
     d.slots = k;
     d.out = out_t;
     LAUNCH(c, K_DOWN, launch_down_combine(m->dtype, d, c->stream));
@@ -909,7 +964,7 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
   return HALE_OK;
 }
 
-static PrefillLayer prefill_layer(hale_moe* m) {
+static PrefillLayer prefill_layer(hale_moe* m, const TokScratch& s) {
   PrefillLayer L{};
   L.dtype = m->dtype;
   L.E = (int)m->E;
@@ -928,33 +983,54 @@ static PrefillLayer prefill_layer(hale_moe* m) {
   L.gs_elems = m->gs_elems;
   L.dc_bytes = m->dc_bytes;
   L.ds_elems = m->ds_elems;
-  L.act = m->act;
-  L.logits = m->logits;
-  L.tok_counters = m->tok_counters;
-  L.route_idx = m->route_idx;
-  L.route_w = m->route_w;
+  L.act = s.act;
+  L.logits = s.logits;
+  L.route_idx = s.route_idx;
+  L.route_w = s.route_w;
   L.stats = m->stats;
   return L;
 }
 
-static int moe_forward_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
-                               float* dout) {
+// Checks that apply to every forward: a pending pack load, every expert
+// present, a router or logits.
+static int moe_forward_check(hale_moe* m, const float* dlogits) {
   int rc = moe_wait_load(m);
   if (rc) return rc;
   rc = check_all_present(m);
   if (rc) return rc;
-  rc = moe_reserve(m, ntok);
-  if (rc) return rc;
-  if (ntok >= prefill_min_tokens(m->k)) {
-    if (!m->router && !dlogits)
-      return fail(m->ctx, HALE_EINVAL, "layer has no router: logits are required");
-    PrefillLayer L = prefill_layer(m);
-    hipError_t e = prefill_enqueue(L, m->pw, ntok, dx, dlogits, dout, m->ctx->stream,
-                                   ctx_hook(m->ctx));
-    if (e != hipSuccess) return fail(m->ctx, HALE_EHIP, "grouped prefill: %s", hipGetErrorString(e));
+  if (!m->router && !dlogits) return fail(m->ctx, HALE_EINVAL, "layer has no router: logits are required");
+  return HALE_OK;
+}
+
+// Enqueues MoeLayer::forward over ntok tokens with the given per-token
+// scratch and (ntok >= prefill_min_tokens) grouped workspace.  top_k = 0
+// routes nowhere: the reference's forward leaves out at zero.
+static int moe_forward_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
+                               float* dout, const TokScratch& s, void* pws) {
+  hale_ctx* c = m->ctx;
+  if (m->k == 0) {
+    LAUNCH(c, K_FILL, launch_fill(dout, ntok * m->H, 0.0f, c->stream));
     return HALE_OK;
   }
-  return moe_decode_enqueue(m, ntok, dx, dlogits, dout);
+  if (ntok >= prefill_min_tokens(m->k)) {
+    PrefillLayer L = prefill_layer(m, s);
+    hipError_t e = prefill_enqueue(L, pws, ntok, dx, dlogits, dout, c->stream, ctx_hook(c));
+    if (e != hipSuccess) return fail(c, HALE_EHIP, "grouped prefill: %s", hipGetErrorString(e));
+    return HALE_OK;
+  }
+  return moe_decode_enqueue(m, ntok, dx, dlogits, dout, s);
+}
+
+// Scratch and workspace of a forward from the layer's own (growing) buffers.
+static int moe_forward_scratch(hale_moe* m, size_t ntok, TokScratch* s, void** pws) {
+  int rc = moe_reserve(m, ntok, s);
+  if (rc) return rc;
+  *pws = nullptr;
+  if (m->k > 0 && ntok >= prefill_min_tokens(m->k)) {
+    PrefillLayer L = prefill_layer(m, *s);
+    rc = moe_prefill_ws(m, L, ntok, pws);
+  }
+  return rc;
 }
 
 extern "C" int hale_moe_forward_device(hale_moe* m, size_t ntok, const float* d_x,
@@ -965,12 +1041,18 @@ extern "C" int hale_moe_forward_device(hale_moe* m, size_t ntok, const float* d_
   if (ntok == 0) return HALE_OK;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
-  int rc = moe_forward_enqueue(m, ntok, d_x, d_logits, d_out);
+  int rc = moe_forward_check(m, d_logits);
   if (rc) return rc;
-  if (d_index)
-    HIPCHK(c, hipMemcpyAsync(d_index, m->route_idx, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
-  if (d_weight)
-    HIPCHK(c, hipMemcpyAsync(d_weight, m->route_w, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
+  TokScratch s;
+  void* pws;
+  rc = moe_forward_scratch(m, ntok, &s, &pws);
+  if (rc) return rc;
+  rc = moe_forward_enqueue(m, ntok, d_x, d_logits, d_out, s, pws);
+  if (rc) return rc;
+  if (d_index && m->k)
+    HIPCHK(c, hipMemcpyAsync(d_index, s.route_idx, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (d_weight && m->k)
+    HIPCHK(c, hipMemcpyAsync(d_weight, s.route_w, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
   return HALE_OK;
 }
 
@@ -981,21 +1063,29 @@ extern "C" int hale_moe_forward(hale_moe* m, size_t ntok, const float* x, const 
   if (ntok == 0) return HALE_OK;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_forward_check(m, logits);
+  if (rc) return rc;
   size_t xb = ntok * m->H * 4, lb = logits ? ntok * m->E * 4 : 0;
   size_t o1 = align_up(xb, 256), o2 = o1 + align_up(xb, 256);
-  void* s;
-  int rc = ctx_scratch(c, o2 + lb, &s);
+  void* sp;
+  rc = ctx_scratch(c, o2 + lb, &sp);
   if (rc) return rc;
-  float* dx = (float*)s;
-  float* dout = (float*)((char*)s + o1);
-  float* dl = logits ? (float*)((char*)s + o2) : nullptr;
+  float* dx = (float*)sp;
+  float* dout = (float*)((char*)sp + o1);
+  float* dl = logits ? (float*)((char*)sp + o2) : nullptr;
+  TokScratch s;
+  void* pws;
+  rc = moe_forward_scratch(m, ntok, &s, &pws);
+  if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream));
   if (logits) HIPCHK(c, hipMemcpyAsync(dl, logits, lb, hipMemcpyHostToDevice, c->stream));
-  rc = moe_forward_enqueue(m, ntok, dx, dl, dout);
+  rc = moe_forward_enqueue(m, ntok, dx, dl, dout, s, pws);
   if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync(out, dout, xb, hipMemcpyDeviceToHost, c->stream));
-  if (index) HIPCHK(c, hipMemcpyAsync(index, m->route_idx, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
-  if (weight) HIPCHK(c, hipMemcpyAsync(weight, m->route_w, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  if (index && m->k)
+    HIPCHK(c, hipMemcpyAsync(index, s.route_idx, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  if (weight && m->k)
+    HIPCHK(c, hipMemcpyAsync(weight, s.route_w, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   return HALE_OK;
 }
@@ -1006,19 +1096,20 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
   if (!m->router) return fail(c, HALE_EINVAL, "layer has no router matrix");
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
-  int rc = moe_reserve(m, 1);
+  if (m->k == 0) return HALE_OK;  // top_k of nothing: no routes
+  TokScratch s;
+  int rc = moe_reserve(m, 1, &s);
   if (rc) return rc;
-  void* s;
-  rc = ctx_scratch(c, m->H * 4, &s);
+  void* sp;
+  rc = ctx_scratch(c, m->H * 4, &sp);
   if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync(s, x, m->H * 4, hipMemcpyHostToDevice, c->stream));
-  LAUNCH(c, K_ROUTE, launch_route_logits(m->router, (const float*)s, (int)m->H, (int)m->E, 1,
-                                         m->act, m->logits, c->stream));
-  if (m->k > 0)
-    LAUNCH(c, K_ROUTE, launch_route_select(m->logits, (int)m->E, (int)m->k, m->normalize, 1,
-                                           m->route_idx, m->route_w, nullptr, c->stream));
-  HIPCHK(c, hipMemcpyAsync(index, m->route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipMemcpyAsync(weight, m->route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpyAsync(sp, x, m->H * 4, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_ROUTE, launch_route_logits(m->router, (const float*)sp, (int)m->H, (int)m->E, 1,
+                                         s.act, s.logits, c->stream));
+  LAUNCH(c, K_ROUTE, launch_route_select(s.logits, (int)m->E, (int)m->k, m->normalize, 1,
+                                         s.route_idx, s.route_w, nullptr, c->stream));
+  HIPCHK(c, hipMemcpyAsync(index, s.route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpyAsync(weight, s.route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   return HALE_OK;
 }
@@ -1575,6 +1666,8 @@ extern "C" int hale_graph_end(hale_ctx* c, hale_graph** out) {
     delete g;
     return fail(c, HALE_EHIP, "instantiate: %s", hipGetErrorString(e));
   }
+  std::lock_guard<std::recursive_mutex> lk(c->mu);
+  c->live_graphs++;
   *out = g;
   return HALE_OK;
 }
@@ -1590,9 +1683,15 @@ extern "C" int hale_graph_launch(hale_graph* g) {
 
 extern "C" void hale_graph_destroy(hale_graph* g) {
   if (!g) return;
-  std::lock_guard<std::recursive_mutex> lk(g->ctx->mu);
-  (void)hipStreamSynchronize(g->ctx->stream);
+  hale_ctx* c = g->ctx;
+  std::lock_guard<std::recursive_mutex> lk(c->mu);
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
   (void)hipGraphExecDestroy(g->exec);
   (void)hipGraphDestroy(g->graph);
   delete g;
+  if (--c->live_graphs == 0) {  // no graph can use the retired scratch any more
+    for (void* p : c->retired) (void)hipFree(p);
+    c->retired.clear();
+  }
 }

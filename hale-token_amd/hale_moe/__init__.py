@@ -248,12 +248,14 @@ class Context:
     def capture(self, fn) -> "Graph":
         """Records the device work `fn()` enqueues into a replayable graph."""
         self.check(lib().hale_graph_begin(self.handle), "graph_begin")
+        g = _vp()
         try:
             fn()
-        finally:
-            g = _vp()
-            rc = lib().hale_graph_end(self.handle, C.byref(g))
-        self.check(rc, "graph_end")
+        except BaseException:
+            if lib().hale_graph_end(self.handle, C.byref(g)) == OK:
+                lib().hale_graph_destroy(g)  # the partial recording is not kept
+            raise
+        self.check(lib().hale_graph_end(self.handle, C.byref(g)), "graph_end")
         return Graph(self, g)
 
     def close(self):

@@ -163,7 +163,9 @@ int hale_expert_forward(hale_ctx *ctx, const hale_matrix *gate,
  * (src/expert/mod.rs:128-137) that keeps all E experts of the layer
  * resident in HBM.  `router` is the f32 [E][H] router matrix, or NULL for a
  * layer whose router logits are supplied to hale_moe_forward.
- * normalize_topk: ModelConfig::normalize_topk (src/config.rs:205-208). */
+ * normalize_topk: ModelConfig::normalize_topk (src/config.rs:205-208).
+ * top_k is clamped to num_experts (top_k, src/ops/topk.rs:45); top_k = 0
+ * routes every token nowhere, so forward leaves out at zero. */
 int hale_moe_create(hale_ctx *ctx, uint32_t layer, size_t num_experts,
                     size_t hidden, size_t inter, int dtype, size_t top_k,
                     int normalize_topk, const hale_matrix *router,
@@ -352,7 +354,17 @@ int hale_kernel_kinds(void);
 const char *hale_kernel_name(int kind);
 
 /* Graph capture of the context's stream: the _device entry points called
- * between begin and end are recorded (not run) and replayed by launch. */
+ * between begin and end are recorded (not run) and replayed by launch.
+ * Rules:
+ *   - Scratch (the context's, a layer's per-token scratch and grouped
+ *     workspace) only grows outside a capture.  A call that would have to
+ *     grow it while the stream is being captured fails with HALE_EINVAL and
+ *     records nothing; make the same call once before the capture.
+ *   - A graph keeps the addresses it was captured with.  Scratch that a
+ *     later call outgrows while any graph of the context exists is kept,
+ *     not freed, until the last of those graphs is destroyed, so an older
+ *     graph replays correctly after a larger call.
+ *   - Matrices, layers and attention blocks a graph uses must outlive it. */
 typedef struct hale_graph hale_graph;
 int hale_graph_begin(hale_ctx *ctx);
 int hale_graph_end(hale_ctx *ctx, hale_graph **out);

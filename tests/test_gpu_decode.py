@@ -200,18 +200,35 @@ def test_moe_multi_token_equals_per_token(ctx, qwen30b_q4):
     assert_parity(out, o_out)
 
 
-def test_routing_stats_count_selections(ctx):
+def test_routing_stats_count_decode_selections(ctx):
+    """The decode path (1-7 tokens per call) counts each token's k experts
+    in the gate/up prologue."""
+    L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 8, 3, seed=5)
+    moe = make_layer(ctx, L, layer_id=3)
+    xs = O.normal(6, 10 * 64).reshape(10, 64)
+    idx = []
+    for t in range(7):  # one token at a time
+        _, i, _ = moe.forward(xs[t], return_routes=True)
+        idx.append(i)
+    _, i3, _ = moe.forward(xs[7:10], return_routes=True)  # 3 tokens in one call
+    idx = np.concatenate([np.stack(idx), i3])
+    counts = moe.experts.routing_counts()
+    assert counts.sum() == 30
+    assert (counts == np.bincount(idx.ravel(), minlength=8)).all()
+    assert moe.experts.fetch([H.ExpertKey(3, 1)]) == [H.ExpertKey(3, 1)]
+    with pytest.raises(KeyError):
+        moe.experts.fetch([H.ExpertKey(3, 8)])
+
+
+def test_routing_stats_count_grouped_selections(ctx):
+    """The grouped path (8+ tokens) adds each expert's group size once."""
     L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 8, 3, seed=5)
     moe = make_layer(ctx, L, layer_id=3)
     xs = O.normal(6, 10 * 64).reshape(10, 64)
     _, idx, _ = moe.forward(xs, return_routes=True)
     counts = moe.experts.routing_counts()
     assert counts.sum() == 30
-    for e in range(8):
-        assert counts[e] == int((idx == e).sum())
-    assert moe.experts.fetch([H.ExpertKey(3, 1)]) == [H.ExpertKey(3, 1)]
-    with pytest.raises(KeyError):
-        moe.experts.fetch([H.ExpertKey(3, 8)])
+    assert (counts == np.bincount(idx.ravel(), minlength=8)).all()
 
 
 def test_missing_expert_is_reported(ctx):
@@ -221,9 +238,11 @@ def test_missing_expert_is_reported(ctx):
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-def test_moe_logits_given_zipf_routing(ctx, dtype):
-    """Router logits supplied directly (the skewed-routing workloads)."""
-    E, Hd, I, k, T = 32, 256, 64, 4, 8
+@pytest.mark.parametrize("T", [7, 8])
+def test_moe_logits_given_zipf_routing(ctx, dtype, T):
+    """Router logits supplied directly (the skewed-routing workloads): 7
+    tokens take the decode path, 8 the grouped path."""
+    E, Hd, I, k = 32, 256, 64, 4
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
     moe = make_layer(ctx, L)
     rng = np.random.default_rng(1)
@@ -318,4 +337,66 @@ def test_moe_probability_tie_hidden_in_exp_values(ctx, k):
     assert (idx == o_idx).all()
     assert same_bits(w, o_w)
     assert_parity(out, o_out)
+    moe.close()
+
+
+@pytest.fixture(scope="module")
+def qwen235b_q4(ctx):
+    """The Qwen3-235B-A22B decode shape: 128 q4_0 experts, H 4096, I 1536,
+    top-8 renormalised, f32 router [128 x 4096]."""
+    L = O.OracleMoe.synthetic(O.Q4_0, 4096, 1536, 128, 8, normalize_topk=True, seed=303)
+    moe = make_layer(ctx, L)
+    yield L, moe
+    moe.close()
+
+
+def test_moe_decode_qwen235b_q4_bit_exact(ctx, qwen235b_q4):
+    L, moe = qwen235b_q4
+    xs = O.normal(5000, 4 * 4096).reshape(4, 4096)
+    for t in range(4):  # one token per call, as the decode loop calls it
+        out, idx, w = moe.forward(xs[t], return_routes=True)
+        o_out, o_idx, o_w = L.forward(xs[t], nthreads=8)
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+    out, idx, w = moe.forward(xs, return_routes=True)  # 4 tokens in one call
+    o_out, o_idx, o_w = L.prefill(xs, nthreads=8)
+    assert (idx == o_idx).all()
+    assert same_bits(w, o_w)
+    assert_parity(out, o_out)
+
+
+@pytest.mark.parametrize("dtype,hidden,inter", [(H.Q4_0, 2048, 2080), (H.Q4_0, 4096, 2080),
+                                                (H.Q8_0, 2048, 1056), (H.Q8_0, 4096, 1056)])
+def test_moe_decode_down_chunk_boundary(ctx, dtype, hidden, inter):
+    """Down + combine over more units (slot, block) than one chunk holds
+    (512 for q4_0, 256 for q8_0), with slot 7 straddling the chunk boundary
+    (8 slots x 65 blocks = 520; 8 x 33 = 264): the running per-slot sums cross
+    chunks.  H 2048 runs the 8-wave kernel, H 4096 the 4-wave one."""
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, 12, 8, normalize_topk=True,
+                              seed=hidden + inter)
+    moe = make_layer(ctx, L)
+    for seed in range(2):
+        x = O.normal(8000 + seed, hidden)
+        out, idx, w = moe.forward(x, return_routes=True)
+        o_out, o_idx, o_w = L.forward(x, nthreads=8)
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+    moe.close()
+
+
+def test_moe_top_k_zero_routes_nowhere(ctx):
+    """top_k = 0: top_k returns nothing, so the reference's forward leaves
+    the output at zero on the decode and the grouped path alike."""
+    L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 4, 0, normalize_topk=True, seed=2)
+    moe = make_layer(ctx, L)
+    assert moe.route(O.normal(1, 64)) == []
+    for T in (1, 3, 12):
+        xs = O.normal(T, T * 64).reshape(T, 64)
+        out, idx, w = moe.forward(xs, return_routes=True)
+        o_out, _, _ = L.prefill(xs)
+        assert idx.shape == (T, 0)
+        assert same_bits(out, o_out) and not out.any()
+    assert not moe.experts.routing_counts().any()
     moe.close()

@@ -2,8 +2,9 @@
 the oracle's token-at-a-time prefill (src/model/transformer.rs:231-239).
 
 Bar: bit-exact outputs, routes and weights (rel-L2 <= 1e-5 asserted too).
-Tokens are independent, so at the largest shape a sample of tokens is
-checked against the oracle while the GPU computes all of them.
+Tokens are independent, so at the largest shape (2048 tokens) a sample of
+tokens is checked against the oracle while the GPU computes all of them; the
+512-token workload is checked token by token in full.
 """
 import numpy as np
 import pytest
@@ -94,9 +95,7 @@ def test_grouped_qwen30b_prefill_512_q8(ctx):
     moe = make_layer(ctx, L)
     xs = O.normal(7, T * Hd).reshape(T, Hd)
     logits = zipf_logits(T, E, 1.1, seed=3)
-    rng = np.random.default_rng(0)
-    sample = sorted(set(rng.choice(T, 48, replace=False).tolist()) | {0, T - 1})
-    _, idx = check(moe, L, xs, logits, sample=sample)
+    _, idx = check(moe, L, xs, logits)  # every token against the oracle
     # routing counts (added once per expert by the grouping kernel) equal
     # the selections, over two forwards
     moe.forward(xs, logits=logits)

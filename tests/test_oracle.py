@@ -321,6 +321,87 @@ def test_softmax_reference_cases_and_closed_forms():
     assert abs(q[1] / q[0] - 2.0) < 1e-6
 
 
+def _e(v) -> np.float32:
+    return np.float32(O.expf(float(v)))
+
+
+def _f32_exp(v) -> np.float32:
+    """exp rounded once to f32 (the correctly rounded value, independent of
+    the oracle)."""
+    return np.float32(math.exp(float(np.float32(v))))
+
+
+def test_softmax_sums_in_index_order():
+    # activation.rs:14-17: `sum += *v` over the slice in index order.  With
+    # exp values 1, e, e, e and e just above 2^-24, each in-order addition
+    # rounds up by one ulp of 1 (sum 1 + 3 * 2^-23); a pairwise sum
+    # (1 + e) + (e + e) gives 1 + 2 * 2^-23 and a reversed sum
+    # ((e + e) + e) + 1 also 1 + 2 * 2^-23.
+    f = np.float32
+    l = f(-16.63553)
+    e = _f32_exp(l)
+    assert f(2.0 ** -24) < e < f(2.0 ** -24 * 1.01)
+    assert f(O.expf(float(l))) == e and O.expf(0.0) == 1.0
+    es = [f(1.0), e, e, e]
+    in_order = f(0.0)
+    for v in es:
+        in_order = f(in_order + v)
+    assert in_order == f(1.0 + 3 * 2.0 ** -23)
+    pairwise = f(f(es[0] + es[1]) + f(es[2] + es[3]))
+    reverse = f(f(f(es[3] + es[2]) + es[1]) + es[0])
+    assert pairwise == reverse == f(1.0 + 2 * 2.0 ** -23)
+    p = O.softmax([0.0, float(l), float(l), float(l)])
+    assert p[0] == f(1.0) / in_order and p[1] == e / in_order
+    assert p[0] != f(1.0) / pairwise
+    # the max is subtracted before exp: logits 100, 100 + l, ... give
+    # exp(0) = 1 for the first, exp((100 + l) - 100) for the others, summed
+    # in the same order
+    m = f(100.0)
+    d = _e(f(f(m + l) - m))
+    s3 = f(f(f(f(1.0) + d) + d) + d)
+    q = O.softmax([float(m)] + [float(f(m + l))] * 3)
+    assert q[0] == f(1.0) / s3 and q[1] == d / s3
+
+
+def test_softmax_divides_each_value_by_the_sum():
+    # activation.rs:18-20: `*v /= sum`, one correctly rounded division per
+    # value, not a multiplication by 1 / sum.  Exp values 1 and exp(-l) for
+    # a few logits: the ones where v / sum and v * (1 / sum) differ must give
+    # the division.
+    f = np.float32
+    differ = 0
+    for l in np.linspace(-3.0, -0.1, 60, dtype=np.float32):
+        e = _f32_exp(l)
+        assert f(O.expf(float(l))) == e
+        s = f(f(1.0) + e)
+        p = O.softmax([0.0, float(l)])
+        assert p[0] == f(1.0) / s and p[1] == e / s
+        if p[1] != e * (f(1.0) / s) or p[0] != f(1.0) * (f(1.0) / s):
+            differ += 1
+    assert differ >= 5  # the two forms really are told apart
+
+
+def test_silu_divides_by_one_plus_exp():
+    # activation.rs:5-7: x / (1 + exp(-x)).  The plausible alternatives,
+    # x * (1 / (1 + exp(-x))) (x * sigmoid) and x * sigmoid computed from
+    # exp(x) / (1 + exp(x)), round differently for some x; the oracle must
+    # give the division form for every x.  exp is the oracle's, which
+    # tests/test_expf.py holds equal to glibc expf on every f32 input.
+    f = np.float32
+    differ_recip = differ_sig = 0
+    for x in np.linspace(-12.0, 12.0, 481, dtype=np.float32):
+        en = f(O.expf(float(-x)))
+        assert abs(float(en) / math.exp(-float(x)) - 1.0) < 2e-7
+        div = f(x / f(f(1.0) + en))
+        assert f(O.silu(float(x))) == div, x
+        recip = f(x * f(f(1.0) / f(f(1.0) + en)))
+        ep = f(O.expf(float(x)))
+        sig = f(x * f(ep / f(f(1.0) + ep)))
+        differ_recip += recip != div
+        differ_sig += sig != div
+    assert differ_recip >= 20 and differ_sig >= 20
+
+
 def test_expf_is_glibc():
     for v in (-103.0, -20.5, -1.0, 0.0, 1e-7, 0.5, 1.0, 10.0, 88.5, 89.0):
         assert O.expf(v) == float(np.float32(math.exp(np.float32(v)))) or \
