@@ -58,6 +58,8 @@ struct hale_ctx {
   // freed memory; the last hale_graph_destroy frees it.
   int live_graphs = 0;
   std::vector<void*> retired;
+  // this device's copy of the fixed scratch array (forward without allocation)
+  void* fixed_scratch = nullptr;
 };
 
 struct hale_graph {
@@ -142,6 +144,37 @@ static bool quantized(int dtype) { return dtype == HALE_Q8_0 || dtype == HALE_Q4
 static int moe_wait_load(hale_moe* m);
 
 // ---------------------------------------------------------------------------
+// fixed scratch of the forward that allocates nothing
+// ---------------------------------------------------------------------------
+//
+// hale_moe_forward_device_noalloc takes its per-token scratch and grouped
+// workspace from this array instead of allocating.  Every device the library
+// runs on holds its own copy until the process ends.  In host code the name
+// `scratch` only stands for the array; the device address of a device's
+// copy comes from hipGetSymbolAddress, looked up once per device when the
+// first context on it is created, and only that address is ever handed to
+// kernels or copies.
+
+static __device__ __align__(256) unsigned char scratch[HALE_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_fixed_mu;
+static std::vector<void*> g_fixed_ptr;  // device index -> address of its copy
+
+// The device address of `scratch` on `device`, which must be current.
+static hipError_t fixed_scratch_address(int device, void** out) {
+  std::lock_guard<std::mutex> g(g_fixed_mu);
+  if ((size_t)device >= g_fixed_ptr.size()) g_fixed_ptr.resize((size_t)device + 1, nullptr);
+  if (!g_fixed_ptr[device]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_fixed_ptr[device] = p;
+  }
+  *out = g_fixed_ptr[device];
+  return hipSuccess;
+}
+
+// ---------------------------------------------------------------------------
 // context
 // ---------------------------------------------------------------------------
 
@@ -160,6 +193,11 @@ extern "C" int hale_ctx_create(int device, hale_ctx** out) {
       (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
     delete c;
     return fail(nullptr, HALE_EHIP, "stream creation failed: %s", hipGetErrorString(e));
+  }
+  if ((e = fixed_scratch_address(device, &c->fixed_scratch)) != hipSuccess) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return fail(nullptr, HALE_EHIP, "fixed scratch lookup failed: %s", hipGetErrorString(e));
   }
   *out = c;
   return HALE_OK;
@@ -1048,6 +1086,46 @@ extern "C" int hale_moe_forward_device(hale_moe* m, size_t ntok, const float* d_
   rc = moe_forward_scratch(m, ntok, &s, &pws);
   if (rc) return rc;
   rc = moe_forward_enqueue(m, ntok, d_x, d_logits, d_out, s, pws);
+  if (rc) return rc;
+  if (d_index && m->k)
+    HIPCHK(c, hipMemcpyAsync(d_index, s.route_idx, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (d_weight && m->k)
+    HIPCHK(c, hipMemcpyAsync(d_weight, s.route_w, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
+  return HALE_OK;
+}
+
+// Keeps the per-kernel profiler off for the duration of a call (its event
+// brackets create HIP events).
+struct ProfPause {
+  hale_ctx* c;
+  bool was;
+  explicit ProfPause(hale_ctx* ctx) : c(ctx), was(ctx->prof_on) { c->prof_on = false; }
+  ~ProfPause() { c->prof_on = was; }
+};
+
+extern "C" int hale_moe_forward_device_noalloc(hale_moe* m, size_t ntok, const float* d_x,
+                                               const float* d_logits, float* d_out,
+                                               uint32_t* d_index, float* d_weight) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !d_x || !d_out) return fail(c, HALE_EINVAL, "moe_forward_noalloc: NULL argument");
+  if (ntok == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  if (!c->fixed_scratch) return fail(c, HALE_EHIP, "no fixed scratch on device %d", c->device);
+  int rc = moe_forward_check(m, d_logits);
+  if (rc) return rc;
+  char* base = (char*)c->fixed_scratch;
+  const size_t tb = align_up(tok_scratch_bytes(m, ntok), 256);
+  const TokScratch s = tok_scratch_carve(m, base, ntok);
+  const bool grouped = m->k > 0 && ntok >= prefill_min_tokens(m->k);
+  const size_t need = tb + (grouped ? prefill_workspace_bytes(prefill_layer(m, s), ntok) : 0);
+  if (need > (size_t)HALE_NOALLOC_SCRATCH_BYTES)
+    return fail(c, HALE_EINVAL,
+                "moe_forward_noalloc: %zu tokens need %zu bytes of scratch, the fixed scratch "
+                "holds %zu",
+                ntok, need, (size_t)HALE_NOALLOC_SCRATCH_BYTES);
+  ProfPause pause(c);
+  rc = moe_forward_enqueue(m, ntok, d_x, d_logits, d_out, s, grouped ? base + tb : nullptr);
   if (rc) return rc;
   if (d_index && m->k)
     HIPCHK(c, hipMemcpyAsync(d_index, s.route_idx, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));

@@ -75,6 +75,7 @@ SIGNATURES = {
     "hale_moe_route": (C.c_int, [_vp, _fp, _u32p, _fp]),
     "hale_moe_forward": (C.c_int, [_vp, _sz, _fp, _fp, _fp, _u32p, _fp]),
     "hale_moe_forward_device": (C.c_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
+    "hale_moe_forward_device_noalloc": (C.c_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "hale_moe_set_experts_device": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _vp, _vp, _vp]),
     "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
     "hale_pack_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
@@ -782,6 +783,15 @@ class MoeLayer:
                                                      _vp(d_index) if d_index else None,
                                                      _vp(d_weight) if d_weight else None),
                        "MoeLayer::forward")
+
+    def forward_device_noalloc(self, ntok: int, d_x: int, d_out: int, d_logits: int = 0,
+                               d_index: int = 0, d_weight: int = 0):
+        """forward_device without any allocation: the scratch is the
+        library's fixed per-device array (ValueError when it is too small)."""
+        self.ctx.check(lib().hale_moe_forward_device_noalloc(
+            self.handle, ntok, _vp(d_x), _vp(d_logits) if d_logits else None, _vp(d_out),
+            _vp(d_index) if d_index else None, _vp(d_weight) if d_weight else None),
+            "MoeLayer::forward (no allocation)")
 
     def set_expert_matrices(self, e: int, expert: Expert):
         self.ctx.check(lib().hale_moe_set_expert_matrices(self.handle, e, expert.gate.handle,

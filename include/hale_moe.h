@@ -208,6 +208,26 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
                             const float *d_logits, float *d_out,
                             uint32_t *d_index, float *d_weight);
 
+/* Bytes of the fixed device scratch of hale_moe_forward_device_noalloc. */
+#define HALE_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* No counterpart in the reference: hale_moe_forward_device for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, results
+ * and errors, but the per-token scratch and the grouped workspace come from
+ * a fixed array of HALE_NOALLOC_SCRATCH_BYTES per device, held until the
+ * process ends; the call makes no device or host allocation.  A forward
+ * whose scratch would exceed it (about 16 MiB: for H 2048 and top-8, up to
+ * roughly 190 tokens on the grouped path) fails with HALE_EINVAL before
+ * anything is enqueued.  Every context on one device shares that device's
+ * array, which keeps the last call's contents (nothing in it must start at
+ * zero): calls that overlap in time on one device, from different contexts
+ * or streams, race. */
+int hale_moe_forward_device_noalloc(hale_moe *moe, size_t ntok,
+                                    const float *d_x, const float *d_logits,
+                                    float *d_out, uint32_t *d_index,
+                                    float *d_weight);
+
 /* Registers experts first .. first+count-1 from device buffers holding
  * their reference-layout bytes back to back: d_gate/d_up [count][I][H],
  * d_down [count][H][I] (bulk form of hale_moe_set_expert_device). */
