@@ -6,7 +6,12 @@ top-8 renormalised, weighted combine.  One step is one token through one
 MoE layer.  48 such layers (the model's depth, 16.3 GB) stay resident in HBM
 and consecutive steps visit consecutive layers with fresh inputs, so every
 step reads weights that are not in the 256 MB last-level cache.  The steps
-are replayed from a captured HIP graph.
+are replayed from a captured HIP graph of one pass over the 48 layers: at
+least 20 replays and at least --steps steps, each replay timed on its own
+(HIP events on the library's stream); `value` and `ms_per_step` come from the
+median replay, `timing` gives the median, min and max per step.  `warmup` is
+the number of eager steps run before the capture (at least one per layer,
+which also sizes each layer's scratch).
 
 value: algorithmic bytes per step (8 routed experts x 2,654,208 B + the
 1,048,576 B router) x steps / time, in GB/s.  roofline: the dominant
@@ -16,7 +21,10 @@ roofline.traffic: HBM bytes per launch of that kernel from the FETCH_SIZE and
 WRITE_SIZE counter passes, each scaled by what the counter reads for the
 plain copy kernel, as committed in profiles/traffic_decode_q4_qwen3_30b.txt.
 cpu_baseline: the oracle (C restatement of the reference CPU algorithm)
-on one layer of the same shape, on this host's cores.
+on one layer of the same shape on this host, built -march=x86-64 and
+-march=native, each on all threads and on one; medians of at least 20 tokens.
+expert: one q8_0 Qwen3-30B expert (Expert::forward, 1 token), 128 distinct
+experts in turn (cold weights).
 decode_more: Mixtral-8x7B- and Qwen3-235B-shaped decode layers, same timing.
 float_matvec: WeightMatrix::matvec over float weights (a bf16 vocabulary
 projection and a dense f32 matrix), GB/s of weight bytes.
@@ -24,7 +32,9 @@ attention: RMSNorm + Attention::forward of one token with 4096 cached
 positions (Qwen3-30B-A3B shape, bf16 projections), per-kernel times.
 prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
 2048 tokens q4_0 H 4096 I 1536; 128 experts, top-8, Zipf-skewed routing)
-with tokens/s, TOPS and the fraction of the int8 MFMA peak.
+with tokens/s, TOPS, the fraction of the int8 MFMA peak and a roofline
+block for the dominant grouped kernel (HBM for the 512-token workload,
+int8 MFMA for the 2048-token one).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--prefill-only] [--decode-eager]
@@ -56,10 +66,10 @@ DECODE_MORE = [
     ("qwen3-235b-a22b decode q4_0", H.Q4_0, 4096, 1536, 128, 8, 6),
 ]
 
-# prefill workloads: (name, dtype, hidden, inter, experts, top_k, tokens)
+# prefill workloads: (name, dtype, hidden, inter, experts, top_k, tokens, roofline bound)
 PREFILL = [
-    ("qwen3-30b-a3b prefill 512 tok q8_0", H.Q8_0, 2048, 768, 128, 8, 512),
-    ("qwen3-235b-a22b prefill 2048 tok q4_0", H.Q4_0, 4096, 1536, 128, 8, 2048),
+    ("qwen3-30b-a3b prefill 512 tok q8_0", H.Q8_0, 2048, 768, 128, 8, 512, "hbm"),
+    ("qwen3-235b-a22b prefill 2048 tok q4_0", H.Q4_0, 4096, 1536, 128, 8, 2048, "mfma"),
 ]
 
 
@@ -106,7 +116,7 @@ def build_layers(ctx, nlayers, seed=1234, dtype=DTYPE, hid=HID, inter=INTER, exp
     return layers
 
 
-def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps):
+def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfma"):
     """One MoE layer forward over `tokens` tokens with Zipf-skewed routing."""
     from hale_moe.synth import zipf_logits
 
@@ -150,6 +160,22 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps):
                                                       "min": int(groups.min())},
         "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()},
     }
+    # roofline of the dominant grouped kernel: algorithmic weight bytes (every
+    # touched expert's planes once) against HBM, or int8 ops against the MFMA
+    A = tokens * topk
+    per_launch = {"grouped_gate_up": (touched * 2 * inter * H.row_bytes(dtype, hid), 2.0 * A * 2 * hid * inter),
+                  "grouped_down": (touched * hid * H.row_bytes(dtype, inter), 2.0 * A * hid * inter)}
+    dom = max((k for k in prof if k in per_launch), key=lambda k: prof[k][0])
+    dom_s = prof[dom][0] / prof[dom][1] / 1000.0
+    nbytes, nops = per_launch[dom]
+    if bound == "hbm":
+        ach, peak, unit = nbytes / dom_s / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        ach, peak, unit = nops / dom_s / 1e12, INT8_PEAK_OPS / 1e12, "TOP/s"
+    res["roofline"] = {"bound": bound, "kernel": dom, "achieved": round(ach, 1), "peak": peak,
+                       "unit": unit, "frac": round(ach / peak, 4),
+                       "traffic": measured_traffic(PREFILL_TRAFFIC[name]).get(dom),
+                       "bytes_per_launch": nbytes, "ops_per_launch": nops}
     for b in (dl, dx, dout, didx):
         b.free()
     moe.close()
@@ -196,14 +222,18 @@ def decode_eager(args):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode_q4_qwen3_30b.txt")
+PREFILL_TRAFFIC = {
+    "qwen3-30b-a3b prefill 512 tok q8_0": os.path.join(ROOT, "profiles", "traffic_prefill_q8_512.txt"),
+    "qwen3-235b-a22b prefill 2048 tok q4_0": os.path.join(ROOT, "profiles", "traffic_prefill_q4_2048.txt"),
+}
 
 
-def measured_traffic():
-    """HBM bytes per launch by kernel, from the committed counter summary
+def measured_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch by kernel, from a committed counter summary
     (lines `traffic <kernel> <bytes>`), or {} when it is absent."""
     out = {}
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 p = line.split()
                 if len(p) == 3 and p[0] == "traffic":
@@ -254,6 +284,64 @@ def gpu_decode_more(name, dtype, hid, inter, experts, topk, nlayers, reps=20):
             "GB_per_s": round(bytes_step / us / 1e3, 1),
             "pct_hbm_peak": round(100 * bytes_step / us / 1e3 / HBM_PEAK_GBS, 2),
             "layers_resident": nlayers,
+            "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
+
+
+def gpu_expert(copies=128, reps=20):
+    """Expert::forward of one q8_0 Qwen3-30B-shaped expert (H 2048, I 768):
+    `copies` distinct experts (5 MB each, 640 MB in all) visited in turn so
+    the weights are cold, replayed from a graph; GB/s of expert bytes."""
+    ctx = H.Context(0)
+    hid, inter, dt = 2048, 768, H.Q8_0
+    vals = ctx.malloc(inter * hid * 4)
+    enc = ctx.malloc(inter * H.row_bytes(dt, hid))
+    experts = []
+    for c in range(copies):
+        mats = []
+        for j, (rows, cols) in enumerate(((inter, hid), (inter, hid), (hid, inter))):
+            vals.fill_normal(31 + 3 * c + j, rows * cols, 0.0, 0.02)
+            ctx.check(H.lib().hale_encode_rows_device(ctx.handle, dt, rows, cols, H._vp(vals.address),
+                                                      H._vp(enc.address)), "encode")
+            h = H._vp()
+            ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, dt, rows, cols, H._vp(enc.address),
+                                                        rows * H.row_bytes(dt, cols), H.C.byref(h)), "upload")
+            mats.append(H.WeightMatrix(ctx, h, rows, cols, dt))
+        experts.append(H.Expert(*mats))
+    vals.free()
+    enc.free()
+    xs = ctx.malloc(16 * hid * 4)
+    xs.fill_normal(8, 16 * hid, 0.0, 1.0)
+    out = ctx.malloc(hid * 4)
+
+    def step(s):
+        experts[s % copies].forward_device(xs.offset((s % 16) * hid * 4), out.address)
+
+    for s in range(copies):
+        step(s)
+    ctx.synchronize()
+    graph = ctx.capture(lambda: [step(s) for s in range(copies)])
+    graph.launch()
+    ctx.synchronize()
+    times = time_replays(ctx, graph, reps)
+    ctx.profile(True)
+    ctx.profile_reset()
+    for s in range(copies):
+        step(s)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    graph.close()
+    for x in experts:
+        for m in (x.gate, x.up, x.down):
+            m.close()
+    ctx.close()
+    nbytes = expert_bytes(dt, hid, inter)
+    us = 1000 * float(np.median(times)) / copies
+    return {"workload": "Qwen3-30B-A3B expert forward q8_0 (H 2048, I 768), 1 token, "
+                        f"{copies} distinct experts in turn (cold)",
+            "bytes_per_step": nbytes, "us_per_step": round(us, 3),
+            "GB_per_s": round(nbytes / us / 1e3, 1),
+            "pct_hbm_peak": round(100 * nbytes / us / 1e3 / HBM_PEAK_GBS, 2),
+            "timing": replay_stats(times, copies),
             "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
 
 
@@ -390,6 +478,25 @@ def gpu_attention(name, dtype, hid, nh, nkv, hd, qk, positions, timed=64):
             "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
 
 
+def time_replays(ctx, graph, reps):
+    """Times `reps` graph replays one by one (HIP events on the library's
+    stream around each launch); returns the per-replay times in ms."""
+    out = []
+    for _ in range(reps):
+        ctx.timer_start()
+        graph.launch()
+        out.append(ctx.timer_stop())
+    return out
+
+
+def replay_stats(times_ms, steps_per_replay):
+    t = np.asarray(times_ms)
+    return {"replays": int(t.size), "steps_per_replay": steps_per_replay,
+            "us_per_step_median": round(1000 * float(np.median(t)) / steps_per_replay, 3),
+            "us_per_step_min": round(1000 * float(t.min()) / steps_per_replay, 3),
+            "us_per_step_max": round(1000 * float(t.max()) / steps_per_replay, 3)}
+
+
 def gpu_decode(args):
     ctx = H.Context(0)
     t0 = time.time()
@@ -404,20 +511,21 @@ def gpu_decode(args):
     def step(s):
         layers[s % L].forward_device(1, xs.offset((s % nx) * HID * 4), out.address)
 
-    for s in range(max(args.warmup, L)):   # eager warm-up (also sizes every layer's scratch)
+    warm = max(args.warmup, L)
+    for s in range(warm):   # eager warm-up (also sizes every layer's scratch)
         step(s)
     ctx.synchronize()
-    # one graph = one pass over all layers
+    # one graph = one pass over all layers; at least 20 replays and at least
+    # the requested steps, each replay timed on its own
     graph = ctx.capture(lambda: [step(s) for s in range(L)])
     graph.launch()
     ctx.synchronize()
-    reps = max(1, args.steps // L)
+    reps = max(20, -(-args.steps // L))
     steps = reps * L
-    ctx.timer_start()
-    for _ in range(reps):
-        graph.launch()
-    ms = ctx.timer_stop()
-    log(f"timed {steps} steps in {ms:.3f} ms ({1000 * ms / steps:.2f} us/step)")
+    times = time_replays(ctx, graph, reps)
+    ms = float(np.median(times)) * reps  # the median replay, scaled to all timed steps
+    log(f"timed {steps} steps in {reps} replays: median {1000 * np.median(times) / L:.2f} us/step "
+        f"(min {1000 * min(times) / L:.2f}, max {1000 * max(times) / L:.2f})")
 
     # per-kernel durations: eager pass with events around every launch
     ctx.profile(True)
@@ -430,25 +538,59 @@ def gpu_decode(args):
     for m in layers:
         m.close()
     ctx.close()
-    return steps, ms, prof
+    return steps, ms, prof, warm, replay_stats(times, L)
 
 
-def cpu_baseline(budget_s, nthreads):
-    """The oracle on one layer of the same shape: tokens for about budget_s."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(budget_s):
+    """The oracle (the C restatement of the reference's CPU algorithm) on one
+    layer of the decode workload's shape, one token per iteration: built at
+    -march=x86-64 (what a default cargo build targets) and at -march=native
+    (compiled here for this host), each on all host threads and on one.  At
+    least 20 timed iterations per variant after a warm-up; medians."""
+    import shutil
+    import subprocess
+    import tempfile
+
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
-    variant = "_v3"
+    nall = os.cpu_count() or 1
     L = O.OracleMoe.synthetic(O.Q4_0, HID, INTER, E, TOPK, normalize_topk=True, seed=77,
-                              nthreads=nthreads)
+                              nthreads=nall)
     xs = O.normal(5, 16 * HID).reshape(16, HID)
-    L.forward(xs[0], nthreads=nthreads, variant=variant)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        L.forward(xs[n % 16], nthreads=nthreads, variant=variant)
-        n += 1
-    dt = time.perf_counter() - t0
-    return n, dt
+    variants = [("x86-64", "")]
+    tmp = tempfile.mkdtemp(prefix="hale_oracle_native_")
+    try:
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "native",
+                        f"NATIVE_OUT={tmp}"], check=True, capture_output=True)
+        variants.append(("native", os.path.join(tmp, "libhale_oracle_native.so")))
+    except (subprocess.CalledProcessError, OSError) as e:
+        log(f"cpu baseline: -march=native build failed ({e}); reporting x86-64 only")
+    res = {}
+    for name, variant in variants:
+        for nt in (nall, 1):
+            L.forward(xs[0], nthreads=nt, variant=variant)
+            times, t0 = [], time.perf_counter()
+            while len(times) < 20 or time.perf_counter() - t0 < budget_s:
+                a = time.perf_counter()
+                L.forward(xs[len(times) % 16], nthreads=nt, variant=variant)
+                times.append(time.perf_counter() - a)
+            med = float(np.median(times))
+            res[(name, nt)] = (med, len(times))
+            log(f"cpu {name} {nt} threads: {1e3 * med:.2f} ms/token over {len(times)} tokens")
+    shutil.rmtree(tmp, ignore_errors=True)
+    return nall, res
 
 
 def main():
@@ -458,7 +600,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="minimum timed seconds per CPU-baseline variant (4 variants)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill workloads (for counter runs)")
@@ -478,13 +621,13 @@ def main():
         print(json.dumps({"decode_eager_steps": decode_eager(args)}), flush=True)
         return
     if args.prefill_only:
-        res = [gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=3)
-               for (name, dt, hid, inter, ex, k, tok) in PREFILL]
+        res = [gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=3, bound=bound)
+               for (name, dt, hid, inter, ex, k, tok, bound) in PREFILL]
         print(json.dumps({"prefill": res}), flush=True)
         return
 
     bytes_step = TOPK * expert_bytes(DTYPE, HID, INTER) + E * HID * 4
-    steps, ms, prof = gpu_decode(args)
+    steps, ms, prof, warm, rstats = gpu_decode(args)
     sec = ms / 1000.0
     gbs = bytes_step * steps / sec / 1e9
 
@@ -501,6 +644,11 @@ def main():
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
                 "traffic": measured_traffic().get(dom), "bytes_per_launch": launch_bytes.get(dom)}
+
+    expert = None
+    if not args.no_prefill:
+        expert = gpu_expert()
+        log(f"expert q8_0 2048x768: {expert['us_per_step']} us, {expert['GB_per_s']} GB/s")
 
     more = []
     if not args.no_prefill:
@@ -522,23 +670,26 @@ def main():
 
     prefill = []
     if not args.no_prefill:
-        for (name, dt, hid, inter, ex, k, tok) in PREFILL:
-            prefill.append(gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=10))
+        for (name, dt, hid, inter, ex, k, tok, bound) in PREFILL:
+            prefill.append(gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=10, bound=bound))
             log(f"prefill {name}: {prefill[-1]['ms']} ms, {prefill[-1]['tokens_per_s']} tok/s, "
                 f"{prefill[-1]['pct_int8_mfma_peak']}% int8 MFMA")
 
     cpu = None
     if not args.no_cpu:
-        nthreads = min(16, os.cpu_count() or 1)
-        n_all, dt_all = cpu_baseline(args.cpu_seconds, nthreads)
-        n_one, dt_one = cpu_baseline(args.cpu_seconds / 2, 1)
-        cpu = {"value": round(bytes_step * n_all / dt_all / 1e9, 2), "unit": "GB/s", "cores": nthreads,
+        nall, res = cpu_baseline(args.cpu_seconds)
+        med, n = res[("x86-64", nall)]
+        cpu = {"value": round(bytes_step / med / 1e9, 3), "unit": "GB/s", "cores": nall,
                "kind": "port",
-               "sample": f"oracle MoE layer forward (q4_0, 128 experts, top-8, H 2048, I 768), one "
-                         f"340 MB layer, {n_all} tokens in {dt_all:.1f}s on {nthreads} threads; "
-                         f"1 thread: {bytes_step * n_one / dt_one / 1e9:.2f} GB/s ({n_one} tokens)",
-               "tokens_per_s": round(n_all / dt_all, 1),
-               "single_core_value": round(bytes_step * n_one / dt_one / 1e9, 3)}
+               "sample": f"oracle MoeLayer::forward (q4_0, 128 experts, top-8, H 2048, I 768; one "
+                         f"340 MB layer, one token per iteration), median of {n} tokens, built "
+                         f"-O3 -march=x86-64, {nall} threads on {cpu_model()}",
+               "tokens_per_s": round(1.0 / med, 1),
+               "cpu_model": cpu_model(),
+               "variants": {f"{name} {nt} thread{'s' if nt > 1 else ''}":
+                            {"GB_per_s": round(bytes_step / m / 1e9, 3), "ms_per_token": round(1e3 * m, 3),
+                             "tokens": c}
+                            for (name, nt), (m, c) in res.items()}}
 
     line = {
         "metric": METRIC,
@@ -546,7 +697,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warm,
         "ms_per_step": round(ms / steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -561,7 +712,9 @@ def main():
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "moe_layer_tokens_per_s": round(steps / sec, 1),
         "roofline": roofline,
+        "timing": rstats,
         "kernels": kernels,
+        "expert": expert,
         "decode_more": more,
         "float_matvec": fmv,
         "attention": attn,

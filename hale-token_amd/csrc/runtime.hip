@@ -664,28 +664,35 @@ extern "C" int hale_matvec_block_sums(hale_ctx* c, const hale_matrix* m, const f
 // expert
 // ---------------------------------------------------------------------------
 
-extern "C" int hale_expert_forward(hale_ctx* c, const hale_matrix* gate, const hale_matrix* up,
-                                   const hale_matrix* down, const float* x, float* out) {
-  if (!c || !gate || !up || !down || !x || !out) return fail(c, HALE_EINVAL, "expert_forward: NULL argument");
+static int expert_check(hale_ctx* c, const hale_matrix* gate, const hale_matrix* up,
+                        const hale_matrix* down) {
   if (!quantized(gate->dtype) || gate->dtype != up->dtype || gate->dtype != down->dtype)
     return fail(c, HALE_EINVAL, "expert matrices must share one quantized dtype");
   size_t I = gate->rows, H = gate->cols;
   if (up->rows != I || up->cols != H || down->rows != H || down->cols != I)
     return fail(c, HALE_EINVAL, "expert shapes: gate %zux%zu up %zux%zu down %zux%zu", gate->rows,
                 gate->cols, up->rows, up->cols, down->rows, down->cols);
-  std::lock_guard<std::recursive_mutex> g(c->mu);
-  HIPCHK(c, hipSetDevice(c->device));
-  size_t nbh = H / HALE_QK, nbi = I / HALE_QK;
-  size_t o1 = align_up(H * 4, 256), o2 = o1 + align_up(H * 4, 256);
-  size_t o3 = o2 + align_up(nbh * sizeof(ActBlock), 256);
+  return HALE_OK;
+}
+
+// Bytes of scratch expert_enqueue needs after `lead` bytes of the caller's.
+static size_t expert_scratch_bytes(const hale_matrix* gate, size_t lead) {
+  const size_t nbh = gate->cols / HALE_QK, nbi = gate->rows / HALE_QK;
+  return lead + align_up(nbh * sizeof(ActBlock), 256) + nbi * sizeof(ActBlock);
+}
+
+// Enqueues Expert::forward for device x/out: q8 activation blocks of x, the
+// gate/up GEMV with SiLU and requantization, the down GEMV.  The activation
+// blocks live in the context scratch from byte `lead` on (the caller's own
+// staging sits before it).
+static int expert_enqueue(hale_ctx* c, const hale_matrix* gate, const hale_matrix* up,
+                          const hale_matrix* down, const float* dx, float* dout, size_t lead) {
+  const size_t I = gate->rows, H = gate->cols, nbh = H / HALE_QK, nbi = I / HALE_QK;
   void* s;
-  int rc = ctx_scratch(c, o3 + nbi * sizeof(ActBlock), &s);
+  int rc = ctx_scratch(c, expert_scratch_bytes(gate, lead), &s);
   if (rc) return rc;
-  float* dx = (float*)s;
-  float* dout = (float*)((char*)s + o1);
-  ActBlock* act = (ActBlock*)((char*)s + o2);
-  ActBlock* hact = (ActBlock*)((char*)s + o3);
-  HIPCHK(c, hipMemcpyAsync(dx, x, H * 4, hipMemcpyHostToDevice, c->stream));
+  ActBlock* act = (ActBlock*)((char*)s + lead);
+  ActBlock* hact = (ActBlock*)((char*)s + lead + align_up(nbh * sizeof(ActBlock), 256));
   LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nbh, act, c->stream));
   GemvArgs a{};
   a.codes = gate->codes;
@@ -701,9 +708,40 @@ extern "C" int hale_expert_forward(hale_ctx* c, const hale_matrix* gate, const h
   LAUNCH(c, K_GATE_UP, launch_gemv(gate->dtype, EPI_GATE_UP, a, (int)nbi, 1, c->stream));
   GemvArgs d = plain_args(down, hact, dout);
   LAUNCH(c, K_DOWN, launch_gemv(down->dtype, EPI_PLAIN, d, (int)(padded_rows(H) / 64), 1, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_expert_forward(hale_ctx* c, const hale_matrix* gate, const hale_matrix* up,
+                                   const hale_matrix* down, const float* x, float* out) {
+  if (!c || !gate || !up || !down || !x || !out) return fail(c, HALE_EINVAL, "expert_forward: NULL argument");
+  int rc = expert_check(c, gate, up, down);
+  if (rc) return rc;
+  const size_t H = gate->cols, io = align_up(H * 4, 256);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  void* s;
+  rc = ctx_scratch(c, expert_scratch_bytes(gate, 2 * io), &s);  // x, out, then the blocks
+  if (rc) return rc;
+  float* dx = (float*)s;
+  float* dout = (float*)((char*)s + io);
+  HIPCHK(c, hipMemcpyAsync(dx, x, H * 4, hipMemcpyHostToDevice, c->stream));
+  rc = expert_enqueue(c, gate, up, down, dx, dout, 2 * io);
+  if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync(out, dout, H * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   return HALE_OK;
+}
+
+extern "C" int hale_expert_forward_device(hale_ctx* c, const hale_matrix* gate,
+                                          const hale_matrix* up, const hale_matrix* down,
+                                          const float* d_x, float* d_out) {
+  if (!c || !gate || !up || !down || !d_x || !d_out)
+    return fail(c, HALE_EINVAL, "expert_forward: NULL argument");
+  int rc = expert_check(c, gate, up, down);
+  if (rc) return rc;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  return expert_enqueue(c, gate, up, down, d_x, d_out, 0);
 }
 
 // ---------------------------------------------------------------------------

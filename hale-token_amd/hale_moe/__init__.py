@@ -66,6 +66,7 @@ SIGNATURES = {
     "hale_matvec_device": (C.c_int, [_vp, _vp, _vp, _vp]),
     "hale_matvec_block_sums": (C.c_int, [_vp, _vp, _fp, _sz, _i32p]),
     "hale_expert_forward": (C.c_int, [_vp, _vp, _vp, _vp, _fp, _fp]),
+    "hale_expert_forward_device": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "hale_moe_create": (C.c_int, [_vp, C.c_uint32, _sz, _sz, _sz, C.c_int, _sz, C.c_int, _vp,
                                   C.POINTER(_vp)]),
     "hale_moe_destroy": (None, [_vp]),
@@ -491,6 +492,13 @@ class Expert:
                                             self.down.handle, _p(v, _fp), _p(out, _fp)),
                   "Expert::forward")
         return out
+
+    def forward_device(self, d_x: int, d_out: int):
+        """Expert::forward on device buffers, enqueued on the context stream."""
+        ctx = self.gate.ctx
+        ctx.check(lib().hale_expert_forward_device(ctx.handle, self.gate.handle, self.up.handle,
+                                                   self.down.handle, _vp(d_x), _vp(d_out)),
+                  "Expert::forward")
 
 
 @dataclass(frozen=True)

@@ -156,6 +156,11 @@ int hale_matvec_block_sums(hale_ctx *ctx, const hale_matrix *m,
 int hale_expert_forward(hale_ctx *ctx, const hale_matrix *gate,
                         const hale_matrix *up, const hale_matrix *down,
                         const float *x, float *out);
+/* Same on device buffers (d_x 16-byte aligned), enqueued on the context's
+ * stream. */
+int hale_expert_forward_device(hale_ctx *ctx, const hale_matrix *gate,
+                               const hale_matrix *up, const hale_matrix *down,
+                               const float *d_x, float *d_out);
 
 /* ---- MoE layer and its HBM-resident expert provider ------------------ */
 

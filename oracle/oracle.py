@@ -65,7 +65,8 @@ class AttentionDesc(C.Structure):
 
 
 def _load(variant: str = ""):
-    path = os.path.join(_HERE, f"libhale_oracle{variant}.so")
+    # variant: "" / "_v3" next to this file, or the path of a build elsewhere
+    path = variant if os.path.isabs(variant) else os.path.join(_HERE, f"libhale_oracle{variant}.so")
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
     lib = C.CDLL(path)
@@ -119,7 +120,8 @@ _LIBS: dict = {}
 
 
 def lib(variant: str = ""):
-    """The oracle library; variant "" (-march=x86-64) or "_v3" (x86-64-v3)."""
+    """The oracle library; variant "" (-march=x86-64), "_v3" (x86-64-v3) or
+    the absolute path of another build (the -march=native one)."""
     if variant not in _LIBS:
         _LIBS[variant] = _load(variant)
     return _LIBS[variant]

@@ -147,6 +147,25 @@ def test_expert_forward_bit_exact(ctx, dtype, hidden, inter):
     assert_parity(got, want)
 
 
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+def test_expert_forward_device_equals_host(ctx, dtype):
+    hidden, inter = 2048, 768
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, 1, 1, seed=17, with_router=False)
+    ex = H.Expert(H.WeightMatrix.new(ctx, inter, hidden, dtype, L.gate[0]),
+                  H.WeightMatrix.new(ctx, inter, hidden, dtype, L.up[0]),
+                  H.WeightMatrix.new(ctx, hidden, inter, dtype, L.down[0]))
+    x = O.normal(19, hidden)
+    bx, bo = ctx.malloc(hidden * 4), ctx.malloc(hidden * 4)
+    bx.upload(x)
+    ex.forward_device(bx.address, bo.address)
+    got = bo.download(np.float32, hidden)
+    assert same_bits(got, ex.forward(x))
+    assert_parity(got, O.expert_forward(dtype, hidden, inter, L.gate[0], L.up[0], L.down[0], x,
+                                        nthreads=8))
+    bx.free()
+    bo.free()
+
+
 # ---------------------------------------------------------------------------
 # MoeLayer
 # ---------------------------------------------------------------------------
