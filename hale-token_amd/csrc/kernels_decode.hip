@@ -10,6 +10,7 @@
 #pragma clang fp contract(off)
 
 #include <atomic>
+#include <type_traits>
 
 #include "hale_device.h"
 #include "kernels.h"
@@ -332,7 +333,7 @@ __device__ __forceinline__ void topk_rounds(unsigned* key, unsigned& live, int k
   *norm_out = norm;
 }
 
-constexpr int RS_SCRATCH = 2 * ROUTE_MAX_E + 4 * 64;
+constexpr int RS_SCRATCH = ROUTE_MAX_E + 4 * 64;
 
 template <int PER>  // elements per lane: E <= 64 * PER
 __device__ __forceinline__ void route_select_t(const float* lg, int E, int k, int normalize,
@@ -384,6 +385,8 @@ __device__ __forceinline__ void route_select_t(const float* lg, int E, int k, in
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// E <= ME
+template <int ME = ROUTE_MAX_E>
 __device__ __forceinline__ void route_select(const float* lg, int E, int k, int normalize,
                                              int* sel_idx, float* sel_w, const ExpTable& tab,
                                              float* rs) {
@@ -391,131 +394,225 @@ __device__ __forceinline__ void route_select(const float* lg, int E, int k, int 
     route_select_t<1>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
   else if (E <= 128)
     route_select_t<2>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
-  else if (E <= 256)
-    route_select_t<4>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
+  else if (ME <= 256 || E <= 256)
+    route_select_t<(ME < 256 ? 2 : 4)>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
   else if (E <= 512)
     route_select_t<8>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
   else
     route_select_t<16>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
 }
 
-// The same selection split over waves 0 and 1 of a work-group, for the
-// gate/up prologue (every wave of the work-group passes the two barriers
-// inside).  Ranking by logit gives the reference's order unless rounding
-// makes two
-// probabilities equal (the map logit -> exp(logit - max) -> probability is
-// non-decreasing).  Wave 0 ranks by logit while wave 1 takes the max, the
-// exp values, the in-order sum and the probability keys; then wave 0 checks
-// the ranking against the probabilities: each chosen pair, and the last
-// chosen against every unchosen element, must be in (probability desc,
-// index asc) order.  If a check fails it ranks again by probability.
-// Either way the result is the reference's.  rs: RS_SCRATCH words of LDS.
-template <int PER>
-__device__ __forceinline__ void route_select_pair_t(const float* lg, int E, int k, int normalize,
-                                                    int* sel_idx, float* sel_w, const ExpTable& tab,
-                                                    float* rs, int wave) {
+// Selection in the gate/up prologue, in two parts.
+//
+// Ranking by logit gives the reference's order unless rounding makes two
+// probabilities equal: the map logit -> exp(logit - max) -> probability is
+// non-decreasing, so it can merge two logits into one probability but never
+// swap them.  So every work-group first ranks the experts by logit
+// (rank_by_logit, all threads, no exp), takes the expert of its slot and
+// issues that expert's weight loads at once.  One wave then forms the
+// probabilities while the loads are in flight (verify_selection) and checks
+// the ranking against them: each chosen pair, and the last chosen against
+// every unchosen element, must be in (probability desc, index asc) order.
+// If a check fails it ranks again by probability; a work-group whose slot
+// then holds another expert runs its rows again.  Either way the result is
+// the reference's.
+
+// Selection state in LDS for at most ME experts.
+template <int ME>
+struct SelLds {
+  static constexpr int MAXE = ME;
+  unsigned long long ck[ME];   // order_key(logit) << 32 | ~index
+  unsigned key[ME];            // order_key(logit), then order_key(probability)
+  int rank[ME];                // rank of each element by logit
+  float e[ME];                 // exp(logit - max)
+  float logit[ME];
+  int by_logit[65];            // element of logit rank r <= k
+  float sorted[65];            // and its logit
+  int sel_idx[64];             // the reference's choice, best first
+  float sel_w[64];             // and its renormalised weights
+  int bad;                     // the logit ranking was not the reference's
+};
+
+// rank_i = #{j : key_j > key_i} + #{j < i : key_j == key_i}, the position of
+// element i in (key desc, index asc) order.  ck = key << 32 | ~index orders
+// exactly like (key desc, index asc) read from the top, so rank_i counts
+// the composite keys above ck_i.  Every wave holds all E composite keys in
+// registers (element j at lane j % 64, slot j / 64; zero past E, below
+// every real key) and ranks elements wave, wave + NW, ...: per element one
+// 64-bit compare per slot, a ballot and a scalar popcount.  Writes rank[i],
+// and by_logit[r] / sorted[r] (element and logit of rank r) for r <= k.
+template <int PER, int NW, class Sel>
+__device__ __forceinline__ void rank_by_logit_t(Sel& sl, int E, int k) {
   const int lane = threadIdx.x & 63;
-  float* e_lds = rs;                                  // [E] exp values
-  unsigned* pkey = (unsigned*)(rs + ROUTE_MAX_E);     // [E] probability keys
-  float v[PER];
-  unsigned key[PER];
-  unsigned live = 0;
-  int my_idx = 0;
-  if (wave <= 1) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  unsigned long long kj[PER];
 #pragma unroll
-    for (int m = 0; m < PER; m++) {
-      const int i = lane + 64 * m;
-      v[m] = (i < E) ? lg[i] : -__builtin_huge_valf();
+  for (int m = 0; m < PER; m++) kj[m] = sl.ck[lane + 64 * m];
+  constexpr int B = 8;  // elements whose keys are read together
+  for (int i0 = wave; i0 < E; i0 += B * NW) {
+    unsigned long long ci[B];
+#pragma unroll
+    for (int q = 0; q < B; q++) ci[q] = sl.ck[min(i0 + NW * q, E - 1)];
+    int cnt[B];
+#pragma unroll
+    for (int q = 0; q < B; q++) {
+      cnt[q] = 0;
+#pragma unroll
+      for (int m = 0; m < PER; m++) cnt[q] += __popcll(__ballot(kj[m] > ci[q]));
     }
-    if (wave == 1) {
-      float mx = v[0];
+    // lane q writes element q's rank (and, within the top k + 1, the element
+    // and its logit, read back from the key)
 #pragma unroll
-      for (int m = 1; m < PER; m++) mx = fmaxf(mx, v[m]);
-      mx = wave_max_f32(mx);
-#pragma unroll
-      for (int m = 0; m < PER; m++) v[m] = wave_expf(v[m] - mx, tab);
-#pragma unroll
-      for (int m = 0; m < PER; m++)
-        if (lane + 64 * m < E) e_lds[lane + 64 * m] = v[m];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      float sum = 0.0f;  // sum += exp(v - max), index order
-      if (lane == 0) sum = lds_sum_in_order(e_lds, E, sum);
-      sum = lane_value(sum, 0);
-#pragma unroll
-      for (int m = 0; m < PER; m++)
-        if (lane + 64 * m < E) pkey[lane + 64 * m] = order_key(v[m] / sum);
-    } else {
-#pragma unroll
-      for (int m = 0; m < PER; m++) {
-        key[m] = 0u;
-        if (lane + 64 * m < E) {
-          key[m] = order_key(v[m]);
-          live |= 1u << m;
+    for (int q = 0; q < B; q++) {
+      const int i = i0 + NW * q;
+      if (lane == q && i < E) {
+        sl.rank[i] = cnt[q];
+        if (cnt[q] <= k) {
+          sl.by_logit[cnt[q]] = i;
+          sl.sorted[cnt[q]] = key_value((unsigned)(ci[q] >> 32));
         }
       }
-      float unused_p, unused_norm;
-      topk_rounds<PER>(key, live, k, 0, &my_idx, &unused_p, &unused_norm);
     }
   }
-  __syncthreads();
-  if (wave == 0) {
-    // lane r < k checks chosen r against chosen r + 1.  Every unchosen
-    // element ranks after the last chosen by logit, hence normally no higher
-    // by probability; the ranking fails if one has a larger probability key,
-    // or an equal one at a lower index.  live: unchosen existing elements of
-    // this lane.
-    const int next = __shfl(my_idx, lane + 1);
-    const int last = __shfl(my_idx, k - 1);
-    const unsigned klast = pkey[last];
-    bool bad = false;
-    if (lane + 1 < k) {
-      const unsigned ka = pkey[my_idx], kb = pkey[next];
-      bad = !(ka > kb || (ka == kb && my_idx < next));
-    }
-    unsigned pk[PER];
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-      const int i = lane + 64 * m;
-      pk[m] = (i < E) ? pkey[i] : 0u;
-      if ((live >> m) & 1u) bad = bad || pk[m] > klast || (pk[m] == klast && i < last);
-    }
-    float my_p = 0.0f, norm = 1.0f;
-    if (__ballot(bad) == 0ull) {
-      my_p = lane < k ? key_value(pkey[my_idx]) : 0.0f;
-      if (normalize) {
-        norm = -0.0f;  // Iterator::sum in best-first order
-        for (int r = 0; r < k; r++) norm = norm + lane_value(my_p, r);
-      }
-    } else {  // a tie the exp values did not show: rank by probability
-      unsigned live2 = 0;
-#pragma unroll
-      for (int m = 0; m < PER; m++)
-        if (lane + 64 * m < E) live2 |= 1u << m;
-      topk_rounds<PER>(pk, live2, k, normalize, &my_idx, &my_p, &norm);
-    }
-    if (lane < k) {
-      sel_idx[lane] = my_idx;
-      sel_w[lane] = my_p / norm;
-    }
-  }
-  __syncthreads();
 }
 
-__device__ __forceinline__ void route_select_pair(const float* lg, int E, int k, int normalize,
-                                                  int* sel_idx, float* sel_w, const ExpTable& tab,
-                                                  float* rs, int wave) {
+template <int NW, class Sel>
+__device__ __forceinline__ void rank_by_logit(Sel& sl, int E, int k) {
   if (E <= 64)
-    route_select_pair_t<1>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
+    rank_by_logit_t<1, NW>(sl, E, k);
   else if (E <= 128)
-    route_select_pair_t<2>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
-  else if (E <= 256)
-    route_select_pair_t<4>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
-  else if (E <= 512)
-    route_select_pair_t<8>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
+    rank_by_logit_t<2, NW>(sl, E, k);
+  else if (Sel::MAXE <= 256 || E <= 256)
+    rank_by_logit_t<(Sel::MAXE < 256 ? 2 : 4), NW>(sl, E, k);
   else
-    route_select_pair_t<16>(lg, E, k, normalize, sel_idx, sel_w, tab, rs, wave);
+    rank_by_logit_t<Sel::MAXE / 64, NW>(sl, E, k);
+}
+
+// True when the probabilities must order the k + 1 best logits exactly as
+// the logits do, so that the logit ranking is the reference's top-k.  For
+// consecutive ranks a, b with L_a - L_b > 2^-13 (computed in f32), L_b - L_0
+// >= -60 and every value finite: x = fl(L - L_0) errs by at most 2^-18 for
+// |x| < 64, glibc expf by less than 1 ulp and the division by half an ulp,
+// so p_a / p_b >= exp(2^-13 - 2^-17)(1 - 3 * 2^-23) > 1 and no rounding can
+// merge the two probabilities.  (Equal logits have equal probabilities and
+// keep index order either way.)  Otherwise the selection is checked against
+// the probabilities.  Lane r of each wave checks ranks r - 1, r.
+template <class Sel>
+__device__ __forceinline__ bool ranking_is_safe(const Sel& sl, int E, int k) {
+  const int lane = threadIdx.x & 63;
+  const int n = k < E ? k + 1 : k;  // ranks 0..k exist
+  const float l0 = sl.sorted[0];
+  bool ok = fabsf(l0) <= 3.0e38f;
+  if (lane >= 1 && lane < n) {
+    const float a = sl.sorted[lane - 1], b = sl.sorted[lane];
+    ok = ok && fabsf(b) <= 3.0e38f && b - l0 >= -60.0f && a - b > 0x1p-13f;
+  }
+  if (k >= 64) {  // rank 64 exists only for k = 64 < E
+    if (n == 65) {
+      const float a = sl.sorted[63], b = sl.sorted[64];
+      ok = ok && fabsf(b) <= 3.0e38f && b - l0 >= -60.0f && a - b > 0x1p-13f;
+    }
+  }
+  return __ballot(!ok) == 0ull;
+}
+
+// One whole wave: softmax_in_place over the logits (max, glibc exp, the sum
+// in index order, one division per value), the check of the logit ranking,
+// and the reference's selection and renormalised weights into sel_idx /
+// sel_w (k rounds over the probability keys when the check fails).  The
+// values stay in LDS (element i at lane i % 64, round i / 64), so the check
+// needs few registers beside the weight loads in flight.
+template <class Sel>
+__device__ __forceinline__ void verify_selection(Sel& sl, int E, int k, int normalize,
+                                                 const ExpTable& tab) {
+  const int lane = threadIdx.x & 63;
+  const int rounds = (E + 63) / 64;
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  float mx = -__builtin_huge_valf();
+  for (int m = 0; m < rounds; m++) {
+    const int i = lane + 64 * m;
+    mx = fmaxf(mx, i < E ? sl.logit[i] : -__builtin_huge_valf());
+  }
+  mx = wave_max_f32(mx);  // max is order independent
+  for (int m = 0; m < rounds; m++) {
+    const int i = lane + 64 * m;
+    const float ev = wave_expf((i < E ? sl.logit[i] : -__builtin_huge_valf()) - mx, tab);
+    if (i < E) sl.e[i] = ev;
+  }
+  wave_sync();
+  float sum = 0.0f;  // sum += exp(v - max), index order
+  if (lane == 0) sum = lds_sum_in_order(sl.e, E, sum);
+  sum = lane_value(sum, 0);
+  for (int m = 0; m < rounds; m++) {
+    const int i = lane + 64 * m;
+    if (i < E) sl.key[i] = order_key(sl.e[i] / sum);  // the logit keys are no longer needed
+  }
+  wave_sync();
+  // lane r < k checks chosen r against chosen r + 1; every unchosen element
+  // (logit rank >= k) must rank after the last chosen by probability too
+  int my_idx = lane < k ? sl.by_logit[lane] : 0;
+  const int next = __shfl(my_idx, lane + 1);
+  const int last = __shfl(my_idx, k - 1);
+  const unsigned klast = sl.key[last];
+  bool bad = false;
+  if (lane + 1 < k) {
+    const unsigned ka = sl.key[my_idx], kb = sl.key[next];
+    bad = !(ka > kb || (ka == kb && my_idx < next));
+  }
+  for (int m = 0; m < rounds; m++) {
+    const int i = lane + 64 * m;
+    if (i < E && sl.rank[i] >= k) {
+      const unsigned pk = sl.key[i];
+      bad = bad || pk > klast || (pk == klast && i < last);
+    }
+  }
+  float my_p = 0.0f, norm = 1.0f;
+  const bool any_bad = __ballot(bad) != 0ull;
+  if (!any_bad) {
+    my_p = lane < k ? key_value(sl.key[my_idx]) : 0.0f;
+    if (normalize) {
+      norm = -0.0f;  // Iterator::sum in best-first order
+      for (int r = 0; r < k; r++) norm = norm + lane_value(my_p, r);
+    }
+  } else {
+    // a tie the logits did not show: k rounds over the probability keys;
+    // the wave's largest untaken key is the next best and the lowest index
+    // holding it wins.  Taken keys become 0 (below every real key) and
+    // sl.rank marks them taken (-1), so a real key of 0 stays apart.
+    norm = normalize ? -0.0f : 1.0f;
+    for (int r = 0; r < k; r++) {
+      unsigned loc = 0u;
+      for (int m = 0; m < rounds; m++) {
+        const int i = lane + 64 * m;
+        if (i < E && sl.rank[i] >= 0) loc = sl.key[i] > loc ? sl.key[i] : loc;
+      }
+      const unsigned best = wave_max_u32(loc);
+      int widx = 0x7fffffff;
+      for (int m = 0; m < rounds; m++) {
+        const int i = lane + 64 * m;
+        if (i < E && sl.rank[i] >= 0 && sl.key[i] == best) widx = min(widx, i);
+      }
+      widx = (int)wave_reduce_u32((unsigned)widx, OpMinU());
+      wave_sync();
+      if (lane == 0) sl.rank[widx] = -1;
+      wave_sync();
+      const float pw = key_value(best);
+      if (normalize) norm = norm + pw;
+      if (lane == r) {
+        my_idx = widx;
+        my_p = pw;
+      }
+    }
+  }
+  if (lane < k) {
+    sl.sel_idx[lane] = my_idx;
+    sl.sel_w[lane] = my_p / norm;
+  }
+  if (lane == 0) sl.bad = any_bad ? 1 : 0;
 }
 
 // Standalone routing (MoeLayer::route without the experts, and the grouped
@@ -616,7 +713,7 @@ __device__ __forceinline__ int block_isum(const u32x4* c, const ActBlock* ab) {
 // half as long after the loads land), sixteen for q4_0 gate/up rows that
 // fit one chunk (H <= 2048; with more chunks four loads in flight per lane
 // pipeline worse).
-template <int DT, int EPI, int NW>
+template <int DT, int EPI, int NW, int ME = 256>  // ME: most experts the routed form selects among
 __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   constexpr int CH = Layout<DT>::CH;
   constexpr int UPW = 64 / NW / CH;      // blocks per wave per chunk (64 / NW loads in flight)
@@ -624,9 +721,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   static_assert(UPW % 4 == 0, "terms go in groups of four blocks");
   __shared__ float terms[2][CB][GROUP];
   __shared__ ActBlock s_act[GEMV_MAX_NB];
-  __shared__ int sel_idx[64];
-  __shared__ float sel_w[64];
-  __shared__ __attribute__((aligned(16))) float rs[EPI == EPI_GATE_UP ? RS_SCRATCH : 4];
+  struct NoSel {};
+  __shared__ __attribute__((aligned(16)))
+  typename std::conditional<EPI == EPI_GATE_UP, SelLds<ME>, NoSel>::type sel;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -634,130 +731,184 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   const int slot = blockIdx.y;
   const int nb = a.nb;
 
-  // The activation blocks of this slot go to LDS.  With routing in the
-  // prologue, waves 0 and 1 select the experts from the first instruction on
-  // while the other waves stage the activations (wave 1 joins them after its
-  // part of the selection); otherwise every wave stages and the
-  // weight loads are issued before the staging stores.
-  const bool routing = EPI == EPI_GATE_UP && a.logits != nullptr;
-  const int nstage = routing ? 64 * (NW - 1) : 64 * NW;  // staging threads
-  const int stid = routing ? (int)threadIdx.x - 64 : (int)threadIdx.x;
-  constexpr int APER = (GEMV_MAX_NB * 3 + 64 * (NW - 1) - 1) / (64 * (NW - 1));
+  // Wave w takes blocks w UPW .. w UPW + UPW - 1 of every chunk of CB
+  // blocks.  The activation blocks of this slot go to LDS, each wave staging the
+  // blocks it reads itself, so no work-group barrier stands between the
+  // staging and the terms.  Loads are issued first and stored once the
+  // first weight loads are in flight.
+  constexpr int WNB = (GEMV_MAX_NB + NW - 1) / NW;    // blocks per wave, at most
+  constexpr int APER = (WNB * 3 + 63) / 64;          // 16-byte pieces per lane
+  // block of the wave's t-th block (chunk t / UPW, position t % UPW)
+  auto wave_block = [&](int t) { return (t / UPW) * CB + wave * UPW + t % UPW; };
   u32x4 av[APER];
-  if (stid >= 0) {
+  {
     const u32x4* src = (const u32x4*)(a.act + (size_t)slot * a.act_stride);
 #pragma unroll
     for (int j = 0; j < APER; j++) {
-      const int i = stid + j * nstage;
-      if (i < nb * 3) av[j] = src[i];
+      const int p = lane + 64 * j;  // piece p % 3 of the wave's block p / 3
+      const int b = wave_block(p / 3);
+      if (p < WNB * 3 && b < nb) av[j] = src[b * 3 + p % 3];
     }
   }
   auto stage_act = [&]() {
-    if (stid < 0) return;
     u32x4* dst = (u32x4*)s_act;
 #pragma unroll
     for (int j = 0; j < APER; j++) {
-      const int i = stid + j * nstage;
-      if (i < nb * 3) dst[i] = av[j];
+      const int p = lane + 64 * j;
+      const int b = wave_block(p / 3);
+      if (p < WNB * 3 && b < nb) dst[b * 3 + p % 3] = av[j];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
   ExpTable tab;
   if constexpr (EPI == EPI_GATE_UP) tab.load();
   int expert = a.route_idx ? a.route_idx[slot] : 0;
+  // With router logits given, the expert of this slot is the one of logit
+  // rank `slot` (see ranking_is_safe; otherwise the probabilities check
+  // that choice while the loads fly).  The last column of work-groups holds
+  // the selector: its first work-group runs the reference's selection
+  // (softmax, top-k, renormalisation) and publishes the routes and their
+  // weights for the down projection, beside the rows' work.
+  const bool routing = EPI == EPI_GATE_UP && a.logits != nullptr;
+  bool safe = true;
   if constexpr (EPI == EPI_GATE_UP) {
-    if (routing) {  // choose this token's experts from the router logits
-      if (wave >= 2) stage_act();
-      route_select_pair(a.logits, a.E, a.slots, a.normalize, sel_idx, sel_w, tab, rs, wave);
-      if (wave == 1) stage_act();
-      if (g == 0 && threadIdx.x == 0) {  // one work-group per slot publishes it
-        a.route_out_idx[slot] = sel_idx[slot];
-        a.route_out_w[slot] = sel_w[slot];
-        if (a.stats) atomicAdd(&a.stats[sel_idx[slot]], 1ull);
+    if (routing && g == (int)gridDim.x - 1) {
+      if (slot != 0 || wave != 0) return;
+      route_select<ME>(a.logits, a.E, a.slots, a.normalize, sel.sel_idx, sel.sel_w, tab, sel.e);
+      if (lane < a.slots) {
+        a.route_out_idx[lane] = sel.sel_idx[lane];
+        a.route_out_w[lane] = sel.sel_w[lane];
+        if (a.stats) atomicAdd(&a.stats[sel.sel_idx[lane]], 1ull);
+      }
+      return;
+    }
+    if (routing) {
+      auto& sl = sel;
+      for (int i = threadIdx.x; i < ME; i += 64 * NW) {
+        const float l = i < a.E ? a.logits[i] : 0.0f;
+        sl.logit[i] = l;
+        sl.key[i] = order_key(l);
+        sl.ck[i] = i < a.E ? (unsigned long long)order_key(l) << 32 | (unsigned)~i : 0ull;
       }
       __syncthreads();
-      expert = sel_idx[slot];
+      rank_by_logit<NW>(sl, a.E, a.slots);
+      __syncthreads();
+      expert = sl.by_logit[slot];
+      safe = ranking_is_safe(sl, a.E, a.slots);
     }
   }
 
-  // tile and matrix of this lane's row
-  const uint8_t* cbase;
-  const uint16_t* sbase;
-  size_t tile;
-  if constexpr (EPI == EPI_GATE_UP) {
-    tile = g;
-    cbase = (lane < 32 ? a.codes : a.codes2) + (size_t)expert * a.codes_stride;
-    sbase = (lane < 32 ? a.scales : a.scales2) + (size_t)expert * a.scales_stride;
-  } else {
-    tile = 2 * (size_t)g + (lane >> 5);
-    cbase = a.codes + (size_t)expert * a.codes_stride;
-    sbase = a.scales + (size_t)expert * a.scales_stride;
-  }
-  const int r = lane & 31;
-  const uint8_t* crow = cbase + (tile * nb * CH * TILE + r) * 16;
-  const uint16_t* srow = sbase + tile * nb * TILE + r;
-  const ActBlock* act = s_act;
+  // One pass over this slot's rows of `ex`: loads, block terms, the fold in
+  // block order.  Returns wave 0's row totals.  On the first pass the
+  // activation blocks are staged and (with routing) wave 1 checks the
+  // selection after issuing its first loads.
+  auto pass = [&](int ex, bool first) -> float {
+    // tile and matrix of this lane's row
+    const uint8_t* cbase;
+    const uint16_t* sbase;
+    size_t tile;
+    if constexpr (EPI == EPI_GATE_UP) {
+      tile = g;
+      cbase = (lane < 32 ? a.codes : a.codes2) + (size_t)ex * a.codes_stride;
+      sbase = (lane < 32 ? a.scales : a.scales2) + (size_t)ex * a.scales_stride;
+    } else {
+      tile = 2 * (size_t)g + (lane >> 5);
+      cbase = a.codes + (size_t)ex * a.codes_stride;
+      sbase = a.scales + (size_t)ex * a.scales_stride;
+    }
+    const int r = lane & 31;
+    const uint8_t* crow = cbase + (tile * nb * CH * TILE + r) * 16;
+    const uint16_t* srow = sbase + tile * nb * TILE + r;
+    const ActBlock* act = s_act;
 
-  u32x4 cw[UPW][CH];
-  uint16_t sw[UPW];
-  // Blocks past the end of the row are clamped to the last block (an
-  // in-bounds load whose term is never stored), so the chunk loop has no
-  // branches and all of its loads are in flight together.
-  auto load_block = [&](int ch, int s) {
-    const int b = min(ch * CB + wave + NW * s, nb - 1);
+    u32x4 cw[UPW][CH];
+    uint16_t sw[UPW];
+    // Blocks past the end of the row are clamped to the last block (an
+    // in-bounds load whose term is never stored; the same goes for groups),
+    // so the chunk loop has no branches and all of its loads are in flight
+    // together.  (A clamped block's activation may be another wave's: it
+    // only feeds that discarded term.)
+    auto block_of = [&](int ch, int s) { return min(ch * CB + wave * UPW + s, nb - 1); };
+    auto load_block = [&](int ch, int s) {
+      const int b = block_of(ch, s);
 #pragma unroll
-    for (int c = 0; c < CH; c++)
-      cw[s][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
-    sw[s] = srow[(size_t)b * TILE];
-  };
-  auto load_chunk = [&](int ch) {
+      for (int c = 0; c < CH; c++)
+        cw[s][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
+      sw[s] = srow[(size_t)b * TILE];
+    };
+    auto load_chunk = [&](int ch) {
 #pragma unroll
-    for (int s = 0; s < UPW; s++) load_block(ch, s);
-  };
+      for (int s = 0; s < UPW; s++) load_block(ch, s);
+    };
 
-  float total = 0.0f;
-  const int nchunks = (nb + CB - 1) / CB;
-  load_chunk(0);
-  if (!routing) {
-    stage_act();
-    __syncthreads();
-  }
-  for (int ch = 0; ch < nchunks; ch++) {
-    const int b0 = ch * CB;
-    const int bend = min(nb, b0 + CB);
-    float(*tb)[GROUP] = terms[ch & 1];
-    // Terms in groups of four blocks; each group's registers take the next
-    // chunk's loads as soon as its terms are done.  The scheduling barriers
-    // keep the activation reads of one group live at a time, so the kernel
-    // keeps few VGPRs (83-134: two work-groups per CU).
-    float tv[UPW];
-    const bool more = ch + 1 < nchunks;
+    float total = 0.0f;
+    const int nchunks = (nb + CB - 1) / CB;
+    load_chunk(0);
+    if (first) {
+      stage_act();
+      if constexpr (EPI == EPI_GATE_UP)
+        if (routing && !safe && wave == 1) verify_selection(sel, a.E, a.slots, a.normalize, tab);
+    }
+    for (int ch = 0; ch < nchunks; ch++) {
+      const int b0 = ch * CB;
+      const int bend = min(nb, b0 + CB);
+      float(*tb)[GROUP] = terms[ch & 1];
+      // Terms in groups of four blocks; each group's registers take the next
+      // chunk's loads as soon as its terms are done.  The scheduling barriers
+      // keep the activation reads of one group live at a time, so the kernel
+      // keeps few VGPRs.
+      float tv[UPW];
+      const bool more = ch + 1 < nchunks;
 #pragma unroll
-    for (int s0 = 0; s0 < UPW; s0 += 4) {
+      for (int s0 = 0; s0 < UPW; s0 += 4) {
 #pragma unroll
-      for (int s = s0; s < s0 + 4; s++)
-        tv[s] = block_term<DT>(cw[s], sw[s], act + min(b0 + wave + NW * s, nb - 1));
+        for (int s = s0; s < s0 + 4; s++)
+          tv[s] = block_term<DT>(cw[s], sw[s], act + block_of(ch, s));
 #pragma unroll
-      for (int s = s0; s < s0 + 4; s++) asm volatile("" : "+v"(tv[s]));  // computed here, not at the store
-      __builtin_amdgcn_sched_barrier(0);
-      if (more) {
+        for (int s = s0; s < s0 + 4; s++) asm volatile("" : "+v"(tv[s]));  // computed here, not at the store
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) {
 #pragma unroll
-        for (int s = s0; s < s0 + 4; s++) load_block(ch + 1, s);
+          for (int s = s0; s < s0 + 4; s++) load_block(ch + 1, s);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // Rows past the end of the row's blocks take the clamped terms and are
-    // never folded; an unconditional store keeps each term's computation
-    // where it is written (a conditional one would be sunk into the store's
-    // branch, keeping every input live until then).
+      // Blocks past the end of the row take the clamped terms and are never
+      // folded; an unconditional store keeps each term's computation where it
+      // is written (a conditional one would be sunk into the store's branch,
+      // keeping every input live until then).
 #pragma unroll
-    for (int s = 0; s < UPW; s++) tb[wave + NW * s][lane] = tv[s];
-    __syncthreads();
-    if (wave == 0) total = lds_sum_strided<GROUP>(&tb[0][lane], bend - b0, total);
+      for (int s = 0; s < UPW; s++) tb[wave * UPW + s][lane] = tv[s];
+      __syncthreads();
+      if (wave == 0) {  // the fold chains first when the SIMD has several ready waves
+        __builtin_amdgcn_s_setprio(3);
+        total = lds_sum_strided<GROUP>(&tb[0][lane], bend - b0, total);
+        __builtin_amdgcn_s_setprio(0);
+      }
+    }
+    return total;
+  };
+
+  float total = pass(expert, true);
+  if constexpr (EPI == EPI_GATE_UP) {
+    if (routing && !safe) {
+      // the check finished before the first chunk's barrier
+      auto& sl = sel;
+      const int chosen = sl.sel_idx[slot];
+      if (sl.bad && chosen != expert) {  // uniform: a tie moved this slot to another expert
+        __syncthreads();                 // wave 0 is done with the term buffers
+        total = pass(chosen, false);
+        expert = chosen;
+      }
+    }
   }
   if (wave != 0) return;
 
+  const int r = lane & 31;
   if constexpr (EPI == EPI_PLAIN) {
-    size_t row = tile * TILE + r;
+    const size_t row = (2 * (size_t)g + (lane >> 5)) * TILE + r;
     if (row < (size_t)a.rows) a.out[row] = total;
   } else if constexpr (EPI == EPI_GATE_UP) {
     float u = __shfl(total, lane + 32);
@@ -784,13 +935,19 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
 // for each route in best-first order out = out + w_s * down_s(h_s).  A
 // work-group owns DR = 8 output rows for every slot, so the combine needs no
 // other work-group, and the launch has H / 8 work-groups (256 at H = 2048).
-// Its units are the (slot, block) pairs in slot-major order.  One wave-load
-// covers 8 units x 8 rows: 8 segments of 128 B, each one cache line of the
-// tile layout.  A chunk of CB units is loaded at once (UPW loads in flight
-// per lane) together with its activation blocks; terms go to LDS.  The fold
-// runs on 64 lanes, one per (row, slot): each adds its slot's block terms in
-// block order, which is the reference's per-expert dot product, and the
-// combine then takes the slots in route order.
+//
+// Units are (slot, block) pairs, taken in groups of eight consecutive blocks
+// of one slot: pair p is block group p / slots of slot p % slots.  One
+// wave-load covers one pair for the group's 8 rows: 8 segments of 128 B,
+// each a cache line of the tile layout.  A chunk is CP consecutive pairs,
+// so every slot's blocks advance in every chunk, and with them all 8 x slots
+// fold chains.  Loads run two chunks ahead: chunk c + 2 is issued as soon
+// as chunk c's terms are computed, while chunk c + 1 is in flight.  Each
+// wave stages the activation blocks of its own units in LDS, so only the
+// terms cross waves.  Wave 0 folds chunk c (64 lanes, one per (row, slot)
+// chain, adding its slot's blocks in order: the reference's per-expert dot
+// product) while the other waves compute chunk c + 1; the combine then
+// takes the slots in route order.
 
 // u / n for 0 <= u < 2^20 from a float reciprocal, corrected to the exact
 // quotient (below 2^20 the float estimate is off by at most one)
@@ -802,27 +959,21 @@ __device__ __forceinline__ int div_small(int u, int n, float inv_n) {
 }
 
 constexpr int DR = DOWN_ROWS;   // rows per work-group of k_down_combine
-// Waves per work-group of k_down_combine: 8 when the row groups fit the
-// CUs one work-group each (the terms after the loads land are spread over
-// twice the waves: 7.4 -> 6.2 us at H 2048), else 4, which keeps two
-// work-groups per CU (8 waves need 167 VGPRs: at H 4096, 512 row groups
-// would run in two rounds).
 constexpr int DOWN_MAX_SLOTS = 64;
 
 template <int DT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
-  constexpr int J = 64 / DR;        // units side by side in one wave-load
-  constexpr int UPW = 64 / NW / CH;  // loads of 16 B in flight per lane
-  constexpr int CB = NW * J * UPW;   // units per chunk: 512 (q4_0), 256 (q8_0)
-  static_assert(UPW % 4 == 0, "terms go in groups of four wave-loads");
-  constexpr int AQ = (CB * 3 + 64 * NW - 1) / (64 * NW);
-  constexpr int SPL = DOWN_MAX_SLOTS / 8;  // slots per fold lane
-  // terms of row r at [r][unit]: a fold lane reads its slot's terms from
-  // consecutive addresses (16-byte reads, several in flight); the row pitch
-  // CB + 8 puts the 64 lanes of a term store in distinct banks
-  __shared__ __attribute__((aligned(16))) float terms[DR][CB + 8];
-  __shared__ ActBlock s_act[CB];
+  constexpr int UPW = 4 / CH;        // pairs per wave and chunk (4 loads of 16 B per lane)
+  constexpr int CP = NW * UPW;       // pairs per chunk
+  constexpr int CU = CP * 8;         // units per chunk
+  constexpr int APL = (UPW * 24 + 63) / 64;  // 16-byte activation pieces per lane and chunk
+  constexpr int SPL = DOWN_MAX_SLOTS / 8;    // slots per fold lane
+  // terms of row r at [r][unit]; the row pitch CU + 4 spreads the rows of a
+  // term store over the banks
+  __shared__ __attribute__((aligned(16))) float terms[2][DR][CU + 4];
+  __shared__ ActBlock s_act[NW][UPW * 8];  // each wave's activation blocks of its current chunk
+  __shared__ u32x4 s_scl[NW][UPW * 8];     // and its scales: [pair][block] x 8 rows
   __shared__ float s_tot[DOWN_MAX_SLOTS][DR];
   __shared__ int s_exp[DOWN_MAX_SLOTS];
   __shared__ float s_w[DOWN_MAX_SLOTS];
@@ -832,15 +983,17 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
   const int g = blockIdx.x;
   const int nb = a.nb;
   const int slots = a.slots;
-  const int nunits = slots * nb;
-  const float inv_nb = 1.0f / (float)nb;
+  const int nbg = (nb + 7) / 8;
+  const int npairs = slots * nbg;
+  const int nchunks = (npairs + CP - 1) / CP;
+  const float inv_slots = 1.0f / (float)slots;
   if (threadIdx.x < slots) {
     s_exp[threadIdx.x] = a.route_idx[threadIdx.x];
     s_w[threadIdx.x] = a.route_w[threadIdx.x];
   }
 
-  const int r = lane % DR;          // row within the group
-  const int jl = lane / DR;         // unit within the wave-load
+  const int r = lane % DR;  // row within the group
+  const int j = lane / DR;  // block within the pair's group of eight
   // The four 8-row groups of a 32-row tile share its scale lines; work-group
   // g runs on XCD g % 8, so when the grid is a multiple of 32 the groups of
   // one tile get ids of one residue class: XCD x takes tiles x, x + 8, ...
@@ -853,113 +1006,154 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
   const size_t tile = row0 / TILE;
   const int rt = (int)(row0 % TILE) + r;  // row within its 32-row tile
   const size_t row_off = (tile * nb * CH * TILE + rt) * 16;
-  const size_t srow_off = tile * nb * TILE + rt;
+  // the scales of the group's 8 rows for block b: 16 bytes at
+  // srow_off + b * TILE elements
+  const size_t srow_off = tile * nb * TILE + row0 % TILE;
 
-  u32x4 cw[UPW][CH];
-  uint16_t sw[UPW];
-  u32x4 av[AQ];
-  // unit of load s in the chunk at u0 (past the end: clamped to the last
-  // unit, loaded and never stored)
-  auto unit_of = [&](int u0, int s) { return min(u0 + (s * NW + wave) * J + jl, nunits - 1); };
-  // wave-load s of the chunk at u0 holds at least one unit (wave-uniform)
-  auto live = [&](int u0, int s) { return (s * NW + wave) * J < nunits - u0; };
-  // The expert of each lane's unit comes from LDS; the lookups of a batch of
-  // wave-loads are issued together (and pinned there) before its loads.
-  int ex[UPW];
-  auto lookup = [&](int u0, int s0, int n) {
-#pragma unroll
-    for (int s = s0; s < s0 + n; s++) ex[s] = s_exp[div_small(unit_of(u0, s), nb, inv_nb)];
-#pragma unroll
-    for (int s = s0; s < s0 + n; s++) asm volatile("" : "+v"(ex[s]));
+  struct Buf {
+    u32x4 cw[UPW][CH];
+    u32x4 sv;  // lanes < UPW * 8: the group's 8 rows' scales of one block of one pair
+    u32x4 av[APL];
   };
-  auto load_unit = [&](int u0, int s) {
-    const int u = unit_of(u0, s);
-    const int sl = div_small(u, nb, inv_nb), b = u - sl * nb;
-    const size_t e = (size_t)ex[s];
-    const uint8_t* c0 = a.codes + e * a.codes_stride + row_off;
+  // pair of wave-load s in chunk c (wave-uniform)
+  auto pair_of = [&](int c, int s) { return c * CP + s * NW + wave; };
+  // Issues chunk c's loads into B: every live wave-load's codes and scales,
+  // and the activation blocks of the wave's units.  Blocks past the end of
+  // the row are clamped to the last block (in-bounds; their terms are never
+  // folded).
+  auto issue = [&](Buf& B, int c) {
 #pragma unroll
-    for (int c = 0; c < CH; c++)
-      cw[s][c] = __builtin_nontemporal_load((const u32x4*)(c0 + ((size_t)b * CH + c) * TILE * 16));
-    sw[s] = a.scales[e * a.scales_stride + srow_off + (size_t)b * TILE];
-  };
-  auto load_act = [&](int u0) {
+    for (int s = 0; s < UPW; s++) {
+      const int p = pair_of(c, s);
+      if (p < npairs) {  // wave-uniform
+        const int bg = div_small(p, slots, inv_slots), sl = p - bg * slots;
+        const int b = min(bg * 8 + j, nb - 1);
+        const size_t e = (size_t)s_exp[sl];
+        const uint8_t* c0 = a.codes + e * a.codes_stride + row_off;
 #pragma unroll
-    for (int q = 0; q < AQ; q++) {
-      const int i = threadIdx.x + q * 64 * NW;
-      const int u = u0 + i / 3;
-      if (i < CB * 3 && u < nunits) {
-        const int sl = div_small(u, nb, inv_nb), b = u - sl * nb;
-        av[q] = ((const u32x4*)(a.hact + (size_t)sl * a.hact_stride + b))[i % 3];
+        for (int q = 0; q < CH; q++)
+          B.cw[s][q] = __builtin_nontemporal_load((const u32x4*)(c0 + ((size_t)b * CH + q) * TILE * 16));
+      }
+    }
+    {  // lane l < UPW * 8: block l % 8 of pair l / 8 (clamped like the codes)
+      const int s = lane / 8, p = pair_of(c, s);
+      if (lane < UPW * 8 && p < npairs) {
+        const int bg = div_small(p, slots, inv_slots), sl = p - bg * slots;
+        const int b = min(bg * 8 + lane % 8, nb - 1);
+        const size_t e = (size_t)s_exp[sl];
+        B.sv = *(const u32x4*)(a.scales + e * a.scales_stride + srow_off + (size_t)b * TILE);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < APL; m++) {
+      const int q = lane + 64 * m;  // piece q % 3 of unit q / 3 of the wave's units
+      const int s = q / 24, u = (q % 24) / 3;
+      const int p = pair_of(c, s);
+      if (q < UPW * 24 && p < npairs) {
+        const int bg = div_small(p, slots, inv_slots), sl = p - bg * slots;
+        const int b = min(bg * 8 + u, nb - 1);
+        B.av[m] = ((const u32x4*)(a.hact + (size_t)sl * a.hact_stride + b))[q % 3];
       }
     }
   };
 
-  // fold lane (row r, slot group jl): slots jl, jl + 8, ...; running sums of
-  // the current slot are kept per slot because a chunk may end mid-slot
+  // fold lane (row r, slot group j): slots j, j + 8, ...
   float tot[SPL];
 #pragma unroll
   for (int i = 0; i < SPL; i++) tot[i] = 0.0f;
 
-  load_act(0);      // the activation blocks do not depend on the routes
-  __syncthreads();  // s_exp / s_w
-  lookup(0, 0, UPW);
+  // Chunk c from B: stage the wave's activation blocks, the block terms,
+  // chunk c + 2's loads into B, the terms to LDS; then wave 0 folds them.
+  auto process = [&](Buf& B, int c) {
+    float(*tb)[CU + 4] = terms[c & 1];
 #pragma unroll
-  for (int s = 0; s < UPW; s++)
-    if (live(0, s)) load_unit(0, s);
-  for (int u0 = 0; u0 < nunits; u0 += CB) {
-#pragma unroll
-    for (int q = 0; q < AQ; q++) {
-      const int i = threadIdx.x + q * 64 * NW;
-      if (i < CB * 3 && u0 + i / 3 < nunits) ((u32x4*)s_act)[i] = av[q];
+    for (int m = 0; m < APL; m++) {
+      const int q = lane + 64 * m;
+      if (q < UPW * 24 && pair_of(c, q / 24) < npairs) ((u32x4*)s_act[wave])[q] = B.av[m];
     }
-    __syncthreads();
-    // Terms in groups of four wave-loads; each group's registers take the
-    // next chunk's loads as soon as its terms are done (the asm statements
-    // and scheduling barriers keep that order and the register count low).
-    const bool more = u0 + CB < nunits;
+    if (lane < UPW * 8 && pair_of(c, lane / 8) < npairs) s_scl[wave][lane] = B.sv;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float tv[UPW];
 #pragma unroll
-    for (int s0 = 0; s0 < UPW; s0 += 4) {
-#pragma unroll
-      for (int s = s0; s < s0 + 4; s++)
-        if (live(u0, s)) tv[s] = block_term<DT>(cw[s], sw[s], s_act + (unit_of(u0, s) - u0));
-#pragma unroll
-      for (int s = s0; s < s0 + 4; s++)
-        if (live(u0, s)) asm volatile("" : "+v"(tv[s]));
-      __builtin_amdgcn_sched_barrier(0);
-      if (more) {
-        lookup(u0 + CB, s0, 4);
-#pragma unroll
-        for (int s = s0; s < s0 + 4; s++)
-          if (live(u0 + CB, s)) load_unit(u0 + CB, s);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (more) load_act(u0 + CB);
-    // (s * NW + wave) * J + jl < CB: every store is in the chunk; units past
-    // the end of a live wave-load hold clamped terms that the fold never reads
+    for (int s = 0; s < UPW; s++)
+      if (pair_of(c, s) < npairs)
+        tv[s] = block_term<DT>(B.cw[s], ((const uint16_t*)&s_scl[wave][s * 8 + j])[r], &s_act[wave][s * 8 + j]);
 #pragma unroll
     for (int s = 0; s < UPW; s++)
-      if (live(u0, s)) terms[r][(s * NW + wave) * J + jl] = tv[s];
-    __syncthreads();
+      if (pair_of(c, s) < npairs) asm volatile("" : "+v"(tv[s]));  // computed here, not at the store
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 2 < nchunks) issue(B, c + 2);
+#pragma unroll
+    for (int s = 0; s < UPW; s++)
+      if (pair_of(c, s) < npairs) tb[r][(s * NW + wave) * 8 + j] = tv[s];
+    __syncthreads();  // chunk c's terms are in; wave 0 has folded chunk c - 1
     if (wave == 0) {
-      const int uend = min(nunits, u0 + CB);
+      // The fold chains are the critical path of the chunk: their wave goes
+      // first when the SIMD has several ready waves (the others fill its gaps)
+      __builtin_amdgcn_s_setprio(3);
+      const int pbeg = c * CP, pend = min(npairs, pbeg + CP);
 #pragma unroll
       for (int i = 0; i < SPL; i++) {
-        const int sl = jl + 8 * i;
+        const int sl = j + 8 * i;
         if (sl < slots) {
-          // this slot's units inside the chunk, in block order
-          const int ua = max(u0, sl * nb), ub = min(uend, (sl + 1) * nb);
-          if (ub > ua) tot[i] = lds_sum_in_order(&terms[r][ua - u0], ub - ua, tot[i]);
+          // this slot's pairs in the chunk, in block order: p = sl + q slots,
+          // block group q; each pair's eight terms are read while the
+          // previous pair's are added
+          const int q0 = (pbeg - sl + slots - 1) / slots;
+          const int p0 = sl + q0 * slots;
+          const int np = p0 < pend ? (pend - p0 + slots - 1) / slots : 0;
+          const float* t = &tb[r][(p0 - pbeg) * 8];
+          const int ts = slots * 8;
+          float acc = tot[i];
+          f32x4 x0, x1;
+          if (np > 0) {
+            x0 = *(const f32x4*)t;
+            x1 = *(const f32x4*)(t + 4);
+          }
+          for (int m = 0; m < np; m++) {
+            f32x4 y0 = x0, y1 = x1;
+            if (m + 1 < np) {
+              y0 = *(const f32x4*)(t + (m + 1) * ts);
+              y1 = *(const f32x4*)(t + (m + 1) * ts + 4);
+            }
+            const int n = nb - 8 * (q0 + m);  // blocks of this group inside the row
+            if (n >= 8) {
+              acc = acc + x0.x;
+              acc = acc + x0.y;
+              acc = acc + x0.z;
+              acc = acc + x0.w;
+              acc = acc + x1.x;
+              acc = acc + x1.y;
+              acc = acc + x1.z;
+              acc = acc + x1.w;
+            } else {  // the row's last, partial group
+              const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+              for (int k = 0; k < n; k++) acc = acc + v[k];
+            }
+            x0 = y0;
+            x1 = y1;
+          }
+          tot[i] = acc;
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
-    __syncthreads();  // terms and s_act are rewritten by the next chunk
+  };
+
+  __syncthreads();  // s_exp / s_w
+  Buf A, B;
+  issue(A, 0);
+  if (nchunks > 1) issue(B, 1);
+  for (int c = 0; c < nchunks; c += 2) {
+    process(A, c);
+    if (c + 1 < nchunks) process(B, c + 1);
   }
   if (wave != 0) return;
 #pragma unroll
   for (int i = 0; i < SPL; i++) {
-    const int sl = jl + 8 * i;
+    const int sl = j + 8 * i;
     if (sl < slots) s_tot[sl][r] = tot[i];
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -969,6 +1163,139 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
     float acc = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
     for (int sl = 0; sl < slots; sl++) acc = acc + s_w[sl] * s_tot[sl][lane];
     const size_t row = row0 + lane;
+    if (row < (size_t)a.rows) a.out[row] = acc;
+  }
+}
+
+// The same projection and combine with whole fold chains per wave, used
+// when every slot's activation blocks fit in LDS.  A work-group owns RG
+// output rows for every slot; wave w takes the chains (8 rows, slot) of row
+// subgroup w / SW and slots w % SW, w % SW + SW, ... (SW = min(slots, 8)).
+// A wave walks its slot's blocks in groups of eight: lane 8 r + j holds row
+// r, block 8 q + j of group q, so one wave-load is 8 cache lines of the tile
+// layout.  D groups are in flight; each group's terms fold into the row's
+// running sum as soon as they are computed, in block order, by DPP adds
+// within the row's 8 lanes, so no other wave or barrier is waited for until
+// the combine.  RG = 16 for 2 or 3 slots (4 or 6 waves), 32 for 1 (4
+// waves); the launcher takes it for 1 to 3 slots.
+constexpr int DOWN_ACT_MAX = 1024;  // activation blocks staged in LDS (48 KB)
+
+__host__ __device__ inline int down_chain_rows(int slots) { return slots >= 4 ? 8 : (slots >= 2 ? 16 : 32); }
+__host__ __device__ inline int down_chain_waves(int slots) {
+  return down_chain_rows(slots) / 8 * (slots < 8 ? slots : 8);
+}
+
+template <int DT, int D>  // D: groups in flight per wave, a multiple of 4
+__global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
+  constexpr int CH = Layout<DT>::CH;
+  static_assert(D % 4 == 0, "groups go in batches of four");
+  __shared__ ActBlock s_act[DOWN_ACT_MAX];
+  __shared__ float s_tot[DOWN_MAX_SLOTS][32];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x;
+  const int nb = a.nb, slots = a.slots;
+  const int nbg = (nb + 7) / 8;
+  const int sw = slots < 8 ? slots : 8;
+  const int rg = down_chain_rows(slots);
+  const int sub = wave / sw, scls = wave % sw;
+  // every slot's activation blocks (independent of the routes): loads
+  // issued first, stored after the first weight loads
+  constexpr int APT = (DOWN_ACT_MAX * 3 + 255) / 256;  // pieces per thread, at most (256+ threads)
+  const int npieces = slots * nb * 3;
+  u32x4 av[APT];
+#pragma unroll
+  for (int m = 0; m < APT; m++) {
+    const int i = threadIdx.x + m * blockDim.x;
+    if (i < npieces) {
+      const int sl = i / (nb * 3), rem = i - sl * nb * 3;
+      av[m] = ((const u32x4*)(a.hact + (size_t)sl * a.hact_stride))[rem];
+    }
+  }
+  // The row groups of a 32-row tile share its scale lines; work-group g runs
+  // on XCD g % 8, so when the grid allows the groups of one tile get ids of
+  // one residue class (a permutation of the row groups).
+  const int per_tile = 32 / rg;
+  size_t row0 = (size_t)g * rg;
+  if (per_tile > 1 && gridDim.x % (8 * per_tile) == 0) {
+    const int gx = g & 7, gj = g >> 3;
+    row0 = (size_t)(gx + 8 * (gj / per_tile)) * TILE + (size_t)(gj % per_tile) * rg;
+  }
+  const int r = lane >> 3, j = lane & 7;
+  const size_t rowg = row0 + (size_t)sub * 8;
+  const size_t tile = rowg / TILE;
+  const int rt = (int)(rowg % TILE) + r;
+  const size_t row_off = (tile * nb * CH * TILE + rt) * 16;
+  const size_t srow_off = tile * nb * TILE + rt;
+
+  u32x4 cw[D][CH];
+  uint16_t sc[D];
+  const uint8_t* cbase;
+  const uint16_t* sbase;
+  // group q's loads into ring slot d (groups past the end are clamped to
+  // the last: in-bounds loads that are never used)
+  auto load = [&](int d, int q) {
+    const int b = min(min(q, nbg - 1) * 8 + j, nb - 1);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+      cw[d][c] = __builtin_nontemporal_load((const u32x4*)(cbase + ((size_t)b * CH + c) * TILE * 16));
+    sc[d] = sbase[(size_t)b * TILE];
+  };
+  auto start_chain = [&](int sl) {
+    const size_t e = (size_t)__builtin_amdgcn_readfirstlane(a.route_idx[sl]);
+    cbase = a.codes + e * a.codes_stride + row_off;
+    sbase = a.scales + e * a.scales_stride + srow_off;
+#pragma unroll
+    for (int d = 0; d < D; d++) load(d, d);
+  };
+  start_chain(scls);
+#pragma unroll
+  for (int m = 0; m < APT; m++) {
+    const int i = threadIdx.x + m * blockDim.x;
+    if (i < npieces) ((u32x4*)s_act)[i] = av[m];
+  }
+  __syncthreads();  // s_act
+
+  for (int sl = scls; sl < slots; sl += sw) {
+    if (sl != scls) start_chain(sl);
+    const ActBlock* act = s_act + (size_t)sl * nb;
+    float acc = 0.0f;  // row r's dot product (valid in lane 8 r)
+    for (int q0 = 0; q0 < nbg; q0 += D) {
+#pragma unroll
+      for (int d0 = 0; d0 < D; d0 += 4) {
+        const int qb = q0 + d0;
+        if (qb < nbg) {  // wave-uniform; the batch's four terms, then their sums in order
+          float t[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) t[i] = block_term<DT>(cw[d0 + i], sc[d0 + i], act + min((qb + i) * 8 + j, nb - 1));
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            // groups past the row's end have n <= 0 and add nothing
+            const int n = nb - (qb + i) * 8;  // blocks of the group inside the row
+            const float ti = t[i];
+            acc = n > 0 ? acc + ti : acc;
+#define HALE_ROW_TERM(k)                                                                        \
+  {                                                                                             \
+    const float tk = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ti), 0x100 + (k), 0xF, 0xF, false)); \
+    acc = (k) < n ? acc + tk : acc;                                                             \
+  }
+            HALE_ROW_TERM(1) HALE_ROW_TERM(2) HALE_ROW_TERM(3) HALE_ROW_TERM(4)
+            HALE_ROW_TERM(5) HALE_ROW_TERM(6) HALE_ROW_TERM(7)
+#undef HALE_ROW_TERM
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) load(d0 + i, qb + i + D);
+      }
+    }
+    if (j == 0) s_tot[sl][sub * 8 + r] = acc;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < rg) {
+    float acc = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
+    for (int sl = 0; sl < slots; sl++) acc = acc + a.route_w[sl] * s_tot[sl][threadIdx.x];
+    const size_t row = row0 + threadIdx.x;
     if (row < (size_t)a.rows) a.out[row] = acc;
   }
 }
@@ -1089,10 +1416,13 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   if (a.nb < 1 || a.nb > GEMV_MAX_NB) return hipErrorInvalidValue;
   if (a.logits && (epi != EPI_GATE_UP || a.E > ROUTE_MAX_E || slots > 64 || slots > a.E))
     return hipErrorInvalidValue;
-  dim3 grid(groups, slots);
-#define HALE_GEMV_CASE(D, E, W)                               \
-  if (dtype == D && epi == E) {                               \
-    return launch(k_gemv<D, E, W>, grid, 64 * W, 0, st, a);   \
+  // gate/up with routing: one more column of work-groups for the selector
+  dim3 grid(groups + (a.logits ? 1 : 0), slots);
+  const bool many = a.logits && a.E > 256;  // selection state for up to 1024 experts
+#define HALE_GEMV_CASE(D, E, W)                                                       \
+  if (dtype == D && epi == E) {                                                       \
+    if (many) return launch(k_gemv<D, E, W, ROUTE_MAX_E>, grid, 64 * W, 0, st, a);    \
+    return launch(k_gemv<D, E, W>, grid, 64 * W, 0, st, a);                           \
   }
   HALE_GEMV_CASE(Q8_0, EPI_PLAIN, 4)
   HALE_GEMV_CASE(Q8_0, EPI_GATE_UP, 8)
@@ -1107,23 +1437,25 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   const unsigned groups = (unsigned)(padded_rows((size_t)a.rows) / DR);
   if (groups == 0) return hipSuccess;
   if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS) return hipErrorInvalidValue;
-  // CUs of the current device, looked up once per device
-  static std::atomic<int> cu_count[64];
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  int cus = dev < 64 ? cu_count[dev].load(std::memory_order_relaxed) : 0;
-  if (cus == 0) {
-    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-    if (dev < 64) cu_count[dev].store(cus, std::memory_order_relaxed);
+  // A wave per (slot, 8 rows) pays off when few routes leave many rows per
+  // work-group (top-1..3); top-4 and wider use the block-group pipeline.
+  if (a.slots <= 3 && a.slots * a.nb <= DOWN_ACT_MAX) {
+    const int rg = down_chain_rows(a.slots);
+    const unsigned grid = (unsigned)(padded_rows((size_t)a.rows) / rg);
+    const unsigned threads = 64 * down_chain_waves(a.slots);
+    const int nbg = (a.nb + 7) / 8;
+#define HALE_DOWN_CHAIN(D)                                                                  \
+  do {                                                                                      \
+    if (dtype == Q8_0) return launch(k_down_chain<Q8_0, D>, grid, threads, 0, st, a);       \
+    if (dtype == Q4_0) return launch(k_down_chain<Q4_0, D>, grid, threads, 0, st, a);       \
+  } while (0)
+    if (nbg <= 4) HALE_DOWN_CHAIN(4);
+    if (nbg <= 8 || dtype == Q8_0) HALE_DOWN_CHAIN(8);
+    HALE_DOWN_CHAIN(16);
+#undef HALE_DOWN_CHAIN
   }
-  if (groups <= (unsigned)cus) {
-    if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 8>, groups, 512, 0, st, a);
-    if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 8>, groups, 512, 0, st, a);
-  }
-  if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 4>, groups, 256, 0, st, a);
-  if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 4>, groups, 256, 0, st, a);
+  if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 8>, groups, 512, 0, st, a);
+  if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 8>, groups, 512, 0, st, a);
   return hipErrorInvalidValue;
 }
 

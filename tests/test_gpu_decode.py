@@ -305,11 +305,12 @@ def test_moe_decode_mixtral_q4_bit_exact(ctx):
 @pytest.mark.parametrize("hidden,E,k", [(4096, 16, 3), (4096, 8, 8), (4160, 8, 2), (2048, 8, 8),
                                         (2080, 8, 4)])
 def test_moe_decode_wide_hidden(ctx, dtype, hidden, E, k):
-    # wide hidden sizes for both dtypes (H 4160: 520 row groups, not a
-    # multiple of 32, so the down kernel's XCD permutation of the row groups
-    # is off); 2, 3, 4 and 8 slots per token.  H 2048: one-chunk gate/up rows
-    # (16 waves for q4_0) and 256 down row groups (8 waves); H 2080: 65
-    # blocks (8 waves, two chunks) and 264 row groups (4 waves)
+    # wide hidden sizes for both dtypes; 2, 3, 4 and 8 slots per token.
+    # 2 and 3 slots run the whole-chain down kernel (16-row groups: H 4160
+    # gives 260 work-groups, not a multiple of 16, so its XCD permutation is
+    # off), 4 and 8 the pipelined one (8-row groups: H 2080 gives 260, its
+    # permutation off too).  Gate/up: H 2048 is one chunk per row (16 waves
+    # for q4_0), H 2080 is 65 blocks (8 waves, two chunks)
     L = O.OracleMoe.synthetic(dtype, hidden, 256, E, k, normalize_topk=True, seed=hidden + E + k)
     moe = make_layer(ctx, L)
     for seed in range(2):
@@ -388,15 +389,43 @@ def test_moe_decode_qwen235b_q4_bit_exact(ctx, qwen235b_q4):
 @pytest.mark.parametrize("dtype,hidden,inter", [(H.Q4_0, 2048, 2080), (H.Q4_0, 4096, 2080),
                                                 (H.Q8_0, 2048, 1056), (H.Q8_0, 4096, 1056)])
 def test_moe_decode_down_chunk_boundary(ctx, dtype, hidden, inter):
-    """Down + combine over more units (slot, block) than one chunk holds
-    (512 for q4_0, 256 for q8_0), with slot 7 straddling the chunk boundary
-    (8 slots x 65 blocks = 520; 8 x 33 = 264): the running per-slot sums cross
-    chunks.  H 2048 runs the 8-wave kernel, H 4096 the 4-wave one."""
+    """Pipelined down + combine over more (slot, 8-block group) pairs than one
+    chunk holds (32 for q4_0, 16 for q8_0): 8 slots x 9 groups = 72 and
+    8 x 5 = 40 pairs, with slot 3 straddling the first chunk boundary, so the
+    running per-slot sums cross chunks.  H 2048 and 4096: 256 and 512
+    work-groups, the XCD permutation on."""
     L = O.OracleMoe.synthetic(dtype, hidden, inter, 12, 8, normalize_topk=True,
                               seed=hidden + inter)
     moe = make_layer(ctx, L)
     for seed in range(2):
         x = O.normal(8000 + seed, hidden)
+        out, idx, w = moe.forward(x, return_routes=True)
+        o_out, o_idx, o_w = L.forward(x, nthreads=8)
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+    moe.close()
+
+
+@pytest.mark.parametrize("dtype,hidden,inter,E,k", [
+    (H.Q4_0, 2048, 2080, 6, 1),    # 1 slot: 32-row groups; 65 blocks, 9 groups: ring of 16, one partial batch
+    (H.Q8_0, 2080, 2080, 6, 1),    # q8_0 ring of 8; 66 groups of 32 over the rows padded to 2112
+    (H.Q4_0, 4160, 1056, 6, 2),    # 33 blocks, 5 groups: ring of 8; 260 groups of 16, no permutation
+    (H.Q8_0, 4096, 1056, 6, 3),    # 3 slots: 6 waves; 256 groups of 16, permuted
+    (H.Q4_0, 2048, 10912, 4, 3),   # 3 x 341 = 1023 activation blocks: the LDS limit, ring of 16
+    (H.Q4_0, 2048, 11264, 4, 3),   # 3 x 352 = 1056 blocks: over the limit, pipelined kernel
+])
+def test_moe_decode_down_whole_chain(ctx, dtype, hidden, inter, E, k):
+    """Top-1 to top-3 down + combine run one wave per (slot, 8 rows) with
+    all activation blocks in LDS, folding each row's chain in block order by
+    lane shifts: row-group sizes, ring depths, partial last batches, the
+    XCD permutation on and off, and the LDS-size switch to the pipelined
+    kernel."""
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=True,
+                              seed=hidden + inter + k)
+    moe = make_layer(ctx, L)
+    for seed in range(2):
+        x = O.normal(8100 + seed, hidden)
         out, idx, w = moe.forward(x, return_routes=True)
         o_out, o_idx, o_w = L.forward(x, nthreads=8)
         assert list(idx) == list(o_idx)
