@@ -106,6 +106,13 @@ hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales
                          size_t cols, uint8_t* aos, hipStream_t st);
 hipError_t launch_encode(int dtype, const float* values, size_t nblocks, uint8_t* out,
                          hipStream_t st);
+// decode_row over n values of reference-layout rows laid end to end (any
+// dtype, any base alignment)
+hipError_t launch_decode_ref(int dtype, const void* src, size_t n, float* out, hipStream_t st);
+// rows row0 .. row0 + nrows - 1 of a tiled q8_0 / q4_0 matrix -> out[nrows][cols]
+hipError_t launch_decode_tiles(int dtype, const uint8_t* codes, const uint16_t* scales,
+                               size_t row0, size_t nrows, size_t cols, float* out,
+                               hipStream_t st);
 hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipStream_t st);
 hipError_t launch_route_logits(const float* router, const float* x, int H, int E, int T,
                                ActBlock* act, float* logits, hipStream_t st);
@@ -173,6 +180,7 @@ enum KernelKind : int {
   K_NORM,
   K_ATTENTION,
   K_GATHER,
+  K_DECODE,
   K_KINDS
 };
 

@@ -79,6 +79,83 @@ __global__ __launch_bounds__(256) void k_unpack(const uint8_t* __restrict__ code
 }
 
 // ===========================================================================
+// Decoding: decode_row (src/tensor/quant.rs:236-269), WeightMatrix::to_f32
+// ===========================================================================
+
+// half's f16::to_f32 (F16C, fcvtl or its software path alike): exact; a NaN
+// keeps its sign and payload and gets the quiet bit.
+__device__ __forceinline__ float h2f_quiet(uint16_t h) {
+  if ((h & 0x7c00u) == 0x7c00u && (h & 0x3ffu))
+    return __uint_as_float(((unsigned)(h & 0x8000u) << 16) | 0x7fc00000u | ((unsigned)(h & 0x3ffu) << 13));
+  return h2f(h);
+}
+
+// little-endian u16 from two byte loads (any alignment)
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// decode_row over n values of reference-layout rows laid end to end (a row's
+// blocks follow the previous row's, so value i is block i / 32, position
+// i % 32 of the run).  One thread per value.  A: the base is aligned to the
+// dtype's element or scale size, so values and scales load whole;
+// otherwise by bytes, as the reference's unaligned fallback reads them.
+template <int DT, bool A>
+__global__ __launch_bounds__(256) void k_decode_ref(const uint8_t* __restrict__ src, size_t n,
+                                                    float* __restrict__ out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float v;
+  if constexpr (DT == F32) {
+    const uint8_t* p = src + 4 * i;
+    const unsigned u = A ? *(const unsigned*)p
+                         : (unsigned)p[0] | (unsigned)p[1] << 8 | (unsigned)p[2] << 16 | (unsigned)p[3] << 24;
+    v = __uint_as_float(u);
+  } else if constexpr (DT == F16) {
+    v = h2f_quiet(A ? ((const uint16_t*)src)[i] : ld_u16(src + 2 * i));
+  } else if constexpr (DT == BF16) {
+    v = __uint_as_float((unsigned)(A ? ((const uint16_t*)src)[i] : ld_u16(src + 2 * i)) << 16);
+  } else {
+    constexpr int BB = DT == Q8_0 ? 34 : 18;
+    const uint8_t* blk = src + (i / QK) * BB;
+    const int j = (int)(i % QK);
+    const float scale = h2f_quiet(A ? *(const uint16_t*)blk : ld_u16(blk));
+    if constexpr (DT == Q8_0) {
+      v = scale * (float)(int8_t)blk[2 + j];
+    } else {
+      const unsigned byte = blk[2 + (j & 15)];
+      v = scale * ((float)(j < 16 ? byte & 15u : byte >> 4) - 8.0f);
+    }
+  }
+  out[i] = v;
+}
+
+// The same values read from the HBM tile planes: rows row0 .. row0 + nrows - 1
+// of a q8_0 / q4_0 matrix into out[nrows][nb * 32].  One thread per value.
+template <int DT>
+__global__ __launch_bounds__(256) void k_decode_tiles(const uint8_t* __restrict__ codes,
+                                                      const uint16_t* __restrict__ scales,
+                                                      size_t row0, size_t nrows, int nb,
+                                                      float* __restrict__ out) {
+  constexpr int CH = Layout<DT>::CH;
+  const size_t cols = (size_t)nb * QK;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nrows * cols) return;
+  const size_t row = row0 + i / cols;
+  const int c = (int)(i % cols), b = c / QK, j = c % QK;
+  const size_t tile = row / TILE;
+  const int r = (int)(row % TILE);
+  const float scale = h2f_quiet(scales[(tile * nb + b) * TILE + r]);
+  const uint8_t* piece = codes + (((tile * nb + b) * CH + (CH == 2 ? j / 16 : 0)) * TILE + r) * 16;
+  float v;
+  if constexpr (DT == Q8_0) {
+    v = scale * (float)(int8_t)piece[j % 16];
+  } else {
+    const unsigned byte = piece[j & 15];
+    v = scale * ((float)(j < 16 ? byte & 15u : byte >> 4) - 8.0f);
+  }
+  out[i] = v;
+}
+
+// ===========================================================================
 // Weight quantization: encode_row (src/tensor/quant.rs:274-321)
 // ===========================================================================
 
@@ -198,9 +275,12 @@ __global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, 
 // Two parts.  k_route_logits (grid (E, T), 64 threads) computes logit e of
 // token t with the 8-lane f32 order of dot_f32 (quant.rs:37-41,152-194) and
 // quantizes a share of token t's activation blocks.  route_select (one
-// wave) turns E logits into the top-k experts and their weights; the
-// gate/up kernel runs it in every work-group's prologue, so no work-group
-// ever waits for another.
+// wave) turns E logits into the top-k experts and their weights.  On the
+// decode path the gate/up kernel selects by itself: every work-group ranks
+// the logits to find its slot's expert, and one extra work-group runs
+// route_select and publishes the routes, so no work-group waits for
+// another.  k_route_select runs it for standalone routing and the grouped
+// path, one wave per token.
 
 constexpr int ROUTE_MAX_H = 8192;
 constexpr int ROUTE_MAX_E = 1024;
@@ -1380,6 +1460,36 @@ hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales
   if (n == 0) return hipSuccess;
   if (dtype == Q8_0) return launch(k_unpack<Q8_0>, blocks_for(n, 256), 256, 0, st, codes, scales, rows, nb, aos);
   return launch(k_unpack<Q4_0>, blocks_for(n, 256), 256, 0, st, codes, scales, rows, nb, aos);
+}
+
+hipError_t launch_decode_ref(int dtype, const void* src, size_t n, float* out, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  const uint8_t* b = (const uint8_t*)src;
+  const bool a = (uintptr_t)src % (dtype == F32 ? 4 : 2) == 0;
+#define HALE_DECODE_REF(D)                                                            \
+  if (dtype == D)                                                                     \
+    return a ? launch(k_decode_ref<D, true>, grid, 256, 0, st, b, n, out)            \
+             : launch(k_decode_ref<D, false>, grid, 256, 0, st, b, n, out);
+  HALE_DECODE_REF(F32)
+  HALE_DECODE_REF(F16)
+  HALE_DECODE_REF(BF16)
+  HALE_DECODE_REF(Q8_0)
+  HALE_DECODE_REF(Q4_0)
+#undef HALE_DECODE_REF
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_tiles(int dtype, const uint8_t* codes, const uint16_t* scales,
+                               size_t row0, size_t nrows, size_t cols, float* out,
+                               hipStream_t st) {
+  const size_t n = nrows * cols;
+  if (n == 0) return hipSuccess;
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  const int nb = (int)(cols / QK);
+  if (dtype == Q8_0) return launch(k_decode_tiles<Q8_0>, grid, 256, 0, st, codes, scales, row0, nrows, nb, out);
+  if (dtype == Q4_0) return launch(k_decode_tiles<Q4_0>, grid, 256, 0, st, codes, scales, row0, nrows, nb, out);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_encode(int dtype, const float* values, size_t nblocks, uint8_t* out,

@@ -543,6 +543,8 @@ extern "C" int hale_encode_rows_device(hale_ctx* c, int dtype, size_t rows, size
   if (!c || !d_values || !d_bytes) return fail(c, HALE_EINVAL, "encode: NULL argument");
   int rc = encode_check(c, dtype, rows, cols);
   if (rc) return rc;
+  if (quantized(dtype) && (uintptr_t)d_values % 16)  // the block encoder loads float4
+    return fail(c, HALE_EINVAL, "encode: values must be 16-byte aligned for q8_0 / q4_0");
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
   return encode_enqueue(c, dtype, rows, cols, d_values, d_bytes);
@@ -568,6 +570,127 @@ extern "C" int hale_encode_rows(hale_ctx* c, int dtype, size_t rows, size_t cols
   HIPCHK(c, hipMemcpyAsync(bytes, db, nout, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// decoding and conversion
+// ---------------------------------------------------------------------------
+
+static int decode_check(hale_ctx* c, int dtype, size_t cols) {
+  if (dtype < HALE_F32 || dtype > HALE_Q4_0) return fail(c, HALE_EINVAL, "decode: unknown dtype %d", dtype);
+  if (hale_row_bytes(dtype, cols) < 0)
+    return fail(c, HALE_EINVAL, "%s needs row length divisible by 32, got %zu", dtype == HALE_Q8_0 ? "Q8_0" : "Q4_0", cols);
+  return HALE_OK;
+}
+
+extern "C" int hale_decode_rows_device(hale_ctx* c, int dtype, size_t rows, size_t cols,
+                                       const void* d_bytes, float* d_values) {
+  if (!c || !d_bytes || !d_values) return fail(c, HALE_EINVAL, "decode: NULL argument");
+  int rc = decode_check(c, dtype, cols);
+  if (rc) return rc;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  LAUNCH(c, K_DECODE, launch_decode_ref(dtype, d_bytes, rows * cols, d_values, c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_decode_rows(hale_ctx* c, int dtype, size_t rows, size_t cols,
+                                const void* bytes, float* values) {
+  if (!c || !bytes || !values) return fail(c, HALE_EINVAL, "decode: NULL argument");
+  int rc = decode_check(c, dtype, cols);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t nin = rows * (size_t)hale_row_bytes(dtype, cols), nout = rows * cols * 4;
+  void* s;
+  rc = ctx_scratch(c, align_up(nin, 256) + nout, &s);
+  if (rc) return rc;
+  uint8_t* db = (uint8_t*)s;
+  float* dv = (float*)((char*)s + align_up(nin, 256));
+  HIPCHK(c, hipMemcpyAsync(db, bytes, nin, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, K_DECODE, launch_decode_ref(dtype, db, rows * cols, dv, c->stream));
+  HIPCHK(c, hipMemcpyAsync(values, dv, nout, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// Enqueues rows first .. first + count - 1 of m, decoded, into dv[count][cols].
+static int matrix_rows_enqueue(hale_ctx* c, const hale_matrix* m, size_t first, size_t count,
+                               float* dv) {
+  if (quantized(m->dtype)) {
+    LAUNCH(c, K_DECODE, launch_decode_tiles(m->dtype, m->codes, m->scales, first, count, m->cols, dv, c->stream));
+  } else {
+    const size_t rb = (size_t)hale_row_bytes(m->dtype, m->cols);
+    LAUNCH(c, K_DECODE, launch_decode_ref(m->dtype, (const uint8_t*)m->raw + first * rb, count * m->cols, dv, c->stream));
+  }
+  return HALE_OK;
+}
+
+extern "C" int hale_matrix_rows_to_f32_device(hale_ctx* c, const hale_matrix* m, size_t first,
+                                              size_t count, float* d_values) {
+  if (!c || !m || !d_values) return fail(c, HALE_EINVAL, "row_to_f32: NULL argument");
+  if (first > m->rows || count > m->rows - first)
+    return fail(c, HALE_EINVAL, "rows %zu..%zu of a %zu-row matrix", first, first + count, m->rows);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  return matrix_rows_enqueue(c, m, first, count, d_values);
+}
+
+extern "C" int hale_matrix_to_f32(hale_ctx* c, const hale_matrix* m, float* values, size_t n) {
+  if (!c || !m || !values) return fail(c, HALE_EINVAL, "to_f32: NULL argument");
+  if (n != m->rows * m->cols)
+    return fail(c, HALE_EINVAL, "to_f32 of a %zux%zu matrix needs %zu values, got %zu", m->rows, m->cols,
+                m->rows * m->cols, n);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  void* s;
+  int rc = ctx_scratch(c, n * 4, &s);
+  if (rc) return rc;
+  rc = matrix_rows_enqueue(c, m, 0, m->rows, (float*)s);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync(values, s, n * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+// Rows per pass of hale_matrix_convert: the f32 rows of one pass stay
+// within 64 MiB of scratch.
+static size_t convert_rows_per_pass(size_t cols) { return std::max<size_t>(1, (64u << 20) / (cols * 4)); }
+
+extern "C" int hale_matrix_convert(hale_ctx* c, const hale_matrix* m, int dtype, hale_matrix** out) {
+  if (!c || !m || !out) return fail(c, HALE_EINVAL, "convert: NULL argument");
+  *out = nullptr;
+  int rc = encode_check(c, dtype, m->rows, m->cols);
+  if (rc) return rc;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t rb = (size_t)hale_row_bytes(dtype, m->cols), nbytes = m->rows * rb;
+  void* bytes = nullptr;  // the converted matrix in the reference layout
+  if (hipMalloc(&bytes, nbytes) != hipSuccess)
+    return fail(c, HALE_ENOMEM, "device allocation of %zu bytes", nbytes);
+  if (dtype == m->dtype && !quantized(dtype)) {
+    rc = hipMemcpyAsync(bytes, m->raw, nbytes, hipMemcpyDeviceToDevice, c->stream) == hipSuccess
+             ? HALE_OK
+             : fail(c, HALE_EHIP, "convert: copy failed");
+  } else if (dtype == m->dtype) {
+    rc = launch_unpack(dtype, m->codes, m->scales, m->rows, m->cols, (uint8_t*)bytes, c->stream) == hipSuccess
+             ? HALE_OK
+             : fail(c, HALE_EHIP, "convert: unpack failed");
+  } else {  // to_f32, then from_f32 into the new dtype, a pass of rows at a time
+    const size_t per = convert_rows_per_pass(m->cols);
+    void* s = nullptr;
+    rc = ctx_scratch(c, std::min(per, m->rows) * m->cols * 4, &s);
+    for (size_t r = 0; rc == HALE_OK && r < m->rows; r += per) {
+      const size_t n = std::min(per, m->rows - r);
+      rc = matrix_rows_enqueue(c, m, r, n, (float*)s);
+      if (rc == HALE_OK) rc = encode_enqueue(c, dtype, n, m->cols, (const float*)s, (uint8_t*)bytes + r * rb);
+    }
+  }
+  if (rc == HALE_OK) rc = matrix_create(c, dtype, m->rows, m->cols, bytes, nbytes, true, out);
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipFree(bytes);
+  return rc;
 }
 
 // ---------------------------------------------------------------------------
@@ -1067,14 +1190,19 @@ static PrefillLayer prefill_layer(hale_moe* m, const TokScratch& s) {
   return L;
 }
 
-// Checks that apply to every forward: a pending pack load, every expert
-// present, a router or logits.
-static int moe_forward_check(hale_moe* m, const float* dlogits) {
+// Checks that apply to every forward: device x 16-byte aligned (the router
+// reads it as float4) and device logits float-aligned (host buffers are
+// staged, dx NULL), a pending pack load, every expert present, a router or
+// logits.
+static int moe_forward_check(hale_moe* m, const float* dx, const float* logits) {
+  if (dx && (uintptr_t)dx % 16) return fail(m->ctx, HALE_EINVAL, "moe_forward: x must be 16-byte aligned");
+  if (dx && (uintptr_t)logits % 4)
+    return fail(m->ctx, HALE_EINVAL, "moe_forward: logits must be 4-byte aligned");
   int rc = moe_wait_load(m);
   if (rc) return rc;
   rc = check_all_present(m);
   if (rc) return rc;
-  if (!m->router && !dlogits) return fail(m->ctx, HALE_EINVAL, "layer has no router: logits are required");
+  if (!m->router && !logits) return fail(m->ctx, HALE_EINVAL, "layer has no router: logits are required");
   return HALE_OK;
 }
 
@@ -1117,7 +1245,7 @@ extern "C" int hale_moe_forward_device(hale_moe* m, size_t ntok, const float* d_
   if (ntok == 0) return HALE_OK;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
-  int rc = moe_forward_check(m, d_logits);
+  int rc = moe_forward_check(m, d_x, d_logits);
   if (rc) return rc;
   TokScratch s;
   void* pws;
@@ -1150,7 +1278,7 @@ extern "C" int hale_moe_forward_device_noalloc(hale_moe* m, size_t ntok, const f
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
   if (!c->fixed_scratch) return fail(c, HALE_EHIP, "no fixed scratch on device %d", c->device);
-  int rc = moe_forward_check(m, d_logits);
+  int rc = moe_forward_check(m, d_x, d_logits);
   if (rc) return rc;
   char* base = (char*)c->fixed_scratch;
   const size_t tb = align_up(tok_scratch_bytes(m, ntok), 256);
@@ -1179,7 +1307,7 @@ extern "C" int hale_moe_forward(hale_moe* m, size_t ntok, const float* x, const 
   if (ntok == 0) return HALE_OK;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   HIPCHK(c, hipSetDevice(c->device));
-  int rc = moe_forward_check(m, logits);
+  int rc = moe_forward_check(m, nullptr, logits);
   if (rc) return rc;
   size_t xb = ntok * m->H * 4, lb = logits ? ntok * m->E * 4 : 0;
   size_t o1 = align_up(xb, 256), o2 = o1 + align_up(xb, 256);
@@ -1743,7 +1871,7 @@ extern "C" const char* hale_kernel_name(int kind) {
   static const char* names[K_KINDS] = {"route", "gate_up", "down", "act_quant", "gemv", "encode",
                                        "repack", "fill", "group", "grouped_gate_up",
                                        "grouped_down", "combine", "copy", "rms_norm",
-                                       "attention", "gather"};
+                                       "attention", "gather", "decode"};
   return kind >= 0 && kind < K_KINDS ? names[kind] : "";
 }
 

@@ -62,6 +62,11 @@ SIGNATURES = {
     "hale_quantize_q8_act": (C.c_int, [_vp, _fp, _sz, _fp, _i8p]),
     "hale_encode_rows": (C.c_int, [_vp, C.c_int, _sz, _sz, _fp, _vp]),
     "hale_encode_rows_device": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _vp]),
+    "hale_decode_rows": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _fp]),
+    "hale_decode_rows_device": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _vp]),
+    "hale_matrix_rows_to_f32_device": (C.c_int, [_vp, _vp, _sz, _sz, _vp]),
+    "hale_matrix_to_f32": (C.c_int, [_vp, _vp, _fp, _sz]),
+    "hale_matrix_convert": (C.c_int, [_vp, _vp, C.c_int, _vp]),
     "hale_matvec": (C.c_int, [_vp, _vp, _fp, _sz, _fp, _sz]),
     "hale_matvec_device": (C.c_int, [_vp, _vp, _vp, _vp]),
     "hale_matvec_block_sums": (C.c_int, [_vp, _vp, _fp, _sz, _i32p]),
@@ -394,6 +399,33 @@ def encode_row(ctx: Context, dtype, values) -> np.ndarray:
     return encode_rows(ctx, dtype, _f32(values).reshape(1, -1))
 
 
+def decode_rows(ctx: Context, dtype, data, rows: int, cols: int) -> np.ndarray:
+    """decode_row over `rows` reference-layout rows laid end to end, on the
+    GPU (src/tensor/quant.rs:236-269): [rows][cols] f32."""
+    dt = parse_dtype(dtype)
+    b = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+    if b.size != rows * row_bytes(dt, cols):
+        raise ValueError(f"{rows} rows of {cols} {dt} values need {rows * row_bytes(dt, cols)} bytes, got {b.size}")
+    out = np.zeros((rows, cols), dtype=np.float32)
+    ctx.check(lib().hale_decode_rows(ctx.handle, dt, rows, cols, b.ctypes.data_as(_vp),
+                                     _p(out, _fp)), "decode_row")
+    return out
+
+
+def decode_row(ctx: Context, dtype, row, out: np.ndarray | None = None) -> np.ndarray:
+    """decode_row (src/tensor/quant.rs:236-269) of one row into `out`
+    (`out.len()` values, as the reference takes the length from out)."""
+    dt = parse_dtype(dtype)
+    b = np.ascontiguousarray(row, dtype=np.uint8).reshape(-1)
+    blk = QK if dt in (Q8_0, Q4_0) else 1  # values per storage block
+    n = out.size if out is not None else b.size // row_bytes(dt, blk) * blk
+    res = decode_rows(ctx, dt, b[:row_bytes(dt, n)], 1, n).reshape(-1)
+    if out is not None:
+        out[...] = res
+        return out
+    return res
+
+
 class WeightMatrix:
     """A rows x cols matrix resident in HBM (src/tensor/matrix.rs:19-25)."""
 
@@ -442,6 +474,45 @@ class WeightMatrix:
         self.ctx.check(lib().hale_matrix_download(self.ctx.handle, self.handle,
                                                   out.ctypes.data_as(_vp), out.size), "bytes")
         return out
+
+    def row_to_f32(self, r: int, out: np.ndarray | None = None) -> np.ndarray:
+        """WeightMatrix::row_to_f32 (src/tensor/matrix.rs:88-92), decoded on
+        the GPU from the HBM layout."""
+        if out is not None and out.size != self._cols:
+            raise ValueError(f"row_to_f32 needs {self._cols} values, got {out.size}")
+        return self.rows_to_f32(r, 1, out=out).reshape(-1)
+
+    def rows_to_f32(self, first: int, count: int, out: np.ndarray | None = None) -> np.ndarray:
+        """Rows first .. first+count-1 as [count][cols] f32."""
+        buf = self.ctx.malloc(max(1, count * self._cols * 4))
+        try:
+            self.ctx.check(lib().hale_matrix_rows_to_f32_device(self.ctx.handle, self.handle, first,
+                                                                count, _vp(buf.address)),
+                           "row_to_f32")
+            self.ctx.synchronize()
+            res = buf.download(np.float32, count * self._cols).reshape(count, self._cols)
+        finally:
+            buf.free()
+        if out is not None:
+            out.reshape(count, self._cols)[...] = res
+            return out
+        return res
+
+    def to_f32(self) -> np.ndarray:
+        """WeightMatrix::to_f32 (src/tensor/matrix.rs:95-102): row-major f32."""
+        out = np.zeros(self._rows * self._cols, dtype=np.float32)
+        self.ctx.check(lib().hale_matrix_to_f32(self.ctx.handle, self.handle, _p(out, _fp), out.size),
+                       "to_f32")
+        return out
+
+    def convert(self, dtype) -> "WeightMatrix":
+        """WeightMatrix::convert (src/tensor/matrix.rs:104-109): re-encoded on
+        the GPU as a new resident matrix."""
+        dt = parse_dtype(dtype)
+        h = _vp()
+        self.ctx.check(lib().hale_matrix_convert(self.ctx.handle, self.handle, dt, C.byref(h)),
+                       "WeightMatrix::convert")
+        return WeightMatrix(self.ctx, h, self._rows, self._cols, dt)
 
     def matvec(self, x, out: np.ndarray | None = None) -> np.ndarray:
         """WeightMatrix::matvec (src/tensor/matrix.rs:115-126)."""

@@ -125,9 +125,42 @@ int hale_quantize_q8_act(hale_ctx *ctx, const float *x, size_t n,
  * rows*row_bytes. */
 int hale_encode_rows(hale_ctx *ctx, int dtype, size_t rows, size_t cols,
                      const float *values, void *bytes);
+/* Same on device buffers, enqueued on the context's stream (d_values
+ * 16-byte aligned for Q8_0 / Q4_0). */
 int hale_encode_rows_device(hale_ctx *ctx, int dtype, size_t rows,
                             size_t cols, const float *d_values,
                             void *d_bytes);
+
+/* Ref: decode_row (src/tensor/quant.rs:236-269), applied to each of `rows`
+ * reference-layout rows laid end to end (rows*row_bytes bytes, any
+ * alignment, as the reference's unaligned fallback allows): F32 copied,
+ * F16 through half's to_f32 (exact; a NaN gets the quiet bit), BF16 shifted
+ * into the upper half, Q8_0 scale*q, Q4_0 scale*(nibble-8) with the low
+ * nibbles first.  values gets rows*cols f32.  Host buffers. */
+int hale_decode_rows(hale_ctx *ctx, int dtype, size_t rows, size_t cols,
+                     const void *bytes, float *values);
+int hale_decode_rows_device(hale_ctx *ctx, int dtype, size_t rows,
+                            size_t cols, const void *d_bytes,
+                            float *d_values);
+/* Ref: WeightMatrix::row_to_f32 (src/tensor/matrix.rs:88-92) for rows
+ * first .. first+count-1 (count 1: the embedding lookup of
+ * src/model/transformer.rs:185), decoded straight from the HBM layout into
+ * d_values[count][cols], enqueued on the context's stream.  HALE_EINVAL
+ * for rows past the end. */
+int hale_matrix_rows_to_f32_device(hale_ctx *ctx, const hale_matrix *m,
+                                   size_t first, size_t count,
+                                   float *d_values);
+/* Ref: WeightMatrix::to_f32 (src/tensor/matrix.rs:95-102): every row into
+ * values[rows*cols] (host memory); n must be rows*cols. */
+int hale_matrix_to_f32(hale_ctx *ctx, const hale_matrix *m, float *values,
+                       size_t n);
+/* Ref: WeightMatrix::convert (src/tensor/matrix.rs:104-109): the matrix
+ * re-encoded in `dtype` as a new resident matrix (to_f32, then from_f32's
+ * encode_row per row), both on the GPU; the same dtype gives a copy.
+ * HALE_EINVAL when `dtype` needs a row length divisible by 32 and cols is
+ * not. */
+int hale_matrix_convert(hale_ctx *ctx, const hale_matrix *m, int dtype,
+                        hale_matrix **out);
 
 /* ---- matvec ---------------------------------------------------------- */
 
@@ -205,7 +238,9 @@ int hale_moe_route(hale_moe *moe, const float *x, uint32_t *index,
  * (src/model/transformer.rs:231-239) computed as one expert-grouped batch:
  * token t's output equals MoeLayer::forward(x_t).  x and out are
  * [ntok][H].  logits: NULL to run the router matvec, else [ntok][E] router
- * outputs used as given.  index/weight: NULL or [ntok][top_k]. */
+ * outputs used as given.  index/weight: NULL or [ntok][top_k].  The
+ * _device form takes device buffers, enqueued on the context's stream:
+ * d_x 16-byte aligned and d_logits 4-byte aligned, else HALE_EINVAL. */
 int hale_moe_forward(hale_moe *moe, size_t ntok, const float *x,
                      const float *logits, float *out, uint32_t *index,
                      float *weight);

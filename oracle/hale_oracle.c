@@ -108,7 +108,8 @@ float orc_f16_to_f32(uint16_t h) {
     float mag = (float)m * 0x1p-24f; /* exact: m < 2^10 */
     return u2f(f2u(mag) | sign);
   }
-  if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+  if (e == 31) /* inf, or a NaN: payload kept, quiet bit set (F16C, fcvtl, half's fallback) */
+    return u2f(sign | 0x7f800000u | (m ? 0x400000u : 0u) | (m << 13));
   return u2f(sign | ((e - 15 + 127) << 23) | (m << 13));
 }
 

@@ -448,3 +448,26 @@ def test_moe_top_k_zero_routes_nowhere(ctx):
         assert same_bits(out, o_out) and not out.any()
     assert not moe.experts.routing_counts().any()
     moe.close()
+
+
+def test_moe_forward_device_rejects_misaligned_x(ctx):
+    """The router reads device x as float4: a d_x that is not 16-byte
+    aligned (or d_logits not float-aligned) fails with ValueError before
+    anything is enqueued; aligned buffers at any 16-byte offset work."""
+    L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 4, 2, normalize_topk=True, seed=3)
+    moe = make_layer(ctx, L)
+    x = O.normal(5, 64)
+    bx, bo, bl = ctx.malloc(64 * 4 + 64), ctx.malloc(64 * 4), ctx.malloc(4 * 4 + 8)
+    for off in (4, 8, 12):
+        with pytest.raises(ValueError, match="16-byte aligned"):
+            moe.forward_device(1, bx.address + off, bo.address)
+    with pytest.raises(ValueError, match="4-byte aligned"):
+        moe.forward_device(1, bx.address, bo.address, d_logits=bl.address + 2)
+    bx.upload(np.concatenate([np.zeros(4, np.float32), x]))
+    moe.forward_device(1, bx.address + 16, bo.address)
+    ctx.synchronize()
+    o_out, _, _ = L.forward(x)
+    assert same_bits(bo.download(np.float32, 64), o_out)
+    for b in (bx, bo, bl):
+        b.free()
+    moe.close()
