@@ -41,6 +41,8 @@ struct PackLoad {
   std::thread th;
   int rc = HALE_OK;  // written by the thread before it ends
   std::string err;
+  uint64_t bytes = 0;   // record bytes read, and the wall-clock seconds from
+  double seconds = 0;   // the first read to the last repack on the device
   void join() {
     if (th.joinable()) th.join();
   }
@@ -63,6 +65,7 @@ struct hale_pack {
   void* dstage[2] = {nullptr, nullptr};
   hipEvent_t copied[2] = {nullptr, nullptr};  // slot's host->device copy done
   std::shared_ptr<hale::PackLoad> load;  // the running (or last) load
+  std::vector<hale_moe*> layers;  // layers whose source this pack is (cleared on close)
 };
 
 namespace hale {

@@ -8,6 +8,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -75,6 +76,7 @@ struct hale_matrix {
   uint8_t* codes = nullptr;    // quantized: tile planes
   uint16_t* scales = nullptr;
   uint8_t* raw = nullptr;      // f32 / f16 / bf16: the row-major bytes as given
+  bool view = false;           // a view of a MoE layer's expert: the layer owns it
 };
 
 struct hale_moe {
@@ -101,6 +103,13 @@ struct hale_moe {
   // `loaded`, recorded on the pack's stream after the last upload)
   std::shared_ptr<hale::PackLoad> load;
   hipEvent_t loaded = nullptr;
+  // the provider surface: the pack that fetch misses load from, CacheStats
+  // counters, selections recorded by fetch, and per-expert matrix views
+  hale_pack* source = nullptr;
+  uint64_t fetch_hits = 0, misses = 0, bytes_loaded = 0;
+  double load_seconds = 0;
+  std::vector<uint64_t> fetch_counts;  // [E]
+  std::vector<hale_matrix*> views;     // [E][gate, up, down], made by the first fetch
 };
 
 // ---------------------------------------------------------------------------
@@ -449,7 +458,7 @@ extern "C" int hale_matrix_upload_device(hale_ctx* c, int dtype, size_t rows, si
 }
 
 extern "C" void hale_matrix_destroy(hale_matrix* m) {
-  if (!m) return;
+  if (!m || m->view) return;
   std::lock_guard<std::recursive_mutex> g(m->ctx->mu);
   (void)hipSetDevice(m->ctx->device);
   (void)hipStreamSynchronize(m->ctx->stream);
@@ -637,21 +646,31 @@ extern "C" int hale_matrix_rows_to_f32_device(hale_ctx* c, const hale_matrix* m,
   return matrix_rows_enqueue(c, m, first, count, d_values);
 }
 
+extern "C" int hale_matrix_rows_to_f32(hale_ctx* c, const hale_matrix* m, size_t first,
+                                       size_t count, float* values) {
+  if (!c || !m || !values) return fail(c, HALE_EINVAL, "row_to_f32: NULL argument");
+  if (first > m->rows || count > m->rows - first)
+    return fail(c, HALE_EINVAL, "rows %zu..%zu of a %zu-row matrix", first, first + count, m->rows);
+  if (count == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t n = count * m->cols;
+  void* s;
+  int rc = ctx_scratch(c, n * 4, &s);
+  if (rc) return rc;
+  rc = matrix_rows_enqueue(c, m, first, count, (float*)s);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync(values, s, n * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
 extern "C" int hale_matrix_to_f32(hale_ctx* c, const hale_matrix* m, float* values, size_t n) {
   if (!c || !m || !values) return fail(c, HALE_EINVAL, "to_f32: NULL argument");
   if (n != m->rows * m->cols)
     return fail(c, HALE_EINVAL, "to_f32 of a %zux%zu matrix needs %zu values, got %zu", m->rows, m->cols,
                 m->rows * m->cols, n);
-  std::lock_guard<std::recursive_mutex> g(c->mu);
-  HIPCHK(c, hipSetDevice(c->device));
-  void* s;
-  int rc = ctx_scratch(c, n * 4, &s);
-  if (rc) return rc;
-  rc = matrix_rows_enqueue(c, m, 0, m->rows, (float*)s);
-  if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync(values, s, n * 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  return HALE_OK;
+  return hale_matrix_rows_to_f32(c, m, 0, m->rows, values);
 }
 
 // Rows per pass of hale_matrix_convert: the f32 rows of one pass stay
@@ -970,6 +989,8 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   m->dc_bytes = code_plane_bytes(dtype, H, I);
   m->ds_elems = scale_plane_bytes(H, I) / 2;
   m->present.assign(E, 0);
+  m->fetch_counts.assign(E, 0);
+  m->views.assign(3 * E, nullptr);
   hipError_t e = hipSuccess;
 #define ALLOC(p, n) \
   if (e == hipSuccess) e = hipMalloc(&(p), (n))
@@ -1014,6 +1035,11 @@ extern "C" void hale_moe_destroy(hale_moe* m) {
   (void)hipFree(m->stats);
   (void)hipFree(m->hact);
   (void)hipFree(m->router);
+  for (hale_matrix* v : m->views) delete v;
+  if (m->source) {
+    auto& ls = m->source->layers;
+    ls.erase(std::remove(ls.begin(), ls.end(), m), ls.end());
+  }
   delete m;
 }
 
@@ -1098,6 +1124,8 @@ static int moe_wait_load(hale_moe* m) {
   if (L->rc != HALE_OK) return fail(c, L->rc, "%s", L->err.c_str());
   HIPCHK(c, hipStreamWaitEvent(c->stream, m->loaded, 0));
   std::fill(m->present.begin(), m->present.end(), (char)1);
+  m->bytes_loaded += L->bytes;
+  m->load_seconds += L->seconds;
   return HALE_OK;
 }
 
@@ -1365,6 +1393,138 @@ extern "C" int hale_moe_routing_counts(hale_moe* m, uint64_t* counts) {
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipMemcpyAsync(counts, m->stats, m->E * 8, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  for (size_t e = 0; e < m->E; e++) counts[e] += m->fetch_counts[e];
+  return HALE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// the provider surface: ExpertProvider::{fetch, stats, routing_stats}
+// ---------------------------------------------------------------------------
+
+extern "C" int hale_moe_expert_present(hale_moe* m, uint32_t expert, int* present) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !present) return fail(c, HALE_EINVAL, "expert_present: NULL argument");
+  if (expert >= m->E) return fail(c, HALE_EINVAL, "expert %u of %zu", expert, m->E);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_wait_load(m);
+  if (rc) return rc;
+  *present = m->present[expert] ? 1 : 0;
+  return HALE_OK;
+}
+
+// The layer's view of expert e's three matrices (made on first use).
+static hale_matrix* expert_view(hale_moe* m, uint32_t e, int which) {
+  hale_matrix*& v = m->views[3 * (size_t)e + which];
+  if (v) return v;
+  v = new (std::nothrow) hale_matrix;
+  if (!v) return nullptr;
+  v->ctx = m->ctx;
+  v->dtype = m->dtype;
+  v->view = true;
+  if (which < 2) {
+    v->rows = m->I;
+    v->cols = m->H;
+    v->codes = (which == 0 ? m->gate_c : m->up_c) + e * m->gc_bytes;
+    v->scales = (which == 0 ? m->gate_s : m->up_s) + e * m->gs_elems;
+  } else {
+    v->rows = m->H;
+    v->cols = m->I;
+    v->codes = m->down_c + e * m->dc_bytes;
+    v->scales = m->down_s + e * m->ds_elems;
+  }
+  return v;
+}
+
+// ExpertSource::load for a pack (one positioned read of the record), then
+// the upload into the layer's planes.
+static int load_from_source(hale_moe* m, uint32_t e) {
+  hale_pack* p = m->source;
+  const hale::PackHeader& h = p->h;
+  uint64_t off = 0;
+  std::string err;
+  if (!hale::pack_offset_of(h, m->layer, e, &off, &err)) return fail(m->ctx, HALE_EPACK, "%s", err.c_str());
+  std::vector<uint8_t> rec(h.record_bytes);
+  if (!hale::pack_pread(p, rec.data(), rec.size(), off, &err)) return fail(m->ctx, HALE_EIO, "%s", err.c_str());
+  const size_t ng = m->I * (size_t)hale_row_bytes(m->dtype, m->H);
+  const size_t nd = m->H * (size_t)hale_row_bytes(m->dtype, m->I);
+  return set_expert(m, e, rec.data(), rec.data() + ng, rec.data() + 2 * ng, ng, nd, false);
+}
+
+extern "C" int hale_moe_fetch(hale_moe* m, const uint32_t* experts, size_t n,
+                              const hale_matrix** gate, const hale_matrix** up,
+                              const hale_matrix** down) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || (n && !experts)) return fail(c, HALE_EINVAL, "fetch: NULL argument");
+  for (size_t i = 0; i < n; i++)
+    if (experts[i] >= m->E) return fail(c, HALE_EINVAL, "fetch: expert %u of %zu", experts[i], m->E);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_wait_load(m);
+  if (rc) return rc;
+  for (size_t i = 0; i < n; i++) m->fetch_counts[experts[i]]++;  // routing.record, before any load
+  // pass 1: hits; pass 2: misses from the source, timed as one load
+  uint64_t hits = 0;
+  std::vector<uint32_t> missing;
+  for (size_t i = 0; i < n; i++) {
+    const uint32_t e = experts[i];
+    if (m->present[e])
+      hits++;
+    else if (std::find(missing.begin(), missing.end(), e) == missing.end())
+      missing.push_back(e);
+  }
+  if (!missing.empty() && !m->source)
+    return fail(c, HALE_ENOTFOUND, "expert L%uE%u is not resident and the layer has no source",
+                m->layer, missing[0]);
+  // a key missing twice in one request is loaded once and counted as two
+  // misses, as the reference counts every request its first pass missed
+  const auto t0 = std::chrono::steady_clock::now();
+  for (uint32_t e : missing) {
+    rc = load_from_source(m, e);
+    if (rc) return rc;
+  }
+  const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  const uint64_t nmiss = n - hits;
+  m->fetch_hits += hits;
+  m->misses += nmiss;
+  if (nmiss) {
+    m->bytes_loaded += nmiss * (uint64_t)m->source->h.record_bytes;
+    m->load_seconds += dt;
+  }
+  for (size_t i = 0; i < n; i++) {
+    const hale_matrix* v[3];
+    for (int w = 0; w < 3; w++)
+      if (!(v[w] = expert_view(m, experts[i], w))) return fail(c, HALE_ENOMEM, "out of host memory");
+    if (gate) gate[i] = v[0];
+    if (up) up[i] = v[1];
+    if (down) down[i] = v[2];
+  }
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_cache_stats(hale_moe* m, hale_cache_stats* out) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !out) return fail(c, HALE_EINVAL, "cache_stats: NULL argument");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  int rc = moe_wait_load(m);
+  if (rc) return rc;
+  std::vector<uint64_t> sel(m->E);
+  HIPCHK(c, hipMemcpyAsync(sel.data(), m->stats, m->E * 8, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  uint64_t forward_sel = 0;
+  for (uint64_t v : sel) forward_sel += v;
+  size_t resident = 0;
+  for (char p : m->present) resident += p ? 1 : 0;
+  const size_t eb = 2 * m->I * (size_t)hale_row_bytes(m->dtype, m->H) +
+                    m->H * (size_t)hale_row_bytes(m->dtype, m->I);
+  *out = hale_cache_stats{};
+  out->pinned_hits = m->fetch_hits + forward_sel;
+  out->misses = m->misses;
+  out->bytes_loaded = m->bytes_loaded;
+  out->load_seconds = m->load_seconds;
+  out->pinned_experts = resident;
+  out->pinned_bytes = resident * eb;
   return HALE_OK;
 }
 
@@ -1416,6 +1576,7 @@ static void pack_loader(hale_pack* p, hale_moe* m, hale::PackLoad* L, uint64_t o
     return false;
   };
   if (!hip(hipSetDevice(p->device), "hipSetDevice")) return;
+  const auto t0 = std::chrono::steady_clock::now();
   for (size_t e0 = 0, it = 0; e0 < m->E; e0 += batch, it++) {
     const int s = (int)(it & 1);
     const size_t n = std::min(batch, m->E - e0);
@@ -1445,7 +1606,11 @@ static void pack_loader(hale_pack* p, hale_moe* m, hale::PackLoad* L, uint64_t o
       if (!hip(r, "repack")) return;
     }
   }
-  hip(hipEventRecord(m->loaded, p->stream), "hipEventRecord");
+  if (!hip(hipEventRecord(m->loaded, p->stream), "hipEventRecord")) return;
+  // the load's wall-clock time ends with its last repack on the device
+  if (!hip(hipEventSynchronize(m->loaded), "hipEventSynchronize")) return;
+  L->bytes = (uint64_t)m->E * rbytes;
+  L->seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
 }
 
 static void pack_free_staging(hale_pack* p) {
@@ -1457,9 +1622,10 @@ static void pack_free_staging(hale_pack* p) {
   p->slot_bytes = 0;
 }
 
-extern "C" int hale_moe_prefetch_pack(hale_moe* m, hale_pack* p) {
-  hale_ctx* c = m ? m->ctx : nullptr;
-  if (!m || !p) return fail(c, HALE_EINVAL, "prefetch_pack: NULL argument");
+// Checks that pack p can serve layer m (same dtype, shapes and record size,
+// the layer present in the pack) and gives the layer's first record offset.
+static int pack_check_layer(hale_moe* m, hale_pack* p, uint64_t* off0) {
+  hale_ctx* c = m->ctx;
   if (p->ctx && p->ctx != c)
     return fail(c, HALE_EINVAL, "the pack already loads into another context's layers");
   const hale::PackHeader& h = p->h;
@@ -1472,18 +1638,63 @@ extern "C" int hale_moe_prefetch_pack(hale_moe* m, hale_pack* p) {
                       m->H * (size_t)hale_row_bytes(m->dtype, m->I);
   if (h.record_bytes != need)
     return fail(c, HALE_EPACK, "record is %zu bytes, expected %zu", h.record_bytes, need);
-  uint64_t off0 = 0;
   std::string err;
-  if (!hale::pack_offset_of(h, m->layer, 0, &off0, &err)) return fail(c, HALE_EPACK, "%s", err.c_str());
-  std::lock_guard<std::recursive_mutex> g(c->mu);
-  HIPCHK(c, hipSetDevice(c->device));
-  if (!p->ctx) {  // first load: bind the pack to this context's device
+  if (!hale::pack_offset_of(h, m->layer, 0, off0, &err)) return fail(c, HALE_EPACK, "%s", err.c_str());
+  return HALE_OK;
+}
+
+// Binds pack p to context c's device (its stream and events) on first use,
+// and makes it layer m's source.  Caller holds c->mu.
+static int pack_bind(hale_moe* m, hale_pack* p) {
+  hale_ctx* c = m->ctx;
+  if (!p->ctx) {
     HIPCHK(c, hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking));
     for (int s = 0; s < 2; s++) HIPCHK(c, hipEventCreateWithFlags(&p->copied[s], hipEventDisableTiming));
     p->ctx = c;
     p->device = c->device;
   }
-  int rc = moe_wait_load(m);  // this layer's previous load
+  if (m->source != p) {
+    if (m->source) {
+      auto& ls = m->source->layers;
+      ls.erase(std::remove(ls.begin(), ls.end(), m), ls.end());
+    }
+    p->layers.push_back(m);
+    m->source = p;
+  }
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_set_source(hale_moe* m, hale_pack* p) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m) return fail(c, HALE_EINVAL, "set_source: NULL layer");
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  if (!p) {
+    if (m->source) {
+      auto& ls = m->source->layers;
+      ls.erase(std::remove(ls.begin(), ls.end(), m), ls.end());
+      m->source = nullptr;
+    }
+    return HALE_OK;
+  }
+  uint64_t off0 = 0;
+  int rc = pack_check_layer(m, p, &off0);
+  if (rc) return rc;
+  return pack_bind(m, p);
+}
+
+extern "C" int hale_moe_prefetch_pack(hale_moe* m, hale_pack* p) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m || !p) return fail(c, HALE_EINVAL, "prefetch_pack: NULL argument");
+  uint64_t off0 = 0;
+  int rc = pack_check_layer(m, p, &off0);
+  if (rc) return rc;
+  const hale::PackHeader& h = p->h;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  rc = pack_bind(m, p);
+  if (rc) return rc;
+  rc = moe_wait_load(m);  // this layer's previous load
   if (rc) return rc;
   if (p->load) p->load->join();  // the pack's previous load (its layer keeps the result)
   // batches of about 64 MiB of records
@@ -1527,6 +1738,7 @@ extern "C" void hale_pack_close(hale_pack* p) {
   if (!p) return;
   if (hale_ctx* c = p->ctx) {
     std::lock_guard<std::recursive_mutex> g(c->mu);
+    for (hale_moe* m : p->layers) m->source = nullptr;
     if (p->load) p->load->join();
     p->load.reset();
     (void)hipSetDevice(p->device);

@@ -65,6 +65,7 @@ SIGNATURES = {
     "hale_decode_rows": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _fp]),
     "hale_decode_rows_device": (C.c_int, [_vp, C.c_int, _sz, _sz, _vp, _vp]),
     "hale_matrix_rows_to_f32_device": (C.c_int, [_vp, _vp, _sz, _sz, _vp]),
+    "hale_matrix_rows_to_f32": (C.c_int, [_vp, _vp, _sz, _sz, _fp]),
     "hale_matrix_to_f32": (C.c_int, [_vp, _vp, _fp, _sz]),
     "hale_matrix_convert": (C.c_int, [_vp, _vp, C.c_int, _vp]),
     "hale_matvec": (C.c_int, [_vp, _vp, _fp, _sz, _fp, _sz]),
@@ -83,6 +84,10 @@ SIGNATURES = {
     "hale_moe_forward_device": (C.c_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "hale_moe_forward_device_noalloc": (C.c_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "hale_moe_set_experts_device": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _vp, _vp, _vp]),
+    "hale_moe_cache_stats": (C.c_int, [_vp, _vp]),
+    "hale_moe_fetch": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _vp]),
+    "hale_moe_expert_present": (C.c_int, [_vp, C.c_uint32, _vp]),
+    "hale_moe_set_source": (C.c_int, [_vp, _vp]),
     "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
     "hale_pack_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "hale_pack_close": (None, [_vp]),
@@ -484,19 +489,18 @@ class WeightMatrix:
 
     def rows_to_f32(self, first: int, count: int, out: np.ndarray | None = None) -> np.ndarray:
         """Rows first .. first+count-1 as [count][cols] f32."""
-        buf = self.ctx.malloc(max(1, count * self._cols * 4))
-        try:
-            self.ctx.check(lib().hale_matrix_rows_to_f32_device(self.ctx.handle, self.handle, first,
-                                                                count, _vp(buf.address)),
-                           "row_to_f32")
-            self.ctx.synchronize()
-            res = buf.download(np.float32, count * self._cols).reshape(count, self._cols)
-        finally:
-            buf.free()
+        res = np.zeros((count, self._cols), dtype=np.float32)
+        self.ctx.check(lib().hale_matrix_rows_to_f32(self.ctx.handle, self.handle, first, count,
+                                                     _p(res, _fp)), "row_to_f32")
         if out is not None:
             out.reshape(count, self._cols)[...] = res
             return out
         return res
+
+    def rows_to_f32_device(self, first: int, count: int, d_values: int):
+        """The same rows into device memory, enqueued on the context stream."""
+        self.ctx.check(lib().hale_matrix_rows_to_f32_device(self.ctx.handle, self.handle, first,
+                                                            count, _vp(d_values)), "row_to_f32")
 
     def to_f32(self) -> np.ndarray:
         """WeightMatrix::to_f32 (src/tensor/matrix.rs:95-102): row-major f32."""
@@ -591,28 +595,86 @@ class Route:
     weight: float
 
 
+@dataclass
+class CacheStats:
+    """CacheStats (src/expert/cache.rs:15-54)."""
+
+    pinned_hits: int = 0
+    lru_hits: int = 0
+    misses: int = 0
+    bytes_loaded: int = 0
+    load_seconds: float = 0.0
+    pinned_experts: int = 0
+    pinned_bytes: int = 0
+    lru_experts: int = 0
+    lru_bytes: int = 0
+    lru_capacity_bytes: int = 0
+    passthrough: bool = False
+
+    def hit_rate(self) -> float:
+        """Fraction of requests served from the resident tiers (0 with none)."""
+        hits = self.pinned_hits + self.lru_hits
+        total = hits + self.misses
+        return hits / total if total else 0.0
+
+    def load_gbps(self) -> float:
+        """Observed source read throughput in GB/s."""
+        return self.bytes_loaded / self.load_seconds / 1e9 if self.load_seconds > 0 else 0.0
+
+
+class _CacheStatsC(C.Structure):
+    _fields_ = [("pinned_hits", C.c_uint64), ("lru_hits", C.c_uint64), ("misses", C.c_uint64),
+                ("bytes_loaded", C.c_uint64), ("load_seconds", C.c_double),
+                ("pinned_experts", C.c_size_t), ("pinned_bytes", C.c_size_t),
+                ("lru_experts", C.c_size_t), ("lru_bytes", C.c_size_t),
+                ("lru_capacity_bytes", C.c_size_t), ("passthrough", C.c_int)]
+
+
 class HbmExpertProvider:
-    """ExpertProvider whose tiers are all HBM: every expert of the layer is
-    resident, so fetch never misses (src/expert/mod.rs:128-137)."""
+    """ExpertProvider (src/expert/mod.rs:128-137) of one MoE layer: the HBM
+    tier holds the resident experts; a fetch miss loads from the layer's
+    source pack (MoeLayer.set_source), as ExpertCache::fetch does
+    (src/expert/cache.rs:124-194)."""
 
     def __init__(self, layer: "MoeLayer"):
         self._layer = layer
 
-    def fetch(self, keys):
-        """Returns the keys' experts in request order; KeyError if absent."""
+    def fetch(self, keys) -> list:
+        """The keys' experts in request order, as Experts whose matrices are
+        views into the layer (valid while the layer is open).  KeyError for a
+        missing expert without a source; ValueError for another layer's key
+        or an index past the layer's experts."""
+        keys = list(keys)
+        L = self._layer
         for k in keys:
-            if k.layer != self._layer.layer or not (0 <= k.expert < self._layer.num_experts) \
-                    or not self._layer._present[k.expert]:
-                raise KeyError(f"expert {k} is not resident")
-        return [self._layer.expert_ref(k.expert) for k in keys]
+            if k.layer != L.layer:
+                raise ValueError(f"key {k} is not in layer {L.layer}")
+        idx = np.array([k.expert for k in keys], dtype=np.uint32)
+        n = idx.size
+        g, u, d = ((_vp * max(n, 1))() for _ in range(3))
+        L.ctx.check(lib().hale_moe_fetch(L.handle, idx.ctypes.data_as(_u32p), n, g, u, d), "fetch")
+        out = []
+        for i in range(n):
+            mats = [WeightMatrix(L.ctx, _vp(h[i]), r, c, L.dtype)
+                    for h, (r, c) in ((g, (L.inter, L.hidden)), (u, (L.inter, L.hidden)),
+                                      (d, (L.hidden, L.inter)))]
+            for m in mats:
+                m._owner = L  # a view: the layer outlives it
+            out.append(Expert(*mats))
+        return out
 
-    def stats(self) -> dict:
-        counts = self.routing_counts()
-        n = int(counts.sum())
-        return {"pinned_hits": n, "lru_hits": 0, "misses": 0, "bytes_loaded": 0,
-                "pinned_experts": int(sum(self._layer._present)),
-                "pinned_bytes": int(sum(self._layer._present)) * self._layer.expert_bytes(),
-                "passthrough": False}
+    def stats(self) -> CacheStats:
+        st = _CacheStatsC()
+        L = self._layer
+        L.ctx.check(lib().hale_moe_cache_stats(L.handle, C.byref(st)), "stats")
+        return CacheStats(*(getattr(st, f) for f, _ in _CacheStatsC._fields_[:-1]),
+                          passthrough=bool(st.passthrough))
+
+    def present(self, e: int) -> bool:
+        v = C.c_int()
+        L = self._layer
+        L.ctx.check(lib().hale_moe_expert_present(L.handle, e, C.byref(v)), "expert_present")
+        return bool(v.value)
 
     def routing_counts(self) -> np.ndarray:
         out = np.zeros(self._layer.num_experts, dtype=np.uint64)
@@ -810,7 +872,6 @@ class MoeLayer:
                                         C.byref(h)), "MoeLayer")
         self.handle = h
         ctx.adopt(self)
-        self._present = [False] * num_experts
         self.experts = HbmExpertProvider(self)
 
     def expert_bytes(self) -> int:
@@ -829,29 +890,32 @@ class MoeLayer:
         self.ctx.check(lib().hale_moe_set_expert(self.handle, e, g.ctypes.data_as(_vp),
                                                  u.ctypes.data_as(_vp), d.ctypes.data_as(_vp),
                                                  g.size, d.size), "set_expert")
-        self._present[e] = True
 
     def set_experts_device(self, first: int, count: int, d_gate: int, d_up: int, d_down: int):
         """Registers experts first..first+count-1 from device buffers of
         back-to-back reference-layout bytes."""
         self.ctx.check(lib().hale_moe_set_experts_device(self.handle, first, count, _vp(d_gate),
                                                          _vp(d_up), _vp(d_down)), "set_experts")
-        for e in range(first, first + count):
-            self._present[e] = True
 
     def load_pack(self, pack: PackExpertSource):
         """Makes every expert of this layer resident from the pack (all
         records of the layer, read and uploaded before returning)."""
         self.ctx.adopt(pack)  # a bound pack closes before its context
         self.ctx.check(lib().hale_moe_load_pack(self.handle, pack.handle), "load_pack")
-        self._present = [True] * self.num_experts
 
     def prefetch_pack(self, pack: PackExpertSource):
         """Starts loading this layer's experts from the pack and returns; the
         layer's next use waits for the load (and raises its error)."""
         self.ctx.adopt(pack)
         self.ctx.check(lib().hale_moe_prefetch_pack(self.handle, pack.handle), "prefetch_pack")
-        self._present = [True] * self.num_experts
+
+    def set_source(self, pack: "PackExpertSource | None"):
+        """Makes the pack this layer's ExpertSource without loading anything:
+        experts.fetch loads missing experts from it (None unbinds)."""
+        if pack is not None:
+            self.ctx.adopt(pack)
+        self.ctx.check(lib().hale_moe_set_source(self.handle, pack.handle if pack is not None else None),
+                       "set_source")
 
     def forward_device(self, ntok: int, d_x: int, d_out: int, d_logits: int = 0,
                        d_index: int = 0, d_weight: int = 0):
@@ -876,7 +940,6 @@ class MoeLayer:
         self.ctx.check(lib().hale_moe_set_expert_matrices(self.handle, e, expert.gate.handle,
                                                           expert.up.handle, expert.down.handle),
                        "set_expert")
-        self._present[e] = True
 
     def route(self, x) -> list[Route]:
         """MoeLayer::route (src/model/moe.rs:36-53)."""

@@ -150,6 +150,10 @@ int hale_decode_rows_device(hale_ctx *ctx, int dtype, size_t rows,
 int hale_matrix_rows_to_f32_device(hale_ctx *ctx, const hale_matrix *m,
                                    size_t first, size_t count,
                                    float *d_values);
+/* Same into host memory (values[count][cols]), returning with the rows in
+ * place. */
+int hale_matrix_rows_to_f32(hale_ctx *ctx, const hale_matrix *m, size_t first,
+                            size_t count, float *values);
 /* Ref: WeightMatrix::to_f32 (src/tensor/matrix.rs:95-102): every row into
  * values[rows*cols] (host memory); n must be rows*cols. */
 int hale_matrix_to_f32(hale_ctx *ctx, const hale_matrix *m, float *values,
@@ -280,6 +284,51 @@ int hale_moe_set_experts_device(hale_moe *moe, uint32_t first, uint32_t count,
  * of this layer since creation.  counts[num_experts]. */
 int hale_moe_routing_counts(hale_moe *moe, uint64_t *counts);
 
+/* Ref: CacheStats (src/expert/cache.rs:15-33), field for field.  The HBM
+ * layer is one tier, reported as the pinned tier: pinned_experts /
+ * pinned_bytes are the resident experts; pinned_hits counts the selections
+ * its forwards served (every selection, since a forward needs every expert
+ * resident) plus the fetch requests that found their expert resident; the
+ * LRU fields stay 0 (nothing is evicted); passthrough is 0.  misses are
+ * fetch requests that loaded from the layer's source.  bytes_loaded and
+ * load_seconds sum every read from a pack into the layer: fetch misses
+ * (expert bytes per miss, as the reference counts them) and whole-layer
+ * loads (hale_moe_load_pack / prefetch_pack, timed from the first read to
+ * the last repack on the device). */
+typedef struct hale_cache_stats {
+  uint64_t pinned_hits;
+  uint64_t lru_hits;
+  uint64_t misses;
+  uint64_t bytes_loaded;
+  double load_seconds;
+  size_t pinned_experts;
+  size_t pinned_bytes;
+  size_t lru_experts;
+  size_t lru_bytes;
+  size_t lru_capacity_bytes;
+  int passthrough;
+} hale_cache_stats;
+
+/* Ref: ExpertProvider::stats (src/expert/mod.rs:133). */
+int hale_moe_cache_stats(hale_moe *moe, hale_cache_stats *out);
+
+/* Ref: ExpertProvider::fetch (src/expert/mod.rs:130) as ExpertCache
+ * implements it (src/expert/cache.rs:124-194), for keys (layer, experts[i])
+ * of this layer: records one selection per key (routing_stats), serves the
+ * resident experts, and loads each missing one from the layer's source
+ * into HBM (hale_moe_set_source; without a source a missing expert is
+ * HALE_ENOTFOUND).  gate/up/down (each NULL or [n]) receive, in request
+ * order, the experts' matrices as views into the layer: usable wherever a
+ * hale_matrix is (hale_matvec, hale_expert_forward[_device], download,
+ * convert), owned by the layer and valid until hale_moe_destroy
+ * (hale_matrix_destroy ignores them).  An expert index >= num_experts is
+ * HALE_EINVAL. */
+int hale_moe_fetch(hale_moe *moe, const uint32_t *experts, size_t n,
+                   const hale_matrix **gate, const hale_matrix **up,
+                   const hale_matrix **down);
+/* Whether expert `expert` is resident (after any pending pack load). */
+int hale_moe_expert_present(hale_moe *moe, uint32_t expert, int *present);
+
 /* ---- expert pack: the file tier under the HBM tier ------------------ */
 
 /* Opens a Hale expert pack ("HALEPACK" magic, u64 LE header length, JSON
@@ -329,6 +378,12 @@ int hale_pack_read_expert(hale_pack *pack, uint32_t layer, uint32_t expert,
  * experts, docs/roadmap.md:13-16). */
 int hale_moe_load_pack(hale_moe *moe, hale_pack *pack);
 int hale_moe_prefetch_pack(hale_moe *moe, hale_pack *pack);
+/* Makes `pack` the layer's source, the ExpertSource behind its HBM tier
+ * (src/expert/mod.rs:110-124), without loading anything: hale_moe_fetch
+ * loads missing experts from it.  Checked like hale_moe_prefetch_pack,
+ * which binds its pack the same way.  NULL unbinds; hale_pack_close
+ * unbinds the pack from every layer. */
+int hale_moe_set_source(hale_moe *moe, hale_pack *pack);
 
 /* ---- the steps on either side of the MoE block ------------------------ */
 

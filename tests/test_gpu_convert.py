@@ -139,6 +139,13 @@ def test_matrix_to_f32_and_rows(ctx, dtype):
     assert same_values(m.rows_to_f32(33, 5), want[33:38], dtype)
     with pytest.raises(ValueError):
         m.rows_to_f32(68, 3)
+    buf = ctx.malloc(7 * cols * 4)
+    m.rows_to_f32_device(60, 7, buf.address)  # the device form, last tile's rows
+    ctx.synchronize()
+    assert same_values(buf.download(np.float32, 7 * cols), want[60:67], dtype)
+    with pytest.raises(ValueError):
+        m.rows_to_f32_device(64, 7, buf.address)
+    buf.free()
     m.close()
 
 

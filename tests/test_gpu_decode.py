@@ -234,9 +234,6 @@ def test_routing_stats_count_decode_selections(ctx):
     counts = moe.experts.routing_counts()
     assert counts.sum() == 30
     assert (counts == np.bincount(idx.ravel(), minlength=8)).all()
-    assert moe.experts.fetch([H.ExpertKey(3, 1)]) == [H.ExpertKey(3, 1)]
-    with pytest.raises(KeyError):
-        moe.experts.fetch([H.ExpertKey(3, 8)])
 
 
 def test_routing_stats_count_grouped_selections(ctx):
