@@ -13,23 +13,9 @@
 #include <vector>
 
 #include "../../include/hale_moe.h"
+#include "pack_header.h"
 
 namespace hale {
-
-// PackHeader (src/expert/pack.rs:55-73)
-struct PackHeader {
-  uint32_t version = 0;
-  int dtype = -1;
-  size_t hidden = 0, inter = 0, num_experts = 0;
-  std::vector<size_t> moe_layers;
-  size_t record_bytes = 0, record_stride = 0, data_offset = 0;
-  // PackHeader::file_size (:96-99)
-  size_t file_size() const { return data_offset + moe_layers.size() * num_experts * record_stride; }
-};
-
-// Parses the JSON header; false (with a message) on malformed input or a
-// missing field.
-bool parse_pack_header(const char* json, size_t len, PackHeader* h, std::string* err);
 
 // Records a failure on a context (hale_last_error) and returns `code`.
 int ctx_fail(hale_ctx* c, int code, const char* fmt, ...);
@@ -74,9 +60,5 @@ namespace hale {
 // message on failure or end of file.
 bool pack_pread(const hale_pack* p, void* dst, size_t n, uint64_t off, std::string* err);
 
-// Record offset of (layer, expert); false with a message when the key is
-// not in the pack (PackHeader::offset_of, src/expert/pack.rs:104-123).
-bool pack_offset_of(const PackHeader& h, uint32_t layer, uint32_t expert, uint64_t* off,
-                    std::string* err);
 
 }  // namespace hale

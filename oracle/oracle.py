@@ -65,7 +65,10 @@ class AttentionDesc(C.Structure):
 
 
 def _load(variant: str = ""):
-    # variant: "" / "_v3" next to this file, or the path of a build elsewhere
+    # variant: "" / "_v3" next to this file, or the path of a build elsewhere;
+    # HALE_ORACLE_LIB replaces the default build (the sanitizer run)
+    if not variant and os.environ.get("HALE_ORACLE_LIB"):
+        variant = os.environ["HALE_ORACLE_LIB"]
     path = variant if os.path.isabs(variant) else os.path.join(_HERE, f"libhale_oracle{variant}.so")
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
