@@ -205,15 +205,25 @@ def copy_calibration(nbytes, reps=5):
 
 def decode_eager(args):
     """Two eager passes over the resident layers (no graph): the run the
-    per-dispatch counter passes profile."""
+    per-dispatch counter passes profile.  --decode-workload picks one of the
+    larger decode layers instead of the headline one."""
     ctx = H.Context(0)
-    layers = build_layers(ctx, args.layers)
-    xs = ctx.malloc(64 * HID * 4)
-    xs.fill_normal(99, 64 * HID, 0.0, 1.0)
-    out = ctx.malloc(HID * 4)
+    hid = HID
+    if args.decode_workload:
+        spec = {w[0]: w for w in DECODE_MORE}.get(args.decode_workload)
+        if spec is None:
+            raise SystemExit(f"unknown decode workload {args.decode_workload!r}: "
+                             f"one of {[w[0] for w in DECODE_MORE]}")
+        _, dt, hid, inter, ex, k, nl = spec
+        layers = build_layers(ctx, nl, dtype=dt, hid=hid, inter=inter, experts=ex, topk=k)
+    else:
+        layers = build_layers(ctx, args.layers)
+    xs = ctx.malloc(64 * hid * 4)
+    xs.fill_normal(99, 64 * hid, 0.0, 1.0)
+    out = ctx.malloc(hid * 4)
     L = len(layers)
     for s in range(2 * L):
-        layers[s % L].forward_device(1, xs.offset((s % 64) * HID * 4), out.address)
+        layers[s % L].forward_device(1, xs.offset((s % 64) * hid * 4), out.address)
     ctx.synchronize()
     for m in layers:
         m.close()
@@ -607,6 +617,8 @@ def main():
                     help="only the prefill workloads (for counter runs)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="only two eager decode passes over the layers (for counter runs)")
+    ap.add_argument("--decode-workload", default="", metavar="NAME",
+                    help="with --decode-eager: one of the larger decode layers")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only time the plain copy kernel over BYTES (counter yardstick)")
     args = ap.parse_args()
