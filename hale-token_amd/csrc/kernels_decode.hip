@@ -482,217 +482,134 @@ __device__ __forceinline__ void route_select(const float* lg, int E, int k, int 
     route_select_t<16>(lg, E, k, normalize, sel_idx, sel_w, tab, rs);
 }
 
-// Selection in the gate/up prologue, in two parts.
+// Selection in the gate/up prologue.
 //
-// Ranking by logit gives the reference's order unless rounding makes two
-// probabilities equal: the map logit -> exp(logit - max) -> probability is
-// non-decreasing, so it can merge two logits into one probability but never
-// swap them.  So every work-group first ranks the experts by logit
-// (rank_by_logit, all threads, no exp), takes the expert of its slot and
-// issues that expert's weight loads at once.  One wave then forms the
-// probabilities while the loads are in flight (verify_selection) and checks
-// the ranking against them: each chosen pair, and the last chosen against
-// every unchosen element, must be in (probability desc, index asc) order.
-// If a check fails it ranks again by probability; a work-group whose slot
-// then holds another expert runs its rows again.  Either way the result is
-// the reference's.
+// A work-group of slot s needs the expert of rank s in the reference's
+// order (probability desc, index asc).  Ranking by logit gives that order
+// unless rounding makes two probabilities of different logits equal: the
+// map logit -> exp(logit - max) -> probability never swaps two logits but
+// may merge them.  So every wave of a work-group, on its own and from
+// registers only (no LDS, no barrier), finds X, the element of logit rank s
+// (select_slot_by_logit), and checks that no rounding can merge X's
+// probability with that of an element of a different logit.  Then X's
+// probability rank equals its logit rank, so X is the reference's choice
+// for slot s, and the wave issues X's weight loads at once.  Otherwise (a
+// near-tie around X, a NaN or an infinity among the logits, all rare) the
+// work-group runs the reference's selection first and takes its slot s.
+// One work-group of the launch publishes the reference's routes and
+// weights for the down projection.
 
-// Selection state in LDS for at most ME experts.
+// Selection state in LDS, used only when the logit ranking is not safe.
 template <int ME>
 struct SelLds {
-  static constexpr int MAXE = ME;
-  unsigned long long ck[ME];   // order_key(logit) << 32 | ~index
-  unsigned key[ME];            // order_key(logit), then order_key(probability)
-  int rank[ME];                // rank of each element by logit
-  float e[ME];                 // exp(logit - max)
-  float logit[ME];
-  int by_logit[65];            // element of logit rank r <= k
-  float sorted[65];            // and its logit
-  int sel_idx[64];             // the reference's choice, best first
-  float sel_w[64];             // and its renormalised weights
-  int bad;                     // the logit ranking was not the reference's
+  float e[ME];        // scratch of route_select
+  int sel_idx[64];    // the reference's choice, best first
+  float sel_w[64];    // and its renormalised weights
 };
 
-// rank_i = #{j : key_j > key_i} + #{j < i : key_j == key_i}, the position of
-// element i in (key desc, index asc) order.  ck = key << 32 | ~index orders
-// exactly like (key desc, index asc) read from the top, so rank_i counts
-// the composite keys above ck_i.  Every wave holds all E composite keys in
-// registers (element j at lane j % 64, slot j / 64; zero past E, below
-// every real key) and ranks elements wave, wave + NW, ...: per element one
-// 64-bit compare per slot, a ballot and a scalar popcount.  Writes rank[i],
-// and by_logit[r] / sorted[r] (element and logit of rank r) for r <= k.
-template <int PER, int NW, class Sel>
-__device__ __forceinline__ void rank_by_logit_t(Sel& sl, int E, int k) {
+// Element X of rank `slot` in (logit total order desc, index asc) among the
+// E logits lg (E <= 64 PER), by one whole wave; element i is held by lane
+// i % 64 in register i / 64.  The wave walks the distinct order keys from
+// the top, one wave maximum per key (each below the last), counting each
+// key's elements with ballots, until the count passes `slot`: X then has
+// key K, the last one visited, and is the (slot - #keys above K)-th element
+// of key K in index order.  At most slot + 2 maxima.  *safe (wave-uniform)
+// tells whether X is certainly the reference's choice for this slot:
+//   - no logit is NaN (a NaN makes every probability NaN) and the largest,
+//     L0, is finite;
+//   - L_X - L0 >= -60, and L_X is finite;
+//   - the next larger logit a (if any) has a - L_X > 2^-13;
+//   - the next smaller logit b (if any) is finite, b - L0 >= -60 and
+//     L_X - b > 2^-13.
+// For a pair of logits u > v with u - v > 2^-13 (computed in f32), v - L0
+// >= -60 and both finite, x = fl(v - L0) errs by at most 2^-18, glibc expf by
+// under one ulp and the division by half an ulp, so p_u / p_v >=
+// exp(2^-13 - 2^-17)(1 - 3 * 2^-23) > 1.  That orders X strictly against a
+// and b and, by the non-decreasing map, against every element beyond them
+// (for those below -60 as well: their exp stays below exp(-60)(1 + 2^-23),
+// under X's); elements of X's own logit have X's probability and keep index
+// order.  So the probability rank of X is its logit rank.
+template <int PER>
+__device__ __forceinline__ int select_slot_by_logit(const float* __restrict__ lg, int E, int slot,
+                                                    bool* safe) {
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  unsigned long long kj[PER];
+  unsigned key[PER];
+  bool has[PER];
+  bool nan = false;
 #pragma unroll
-  for (int m = 0; m < PER; m++) kj[m] = sl.ck[lane + 64 * m];
-  constexpr int B = 8;  // elements whose keys are read together
-  for (int i0 = wave; i0 < E; i0 += B * NW) {
-    unsigned long long ci[B];
-#pragma unroll
-    for (int q = 0; q < B; q++) ci[q] = sl.ck[min(i0 + NW * q, E - 1)];
-    int cnt[B];
-#pragma unroll
-    for (int q = 0; q < B; q++) {
-      cnt[q] = 0;
-#pragma unroll
-      for (int m = 0; m < PER; m++) cnt[q] += __popcll(__ballot(kj[m] > ci[q]));
-    }
-    // lane q writes element q's rank (and, within the top k + 1, the element
-    // and its logit, read back from the key)
-#pragma unroll
-    for (int q = 0; q < B; q++) {
-      const int i = i0 + NW * q;
-      if (lane == q && i < E) {
-        sl.rank[i] = cnt[q];
-        if (cnt[q] <= k) {
-          sl.by_logit[cnt[q]] = i;
-          sl.sorted[cnt[q]] = key_value((unsigned)(ci[q] >> 32));
-        }
-      }
-    }
+  for (int m = 0; m < PER; m++) {
+    const int i = lane + 64 * m;
+    has[m] = i < E;
+    const float v = has[m] ? lg[i] : 0.0f;
+    key[m] = order_key(v);
+    nan = nan || (has[m] && v != v);
   }
-}
-
-template <int NW, class Sel>
-__device__ __forceinline__ void rank_by_logit(Sel& sl, int E, int k) {
-  if (E <= 64)
-    rank_by_logit_t<1, NW>(sl, E, k);
-  else if (E <= 128)
-    rank_by_logit_t<2, NW>(sl, E, k);
-  else if (Sel::MAXE <= 256 || E <= 256)
-    rank_by_logit_t<(Sel::MAXE < 256 ? 2 : 4), NW>(sl, E, k);
-  else
-    rank_by_logit_t<Sel::MAXE / 64, NW>(sl, E, k);
-}
-
-// True when the probabilities must order the k + 1 best logits exactly as
-// the logits do, so that the logit ranking is the reference's top-k.  For
-// consecutive ranks a, b with L_a - L_b > 2^-13 (computed in f32), L_b - L_0
-// >= -60 and every value finite: x = fl(L - L_0) errs by at most 2^-18 for
-// |x| < 64, glibc expf by less than 1 ulp and the division by half an ulp,
-// so p_a / p_b >= exp(2^-13 - 2^-17)(1 - 3 * 2^-23) > 1 and no rounding can
-// merge the two probabilities.  (Equal logits have equal probabilities and
-// keep index order either way.)  Otherwise the selection is checked against
-// the probabilities.  Lane r of each wave checks ranks r - 1, r.
-template <class Sel>
-__device__ __forceinline__ bool ranking_is_safe(const Sel& sl, int E, int k) {
-  const int lane = threadIdx.x & 63;
-  const int n = k < E ? k + 1 : k;  // ranks 0..k exist
-  const float l0 = sl.sorted[0];
-  bool ok = fabsf(l0) <= 3.0e38f;
-  if (lane >= 1 && lane < n) {
-    const float a = sl.sorted[lane - 1], b = sl.sorted[lane];
-    ok = ok && fabsf(b) <= 3.0e38f && b - l0 >= -60.0f && a - b > 0x1p-13f;
-  }
-  if (k >= 64) {  // rank 64 exists only for k = 64 < E
-    if (n == 65) {
-      const float a = sl.sorted[63], b = sl.sorted[64];
-      ok = ok && fabsf(b) <= 3.0e38f && b - l0 >= -60.0f && a - b > 0x1p-13f;
-    }
-  }
-  return __ballot(!ok) == 0ull;
-}
-
-// One whole wave: softmax_in_place over the logits (max, glibc exp, the sum
-// in index order, one division per value), the check of the logit ranking,
-// and the reference's selection and renormalised weights into sel_idx /
-// sel_w (k rounds over the probability keys when the check fails).  The
-// values stay in LDS (element i at lane i % 64, round i / 64), so the check
-// needs few registers beside the weight loads in flight.
-template <class Sel>
-__device__ __forceinline__ void verify_selection(Sel& sl, int E, int k, int normalize,
-                                                 const ExpTable& tab) {
-  const int lane = threadIdx.x & 63;
-  const int rounds = (E + 63) / 64;
-  auto wave_sync = [] {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // the largest key below `bound` (any key when `all`), 0 when there is none
+  auto max_below = [&](unsigned bound, bool all) {
+    unsigned loc = 0u;
+#pragma unroll
+    for (int m = 0; m < PER; m++)
+      if (has[m] && (all || key[m] < bound)) loc = max(loc, key[m]);
+    return wave_max_u32(loc);
   };
-  float mx = -__builtin_huge_valf();
-  for (int m = 0; m < rounds; m++) {
-    const int i = lane + 64 * m;
-    mx = fmaxf(mx, i < E ? sl.logit[i] : -__builtin_huge_valf());
-  }
-  mx = wave_max_f32(mx);  // max is order independent
-  for (int m = 0; m < rounds; m++) {
-    const int i = lane + 64 * m;
-    const float ev = wave_expf((i < E ? sl.logit[i] : -__builtin_huge_valf()) - mx, tab);
-    if (i < E) sl.e[i] = ev;
-  }
-  wave_sync();
-  float sum = 0.0f;  // sum += exp(v - max), index order
-  if (lane == 0) sum = lds_sum_in_order(sl.e, E, sum);
-  sum = lane_value(sum, 0);
-  for (int m = 0; m < rounds; m++) {
-    const int i = lane + 64 * m;
-    if (i < E) sl.key[i] = order_key(sl.e[i] / sum);  // the logit keys are no longer needed
-  }
-  wave_sync();
-  // lane r < k checks chosen r against chosen r + 1; every unchosen element
-  // (logit rank >= k) must rank after the last chosen by probability too
-  int my_idx = lane < k ? sl.by_logit[lane] : 0;
-  const int next = __shfl(my_idx, lane + 1);
-  const int last = __shfl(my_idx, k - 1);
-  const unsigned klast = sl.key[last];
-  bool bad = false;
-  if (lane + 1 < k) {
-    const unsigned ka = sl.key[my_idx], kb = sl.key[next];
-    bad = !(ka > kb || (ka == kb && my_idx < next));
-  }
-  for (int m = 0; m < rounds; m++) {
-    const int i = lane + 64 * m;
-    if (i < E && sl.rank[i] >= k) {
-      const unsigned pk = sl.key[i];
-      bad = bad || pk > klast || (pk == klast && i < last);
+  auto count_eq = [&](unsigned k) {
+    int c = 0;
+#pragma unroll
+    for (int m = 0; m < PER; m++) c += (int)__popcll(__ballot(has[m] && key[m] == k));
+    return c;
+  };
+  const unsigned top = max_below(0u, true);
+  unsigned K = top, above = 0u;
+  int n_above = 0;  // elements with keys above K
+  bool ok = true;
+  for (int it = 0;; it++) {
+    const int c = count_eq(K);
+    if (n_above + c > slot) break;
+    if (it > slot) {  // cannot happen with E > slot; keeps the loop bounded
+      ok = false;
+      break;
     }
+    n_above += c;
+    above = K;
+    K = max_below(K, false);
   }
-  float my_p = 0.0f, norm = 1.0f;
-  const bool any_bad = __ballot(bad) != 0ull;
-  if (!any_bad) {
-    my_p = lane < k ? key_value(sl.key[my_idx]) : 0.0f;
-    if (normalize) {
-      norm = -0.0f;  // Iterator::sum in best-first order
-      for (int r = 0; r < k; r++) norm = norm + lane_value(my_p, r);
-    }
-  } else {
-    // a tie the logits did not show: k rounds over the probability keys;
-    // the wave's largest untaken key is the next best and the lowest index
-    // holding it wins.  Taken keys become 0 (below every real key) and
-    // sl.rank marks them taken (-1), so a real key of 0 stays apart.
-    norm = normalize ? -0.0f : 1.0f;
-    for (int r = 0; r < k; r++) {
-      unsigned loc = 0u;
-      for (int m = 0; m < rounds; m++) {
-        const int i = lane + 64 * m;
-        if (i < E && sl.rank[i] >= 0) loc = sl.key[i] > loc ? sl.key[i] : loc;
-      }
-      const unsigned best = wave_max_u32(loc);
-      int widx = 0x7fffffff;
-      for (int m = 0; m < rounds; m++) {
-        const int i = lane + 64 * m;
-        if (i < E && sl.rank[i] >= 0 && sl.key[i] == best) widx = min(widx, i);
-      }
-      widx = (int)wave_reduce_u32((unsigned)widx, OpMinU());
-      wave_sync();
-      if (lane == 0) sl.rank[widx] = -1;
-      wave_sync();
-      const float pw = key_value(best);
-      if (normalize) norm = norm + pw;
-      if (lane == r) {
-        my_idx = widx;
-        my_p = pw;
+  int j = slot - n_above;  // X's place among the elements of key K
+  int x = 0;
+  bool found = false, any_below = false;
+#pragma unroll
+  for (int m = 0; m < PER; m++) {
+    unsigned long long eq = __ballot(has[m] && key[m] == K);
+    const int c = (int)__popcll(eq);
+    if (!found) {
+      if (j < c) {
+        for (int q = 0; q < j; q++) eq &= eq - 1;
+        x = 64 * m + (int)__builtin_ctzll(eq);
+        found = true;
+      } else {
+        j -= c;
       }
     }
+    any_below = any_below || __ballot(has[m] && key[m] < K) != 0ull;
   }
-  if (lane < k) {
-    sl.sel_idx[lane] = my_idx;
-    sl.sel_w[lane] = my_p / norm;
+  const float l0 = key_value(top), lx = key_value(K);
+  ok = ok && found && __ballot(nan) == 0ull && fabsf(l0) <= 3.0e38f && fabsf(lx) <= 3.0e38f &&
+       lx - l0 >= -60.0f;
+  if (n_above > 0) ok = ok && key_value(above) - lx > 0x1p-13f;
+  if (any_below) {
+    const float lb = key_value(max_below(K, false));
+    ok = ok && fabsf(lb) <= 3.0e38f && lb - l0 >= -60.0f && lx - lb > 0x1p-13f;
   }
-  if (lane == 0) sl.bad = any_bad ? 1 : 0;
+  *safe = ok;
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
+// E <= ME
+template <int ME>
+__device__ __forceinline__ int select_slot(const float* lg, int E, int slot, bool* safe) {
+  if (E <= 64) return select_slot_by_logit<1>(lg, E, slot, safe);
+  if (E <= 128) return select_slot_by_logit<2>(lg, E, slot, safe);
+  if (ME <= 256 || E <= 256) return select_slot_by_logit<(ME < 256 ? 2 : 4)>(lg, E, slot, safe);
+  return select_slot_by_logit<ME / 64>(lg, E, slot, safe);
 }
 
 // Standalone routing (MoeLayer::route without the experts, and the grouped
@@ -845,14 +762,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   ExpTable tab;
   if constexpr (EPI == EPI_GATE_UP) tab.load();
   int expert = a.route_idx ? a.route_idx[slot] : 0;
-  // With router logits given, the expert of this slot is the one of logit
-  // rank `slot` (see ranking_is_safe; otherwise the probabilities check
-  // that choice while the loads fly).  The last column of work-groups holds
-  // the selector: its first work-group runs the reference's selection
-  // (softmax, top-k, renormalisation) and publishes the routes and their
-  // weights for the down projection, beside the rows' work.
+  // With router logits given, every wave selects this slot's expert on its
+  // own (select_slot); a work-group whose choice is not certain runs the
+  // reference's selection first.  The last column of work-groups holds the
+  // selector: its first work-group runs the reference's selection (softmax,
+  // top-k, renormalisation) and publishes the routes and their weights for
+  // the down projection, beside the rows' work.
   const bool routing = EPI == EPI_GATE_UP && a.logits != nullptr;
-  bool safe = true;
   if constexpr (EPI == EPI_GATE_UP) {
     if (routing && g == (int)gridDim.x - 1) {
       if (slot != 0 || wave != 0) return;
@@ -865,26 +781,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
       return;
     }
     if (routing) {
-      auto& sl = sel;
-      for (int i = threadIdx.x; i < ME; i += 64 * NW) {
-        const float l = i < a.E ? a.logits[i] : 0.0f;
-        sl.logit[i] = l;
-        sl.key[i] = order_key(l);
-        sl.ck[i] = i < a.E ? (unsigned long long)order_key(l) << 32 | (unsigned)~i : 0ull;
+      bool safe;
+      expert = select_slot<ME>(a.logits, a.E, slot, &safe);
+      if (!safe) {  // every wave decided alike: uniform over the work-group
+        if (wave == 0) route_select<ME>(a.logits, a.E, a.slots, a.normalize, sel.sel_idx, sel.sel_w, tab, sel.e);
+        __syncthreads();
+        expert = sel.sel_idx[slot];
       }
-      __syncthreads();
-      rank_by_logit<NW>(sl, a.E, a.slots);
-      __syncthreads();
-      expert = sl.by_logit[slot];
-      safe = ranking_is_safe(sl, a.E, a.slots);
     }
   }
 
-  // One pass over this slot's rows of `ex`: loads, block terms, the fold in
-  // block order.  Returns wave 0's row totals.  On the first pass the
-  // activation blocks are staged and (with routing) wave 1 checks the
-  // selection after issuing its first loads.
-  auto pass = [&](int ex, bool first) -> float {
+  // The pass over this slot's rows of `ex`: loads, block terms, the fold in
+  // block order.  Returns wave 0's row totals.  The activation blocks are
+  // staged once the first chunk's loads are in flight.
+  auto pass = [&](int ex) -> float {
     // tile and matrix of this lane's row
     const uint8_t* cbase;
     const uint16_t* sbase;
@@ -926,11 +836,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
     float total = 0.0f;
     const int nchunks = (nb + CB - 1) / CB;
     load_chunk(0);
-    if (first) {
-      stage_act();
-      if constexpr (EPI == EPI_GATE_UP)
-        if (routing && !safe && wave == 1) verify_selection(sel, a.E, a.slots, a.normalize, tab);
-    }
+    stage_act();
     for (int ch = 0; ch < nchunks; ch++) {
       const int b0 = ch * CB;
       const int bend = min(nb, b0 + CB);
@@ -971,19 +877,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
     return total;
   };
 
-  float total = pass(expert, true);
-  if constexpr (EPI == EPI_GATE_UP) {
-    if (routing && !safe) {
-      // the check finished before the first chunk's barrier
-      auto& sl = sel;
-      const int chosen = sl.sel_idx[slot];
-      if (sl.bad && chosen != expert) {  // uniform: a tie moved this slot to another expert
-        __syncthreads();                 // wave 0 is done with the term buffers
-        total = pass(chosen, false);
-        expert = chosen;
-      }
-    }
-  }
+  const float total = pass(expert);
   if (wave != 0) return;
 
   const int r = lane & 31;

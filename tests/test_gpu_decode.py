@@ -468,3 +468,56 @@ def test_moe_forward_device_rejects_misaligned_x(ctx):
     for b in (bx, bo, bl):
         b.free()
     moe.close()
+
+
+def _special_logits(E, case, seed):
+    rng = np.random.default_rng(seed)
+    lg = rng.normal(0.0, 2.0, E).astype(np.float32)
+    ninf, f = np.float32(-np.inf), np.float32
+    if case == "neg_inf":      # fewer finite logits than routes: zero probabilities tie, by index
+        lg[:] = ninf
+        lg[5] = 3.0
+        lg[E - 2] = -200.0
+    elif case == "below_window":  # probabilities that underflow to zero and tie, by index
+        lg[:] = -150.0 - np.arange(E, dtype=np.float32)
+        lg[3], lg[E - 1] = 0.0, -70.0
+    elif case == "signed_zero":   # +0 and -0 are one logit and one probability
+        lg = -np.abs(lg) - 1.0
+        lg[E - 1], lg[1] = f(0.0), f(-0.0)
+    elif case == "exact_ties":
+        lg[[7, 2, 11]] = lg.max() + 1.0
+    elif case == "near_ties":     # neighbours one ulp apart at the top
+        top = f(lg.max() + 1.0)
+        lg[4] = top
+        lg[9] = np.nextafter(top, f(-np.inf))
+        lg[1] = np.nextafter(lg[9], f(-np.inf))
+    elif case == "neg_nan":       # a NaN makes every probability NaN
+        lg[6] = np.frombuffer(np.uint32(0xFFC01234).tobytes(), np.float32)[0]
+    return lg
+
+
+@pytest.mark.parametrize("E", [16, 256, 300])
+@pytest.mark.parametrize("case", ["neg_inf", "below_window", "signed_zero", "exact_ties",
+                                  "near_ties", "neg_nan"])
+def test_moe_decode_special_logits(ctx, E, case):
+    """Router logits given, one token: the work-groups' own expert choice
+    (logit rank, checked for near-ties around it) must equal the reference's
+    probability ranking, or fall back to it.  NaN logits make every weight
+    and output NaN in the reference; NaN payloads are the platform's, so
+    that case compares the routes and the NaN-ness."""
+    k = 4
+    L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, E, k, normalize_topk=True, seed=E, with_router=False)
+    moe = make_layer(ctx, L)
+    for seed in range(2):
+        lg = _special_logits(E, case, seed)
+        x = O.normal(9000 + seed, 64)
+        out, idx, w = moe.forward(x, logits=lg, return_routes=True)
+        o_out, o_idx, o_w = L.forward(x, logits=lg)
+        assert list(idx) == list(o_idx), (case, seed)
+        if case == "neg_nan":
+            assert np.isnan(w).all() and np.isnan(o_w).all()
+            assert np.isnan(out).all() and np.isnan(o_out).all()
+        else:
+            assert same_bits(w, o_w)
+            assert_parity(out, o_out)
+    moe.close()
