@@ -143,6 +143,26 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
         moe.forward_device(tokens, dx.address, dout.address, dl.address)
     prof = ctx.profile_read()
     ctx.profile(False)
+    # the opt-in FMA fold of the grouped down projection: its time, and its
+    # relative L2 distance from the exact output on the same input
+    moe.forward_device(tokens, dx.address, dout.address, dl.address)
+    exact = dout.download(np.float32, tokens * hid).astype(np.float64)
+    moe.set_down_fold("fma")
+    moe.forward_device(tokens, dx.address, dout.address, dl.address)
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        moe.forward_device(tokens, dx.address, dout.address, dl.address)
+    fma_ms = ctx.timer_stop() / reps
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(reps):
+        moe.forward_device(tokens, dx.address, dout.address, dl.address)
+    fma_prof = ctx.profile_read()
+    ctx.profile(False)
+    fma_out = dout.download(np.float32, tokens * hid).astype(np.float64)
+    moe.set_down_fold("exact")
+    fma_rel = float(np.linalg.norm(fma_out - exact) / max(np.linalg.norm(exact), 1e-30))
     idx = didx.download(np.int32, tokens * topk)
     touched = len(np.unique(idx))
     groups = np.bincount(idx, minlength=experts)
@@ -159,6 +179,10 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
                                                       "median": float(np.median(groups)),
                                                       "min": int(groups.min())},
         "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()},
+        "fma_down_fold": {"ms": round(fma_ms, 4), "tokens_per_s": round(tokens / (fma_ms / 1000.0), 1),
+                          "pct_int8_mfma_peak": round(100 * ops / (fma_ms / 1000.0) / INT8_PEAK_OPS, 2),
+                          "grouped_down_avg_us": round(1000 * fma_prof["grouped_down"][0] / fma_prof["grouped_down"][1], 2),
+                          "rel_l2_vs_exact": float(f"{fma_rel:.3e}")},
     }
     # roofline of the dominant grouped kernel: algorithmic weight bytes (every
     # touched expert's planes once) against HBM, or int8 ops against the MFMA
@@ -684,8 +708,10 @@ def main():
     if not args.no_prefill:
         for (name, dt, hid, inter, ex, k, tok, bound) in PREFILL:
             prefill.append(gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=10, bound=bound))
+            f = prefill[-1]["fma_down_fold"]
             log(f"prefill {name}: {prefill[-1]['ms']} ms, {prefill[-1]['tokens_per_s']} tok/s, "
-                f"{prefill[-1]['pct_int8_mfma_peak']}% int8 MFMA")
+                f"{prefill[-1]['pct_int8_mfma_peak']}% int8 MFMA; FMA down fold {f['ms']} ms "
+                f"(rel-L2 {f['rel_l2_vs_exact']:.1e})")
 
     cpu = None
     if not args.no_cpu:

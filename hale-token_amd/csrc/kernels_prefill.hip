@@ -248,9 +248,15 @@ constexpr int CGB = 3;
 // At most 128 VGPRs (four waves per SIMD): the kernel is bound by its VALU
 // work, and a fourth wave hides more of the matrix-core latency than the
 // registers above 128 would save.
-template <int DT, bool GATE_UP>
+// FMA (down projection only): each block term joins its sum in one fused
+// multiply-add, (d_w d_x) * isum + sum rounded once, instead of the
+// reference's product then sum (two roundings); one VALU operation fewer
+// per element and block, at a relative error far below the f32 output's
+// tolerance.  The gate/up output is requantized, so it keeps the exact fold.
+template <int DT, bool GATE_UP, bool FMA = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_grouped(
     GroupedArgs a) {
+  static_assert(!(GATE_UP && FMA), "the gate/up fold is exact");
   constexpr int CH = Layout<DT>::CH;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -352,8 +358,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     }
 #pragma unroll
     for (int j = 0; j < 16; j++) {
-      accg[j] = accg[j] + pg[j] * (float)ig[j];
-      if constexpr (GATE_UP) accu[j] = accu[j] + pu[j] * (float)iu[j];
+      if constexpr (FMA) {
+        accg[j] = __builtin_fmaf(pg[j], (float)ig[j], accg[j]);
+      } else {
+        accg[j] = accg[j] + pg[j] * (float)ig[j];
+        if constexpr (GATE_UP) accu[j] = accu[j] + pu[j] * (float)iu[j];
+      }
     }
   };
   // NS operand sets in a ring: block b + NS - 1 loads while block b
@@ -571,8 +581,12 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
   d.tin = tact;
   d.y = y;
   const unsigned gd = (unsigned)((w.max_tiles * ((L.H + TN - 1) / TN) + 7) / 8 * 8);
-  if (L.dtype == Q8_0)
+  if (L.dtype == Q8_0 && L.down_fold == DOWN_FOLD_FMA)
+    HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q8_0, false, true>, gd, 256, 0, st, d)));
+  else if (L.dtype == Q8_0)
     HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q8_0, false>, gd, 256, 0, st, d)));
+  else if (L.down_fold == DOWN_FOLD_FMA)
+    HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q4_0, false, true>, gd, 256, 0, st, d)));
   else
     HALE_STEP(K_GROUPED_DOWN, (launch(k_grouped<Q4_0, false>, gd, 256, 0, st, d)));
   // 5. route-order combine

@@ -28,7 +28,13 @@ struct PrefillLayer {
   int* route_idx;        // [T][k]
   float* route_w;        // [T][k]
   unsigned long long* stats;  // [E]
+  int down_fold;         // DOWN_FOLD_EXACT or DOWN_FOLD_FMA (grouped down projection)
 };
+
+// Folds of the grouped down projection: the reference's product then sum,
+// or one fused multiply-add per term.
+constexpr int DOWN_FOLD_EXACT = 0;
+constexpr int DOWN_FOLD_FMA = 1;
 
 // Smallest token count routed through the grouped path.
 size_t prefill_min_tokens(size_t k);

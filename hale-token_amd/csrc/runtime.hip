@@ -105,6 +105,7 @@ struct hale_moe {
   hipEvent_t loaded = nullptr;
   // the provider surface: the pack that fetch misses load from, CacheStats
   // counters, selections recorded by fetch, and per-expert matrix views
+  int down_fold = 0;  // grouped down projection: HALE_FOLD_EXACT or HALE_FOLD_FMA
   hale_pack* source = nullptr;
   uint64_t fetch_hits = 0, misses = 0, bytes_loaded = 0;
   double load_seconds = 0;
@@ -1215,6 +1216,7 @@ static PrefillLayer prefill_layer(hale_moe* m, const TokScratch& s) {
   L.route_idx = s.route_idx;
   L.route_w = s.route_w;
   L.stats = m->stats;
+  L.down_fold = m->down_fold == HALE_FOLD_FMA ? DOWN_FOLD_FMA : DOWN_FOLD_EXACT;
   return L;
 }
 
@@ -1383,6 +1385,16 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
   HIPCHK(c, hipMemcpyAsync(index, s.route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipMemcpyAsync(weight, s.route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_set_down_fold(hale_moe* m, int fold) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m) return fail(c, HALE_EINVAL, "set_down_fold: NULL layer");
+  if (fold != HALE_FOLD_EXACT && fold != HALE_FOLD_FMA)
+    return fail(c, HALE_EINVAL, "set_down_fold: unknown fold %d", fold);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  m->down_fold = fold;
   return HALE_OK;
 }
 

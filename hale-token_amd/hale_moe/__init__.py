@@ -88,6 +88,7 @@ SIGNATURES = {
     "hale_moe_fetch": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _vp]),
     "hale_moe_expert_present": (C.c_int, [_vp, C.c_uint32, _vp]),
     "hale_moe_set_source": (C.c_int, [_vp, _vp]),
+    "hale_moe_set_down_fold": (C.c_int, [_vp, C.c_int]),
     "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
     "hale_pack_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "hale_pack_close": (None, [_vp]),
@@ -908,6 +909,15 @@ class MoeLayer:
         layer's next use waits for the load (and raises its error)."""
         self.ctx.adopt(pack)
         self.ctx.check(lib().hale_moe_prefetch_pack(self.handle, pack.handle), "prefetch_pack")
+
+    def set_down_fold(self, fold: str):
+        """Fold of the expert-grouped down projection: "exact" (the
+        reference's bits, the default) or "fma" (one fused multiply-add per
+        term; relative L2 error far below 1e-5)."""
+        f = {"exact": 0, "fma": 1}.get(fold)
+        if f is None:
+            raise ValueError(f"unknown fold {fold!r} (exact or fma)")
+        self.ctx.check(lib().hale_moe_set_down_fold(self.handle, f), "set_down_fold")
 
     def set_source(self, pack: "PackExpertSource | None"):
         """Makes the pack this layer's ExpertSource without loading anything:

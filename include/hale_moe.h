@@ -252,6 +252,19 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
                             const float *d_logits, float *d_out,
                             uint32_t *d_index, float *d_weight);
 
+/* Folds of the expert-grouped down projection (hale_moe_forward with
+ * ntok >= the grouped threshold).  HALE_FOLD_EXACT, the default, adds each
+ * block term (d_w*d_x)*isum to its row sum as the reference does, product
+ * then sum, and returns the reference's bits.  HALE_FOLD_FMA adds it with
+ * one fused multiply-add, one rounding instead of two: the down output
+ * then agrees with the reference to a relative L2 error far below 1e-5,
+ * not bit for bit.  No counterpart in the reference; for callers that
+ * accept that tolerance in exchange for a faster prefill.  The gate/up
+ * projection and the decode path (1..7 tokens) stay exact in both. */
+#define HALE_FOLD_EXACT 0
+#define HALE_FOLD_FMA 1
+int hale_moe_set_down_fold(hale_moe *moe, int fold);
+
 /* Bytes of the fixed device scratch of hale_moe_forward_device_noalloc. */
 #define HALE_NOALLOC_SCRATCH_BYTES (16u << 20)
 

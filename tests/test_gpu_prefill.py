@@ -126,3 +126,37 @@ def test_grouped_equals_decode_path(ctx):
     batch = moe.forward(xs)
     for t in range(T):
         assert same_bits(moe.forward(xs[t]), batch[t])
+
+
+@pytest.mark.parametrize("dtype,Hd,I,E,k,T,seed", [
+    (O.Q8_0, 2048, 768, 128, 8, 512, 33),    # the Qwen3-30B-A3B prefill shape
+    (O.Q4_0, 4096, 1536, 128, 8, 2048, 44),  # the Qwen3-235B-A22B prefill shape
+    (O.Q4_0, 256, 64, 16, 4, 40, 5),
+])
+def test_grouped_fma_down_fold_within_tolerance(ctx, dtype, Hd, I, E, k, T, seed):
+    """The opt-in FMA fold of the grouped down projection: routes and
+    weights unchanged, every checked token within rel-L2 1e-5 of the
+    oracle's MoeLayer::forward (not bit-exact by design), and switching back
+    to the exact fold restores the reference's bits."""
+    L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=seed, with_router=False)
+    moe = make_layer(ctx, L)
+    xs = O.normal(seed + 1, T * Hd).reshape(T, Hd)
+    logits = zipf_logits(T, E, 1.1, seed=seed)
+    moe.set_down_fold("fma")
+    out, idx, w = moe.forward(xs, logits=logits, return_routes=True)
+    sample = range(T) if T <= 512 else sorted(
+        set(np.random.default_rng(2).choice(T, 24, replace=False).tolist()) | {0, T - 1})
+    worst = 0.0
+    for t in sample:
+        o, o_idx, o_w = L.forward(xs[t], logits=logits[t], nthreads=8)
+        assert list(idx[t]) == list(o_idx) and same_bits(w[t], o_w)
+        worst = max(worst, rel_l2(out[t], o))
+    assert worst <= REL_L2, worst
+    moe.set_down_fold("exact")
+    exact = moe.forward(xs[:16], logits=logits[:16])
+    for t in range(16):
+        o, _, _ = L.forward(xs[t], logits=logits[t], nthreads=8)
+        assert same_bits(exact[t], o)
+    with pytest.raises(ValueError):
+        moe.set_down_fold("fast")
+    moe.close()
