@@ -1150,9 +1150,11 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
 // layout.  D groups are in flight; each group's terms fold into the row's
 // running sum as soon as they are computed, in block order, by DPP adds
 // within the row's 8 lanes, so no other wave or barrier is waited for until
-// the combine.  RG = 16 for 2 or 3 slots (4 or 6 waves), 32 for 1 (4
+// the combine.  The chain's scales are staged in LDS first, in 16-byte
+// pieces (a block's scales for the wave's 8 rows).  RG = 16 for 2 or 3 slots (4 or 6 waves), 32 for 1 (4
 // waves); the launcher takes it for 1 to 3 slots.
 constexpr int DOWN_ACT_MAX = 1024;  // activation blocks staged in LDS (48 KB)
+constexpr int DOWN_SCL_MAX = 4096;  // 16-byte scale pieces staged in LDS (64 KB): waves x blocks
 
 __host__ __device__ inline int down_chain_rows(int slots) { return slots >= 4 ? 8 : (slots >= 2 ? 16 : 32); }
 __host__ __device__ inline int down_chain_waves(int slots) {
@@ -1164,16 +1166,18 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
   static_assert(D % 4 == 0, "groups go in batches of four");
   __shared__ ActBlock s_act[DOWN_ACT_MAX];
+  // each wave's scales: one 16-byte piece (its 8 rows) per block, wave w at
+  // [w * nb, (w + 1) * nb)
+  __shared__ u32x4 s_scl[DOWN_SCL_MAX];
   __shared__ float s_tot[DOWN_MAX_SLOTS][32];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x;
-  const int nb = a.nb, slots = a.slots;
+  const int nb = a.nb, slots = a.slots;  // slots <= 3: one chain per wave
   const int nbg = (nb + 7) / 8;
-  const int sw = slots < 8 ? slots : 8;
   const int rg = down_chain_rows(slots);
-  const int sub = wave / sw, scls = wave % sw;
+  const int sub = wave / slots, sl = wave % slots;
   // every slot's activation blocks (independent of the routes): loads
   // issued first, stored after the first weight loads
   constexpr int APT = (DOWN_ACT_MAX * 3 + 255) / 256;  // pieces per thread, at most (256+ threads)
@@ -1201,38 +1205,46 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   const size_t tile = rowg / TILE;
   const int rt = (int)(rowg % TILE) + r;
   const size_t row_off = (tile * nb * CH * TILE + rt) * 16;
-  const size_t srow_off = tile * nb * TILE + rt;
 
   u32x4 cw[D][CH];
-  uint16_t sc[D];
-  const uint8_t* cbase;
-  const uint16_t* sbase;
-  // group q's loads into ring slot d (groups past the end are clamped to
+  const size_t e = (size_t)__builtin_amdgcn_readfirstlane(a.route_idx[sl]);
+  const uint8_t* cbase = a.codes + e * a.codes_stride + row_off;
+  // group q's codes into ring slot d (groups past the end are clamped to
   // the last: in-bounds loads that are never used)
   auto load = [&](int d, int q) {
     const int b = min(min(q, nbg - 1) * 8 + j, nb - 1);
 #pragma unroll
     for (int c = 0; c < CH; c++)
       cw[d][c] = __builtin_nontemporal_load((const u32x4*)(cbase + ((size_t)b * CH + c) * TILE * 16));
-    sc[d] = sbase[(size_t)b * TILE];
   };
-  auto start_chain = [&](int sl) {
-    const size_t e = (size_t)__builtin_amdgcn_readfirstlane(a.route_idx[sl]);
-    cbase = a.codes + e * a.codes_stride + row_off;
-    sbase = a.scales + e * a.scales_stride + srow_off;
 #pragma unroll
-    for (int d = 0; d < D; d++) load(d, d);
-  };
-  start_chain(scls);
+  for (int d = 0; d < D; d++) load(d, d);
+  // The chain's scales: the 8 rows' scales of a block are 16 contiguous bytes
+  // of the tile's scale line, so a lane loads whole pieces (blocks lane,
+  // lane + 64, ...) and parks them in LDS; a per-block 2-byte load per lane
+  // would touch 8 lines per group for 128 useful bytes.
+  u32x4* scl = s_scl + wave * nb;
+  {
+    const u32x4* sp = (const u32x4*)(a.scales + e * a.scales_stride + tile * nb * TILE + (rowg % TILE));
+    for (int b0 = 0; b0 < nb; b0 += 8 * 64) {
+      u32x4 v[8];
+#pragma unroll
+      for (int m = 0; m < 8; m++)
+        if (b0 + lane + 64 * m < nb) v[m] = sp[(size_t)(b0 + lane + 64 * m) * (TILE * 2 / 16)];
+#pragma unroll
+      for (int m = 0; m < 8; m++)
+        if (b0 + lane + 64 * m < nb) scl[b0 + lane + 64 * m] = v[m];
+    }
+  }
+  const uint16_t* scl16 = (const uint16_t*)scl;
 #pragma unroll
   for (int m = 0; m < APT; m++) {
     const int i = threadIdx.x + m * blockDim.x;
     if (i < npieces) ((u32x4*)s_act)[i] = av[m];
   }
-  __syncthreads();  // s_act
+  __syncthreads();  // s_act, s_scl
 
-  for (int sl = scls; sl < slots; sl += sw) {
-    if (sl != scls) start_chain(sl);
+  {
     const ActBlock* act = s_act + (size_t)sl * nb;
     float acc = 0.0f;  // row r's dot product (valid in lane 8 r)
     for (int q0 = 0; q0 < nbg; q0 += D) {
@@ -1242,7 +1254,10 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
         if (qb < nbg) {  // wave-uniform; the batch's four terms, then their sums in order
           float t[4];
 #pragma unroll
-          for (int i = 0; i < 4; i++) t[i] = block_term<DT>(cw[d0 + i], sc[d0 + i], act + min((qb + i) * 8 + j, nb - 1));
+          for (int i = 0; i < 4; i++) {
+            const int b = min((qb + i) * 8 + j, nb - 1);
+            t[i] = block_term<DT>(cw[d0 + i], scl16[b * 8 + r], act + b);
+          }
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             // groups past the row's end have n <= 0 and add nothing
@@ -1268,7 +1283,7 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   __syncthreads();
   if ((int)threadIdx.x < rg) {
     float acc = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
-    for (int sl = 0; sl < slots; sl++) acc = acc + a.route_w[sl] * s_tot[sl][threadIdx.x];
+    for (int s2 = 0; s2 < slots; s2++) acc = acc + a.route_w[s2] * s_tot[s2][threadIdx.x];
     const size_t row = row0 + threadIdx.x;
     if (row < (size_t)a.rows) a.out[row] = acc;
   }
@@ -1443,7 +1458,8 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS) return hipErrorInvalidValue;
   // A wave per (slot, 8 rows) pays off when few routes leave many rows per
   // work-group (top-1..3); top-4 and wider use the block-group pipeline.
-  if (a.slots <= 3 && a.slots * a.nb <= DOWN_ACT_MAX) {
+  if (a.slots <= 3 && a.slots * a.nb <= DOWN_ACT_MAX &&
+      down_chain_waves(a.slots) * a.nb <= DOWN_SCL_MAX) {
     const int rg = down_chain_rows(a.slots);
     const unsigned grid = (unsigned)(padded_rows((size_t)a.rows) / rg);
     const unsigned threads = 64 * down_chain_waves(a.slots);
