@@ -316,8 +316,10 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
     }
   }
 
-  // activation quantization share: half-wave hw takes blocks hw + 8 (e + gx i)
-  for (int bb = (tid >> 5) + 8 * e; bb < nb; bb += 8 * gx) {
+  // activation quantization share: half-wave hw of work-group e takes blocks
+  // e + gx (hw + 8 i), so the blocks spread over all work-groups (one each
+  // while nb <= E) rather than loading the first few
+  for (int bb = e + gx * (tid >> 5); bb < nb; bb += 8 * gx) {
     float v = xt[bb * QK + (lane & 31)];
     float scale;
     int qsum;
@@ -1258,21 +1260,34 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
             const int b = min((qb + i) * 8 + j, nb - 1);
             t[i] = block_term<DT>(cw[d0 + i], scl16[b * 8 + r], act + b);
           }
+#define HALE_ROW_TERM(k) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ti), 0x100 + (k), 0xF, 0xF, false))
+          if (qb + 4 <= nb / 8) {  // four whole groups (wave-uniform): plain adds in block order
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            // groups past the row's end have n <= 0 and add nothing
-            const int n = nb - (qb + i) * 8;  // blocks of the group inside the row
-            const float ti = t[i];
-            acc = n > 0 ? acc + ti : acc;
-#define HALE_ROW_TERM(k)                                                                        \
-  {                                                                                             \
-    const float tk = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ti), 0x100 + (k), 0xF, 0xF, false)); \
-    acc = (k) < n ? acc + tk : acc;                                                             \
-  }
-            HALE_ROW_TERM(1) HALE_ROW_TERM(2) HALE_ROW_TERM(3) HALE_ROW_TERM(4)
-            HALE_ROW_TERM(5) HALE_ROW_TERM(6) HALE_ROW_TERM(7)
-#undef HALE_ROW_TERM
+            for (int i = 0; i < 4; i++) {
+              const float ti = t[i];
+              acc = acc + ti;
+              acc = acc + HALE_ROW_TERM(1);
+              acc = acc + HALE_ROW_TERM(2);
+              acc = acc + HALE_ROW_TERM(3);
+              acc = acc + HALE_ROW_TERM(4);
+              acc = acc + HALE_ROW_TERM(5);
+              acc = acc + HALE_ROW_TERM(6);
+              acc = acc + HALE_ROW_TERM(7);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              // groups past the row's end have n <= 0 and add nothing
+              const int n = nb - (qb + i) * 8;  // blocks of the group inside the row
+              const float ti = t[i];
+              acc = n > 0 ? acc + ti : acc;
+#define HALE_ROW_TERM_IF(k) acc = (k) < n ? acc + HALE_ROW_TERM(k) : acc;
+              HALE_ROW_TERM_IF(1) HALE_ROW_TERM_IF(2) HALE_ROW_TERM_IF(3) HALE_ROW_TERM_IF(4)
+              HALE_ROW_TERM_IF(5) HALE_ROW_TERM_IF(6) HALE_ROW_TERM_IF(7)
+#undef HALE_ROW_TERM_IF
+            }
           }
+#undef HALE_ROW_TERM
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) load(d0 + i, qb + i + D);
