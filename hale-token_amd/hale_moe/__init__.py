@@ -539,7 +539,9 @@ class WeightMatrix:
         return out
 
     def close(self):
-        if getattr(self, "handle", None) and self.ctx.alive:
+        # a view from ExpertProvider.fetch belongs to its layer: nothing to free
+        # here, and the layer may already be gone
+        if getattr(self, "handle", None) and self.ctx.alive and not getattr(self, "_view", False):
             lib().hale_matrix_destroy(self.handle)
         self.handle = None
 
@@ -660,7 +662,8 @@ class HbmExpertProvider:
                     for h, (r, c) in ((g, (L.inter, L.hidden)), (u, (L.inter, L.hidden)),
                                       (d, (L.hidden, L.inter)))]
             for m in mats:
-                m._owner = L  # a view: the layer outlives it
+                m._view = True
+                m._owner = L  # keeps the Python layer object alive
             out.append(Expert(*mats))
         return out
 

@@ -186,3 +186,19 @@ def test_views_belong_to_the_layer(ctx, oracle_layer):
     assert same_bits(ex2.forward(x), expert_out(L, 4, x))
     assert same_bits(moe.forward(x), want)
     moe.close()
+
+
+def test_views_outliving_their_layer_free_nothing(ctx, oracle_layer):
+    """A fetched expert kept after its layer is closed: closing or dropping
+    it must not touch the layer's (freed) memory."""
+    L = oracle_layer
+    moe = new_layer(ctx, L, range(E))
+    ex = moe.experts.fetch([H.ExpertKey(LAYER, 1)])[0]
+    moe.close()
+    for m in (ex.gate, ex.up, ex.down):
+        m.close()
+    del ex
+    moe2 = new_layer(ctx, L, range(E))  # the context still works
+    x = O.normal(16, HID)
+    assert same_bits(moe2.experts.fetch([H.ExpertKey(LAYER, 1)])[0].forward(x), expert_out(L, 1, x))
+    moe2.close()
