@@ -80,6 +80,10 @@ struct GemvArgs {
   int* route_out_idx;
   float* route_out_w;
   unsigned long long* stats;
+  // set by launch_gemv (EPI_GATE_UP): the rows' 32-row tiles and the tiles
+  // per work-group
+  int tiles;
+  int ipw;
 };
 
 // Arguments of the down projection + combine (k_down_combine).

@@ -793,26 +793,56 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
     }
   }
 
-  // The pass over this slot's rows of `ex`: loads, block terms, the fold in
-  // block order.  Returns wave 0's row totals.  The activation blocks are
-  // staged once the first chunk's loads are in flight.
-  auto pass = [&](int ex) -> float {
-    // tile and matrix of this lane's row
+  // Wave 0's outputs of one item from its row totals: the plain rows, or
+  // gate/up's h = silu(g) * u requantized.
+  const int r = lane & 31;
+  auto finish = [&](int tile, float total) {
+    if constexpr (EPI == EPI_PLAIN) {
+      const size_t row = (2 * (size_t)g + (lane >> 5)) * TILE + r;
+      if (row < (size_t)a.rows) a.out[row] = total;
+    } else if constexpr (EPI == EPI_GATE_UP) {
+      float u = __shfl(total, lane + 32);
+      float h = wave_silu(total, tab) * u;  // lanes 0-31: *g = silu(*g) * u
+      float scale;
+      int qsum;
+      int q = quant_block_lane(h, &scale, &qsum);
+      if (lane < 32) {
+        ActBlock* hb = a.hact + (size_t)slot * a.hact_stride + tile;
+        hb->q[lane] = (int8_t)q;
+        if (lane == 0) {
+          hb->scale = scale;
+          hb->qsum = qsum;
+        }
+      }
+    }
+  };
+
+  // The items of this work-group: gate/up tiles t0 .. t0 + nit - 1 (one
+  // slot, so one expert and one activation), or the plain rows' 64-row
+  // group g.  Their chunks run as one sequence: the loads of chunk c + 1,
+  // the next item's first chunk included, are issued while chunk c's terms
+  // are formed, and wave 0 folds each item's chunks in block order and
+  // writes its outputs after its last one.
+  const int ipw = EPI == EPI_GATE_UP ? a.ipw : 1;
+  const int t0 = g * ipw;
+  const int nit = EPI == EPI_GATE_UP ? min(ipw, a.tiles - t0) : 1;
+  {
+    const int ex = expert;
+    // planes of this lane's matrix
     const uint8_t* cbase;
     const uint16_t* sbase;
-    size_t tile;
     if constexpr (EPI == EPI_GATE_UP) {
-      tile = g;
       cbase = (lane < 32 ? a.codes : a.codes2) + (size_t)ex * a.codes_stride;
       sbase = (lane < 32 ? a.scales : a.scales2) + (size_t)ex * a.scales_stride;
     } else {
-      tile = 2 * (size_t)g + (lane >> 5);
       cbase = a.codes + (size_t)ex * a.codes_stride;
       sbase = a.scales + (size_t)ex * a.scales_stride;
     }
-    const int r = lane & 31;
-    const uint8_t* crow = cbase + (tile * nb * CH * TILE + r) * 16;
-    const uint16_t* srow = sbase + tile * nb * TILE + r;
+    auto tile_of = [&](int it) -> size_t {
+      return EPI == EPI_GATE_UP ? (size_t)(t0 + it) : 2 * (size_t)g + (lane >> 5);
+    };
+    auto crow_of = [&](int it) { return cbase + (tile_of(it) * nb * CH * TILE + r) * 16; };
+    auto srow_of = [&](int it) { return sbase + tile_of(it) * nb * TILE + r; };
     const ActBlock* act = s_act;
 
     u32x4 cw[UPW][CH];
@@ -823,32 +853,38 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
     // together.  (A clamped block's activation may be another wave's: it
     // only feeds that discarded term.)
     auto block_of = [&](int ch, int s) { return min(ch * CB + wave * UPW + s, nb - 1); };
-    auto load_block = [&](int ch, int s) {
+    auto load_block = [&](const uint8_t* crow, const uint16_t* srow, int ch, int s) {
       const int b = block_of(ch, s);
 #pragma unroll
       for (int c = 0; c < CH; c++)
         cw[s][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
       sw[s] = srow[(size_t)b * TILE];
     };
-    auto load_chunk = [&](int ch) {
-#pragma unroll
-      for (int s = 0; s < UPW; s++) load_block(ch, s);
-    };
 
     float total = 0.0f;
     const int nchunks = (nb + CB - 1) / CB;
-    load_chunk(0);
+    const int nc = nit * nchunks;
+    {
+      const uint8_t* crow = crow_of(0);
+      const uint16_t* srow = srow_of(0);
+#pragma unroll
+      for (int s = 0; s < UPW; s++) load_block(crow, srow, 0, s);
+    }
     stage_act();
-    for (int ch = 0; ch < nchunks; ch++) {
+    for (int c = 0; c < nc; c++) {
+      const int it = c / nchunks, ch = c - it * nchunks;
       const int b0 = ch * CB;
       const int bend = min(nb, b0 + CB);
-      float(*tb)[GROUP] = terms[ch & 1];
+      float(*tb)[GROUP] = terms[c & 1];
       // Terms in groups of four blocks; each group's registers take the next
       // chunk's loads as soon as its terms are done.  The scheduling barriers
       // keep the activation reads of one group live at a time, so the kernel
       // keeps few VGPRs.
       float tv[UPW];
-      const bool more = ch + 1 < nchunks;
+      const bool more = c + 1 < nc;
+      const int itn = (c + 1) / nchunks, chn = c + 1 - itn * nchunks;
+      const uint8_t* crn = crow_of(itn);
+      const uint16_t* srn = srow_of(itn);
 #pragma unroll
       for (int s0 = 0; s0 < UPW; s0 += 4) {
 #pragma unroll
@@ -859,7 +895,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (more) {
 #pragma unroll
-          for (int s = s0; s < s0 + 4; s++) load_block(ch + 1, s);
+          for (int s = s0; s < s0 + 4; s++) load_block(crn, srn, chn, s);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -874,30 +910,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
         __builtin_amdgcn_s_setprio(3);
         total = lds_sum_strided<GROUP>(&tb[0][lane], bend - b0, total);
         __builtin_amdgcn_s_setprio(0);
-      }
-    }
-    return total;
-  };
-
-  const float total = pass(expert);
-  if (wave != 0) return;
-
-  const int r = lane & 31;
-  if constexpr (EPI == EPI_PLAIN) {
-    const size_t row = (2 * (size_t)g + (lane >> 5)) * TILE + r;
-    if (row < (size_t)a.rows) a.out[row] = total;
-  } else if constexpr (EPI == EPI_GATE_UP) {
-    float u = __shfl(total, lane + 32);
-    float h = wave_silu(total, tab) * u;  // lanes 0-31: *g = silu(*g) * u
-    float scale;
-    int qsum;
-    int q = quant_block_lane(h, &scale, &qsum);
-    if (lane < 32) {
-      ActBlock* hb = a.hact + (size_t)slot * a.hact_stride + g;
-      hb->q[lane] = (int8_t)q;
-      if (lane == 0) {
-        hb->scale = scale;
-        hb->qsum = qsum;
+        if (ch == nchunks - 1) {
+          finish(t0 + it, total);
+          total = 0.0f;
+        }
       }
     }
   }
@@ -1450,13 +1466,23 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   if (a.nb < 1 || a.nb > GEMV_MAX_NB) return hipErrorInvalidValue;
   if (a.logits && (epi != EPI_GATE_UP || a.E > ROUTE_MAX_E || slots > 64 || slots > a.E))
     return hipErrorInvalidValue;
-  // gate/up with routing: one more column of work-groups for the selector
-  dim3 grid(groups + (a.logits ? 1 : 0), slots);
   const bool many = a.logits && a.E > 256;  // selection state for up to 1024 experts
-#define HALE_GEMV_CASE(D, E, W)                                                       \
-  if (dtype == D && epi == E) {                                                       \
-    if (many) return launch(k_gemv<D, E, W, ROUTE_MAX_E>, grid, 64 * W, 0, st, a);    \
-    return launch(k_gemv<D, E, W>, grid, 64 * W, 0, st, a);                           \
+  // Gate/up: one work-group per (32-row tile, slot), or per two tiles when
+  // the grid would not be resident at once (at 128 VGPRs and 1024 threads
+  // per CU: 256 work-groups of 16 waves, 512 of 8), so that no second round
+  // runs on a partly filled GPU.  With routing, one more column of
+  // work-groups holds the selector.
+  auto grid_of = [&](int nw) {
+    GemvArgs b = a;
+    b.tiles = groups;
+    b.ipw = epi == EPI_GATE_UP && (long)groups * slots > 256L * (16 / nw) ? 2 : 1;
+    return std::make_pair(dim3((groups + b.ipw - 1) / b.ipw + (a.logits ? 1 : 0), slots), b);
+  };
+#define HALE_GEMV_CASE(D, E, W)                                                             \
+  if (dtype == D && epi == E) {                                                             \
+    const auto gb = grid_of(W);                                                             \
+    if (many) return launch(k_gemv<D, E, W, ROUTE_MAX_E>, gb.first, 64 * W, 0, st, gb.second); \
+    return launch(k_gemv<D, E, W>, gb.first, 64 * W, 0, st, gb.second);                     \
   }
   HALE_GEMV_CASE(Q8_0, EPI_PLAIN, 4)
   HALE_GEMV_CASE(Q8_0, EPI_GATE_UP, 8)

@@ -431,6 +431,28 @@ def test_moe_decode_down_whole_chain(ctx, dtype, hidden, inter, E, k):
     moe.close()
 
 
+@pytest.mark.parametrize("dtype,hidden,inter,E,k", [
+    (H.Q8_0, 256, 2080, 8, 8),     # 65 tiles x 8 slots = 520 > 512 resident (8 waves): 2 per group, odd
+    (H.Q4_0, 2080, 1056, 16, 16),  # 33 x 16 = 528 > 512 (8 waves, two chunks per row): odd
+    (H.Q4_0, 1024, 8256, 2, 2),    # 258 x 2 = 516 > 256 resident (16 waves, one chunk)
+])
+def test_moe_decode_gate_up_two_tiles_per_group(ctx, dtype, hidden, inter, E, k):
+    """Gate/up grids larger than the GPU holds at once give each work-group
+    two tiles (the second one's loads issued under the first one's fold):
+    odd tile counts leave the last group one tile."""
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=True,
+                              seed=hidden + inter + k + 11)
+    moe = make_layer(ctx, L)
+    for seed in range(2):
+        x = O.normal(8300 + seed, hidden)
+        out, idx, w = moe.forward(x, return_routes=True)
+        o_out, o_idx, o_w = L.forward(x, nthreads=8)
+        assert list(idx) == list(o_idx)
+        assert same_bits(w, o_w)
+        assert_parity(out, o_out)
+    moe.close()
+
+
 def test_moe_top_k_zero_routes_nowhere(ctx):
     """top_k = 0: top_k returns nothing, so the reference's forward leaves
     the output at zero on the decode and the grouped path alike."""
