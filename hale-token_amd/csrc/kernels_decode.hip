@@ -1173,6 +1173,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
 // waves); the launcher takes it for 1 to 3 slots.
 constexpr int DOWN_ACT_MAX = 1024;  // activation blocks staged in LDS (48 KB)
 constexpr int DOWN_SCL_MAX = 4096;  // 16-byte scale pieces staged in LDS (64 KB): waves x blocks
+constexpr int DOWN_CHAIN_MAX_NB = 512;  // blocks per row: one scale piece per lane and 64 blocks
 
 __host__ __device__ inline int down_chain_rows(int slots) { return slots >= 4 ? 8 : (slots >= 2 ? 16 : 32); }
 __host__ __device__ inline int down_chain_waves(int slots) {
@@ -1235,31 +1236,33 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
     for (int c = 0; c < CH; c++)
       cw[d][c] = __builtin_nontemporal_load((const u32x4*)(cbase + ((size_t)b * CH + c) * TILE * 16));
   };
-#pragma unroll
-  for (int d = 0; d < D; d++) load(d, d);
   // The chain's scales: the 8 rows' scales of a block are 16 contiguous bytes
   // of the tile's scale line, so a lane loads whole pieces (blocks lane,
   // lane + 64, ...) and parks them in LDS; a per-block 2-byte load per lane
-  // would touch 8 lines per group for 128 useful bytes.
+  // would touch 8 lines per group for 128 useful bytes.  The pieces (at
+  // most 512: the launcher keeps nb <= 512) are loaded before the ring's
+  // codes: loads return in order, so they and the activation pieces can be
+  // parked while the codes are still in flight, and the staging barrier
+  // does not wait for the ring.
   u32x4* scl = s_scl + wave * nb;
+  const u32x4* sp = (const u32x4*)(a.scales + e * a.scales_stride + tile * nb * TILE + (rowg % TILE));
   {
-    const u32x4* sp = (const u32x4*)(a.scales + e * a.scales_stride + tile * nb * TILE + (rowg % TILE));
-    for (int b0 = 0; b0 < nb; b0 += 8 * 64) {
-      u32x4 v[8];
+    u32x4 v[8];
 #pragma unroll
-      for (int m = 0; m < 8; m++)
-        if (b0 + lane + 64 * m < nb) v[m] = sp[(size_t)(b0 + lane + 64 * m) * (TILE * 2 / 16)];
+    for (int m = 0; m < 8; m++)
+      if (lane + 64 * m < nb) v[m] = sp[(size_t)(lane + 64 * m) * (TILE * 2 / 16)];
 #pragma unroll
-      for (int m = 0; m < 8; m++)
-        if (b0 + lane + 64 * m < nb) scl[b0 + lane + 64 * m] = v[m];
-    }
+    for (int d = 0; d < D; d++) load(d, d);
+#pragma unroll
+    for (int m = 0; m < 8; m++)
+      if (lane + 64 * m < nb) scl[lane + 64 * m] = v[m];
   }
-  const uint16_t* scl16 = (const uint16_t*)scl;
 #pragma unroll
   for (int m = 0; m < APT; m++) {
     const int i = threadIdx.x + m * blockDim.x;
     if (i < npieces) ((u32x4*)s_act)[i] = av[m];
   }
+  const uint16_t* scl16 = (const uint16_t*)scl;
   __syncthreads();  // s_act, s_scl
 
   {
@@ -1499,7 +1502,7 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS) return hipErrorInvalidValue;
   // A wave per (slot, 8 rows) pays off when few routes leave many rows per
   // work-group (top-1..3); top-4 and wider use the block-group pipeline.
-  if (a.slots <= 3 && a.slots * a.nb <= DOWN_ACT_MAX &&
+  if (a.slots <= 3 && a.nb <= DOWN_CHAIN_MAX_NB && a.slots * a.nb <= DOWN_ACT_MAX &&
       down_chain_waves(a.slots) * a.nb <= DOWN_SCL_MAX) {
     const int rg = down_chain_rows(a.slots);
     const unsigned grid = (unsigned)(padded_rows((size_t)a.rows) / rg);
