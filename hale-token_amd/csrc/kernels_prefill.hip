@@ -35,8 +35,9 @@ constexpr int GROUP_WAVES = 16;  // waves of the grouping kernel
 constexpr int GROUP_MAX_E = 1024;
 // Activations of the grouped kernels, tile-major: per (tile, 32-column
 // block) the codes as the MFMA's A operand wants them, [K half][32 rows]
-// [16 B], then the 32 rows' f32 scales, so one wave's operand of a block is
-// 1 KB contiguous and its scales one line.  The gate/up input is gathered
+// [16 B] (the halves' element order follows the weight operand: see the
+// grouped matrix products below), then the 32 rows' f32 scales, so one
+// wave's operand of a block is 1 KB contiguous and its scales one line.  The gate/up input is gathered
 // into this layout from the token-major blocks; the requantized SiLU output
 // is written in it by the gate/up kernel for the down kernel.
 constexpr int TACT_CODES = 2 * TM * 16;
@@ -203,18 +204,28 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
 // A work-group takes one tile (expert e, 32 sorted rows) and 128 output
 // columns; wave w owns columns [n0, n0+32).  Per quantization block b a wave
 // issues one 32x32x32 int8 MFMA (two for gate/up): lane l supplies row
-// l%32's 16 activation codes of K half l/32 and column l%32's 16 weight codes
-// of the same half, which is exactly one 16-byte chunk of the tile layout
-// (q4_0: the low nibbles are K 0-15, the high nibbles K 16-31).  Result
-// element j of lane l is row (j%4) + 4*(l/32) + 8*(j/4), column l%32.
+// l%32's 16 activation codes of K half h = l/32 and column l%32's 16 weight
+// codes of the same half.  q8_0: half h is elements 16h..16h+15, exactly one
+// 16-byte chunk of the tile layout.  q4_0: half h is the lane's 8 bytes
+// 8h..8h+7 of the column's chunk, both nibbles: elements 8h..8h+7 (low) then
+// 16+8h..16+8h+7 (high), and the activation tiles hold the codes in that
+// order.  Result element j of lane l is row (j%4) + 4*(l/32) + 8*(j/4),
+// column l%32.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-// B operand from a loaded chunk.  q8_0: the signed codes as they are.  q4_0:
-// the unsigned nibbles n (0..15) of half h; the MFMA's accumulator then starts
-// at -8 * sum(x) of the row so that it ends at sum((n - 8) * x), the same
-// integer as with signed codes.
-template <int DT>
-__device__ __forceinline__ v4i weight_operand(u32x4 v, int h) {
-  if constexpr (DT == Q4_0) v = (v >> (u32x4)(4 * h)) & 0x0f0f0f0fu;
+// B operand from loaded codes.  q8_0: the signed codes of a 16-byte chunk as
+// they are.  q4_0: the unsigned nibbles n (0..15) of the lane's 8 bytes, low
+// nibbles then high; the MFMA's accumulator then starts at -8 * sum(x) of
+// the row so that it ends at sum((n - 8) * x), the same integer as with
+// signed codes.
+__device__ __forceinline__ v4i weight_operand(u32x4 v) {
+  v4i r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+__device__ __forceinline__ v4i weight_operand(u32x2 w) {
+  const u32x4 v = {w[0] & 0x0f0f0f0fu, w[1] & 0x0f0f0f0fu, (w[0] >> 4) & 0x0f0f0f0fu,
+                   (w[1] >> 4) & 0x0f0f0f0fu};
   v4i r;
   __builtin_memcpy(&r, &v, 16);
   return r;
@@ -291,7 +302,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   const auto ru = buffer_rsrc(GATE_UP ? a.codes2 + e * a.codes_stride + cplane : a.codes, cbytes);
   const auto rsu = buffer_rsrc(GATE_UP ? a.scales2 + e * a.scales_stride + splane : a.scales, sbytes);
   const int xoff = h * (TM * 16) + rn * 16, dxoff = TACT_CODES + rn * 4;
-  const int coff = rn * 16 + (DT == Q8_0 ? h * TILE * 16 : 0);
+  const int coff = rn * 16 + (DT == Q8_0 ? h * TILE * 16 : 8 * h);
   const int soff = rn * 2;
 
   // accumulators start at +0.0 like the reference's `let mut total = 0.0`,
@@ -300,7 +311,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 
   // Operands of one block.
   struct Ops {
-    u32x4 xr, wg, wu;
+    using WT = std::conditional_t<DT == Q4_0, u32x2, u32x4>;
+    u32x4 xr;
+    WT wg, wu;
     float dx;
     uint16_t dg, du;
   };
@@ -311,10 +324,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const int ab = b * TACT_BLOCK, cb = b * (CH * TILE * 16), sb = b * (TILE * 2);
     o.xr = __builtin_amdgcn_raw_buffer_load_b128(ra, xoff, ab, 0);
     o.dx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, dxoff, ab, 0));
-    o.wg = __builtin_amdgcn_raw_buffer_load_b128(rg, coff, cb, 0);
+    if constexpr (DT == Q4_0) {
+      o.wg = __builtin_amdgcn_raw_buffer_load_b64(rg, coff, cb, 0);
+    } else {
+      o.wg = __builtin_amdgcn_raw_buffer_load_b128(rg, coff, cb, 0);
+    }
     o.dg = __builtin_amdgcn_raw_buffer_load_b16(rsg, soff, sb, 0);
     if constexpr (GATE_UP) {
-      o.wu = __builtin_amdgcn_raw_buffer_load_b128(ru, coff, cb, 0);
+      if constexpr (DT == Q4_0) {
+        o.wu = __builtin_amdgcn_raw_buffer_load_b64(ru, coff, cb, 0);
+      } else {
+        o.wu = __builtin_amdgcn_raw_buffer_load_b128(ru, coff, cb, 0);
+      }
       o.du = __builtin_amdgcn_raw_buffer_load_b16(rsu, soff, sb, 0);
     }
   };
@@ -328,10 +349,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     __builtin_memcpy(&xa, &o.xr, 16);
     v16i c0 = {};
     if constexpr (DT == Q4_0) c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, minus8, c0, 0, 0, 0);
-    const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(o.wg, h), c0, 0, 0, 0);
+    const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wg), c0, 0, 0, 0);
     v16i iu = {};
     if constexpr (GATE_UP)
-      iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand<DT>(o.wu, h), c0, 0, 0, 0);
+      iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wu), c0, 0, 0, 0);
     // Scale products d_w[col] * d_x[row] of the whole 32x32 tile on the
     // matrix core, which rounds each product exactly like a VALU multiply
     // (only the sign of a zero product can differ, and that cannot reach an
@@ -398,6 +419,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     tab.load();
     const int nbo = a.ncols / QK;
     uint8_t* tb = a.tout + ((size_t)ti * nbo + n0 / QK) * TACT_BLOCK;
+    // element rn of the block: q8_0 half rn / 16, byte rn % 16; q4_0 half
+    // (rn / 8) % 2, byte rn % 8 (+ 8 for elements 16..31)
+    const int qoff = DT == Q4_0 ? ((rn >> 3) & 1) * (TM * 16) + (rn & 7) + 8 * (rn >> 4)
+                                : (rn >> 4) * (TM * 16) + (rn & 15);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       const int row = (j % 4) + 4 * h + 8 * (j / 4);
@@ -405,7 +430,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
       float scale;
       int qsum;
       const int qv = quant_block_lane(hv, &scale, &qsum);
-      tb[(rn >> 4) * (TM * 16) + row * 16 + (rn & 15)] = (uint8_t)(int8_t)qv;
+      tb[qoff + row * 16] = (uint8_t)(int8_t)qv;
       if (rn == 0) *(float*)(tb + TACT_CODES + row * 4) = scale;
     }
   } else {
@@ -420,7 +445,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // Gather of the gate/up input into the tile layout: work-group (tile, 8
 // blocks), thread (block, row): row r of tile ti is token perm[row0 + r] / k
 // (rows past the tile's end repeat its last row).  Grid: max_tiles x
-// ceil(nb / 8); work-groups past the live tile count exit.
+// ceil(nb / 8); work-groups past the live tile count exit.  Q4: the q4_0
+// order of the halves (elements 0-7 and 16-23, then 8-15 and 24-31).
+template <bool Q4>
 __global__ __launch_bounds__(256) void k_gather_tiles(const ActBlock* __restrict__ act, int nb,
                                                       const Tile* __restrict__ tiles,
                                                       const int* __restrict__ ntiles,
@@ -434,8 +461,13 @@ __global__ __launch_bounds__(256) void k_gather_tiles(const ActBlock* __restrict
   const Tile tl = tiles[ti];
   const int tok = perm[tl.row0 + min(r, tl.rows - 1)] / k;
   const ActBlock* src = act + (size_t)tok * nb + b;
-  const u32x4 lo = *(const u32x4*)src->q;
-  const u32x4 hi = *(const u32x4*)(src->q + 16);
+  u32x4 lo = *(const u32x4*)src->q;
+  u32x4 hi = *(const u32x4*)(src->q + 16);
+  if constexpr (Q4) {
+    const u32x4 h0 = {lo[0], lo[1], hi[0], hi[1]}, h1 = {lo[2], lo[3], hi[2], hi[3]};
+    lo = h0;
+    hi = h1;
+  }
   uint8_t* dst = tin + ((size_t)ti * nb + b) * TACT_BLOCK;
   *(u32x4*)(dst + r * 16) = lo;
   *(u32x4*)(dst + TM * 16 + r * 16) = hi;
@@ -547,9 +579,13 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
                             pos_of, tiles, ntiles, L.stats));
   // 3. gather the activations into tiles, then the grouped gate/up with SiLU
   // and requantization
-  HALE_STEP(K_GATHER, launch(k_gather_tiles, dim3((unsigned)w.max_tiles, (unsigned)((nbh + 7) / 8)),
-                             256, 0, st, (const ActBlock*)L.act, nbh, tiles, ntiles, perm, L.k,
-                             tin));
+  const dim3 ggr((unsigned)w.max_tiles, (unsigned)((nbh + 7) / 8));
+  if (L.dtype == Q4_0)
+    HALE_STEP(K_GATHER, launch(k_gather_tiles<true>, ggr, 256, 0, st, (const ActBlock*)L.act, nbh,
+                               tiles, ntiles, perm, L.k, tin));
+  else
+    HALE_STEP(K_GATHER, launch(k_gather_tiles<false>, ggr, 256, 0, st, (const ActBlock*)L.act, nbh,
+                               tiles, ntiles, perm, L.k, tin));
   GroupedArgs g{};
   g.codes = L.gate_c;
   g.scales = L.gate_s;
