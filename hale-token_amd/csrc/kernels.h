@@ -84,7 +84,11 @@ struct GemvArgs {
   // per work-group
   int tiles;
   int ipw;
+  // EPI_GATE_UP of one token: the f32 activation (16-byte aligned, nb <=
+  // GEMV_X_MAX_NB), quantized by the kernel itself in place of act
+  const float* x;
 };
+constexpr int GEMV_X_MAX_NB = 128;
 
 // Arguments of the down projection + combine (k_down_combine).
 struct DownArgs {

@@ -238,16 +238,11 @@ __global__ __launch_bounds__(256) void k_act_quant_any(const float* __restrict__
   }
 }
 
-// The same for 16-byte aligned x; each 8-lane group quantizes one block
-// from one 16-byte load per lane.  The block maximum and the code sum are
-// order-free (max and integer sums), and scale, reciprocal and codes are
-// the expressions of quant_block_lane.
-__global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, size_t nblocks,
-                                                   ActBlock* __restrict__ act) {
-  const size_t blk = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) / 8;
-  const int j = threadIdx.x & 7;
-  if (blk >= nblocks) return;  // uniform across the 8-lane group
-  const f32x4 v = *(const f32x4*)(x + blk * QK + 4 * j);
+// One q8 block from an aligned group of 8 lanes, lane j holding elements
+// 4j..4j+3 as v.  The block maximum and the code sum are order-free (max
+// and integer sums), and scale, reciprocal and codes are the expressions of
+// quant_block_lane.  All 8 lanes of the group must be active.
+__device__ __forceinline__ void quant_block8(f32x4 v, int j, ActBlock* dst) {
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   amax = fmaxf(amax, HALE_DPP_F32(amax, 0xB1));   // lane ^ 1
   amax = fmaxf(amax, HALE_DPP_F32(amax, 0x4E));   // lane ^ 2
@@ -260,12 +255,22 @@ __global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, 
   qs += __builtin_amdgcn_update_dpp(0, qs, 0xB1, 0xF, 0xF, false);
   qs += __builtin_amdgcn_update_dpp(0, qs, 0x4E, 0xF, 0xF, false);
   qs += __builtin_amdgcn_update_dpp(0, qs, 0x141, 0xF, 0xF, false);
-  *(unsigned*)(act[blk].q + 4 * j) = (unsigned)(q0 & 0xff) | (unsigned)(q1 & 0xff) << 8 |
-                                     (unsigned)(q2 & 0xff) << 16 | (unsigned)(q3 & 0xff) << 24;
+  *(unsigned*)(dst->q + 4 * j) = (unsigned)(q0 & 0xff) | (unsigned)(q1 & 0xff) << 8 |
+                                 (unsigned)(q2 & 0xff) << 16 | (unsigned)(q3 & 0xff) << 24;
   if (j == 0) {
-    act[blk].scale = scale;
-    act[blk].qsum = qs;
+    dst->scale = scale;
+    dst->qsum = qs;
   }
+}
+
+// The same for 16-byte aligned x; each 8-lane group quantizes one block
+// from one 16-byte load per lane.
+__global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ x, size_t nblocks,
+                                                   ActBlock* __restrict__ act) {
+  const size_t blk = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) / 8;
+  const int j = threadIdx.x & 7;
+  if (blk >= nblocks) return;  // uniform across the 8-lane group
+  quant_block8(*(const f32x4*)(x + blk * QK + 4 * j), j, act + blk);
 }
 
 // ===========================================================================
@@ -739,8 +744,22 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   constexpr int APER = (WNB * 3 + 63) / 64;          // 16-byte pieces per lane
   // block of the wave's t-th block (chunk t / UPW, position t % UPW)
   auto wave_block = [&](int t) { return (t / UPW) * CB + wave * UPW + t % UPW; };
+  // With x given (gate/up of one expert, 16-byte aligned, at most 16 blocks
+  // per wave: the launcher's check), the activation blocks are quantized
+  // here, each wave its own blocks, 8 lanes per block, instead of read from
+  // a.act: one launch less.
+  constexpr int XPER = 2;  // f32x4 per lane: 16 blocks per wave
+  const bool from_x = EPI == EPI_GATE_UP && a.x != nullptr;  // uniform
+  const int nbw = (nb + CB - 1) / CB * UPW;                  // the wave's blocks (some past nb)
   u32x4 av[APER];
-  {
+  f32x4 xv[XPER];
+  if (from_x) {
+#pragma unroll
+    for (int m = 0; m < XPER; m++) {
+      const int t = (lane >> 3) + 8 * m, b = wave_block(t);
+      if (t < nbw && b < nb) xv[m] = *(const f32x4*)(a.x + (size_t)b * QK + 4 * (lane & 7));
+    }
+  } else {
     const u32x4* src = (const u32x4*)(a.act + (size_t)slot * a.act_stride);
 #pragma unroll
     for (int j = 0; j < APER; j++) {
@@ -750,12 +769,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
     }
   }
   auto stage_act = [&]() {
-    u32x4* dst = (u32x4*)s_act;
+    if (from_x) {
 #pragma unroll
-    for (int j = 0; j < APER; j++) {
-      const int p = lane + 64 * j;
-      const int b = wave_block(p / 3);
-      if (p < WNB * 3 && b < nb) dst[b * 3 + p % 3] = av[j];
+      for (int m = 0; m < XPER; m++) {
+        const int t = (lane >> 3) + 8 * m, b = wave_block(t);
+        if (t < nbw && b < nb) quant_block8(xv[m], lane & 7, s_act + b);  // uniform per 8 lanes
+      }
+    } else {
+      u32x4* dst = (u32x4*)s_act;
+#pragma unroll
+      for (int j = 0; j < APER; j++) {
+        const int p = lane + 64 * j;
+        const int b = wave_block(p / 3);
+        if (p < WNB * 3 && b < nb) dst[b * 3 + p % 3] = av[j];
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1467,6 +1494,8 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
                        hipStream_t st) {
   if (groups == 0 || slots == 0) return hipSuccess;
   if (a.nb < 1 || a.nb > GEMV_MAX_NB) return hipErrorInvalidValue;
+  if (a.x && (epi != EPI_GATE_UP || a.nb > GEMV_X_MAX_NB || ((uintptr_t)a.x & 15)))
+    return hipErrorInvalidValue;
   if (a.logits && (epi != EPI_GATE_UP || a.E > ROUTE_MAX_E || slots > 64 || slots > a.E))
     return hipErrorInvalidValue;
   const bool many = a.logits && a.E > 256;  // selection state for up to 1024 experts

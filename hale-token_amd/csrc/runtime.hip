@@ -836,7 +836,9 @@ static int expert_enqueue(hale_ctx* c, const hale_matrix* gate, const hale_matri
   if (rc) return rc;
   ActBlock* act = (ActBlock*)((char*)s + lead);
   ActBlock* hact = (ActBlock*)((char*)s + lead + align_up(nbh * sizeof(ActBlock), 256));
-  LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nbh, act, c->stream));
+  // the gate/up kernel quantizes an aligned x of up to 128 blocks itself
+  const bool fuse = ((uintptr_t)dx & 15) == 0 && nbh <= (size_t)GEMV_X_MAX_NB;
+  if (!fuse) LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nbh, act, c->stream));
   GemvArgs a{};
   a.codes = gate->codes;
   a.scales = gate->scales;
@@ -844,7 +846,8 @@ static int expert_enqueue(hale_ctx* c, const hale_matrix* gate, const hale_matri
   a.scales2 = up->scales;
   a.nb = (int)nbh;
   a.rows = (int)I;
-  a.act = act;
+  a.act = fuse ? nullptr : act;
+  a.x = fuse ? dx : nullptr;
   a.hact = hact;
   a.hact_stride = (int)nbi;
   a.slots = 1;

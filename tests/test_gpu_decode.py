@@ -166,6 +166,29 @@ def test_expert_forward_device_equals_host(ctx, dtype):
     bo.free()
 
 
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
+@pytest.mark.parametrize("hidden,inter,shift", [(2048, 768, 4), (8192, 96, 0), (4096, 64, 0)])
+def test_expert_forward_device_unfused_activation(ctx, dtype, hidden, inter, shift):
+    """The gate/up kernel quantizes an aligned x of up to 128 blocks itself;
+    a misaligned x (shift bytes) or a wider one (8192: 256 blocks) takes the
+    separate quantization kernel.  Both give the reference's bits."""
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, 1, 1, seed=23 + hidden + shift, with_router=False)
+    ex = H.Expert(H.WeightMatrix.new(ctx, inter, hidden, dtype, L.gate[0]),
+                  H.WeightMatrix.new(ctx, inter, hidden, dtype, L.up[0]),
+                  H.WeightMatrix.new(ctx, hidden, inter, dtype, L.down[0]))
+    x = O.normal(29, hidden)
+    bx, bo = ctx.malloc(hidden * 4 + 16), ctx.malloc(hidden * 4)
+    raw = np.zeros(hidden + 4, np.float32)
+    raw[shift // 4:shift // 4 + hidden] = x
+    bx.upload(raw)
+    ex.forward_device(bx.offset(shift), bo.address)
+    got = bo.download(np.float32, hidden)
+    assert_parity(got, O.expert_forward(dtype, hidden, inter, L.gate[0], L.up[0], L.down[0], x,
+                                        nthreads=8))
+    bx.free()
+    bo.free()
+
+
 # ---------------------------------------------------------------------------
 # MoeLayer
 # ---------------------------------------------------------------------------
