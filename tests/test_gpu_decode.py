@@ -135,8 +135,10 @@ def test_from_f32_quantizes_on_the_gpu(ctx):
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-@pytest.mark.parametrize("hidden,inter", [(2048, 768), (64, 32), (4096, 1536)])
+@pytest.mark.parametrize("hidden,inter", [(2048, 768), (64, 32), (4096, 1536), (1024, 8256)])
 def test_expert_forward_bit_exact(ctx, dtype, hidden, inter):
+    # 1024 x 8256: 258 gate/up tiles, more work-groups than the GPU holds at
+    # once for q4_0 (16 waves): two tiles per work-group
     L = O.OracleMoe.synthetic(dtype, hidden, inter, 1, 1, seed=hidden + inter, with_router=False)
     gate = H.WeightMatrix.new(ctx, inter, hidden, dtype, L.gate[0])
     up = H.WeightMatrix.new(ctx, inter, hidden, dtype, L.up[0])

@@ -112,3 +112,31 @@ def test_graph_of_grouped_forward_replays(ctx, layer):
     g.close()
     for b in (bx, bo):
         b.free()
+
+
+def test_graph_of_two_tile_decode_replays(ctx):
+    """A decode whose gate/up grid is larger than the GPU holds at once (two
+    tiles per work-group) replays bit-exact from a graph, several times, and
+    so does an eager call between the replays."""
+    L = O.OracleMoe.synthetic(O.Q8_0, 256, 2080, 8, 8, normalize_topk=True, seed=31)
+    moe = make_layer(ctx, L)
+    bx, bo = ctx.malloc(256 * 4), ctx.malloc(256 * 4)
+    bx.upload(O.normal(5, 256))
+    moe.forward_device(1, bx.address, bo.address)
+    ctx.synchronize()
+    g = ctx.capture(lambda: moe.forward_device(1, bx.address, bo.address))
+    for rep in range(4):
+        x = O.normal(40 + rep, 256)
+        bx.upload(x)
+        if rep == 2:
+            moe.forward_device(1, bx.address, bo.address)
+        else:
+            g.launch()
+        ctx.synchronize()
+        want, _, _ = L.forward(x, nthreads=8)
+        got = bo.download(np.float32, 256)
+        assert (got.view(np.uint32) == want.view(np.uint32)).all(), rep
+    g.close()
+    moe.close()
+    for b in (bx, bo):
+        b.free()
