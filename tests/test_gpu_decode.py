@@ -169,11 +169,13 @@ def test_expert_forward_device_equals_host(ctx, dtype):
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-@pytest.mark.parametrize("hidden,inter,shift", [(2048, 768, 4), (8192, 96, 0), (4096, 64, 0)])
+@pytest.mark.parametrize("hidden,inter,shift", [(2048, 768, 4), (8192, 96, 0), (4096, 64, 0),
+                                                 (32, 32, 0), (96, 64, 0), (4128, 64, 0)])
 def test_expert_forward_device_unfused_activation(ctx, dtype, hidden, inter, shift):
-    """The gate/up kernel quantizes an aligned x of up to 128 blocks itself;
-    a misaligned x (shift bytes) or a wider one (8192: 256 blocks) takes the
-    separate quantization kernel.  Both give the reference's bits."""
+    """The gate/up kernel quantizes an aligned x of up to 128 blocks itself
+    (here also 1 and 3 blocks); a misaligned x (shift bytes) or a wider one
+    (8192: 256 blocks, 4128: 129) takes the separate quantization kernel.
+    Both give the reference's bits."""
     L = O.OracleMoe.synthetic(dtype, hidden, inter, 1, 1, seed=23 + hidden + shift, with_router=False)
     ex = H.Expert(H.WeightMatrix.new(ctx, inter, hidden, dtype, L.gate[0]),
                   H.WeightMatrix.new(ctx, inter, hidden, dtype, L.up[0]),
@@ -457,6 +459,7 @@ def test_moe_decode_down_whole_chain(ctx, dtype, hidden, inter, E, k):
 
 
 @pytest.mark.parametrize("dtype,hidden,inter,E,k", [
+    (H.Q4_0, 256, 2080, 300, 16),  # 300 experts (the 1024-expert selection) and 65 x 16 > 256 resident
     (H.Q8_0, 256, 2080, 8, 8),     # 65 tiles x 8 slots = 520 > 512 resident (8 waves): 2 per group, odd
     (H.Q4_0, 2080, 1056, 16, 16),  # 33 x 16 = 528 > 512 (8 waves, two chunks per row): odd
     (H.Q4_0, 1024, 8256, 2, 2),    # 258 x 2 = 516 > 256 resident (16 waves, one chunk)
