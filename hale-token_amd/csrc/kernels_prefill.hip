@@ -308,6 +308,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   // accumulators start at +0.0 like the reference's `let mut total = 0.0`,
   // so no sum can become -0.0: the sign of a zero scale product never shows
   v16f accg = {}, accu = {};
+  // 8-row groups of the tile that hold real rows (the others stay at zero:
+  // gate/up then writes h = 0 for them, and down does not store them)
+  const int ngr = __builtin_amdgcn_readfirstlane((tl.rows + 7) >> 3);
 
   // Operands of one block.
   struct Ops {
@@ -349,10 +352,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     __builtin_memcpy(&xa, &o.xr, 16);
     v16i c0 = {};
     if constexpr (DT == Q4_0) c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, minus8, c0, 0, 0, 0);
-    const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wg), c0, 0, 0, 0);
-    v16i iu = {};
-    if constexpr (GATE_UP)
-      iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wu), c0, 0, 0, 0);
     // Scale products d_w[col] * d_x[row] of the whole 32x32 tile on the
     // matrix core, which rounds each product exactly like a VALU multiply
     // (only the sign of a zero product can differ, and that cannot reach an
@@ -377,13 +376,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
       pg = __builtin_amdgcn_mfma_f32_32x32x2f32(use ? o.dx : 0.0f, use ? h2f(o.dg) : 0.0f, v16f{},
                                                 0, 0, 0);
     }
+    // The fold, by 8-row groups: results 4q .. 4q + 3 of a lane are rows
+    // 8q .. 8q + 7 of the tile (both halves of the wave), so a group past the
+    // tile's real rows is skipped as a whole (wave-uniform); its rows'
+    // results are never stored.  Gate's sums are folded before up's product
+    // is formed, so one set of 16 block sums is live at a time.
+    auto fold = [&](v16f& acc, const v16f& p, const v16i& isum) {
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-      if constexpr (FMA) {
-        accg[j] = __builtin_fmaf(pg[j], (float)ig[j], accg[j]);
-      } else {
+      for (int q = 0; q < 4; q++) {
+        if (q < ngr) {
+#pragma unroll
+          for (int j = 4 * q; j < 4 * q + 4; j++) {
+            if constexpr (FMA) {
+              acc[j] = __builtin_fmaf(p[j], (float)isum[j], acc[j]);
+            } else {
+              acc[j] = acc[j] + p[j] * (float)isum[j];
+            }
+          }
+        }
+      }
+    };
+    if constexpr (GATE_UP && DT == Q4_0) {
+      // q4_0 gate/up folds every row: its groups are large (little padding
+      // to skip), and splitting gate from up would cost a second offset
+      // product per block on a kernel that is bound by VALU and MFMA issue
+      const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wg), c0, 0, 0, 0);
+      const v16i iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wu), c0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
         accg[j] = accg[j] + pg[j] * (float)ig[j];
-        if constexpr (GATE_UP) accu[j] = accu[j] + pu[j] * (float)iu[j];
+        accu[j] = accu[j] + pu[j] * (float)iu[j];
+      }
+    } else {
+      fold(accg, pg, __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wg), c0, 0, 0, 0));
+      if constexpr (GATE_UP) {
+        __builtin_amdgcn_sched_barrier(0);
+        fold(accu, pu, __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wu), c0, 0, 0, 0));
       }
     }
   };
@@ -413,8 +441,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   if constexpr (GATE_UP) {
     // h = silu(g) * u, quantized per (row, 32-column block): the 32 columns
     // of a row sit in the 32 lanes of one half.  All 32 rows of the tile are
-    // written; rows past tl.rows repeat the last row's values and only ever
-    // feed result rows that the down kernel does not store.
+    // written; rows past tl.rows (the last row repeated, with h = 0 in q8_0
+    // groups of 8 rows that the fold skipped) only ever feed result rows
+    // that the down kernel does not store.
     ExpTable tab;
     tab.load();
     const int nbo = a.ncols / QK;
