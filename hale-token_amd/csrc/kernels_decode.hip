@@ -1225,8 +1225,12 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   const int rg = down_chain_rows(slots);
   const int sub = wave / slots, sl = wave % slots;
   // every slot's activation blocks (independent of the routes): loads
-  // issued first, stored after the first weight loads
-  constexpr int APT = (DOWN_ACT_MAX * 3 + 255) / 256;  // pieces per thread, at most (256+ threads)
+  // issued first, stored after the first weight loads.  The launcher takes
+  // D = 4 only for rows of at most 32 blocks and q4_0 D = 8 for at most 64,
+  // so those variants hold at most 3 x 8 D blocks; the others up to
+  // DOWN_ACT_MAX.  (Sizing them all for DOWN_ACT_MAX spilled the pieces.)
+  constexpr int MAXB = (D == 4 || (DT == Q4_0 && D == 8)) ? 3 * 8 * D : DOWN_ACT_MAX;
+  constexpr int APT = (MAXB * 3 + 255) / 256;  // pieces per thread, at most (256+ threads)
   const int npieces = slots * nb * 3;
   u32x4 av[APT];
 #pragma unroll
@@ -1295,6 +1299,7 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   {
     const ActBlock* act = s_act + (size_t)sl * nb;
     float acc = 0.0f;  // row r's dot product (valid in lane 8 r)
+#pragma unroll 1
     for (int q0 = 0; q0 < nbg; q0 += D) {
 #pragma unroll
       for (int d0 = 0; d0 < D; d0 += 4) {
@@ -1542,6 +1547,7 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
     if (dtype == Q8_0) return launch(k_down_chain<Q8_0, D>, grid, threads, 0, st, a);       \
     if (dtype == Q4_0) return launch(k_down_chain<Q4_0, D>, grid, threads, 0, st, a);       \
   } while (0)
+    // (k_down_chain sizes its activation staging by these bounds)
     if (nbg <= 4) HALE_DOWN_CHAIN(4);
     if (nbg <= 8 || dtype == Q8_0) HALE_DOWN_CHAIN(8);
     HALE_DOWN_CHAIN(16);
