@@ -347,7 +347,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   const v4i minus8 = {(int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u, (int)0xf8f8f8f8u};
   // `valid` is false for the clamped blocks past the end: their scale
   // products are zero, so they add +0 or -0, which leaves every sum as it is
-  auto compute = [&](const Ops& o, bool valid) {
+  // split (q4_0 gate/up only): gate folded before up's product is formed,
+  // skipping the tile's padded 8-row groups, for tiles that have them
+  auto compute = [&](const Ops& o, bool valid, auto split) {
     v4i xa;
     __builtin_memcpy(&xa, &o.xr, 16);
     v16i c0 = {};
@@ -396,10 +398,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         }
       }
     };
-    if constexpr (GATE_UP && DT == Q4_0) {
-      // q4_0 gate/up folds every row: its groups are large (little padding
-      // to skip), and splitting gate from up would cost a second offset
-      // product per block on a kernel that is bound by VALU and MFMA issue
+    if constexpr (GATE_UP && DT == Q4_0 && !decltype(split)::value) {
+      // q4_0 gate/up of a full tile folds gate and up together: splitting
+      // them costs a second offset product per block, on a kernel that is
+      // bound by VALU and MFMA issue
       const v16i ig = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wg), c0, 0, 0, 0);
       const v16i iu = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wu), c0, 0, 0, 0);
 #pragma unroll
@@ -411,7 +413,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
       fold(accg, pg, __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wg), c0, 0, 0, 0));
       if constexpr (GATE_UP) {
         __builtin_amdgcn_sched_barrier(0);
-        fold(accu, pu, __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wu), c0, 0, 0, 0));
+        // q4_0: the offset product again rather than kept live over the fold
+        v16i c1 = {};
+        if constexpr (DT == Q4_0) c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, minus8, c1, 0, 0, 0);
+        fold(accu, pu, __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, weight_operand(o.wu), c1, 0, 0, 0));
       }
     }
   };
@@ -425,23 +430,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   // some of them next to their use to save registers, and the wave then
   // waits out a whole L2 round trip.
   constexpr int NS = GATE_UP ? 2 : 4;
-  Ops S[NS];
+  auto run = [&](auto split) {
+    Ops S[NS];
 #pragma unroll
-  for (int j = 0; j < NS - 1; j++) load(S[j], min(j, nb - 1));
-  for (int b = 0; b < nb; b += NS) {
+    for (int j = 0; j < NS - 1; j++) load(S[j], min(j, nb - 1));
+    for (int b = 0; b < nb; b += NS) {
 #pragma unroll
-    for (int j = 0; j < NS; j++) {
-      load(S[(j + NS - 1) % NS], min(b + j + NS - 1, nb - 1));
-      __builtin_amdgcn_sched_barrier(0);
-      compute(S[j], b + j < nb);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < NS; j++) {
+        load(S[(j + NS - 1) % NS], min(b + j + NS - 1, nb - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(S[j], b + j < nb, split);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-  }
-
+  };
+  auto epilogue = [&]() {
   if constexpr (GATE_UP) {
     // h = silu(g) * u, quantized per (row, 32-column block): the 32 columns
     // of a row sit in the 32 lanes of one half.  All 32 rows of the tile are
-    // written; rows past tl.rows (the last row repeated, with h = 0 in q8_0
+    // written; rows past tl.rows (the last row repeated, with h = 0 in the
     // groups of 8 rows that the fold skipped) only ever feed result rows
     // that the down kernel does not store.
     ExpTable tab;
@@ -468,6 +475,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
       const int row = (j % 4) + 4 * h + 8 * (j / 4);
       if (row < tl.rows) a.y[(size_t)(tl.row0 + row) * a.ncols + n0 + rn] = accg[j];
     }
+  }
+  };
+  // each path with its own epilogue, so no registers merge between them
+  if (GATE_UP && DT == Q4_0 && ngr < 4) {  // wave-uniform
+    run(std::true_type{});
+    epilogue();
+  } else {
+    run(std::false_type{});
+    epilogue();
   }
 }
 
