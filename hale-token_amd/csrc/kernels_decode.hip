@@ -321,21 +321,15 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
     }
   }
 
-  // activation quantization share: half-wave hw of work-group e takes blocks
-  // e + gx (hw + 8 i), so the blocks spread over all work-groups (one each
-  // while nb <= E) rather than loading the first few
-  for (int bb = e + gx * (tid >> 5); bb < nb; bb += 8 * gx) {
-    float v = xt[bb * QK + (lane & 31)];
-    float scale;
-    int qsum;
-    int q = quant_block_lane(v, &scale, &qsum);
-    ActBlock* ab = act + (size_t)t * nb + bb;
-    ab->q[lane & 31] = (int8_t)q;
-    if ((lane & 31) == 0) {
-      ab->scale = scale;
-      ab->qsum = qsum;
-    }
-  }
+  // activation quantization share, done by waves 1-3 while wave 0 runs the
+  // fold chains: half-wave hw (0..5) of work-group e takes blocks
+  // e + gx (hw + 6 i), so the blocks spread over all work-groups (one each
+  // while nb <= E) rather than loading the first few; the first block's
+  // value loads with the row
+  const int hw = (tid >> 5) - 2;
+  const int bb0 = e + gx * hw;
+  float v0 = 0.0f;
+  if (hw >= 0 && bb0 < nb) v0 = xt[bb0 * QK + (lane & 31)];
 
   // products w[i]*x[i] (each one rounding, order free) into chain-major LDS:
   // chain l holds i = 8s + l at prod[l * stride + s]
@@ -352,7 +346,21 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
     }
   }
   __syncthreads();
-  if (tid >= 64) return;
+  if (tid >= 64) {
+    for (int bb = bb0; bb < nb; bb += 6 * gx) {
+      const float v = bb == bb0 ? v0 : xt[bb * QK + (lane & 31)];
+      float scale;
+      int qsum;
+      const int q = quant_block_lane(v, &scale, &qsum);
+      ActBlock* ab = act + (size_t)t * nb + bb;
+      ab->q[lane & 31] = (int8_t)q;
+      if ((lane & 31) == 0) {
+        ab->scale = scale;
+        ab->qsum = qsum;
+      }
+    }
+    return;
+  }
   // acc[l] += w[8i+l]*x[8i+l] in order of i
   float acc = 0.0f;
   if (lane < 8) acc = lds_sum_in_order_a16(prod + lane * stride, steps, acc);
