@@ -81,12 +81,15 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
   __shared__ int cnt[GROUP_WAVES][GROUP_MAX_E];
   __shared__ int scan_a[GROUP_MAX_E];
   __shared__ int scan_t[GROUP_MAX_E];
+  __shared__ int wsum_a[GROUP_WAVES], wsum_t[GROUP_WAVES];
+  static_assert(GROUP_MAX_E == 64 * GROUP_WAVES, "one thread per expert in the scan");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
   int nbits = 0;
   while ((1 << nbits) < E) nbits++;
-  for (int i = tid; i < GROUP_WAVES * GROUP_MAX_E; i += 64 * GROUP_WAVES) (&cnt[0][0])[i] = 0;
+  for (int q = 0; q < GROUP_WAVES; q++)
+    if (tid < E) cnt[q][tid] = 0;
   __syncthreads();
   const int slice = (A + GROUP_WAVES * 64 - 1) / (GROUP_WAVES * 64) * 64;
   const int a0 = w * slice, a1 = min(A, a0 + slice);
@@ -103,10 +106,9 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
     }
   };
 
-  // pass 1: per-wave counts
-  for (int cb = a0; cb < a1; cb += 64 * GPRE) {
-    int ev[GPRE];
-    load_batch(cb, ev);
+  // pass 1: per-wave counts.  The first batch stays in registers for pass 2
+  // (a wave's whole slice while A <= 16 x 64 x GROUP_WAVES).
+  auto count_batch = [&](int cb, const int* ev) {
 #pragma unroll
     for (int j = 0; j < GPRE; j++) {
       const int a = cb + 64 * j + lane;
@@ -116,35 +118,46 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
       const unsigned long long m = match_mask(e, nbits, valid);
       if (valid && (m >> lane) == 1ull) cnt[w][e] += __popcll(m);  // highest lane of its group
     }
+  };
+  int ev0[GPRE];
+  load_batch(a0, ev0);
+  count_batch(a0, ev0);
+  for (int cb = a0 + 64 * GPRE; cb < a1; cb += 64 * GPRE) {
+    int ev[GPRE];
+    load_batch(cb, ev);
+    count_batch(cb, ev);
   }
   __syncthreads();
 
-  // totals, expert offsets and tile offsets (inclusive scans over experts)
-  for (int e = tid; e < GROUP_MAX_E; e += 64 * GROUP_WAVES) {
+  // totals, expert offsets and tile offsets: inclusive scans over experts,
+  // thread e holding expert e (E <= 1024 = the work-group's threads), a
+  // shuffle scan within each wave, then the totals of the lower waves
+  {
     int tot = 0;
-    if (e < E)
-      for (int q = 0; q < GROUP_WAVES; q++) tot += cnt[q][e];
-    scan_a[e] = tot;
-    scan_t[e] = (tot + TM - 1) / TM;
+    if (tid < E)
+      for (int q = 0; q < GROUP_WAVES; q++) tot += cnt[q][tid];
+    int va = tot, vt = (tot + TM - 1) / TM;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int ua = __shfl_up(va, off), ut = __shfl_up(vt, off);
+      if (lane >= off) {
+        va += ua;
+        vt += ut;
+      }
+    }
+    if (lane == 63) {
+      wsum_a[w] = va;
+      wsum_t[w] = vt;
+    }
+    __syncthreads();
+    for (int q = 0; q < w; q++) {
+      va += wsum_a[q];
+      vt += wsum_t[q];
+    }
+    scan_a[tid] = va;
+    scan_t[tid] = vt;
   }
   __syncthreads();
-  for (int off = 1; off < GROUP_MAX_E; off <<= 1) {
-    int va = 0, vt = 0;
-    for (int e = tid; e < GROUP_MAX_E; e += 64 * GROUP_WAVES) {
-      if (e >= off) {
-        va = scan_a[e - off];
-        vt = scan_t[e - off];
-      }
-    }
-    __syncthreads();
-    for (int e = tid; e < GROUP_MAX_E; e += 64 * GROUP_WAVES) {
-      if (e >= off) {
-        scan_a[e] += va;
-        scan_t[e] += vt;
-      }
-    }
-    __syncthreads();
-  }
   // per-wave bases: offset(e) + counts of lower waves; tile list
   for (int e = tid; e < E; e += 64 * GROUP_WAVES) {
     const int total = cnt[0][e];
@@ -171,9 +184,7 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
   __syncthreads();
 
   // pass 2: stable positions
-  for (int cb = a0; cb < a1; cb += 64 * GPRE) {
-    int ev[GPRE];
-    load_batch(cb, ev);
+  auto scatter_batch = [&](int cb, const int* ev) {
 #pragma unroll
     for (int j = 0; j < GPRE; j++) {
       const int a = cb + 64 * j + lane;
@@ -194,6 +205,12 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+  };
+  scatter_batch(a0, ev0);
+  for (int cb = a0 + 64 * GPRE; cb < a1; cb += 64 * GPRE) {
+    int ev[GPRE];
+    load_batch(cb, ev);
+    scatter_batch(cb, ev);
   }
 }
 
