@@ -436,6 +436,10 @@ def test_moe_decode_down_chunk_boundary(ctx, dtype, hidden, inter):
     (H.Q8_0, 2080, 2080, 6, 1),    # q8_0 ring of 8; 66 groups of 32 over the rows padded to 2112
     (H.Q4_0, 4160, 1056, 6, 2),    # 33 blocks, 5 groups: ring of 8; 260 groups of 16, no permutation
     (H.Q8_0, 4096, 1056, 6, 3),    # 3 slots: 6 waves; 256 groups of 16, permuted
+    (H.Q4_0, 2048, 1024, 8, 3),    # 32 blocks: ring of 4 at its limit, 3 x 32 blocks staged
+    (H.Q8_0, 2048, 1024, 8, 2),    # q8_0 ring of 4 at its limit
+    (H.Q4_0, 2048, 2048, 8, 3),    # 64 blocks: q4_0 ring of 8 at its limit, 3 x 64 blocks staged
+    (H.Q4_0, 4096, 2048, 8, 1),    # the same ring with one slot (4 waves)
     (H.Q4_0, 2048, 10912, 4, 3),   # 3 x 341 = 1023 activation blocks: the LDS limit, ring of 16
     (H.Q4_0, 2048, 11264, 4, 3),   # 3 x 352 = 1056 blocks: over the limit, pipelined kernel
 ])
