@@ -724,7 +724,7 @@ __device__ __forceinline__ int block_isum(const u32x4* c, const ActBlock* ab) {
 // terms of a one-token layer are spread over twice the waves, so they take
 // half as long after the loads land), sixteen for q4_0 gate/up rows that
 // fit one chunk (H <= 2048; with more chunks four loads in flight per lane
-// pipeline worse).
+// pipeline worse) when the layer has at most 256 experts.
 template <int DT, int EPI, int NW, int ME = 256>  // ME: most experts the routed form selects among
 __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   constexpr int CH = Layout<DT>::CH;
@@ -1532,7 +1532,12 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   HALE_GEMV_CASE(Q8_0, EPI_PLAIN, 4)
   HALE_GEMV_CASE(Q8_0, EPI_GATE_UP, 8)
   HALE_GEMV_CASE(Q4_0, EPI_PLAIN, 4)
-  if (a.nb <= 64) HALE_GEMV_CASE(Q4_0, EPI_GATE_UP, 16)
+  // sixteen waves leave 128 VGPRs, too few for the selection state of more
+  // than 256 experts: those layers take the eight-wave form
+  if (dtype == Q4_0 && epi == EPI_GATE_UP && a.nb <= 64 && !many) {
+    const auto gb = grid_of(16);
+    return launch(k_gemv<Q4_0, EPI_GATE_UP, 16>, gb.first, 64 * 16, 0, st, gb.second);
+  }
   HALE_GEMV_CASE(Q4_0, EPI_GATE_UP, 8)
 #undef HALE_GEMV_CASE
   return hipErrorInvalidValue;
