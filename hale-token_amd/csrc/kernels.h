@@ -87,6 +87,12 @@ struct GemvArgs {
   // EPI_GATE_UP of one token: the f32 activation (16-byte aligned, nb <=
   // GEMV_X_MAX_NB), quantized by the kernel itself in place of act
   const float* x;
+  // EPI_GATE_UP with routing over several tokens (tokens > 1; 0 or 1: one):
+  // grid row y is slot y % slots of token y / slots, whose activation is act
+  // + token * act_tstride, logits logits + token * E, routes route_out_* +
+  // token * slots and h blocks hact + y * hact_stride
+  int tokens;
+  int act_tstride;
 };
 constexpr int GEMV_X_MAX_NB = 128;
 
@@ -104,6 +110,9 @@ struct DownArgs {
   const float* route_w;    // [slots]
   int slots;
   float* out;              // [rows]
+  // tokens > 1: token t's routes at route_idx / route_w + t * slots, its h
+  // blocks at hact + t * slots * hact_stride, its output at out + t * rows
+  int tokens;
 };
 
 hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st);

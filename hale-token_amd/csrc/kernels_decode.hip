@@ -740,7 +740,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemv(GemvArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x;
-  const int slot = blockIdx.y;
+  // grid row y: slot y % slots of token y / slots (one token: slot y)
+  const int tok = a.tokens > 1 ? (int)blockIdx.y / a.slots : 0;
+  const int slot = (int)blockIdx.y - tok * a.slots;
+  if (tok > 0) {
+    a.act += (size_t)tok * a.act_tstride;
+    a.logits += (size_t)tok * a.E;
+    a.route_out_idx += (size_t)tok * a.slots;
+    a.route_out_w += (size_t)tok * a.slots;
+    a.hact += (size_t)tok * a.slots * a.hact_stride;
+  }
   const int nb = a.nb;
 
   // Wave w takes blocks w UPW .. w UPW + UPW - 1 of every chunk of CB
@@ -1010,6 +1019,12 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
   const int g = blockIdx.x;
   const int nb = a.nb;
   const int slots = a.slots;
+  if (blockIdx.y > 0) {  // token blockIdx.y of a few-token decode
+    a.route_idx += (size_t)blockIdx.y * slots;
+    a.route_w += (size_t)blockIdx.y * slots;
+    a.hact += (size_t)blockIdx.y * slots * a.hact_stride;
+    a.out += (size_t)blockIdx.y * a.rows;
+  }
   const int nbg = (nb + 7) / 8;
   const int npairs = slots * nbg;
   const int nchunks = (npairs + CP - 1) / CP;
@@ -1229,6 +1244,12 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x;
   const int nb = a.nb, slots = a.slots;  // slots <= 3: one chain per wave
+  if (blockIdx.y > 0) {  // token blockIdx.y of a few-token decode
+    a.route_idx += (size_t)blockIdx.y * slots;
+    a.route_w += (size_t)blockIdx.y * slots;
+    a.hact += (size_t)blockIdx.y * slots * a.hact_stride;
+    a.out += (size_t)blockIdx.y * a.rows;
+  }
   const int nbg = (nb + 7) / 8;
   const int rg = down_chain_rows(slots);
   const int sub = wave / slots, sl = wave % slots;
@@ -1511,6 +1532,9 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
     return hipErrorInvalidValue;
   if (a.logits && (epi != EPI_GATE_UP || a.E > ROUTE_MAX_E || slots > 64 || slots > a.E))
     return hipErrorInvalidValue;
+  const int T = a.tokens > 1 ? a.tokens : 1;
+  if (T > 1 && (!a.logits || a.x || a.slots != slots || (long)slots * T > 65535))
+    return hipErrorInvalidValue;
   const bool many = a.logits && a.E > 256;  // selection state for up to 1024 experts
   // Gate/up: one work-group per (32-row tile, slot), or per two tiles when
   // the grid would not be resident at once (at 128 VGPRs and 1024 threads
@@ -1520,8 +1544,8 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   auto grid_of = [&](int nw) {
     GemvArgs b = a;
     b.tiles = groups;
-    b.ipw = epi == EPI_GATE_UP && (long)groups * slots > 256L * (16 / nw) ? 2 : 1;
-    return std::make_pair(dim3((groups + b.ipw - 1) / b.ipw + (a.logits ? 1 : 0), slots), b);
+    b.ipw = epi == EPI_GATE_UP && (long)groups * slots * T > 256L * (16 / nw) ? 2 : 1;
+    return std::make_pair(dim3((groups + b.ipw - 1) / b.ipw + (a.logits ? 1 : 0), slots * T), b);
   };
 #define HALE_GEMV_CASE(D, E, W)                                                             \
   if (dtype == D && epi == E) {                                                             \
@@ -1544,15 +1568,16 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
 }
 
 hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
-  const unsigned groups = (unsigned)(padded_rows((size_t)a.rows) / DR);
-  if (groups == 0) return hipSuccess;
-  if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS) return hipErrorInvalidValue;
+  const unsigned T = a.tokens > 1 ? (unsigned)a.tokens : 1u;
+  const dim3 groups((unsigned)(padded_rows((size_t)a.rows) / DR), T);
+  if (groups.x == 0) return hipSuccess;
+  if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS || T > 65535) return hipErrorInvalidValue;
   // A wave per (slot, 8 rows) pays off when few routes leave many rows per
   // work-group (top-1..3); top-4 and wider use the block-group pipeline.
   if (a.slots <= 3 && a.nb <= DOWN_CHAIN_MAX_NB && a.slots * a.nb <= DOWN_ACT_MAX &&
       down_chain_waves(a.slots) * a.nb <= DOWN_SCL_MAX) {
     const int rg = down_chain_rows(a.slots);
-    const unsigned grid = (unsigned)(padded_rows((size_t)a.rows) / rg);
+    const dim3 grid((unsigned)(padded_rows((size_t)a.rows) / rg), T);
     const unsigned threads = 64 * down_chain_waves(a.slots);
     const int nbg = (a.nb + 7) / 8;
 #define HALE_DOWN_CHAIN(D)                                                                  \

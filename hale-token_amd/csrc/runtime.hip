@@ -95,7 +95,7 @@ struct hale_moe {
   // per-token scratch (TokScratch, carved from one buffer) for cap_tok tokens
   void* tok_base = nullptr;
   size_t cap_tok = 0;
-  ActBlock* hact = nullptr;  // [k][I/32], the decode path's requantized h
+  ActBlock* hact = nullptr;  // [decode tokens][k][I/32], the decode path's requantized h
   // grouped prefill workspace
   PrefillWorkspace pw;
   // load from an expert pack: pending until the layer's next use waits for
@@ -1005,7 +1005,10 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   ALLOC(m->up_s, E * m->gs_elems * 2);
   ALLOC(m->down_s, E * m->ds_elems * 2);
   ALLOC(m->stats, E * 8);
-  ALLOC(m->hact, std::max<size_t>(m->k, 1) * (I / HALE_QK) * sizeof(ActBlock));
+  // h blocks of every token the decode path takes at once (fewer than
+  // prefill_min_tokens)
+  ALLOC(m->hact, (prefill_min_tokens(m->k) - 1) * std::max<size_t>(m->k, 1) * (I / HALE_QK) *
+                     sizeof(ActBlock));
   if (router) ALLOC(m->router, E * H * 4);
 #undef ALLOC
   if (e == hipSuccess) e = launch_fill((float*)m->stats, 2 * E, 0.0f, c->stream);  // zero counts
@@ -1152,9 +1155,10 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
   else
     LAUNCH(c, K_ROUTE, launch_route_logits(m->router, dx, (int)m->H, (int)m->E, (int)ntok, s.act,
                                            s.logits, c->stream));
+  // every token's gate/up in one launch (grid row = token x k + slot), then
+  // every token's down projection and combine in one
   const float* lg = dlogits ? dlogits : s.logits;
-  for (size_t t = 0; t < ntok; t++) {
-    float* out_t = dout + t * m->H;
+  {
     GemvArgs a{};
     a.codes = m->gate_c;
     a.scales = m->gate_s;
@@ -1164,14 +1168,16 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     a.scales_stride = m->gs_elems;
     a.nb = (int)nbh;
     a.rows = (int)m->I;
-    a.act = s.act + t * nbh;
+    a.act = s.act;
     a.act_stride = 0;
+    a.act_tstride = (int)nbh;
+    a.tokens = (int)ntok;
     a.route_idx = nullptr;  // the prologue selects the experts from the logits
-    a.logits = lg + t * m->E;
+    a.logits = lg;
     a.E = (int)m->E;
     a.normalize = m->normalize;
-    a.route_out_idx = s.route_idx + t * k;
-    a.route_out_w = s.route_w + t * k;
+    a.route_out_idx = s.route_idx;
+    a.route_out_w = s.route_w;
     a.stats = m->stats;
     a.hact = m->hact;
     a.hact_stride = (int)nbi;
@@ -1186,10 +1192,11 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     d.rows = (int)m->H;
     d.hact = m->hact;
     d.hact_stride = (int)nbi;
-    d.route_idx = s.route_idx + t * k;
-    d.route_w = s.route_w + t * k;
+    d.route_idx = s.route_idx;
+    d.route_w = s.route_w;
     d.slots = k;
-    d.out = out_t;
+    d.out = dout;
+    d.tokens = (int)ntok;
     LAUNCH(c, K_DOWN, launch_down_combine(m->dtype, d, c->stream));
   }
   return HALE_OK;

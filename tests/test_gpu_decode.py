@@ -299,6 +299,44 @@ def test_moe_logits_given_zipf_routing(ctx, dtype, T):
     assert_parity(out, o_out)
 
 
+def _few_tokens_check(L, moe, xs):
+    """The decode path over T < 8 tokens at once (one gate/up and one down
+    launch for all of them) against the oracle's token-at-a-time forward,
+    and against the same layer called one token at a time."""
+    out, idx, w = moe.forward(xs, return_routes=True)
+    o_out, o_idx, o_w = L.prefill(xs, nthreads=8)
+    assert (np.asarray(idx) == np.asarray(o_idx)).all()
+    assert same_bits(w, o_w)
+    assert_parity(out, o_out)
+    for t in range(xs.shape[0]):
+        assert same_bits(moe.forward(xs[t]), out[t])
+
+
+@pytest.mark.parametrize("dtype,hidden,inter,E,k,T", [
+    (H.Q8_0, 2048, 768, 32, 8, 3),     # q8_0 gate/up at 8 waves: 24 x 24 tile-slots, one tile per work-group
+    (H.Q8_0, 2048, 768, 32, 8, 5),     # 24 x 40 = 960 > 512: two tiles per work-group
+    (H.Q4_0, 2080, 2080, 6, 2, 5),     # top-2: whole-chain down per token, 65 blocks
+    (H.Q8_0, 1024, 1024, 8, 3, 4),     # top-3 whole chain, q8_0
+    (H.Q4_0, 1024, 256, 8, 1, 6),      # top-1 (32-row chain groups)
+    (H.Q4_0, 256, 64, 300, 16, 3),     # more than 256 experts: eight-wave selection, 16 slots
+    (H.Q4_0, 4160, 64, 16, 4, 2),      # pipelined down at H 4160 (no XCD permutation)
+])
+def test_moe_decode_few_tokens(ctx, dtype, hidden, inter, E, k, T):
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=True,
+                              seed=hidden + inter + E + k + T)
+    moe = make_layer(ctx, L)
+    _few_tokens_check(L, moe, O.normal(9100 + T, T * hidden).reshape(T, hidden))
+    moe.close()
+
+
+@pytest.mark.parametrize("T", [2, 7])
+def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
+    """Config 1's layer over 2 and 7 tokens: 16-wave gate/up with two tiles
+    per work-group (24 tiles x 8 slots x T > 256)."""
+    L, moe = qwen30b_q4
+    _few_tokens_check(L, moe, O.normal(9200 + T, T * 2048).reshape(T, 2048))
+
+
 def test_moe_top_k_clamped_and_unnormalised(ctx):
     L = O.OracleMoe.synthetic(O.Q4_0, 64, 32, 4, 6, normalize_topk=False, seed=3)
     moe = make_layer(ctx, L)
