@@ -539,7 +539,7 @@ def gpu_decode(args):
     nx = 64
     xs = ctx.malloc(nx * HID * 4)
     xs.fill_normal(99, nx * HID, 0.0, 1.0)
-    out = ctx.malloc(HID * 4)
+    out = ctx.malloc(8 * HID * 4)
     L = len(layers)
 
     def step(s):
@@ -569,10 +569,30 @@ def gpu_decode(args):
     prof = ctx.profile_read()
     ctx.profile(False)
     graph.close()
+
+    # a few tokens per step (the decode path up to 7 tokens: one gate/up and
+    # one down launch for all of them), same layers, graph-replayed
+    few = []
+    if not args.no_prefill:
+        for T in (2, 4, 7):
+            def step_t(s, T=T):
+                layers[s % L].forward_device(T, xs.offset((s % (nx - 8)) * HID * 4), out.address)
+            for s in range(L):
+                step_t(s)
+            ctx.synchronize()
+            g = ctx.capture(lambda: [step_t(s) for s in range(L)])
+            g.launch()
+            ctx.synchronize()
+            t = time_replays(ctx, g, 20)
+            g.close()
+            us = 1000 * float(np.median(t)) / L
+            few.append({"tokens": T, "us_per_step": round(us, 2), "us_per_token": round(us / T, 2),
+                        "tokens_per_s": round(1e6 * T / us, 1), "timing": replay_stats(t, L)})
+            log(f"decode {T} tokens per step: {us:.2f} us/step ({us / T:.2f} us/token)")
     for m in layers:
         m.close()
     ctx.close()
-    return steps, ms, prof, warm, replay_stats(times, L)
+    return steps, ms, prof, warm, replay_stats(times, L), few
 
 
 def cpu_model():
@@ -663,7 +683,7 @@ def main():
         return
 
     bytes_step = TOPK * expert_bytes(DTYPE, HID, INTER) + E * HID * 4
-    steps, ms, prof, warm, rstats = gpu_decode(args)
+    steps, ms, prof, warm, rstats, few = gpu_decode(args)
     sec = ms / 1000.0
     gbs = bytes_step * steps / sec / 1e9
 
@@ -753,6 +773,7 @@ def main():
         "timing": rstats,
         "kernels": kernels,
         "expert": expert,
+        "decode_few_tokens": few,
         "decode_more": more,
         "float_matvec": fmv,
         "attention": attn,

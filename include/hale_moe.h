@@ -239,8 +239,9 @@ int hale_moe_route(hale_moe *moe, const float *x, uint32_t *index,
 
 /* Ref: MoeLayer::forward (src/model/moe.rs:56-70) for ntok tokens.  ntok
  * == 1 is decode; ntok > 1 is the reference's token-at-a-time prefill
- * (src/model/transformer.rs:231-239) computed as one expert-grouped batch:
- * token t's output equals MoeLayer::forward(x_t).  x and out are
+ * (src/model/transformer.rs:231-239), computed as one decode pass over all
+ * tokens below the grouped threshold (8) and as one expert-grouped batch
+ * from it: token t's output equals MoeLayer::forward(x_t) either way.  x and out are
  * [ntok][H].  logits: NULL to run the router matvec, else [ntok][E] router
  * outputs used as given.  index/weight: NULL or [ntok][top_k].  The
  * _device form takes device buffers, enqueued on the context's stream:
