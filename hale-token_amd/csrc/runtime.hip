@@ -92,10 +92,13 @@ struct hale_moe {
   size_t gc_bytes = 0, gs_elems = 0, dc_bytes = 0, ds_elems = 0;
   std::vector<char> present;
   unsigned long long* stats = nullptr;  // [E] routing counts
-  // per-token scratch (TokScratch, carved from one buffer) for cap_tok tokens
+  // per-token scratch (TokScratch, carved from one buffer) for cap_tok tokens,
+  // laid out for grouped_min == cap_gmin
   void* tok_base = nullptr;
-  size_t cap_tok = 0;
-  ActBlock* hact = nullptr;  // [decode tokens][k][I/32], the decode path's requantized h
+  size_t cap_tok = 0, cap_gmin = 0;
+  // forwards of at least grouped_min tokens take the expert-grouped path,
+  // fewer the decode path (one pass over all of them)
+  size_t grouped_min = 0;
   // grouped prefill workspace
   PrefillWorkspace pw;
   // load from an expert pack: pending until the layer's next use waits for
@@ -902,14 +905,24 @@ struct TokScratch {
   float* logits;   // [ntok][E]
   int* route_idx;  // [ntok][k]
   float* route_w;  // [ntok][k]
+  ActBlock* hact;  // [decode tokens][k][I/32], the decode path's requantized h
 };
 
+// h blocks are kept for the tokens a decode pass can take: min(ntok,
+// grouped_min - 1), so scratch laid out for more tokens holds at least as many
+static size_t hact_tokens(const hale_moe* m, size_t ntok) {
+  return std::min(ntok, m->grouped_min - 1);
+}
+
 static size_t tok_scratch_bytes(const hale_moe* m, size_t ntok) {
+  const size_t k = std::max<size_t>(m->k, 1);
   return align_up(ntok * (m->H / HALE_QK) * sizeof(ActBlock), 256) + align_up(ntok * m->E * 4, 256) +
-         2 * align_up(ntok * std::max<size_t>(m->k, 1) * 4, 256);
+         2 * align_up(ntok * k * 4, 256) +
+         align_up(hact_tokens(m, ntok) * k * (m->I / HALE_QK) * sizeof(ActBlock), 256);
 }
 
 static TokScratch tok_scratch_carve(const hale_moe* m, void* base, size_t ntok) {
+  const size_t k = std::max<size_t>(m->k, 1);
   char* p = (char*)base;
   TokScratch s;
   s.act = (ActBlock*)p;
@@ -917,15 +930,18 @@ static TokScratch tok_scratch_carve(const hale_moe* m, void* base, size_t ntok) 
   s.logits = (float*)p;
   p += align_up(ntok * m->E * 4, 256);
   s.route_idx = (int*)p;
-  p += align_up(ntok * std::max<size_t>(m->k, 1) * 4, 256);
+  p += align_up(ntok * k * 4, 256);
   s.route_w = (float*)p;
+  p += align_up(ntok * k * 4, 256);
+  s.hact = (ActBlock*)p;
   return s;
 }
 
-// The layer's per-token scratch for at least ntok tokens.
+// The layer's per-token scratch for at least ntok tokens (laid out anew
+// after the grouped threshold changed).
 static int moe_reserve(hale_moe* m, size_t ntok, TokScratch* out) {
   hale_ctx* c = m->ctx;
-  if (m->cap_tok < ntok) {
+  if (m->cap_tok < ntok || m->cap_gmin != m->grouped_min) {
     const size_t bytes = tok_scratch_bytes(m, ntok);
     int rc = growth_allowed(c, "MoE layer scratch", bytes);
     if (rc) return rc;
@@ -938,7 +954,8 @@ static int moe_reserve(hale_moe* m, size_t ntok, TokScratch* out) {
       m->tok_base = nullptr;
       return fail(c, HALE_ENOMEM, "MoE scratch for %zu tokens: %s", ntok, hipGetErrorString(e));
     }
-    m->cap_tok = ntok;
+    m->cap_tok = std::max(ntok, m->cap_tok);
+    m->cap_gmin = m->grouped_min;
   }
   *out = tok_scratch_carve(m, m->tok_base, m->cap_tok);
   return HALE_OK;
@@ -961,6 +978,21 @@ static int moe_prefill_ws(hale_moe* m, const PrefillLayer& L, size_t T, void** o
   }
   *out = m->pw.base;
   return HALE_OK;
+}
+
+// Fewest tokens per forward that take the expert-grouped path.  The
+// grouped path costs about 60 us (Qwen3-30B shape) to 190 us (Mixtral) more
+// than the decode path before its first token, and then adds little per
+// token; the decode path adds each token's k experts' bytes.  Measured
+// crossovers (graph replay, one MI355X): Qwen3-30B q4_0 and q8_0 and
+// Qwen3-235B q4_0 (top-8 of 128) between 12 and 16 tokens, Mixtral (top-2 of
+// 8) between 6 and 8.
+static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_t k) {
+  (void)dtype;
+  (void)E;
+  (void)H;
+  (void)I;
+  return k >= 4 ? 16 : 8;
 }
 
 extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, size_t I, int dtype,
@@ -986,6 +1018,7 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   m->H = H;
   m->I = I;
   m->k = std::min(top_k, E);  // top_k clamps k to the number of scores
+  m->grouped_min = default_grouped_min(dtype, E, H, I, m->k);
   m->dtype = dtype;
   m->normalize = normalize;
   m->gc_bytes = code_plane_bytes(dtype, I, H);
@@ -1005,10 +1038,6 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   ALLOC(m->up_s, E * m->gs_elems * 2);
   ALLOC(m->down_s, E * m->ds_elems * 2);
   ALLOC(m->stats, E * 8);
-  // h blocks of every token the decode path takes at once (fewer than
-  // prefill_min_tokens)
-  ALLOC(m->hact, (prefill_min_tokens(m->k) - 1) * std::max<size_t>(m->k, 1) * (I / HALE_QK) *
-                     sizeof(ActBlock));
   if (router) ALLOC(m->router, E * H * 4);
 #undef ALLOC
   if (e == hipSuccess) e = launch_fill((float*)m->stats, 2 * E, 0.0f, c->stream);  // zero counts
@@ -1040,7 +1069,6 @@ extern "C" void hale_moe_destroy(hale_moe* m) {
   (void)hipFree(m->up_s);
   (void)hipFree(m->down_s);
   (void)hipFree(m->stats);
-  (void)hipFree(m->hact);
   (void)hipFree(m->router);
   for (hale_matrix* v : m->views) delete v;
   if (m->source) {
@@ -1179,7 +1207,7 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     a.route_out_idx = s.route_idx;
     a.route_out_w = s.route_w;
     a.stats = m->stats;
-    a.hact = m->hact;
+    a.hact = s.hact;
     a.hact_stride = (int)nbi;
     a.slots = k;
     LAUNCH(c, K_GATE_UP, launch_gemv(m->dtype, EPI_GATE_UP, a, (int)nbi, k, c->stream));
@@ -1190,7 +1218,7 @@ static int moe_decode_enqueue(hale_moe* m, size_t ntok, const float* dx, const f
     d.scales_stride = m->ds_elems;
     d.nb = (int)nbi;
     d.rows = (int)m->H;
-    d.hact = m->hact;
+    d.hact = s.hact;
     d.hact_stride = (int)nbi;
     d.route_idx = s.route_idx;
     d.route_w = s.route_w;
@@ -1247,7 +1275,7 @@ static int moe_forward_check(hale_moe* m, const float* dx, const float* logits) 
 }
 
 // Enqueues MoeLayer::forward over ntok tokens with the given per-token
-// scratch and (ntok >= prefill_min_tokens) grouped workspace.  top_k = 0
+// scratch and (ntok >= grouped_min) grouped workspace.  top_k = 0
 // routes nowhere: the reference's forward leaves out at zero.
 static int moe_forward_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
                                float* dout, const TokScratch& s, void* pws) {
@@ -1256,7 +1284,7 @@ static int moe_forward_enqueue(hale_moe* m, size_t ntok, const float* dx, const 
     LAUNCH(c, K_FILL, launch_fill(dout, ntok * m->H, 0.0f, c->stream));
     return HALE_OK;
   }
-  if (ntok >= prefill_min_tokens(m->k)) {
+  if (ntok >= m->grouped_min) {
     PrefillLayer L = prefill_layer(m, s);
     hipError_t e = prefill_enqueue(L, pws, ntok, dx, dlogits, dout, c->stream, ctx_hook(c));
     if (e != hipSuccess) return fail(c, HALE_EHIP, "grouped prefill: %s", hipGetErrorString(e));
@@ -1270,7 +1298,7 @@ static int moe_forward_scratch(hale_moe* m, size_t ntok, TokScratch* s, void** p
   int rc = moe_reserve(m, ntok, s);
   if (rc) return rc;
   *pws = nullptr;
-  if (m->k > 0 && ntok >= prefill_min_tokens(m->k)) {
+  if (m->k > 0 && ntok >= m->grouped_min) {
     PrefillLayer L = prefill_layer(m, *s);
     rc = moe_prefill_ws(m, L, ntok, pws);
   }
@@ -1323,7 +1351,7 @@ extern "C" int hale_moe_forward_device_noalloc(hale_moe* m, size_t ntok, const f
   char* base = (char*)c->fixed_scratch;
   const size_t tb = align_up(tok_scratch_bytes(m, ntok), 256);
   const TokScratch s = tok_scratch_carve(m, base, ntok);
-  const bool grouped = m->k > 0 && ntok >= prefill_min_tokens(m->k);
+  const bool grouped = m->k > 0 && ntok >= m->grouped_min;
   const size_t need = tb + (grouped ? prefill_workspace_bytes(prefill_layer(m, s), ntok) : 0);
   if (need > (size_t)HALE_NOALLOC_SCRATCH_BYTES)
     return fail(c, HALE_EINVAL,
@@ -1395,6 +1423,23 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
   HIPCHK(c, hipMemcpyAsync(index, s.route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipMemcpyAsync(weight, s.route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_set_grouped_min_tokens(hale_moe* m, size_t n) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m) return fail(c, HALE_EINVAL, "set_grouped_min_tokens: NULL layer");
+  if (n < 2 || n > HALE_DECODE_MAX_TOKENS + 1)
+    return fail(c, HALE_EINVAL, "set_grouped_min_tokens: %zu is outside 2..%d", n,
+                HALE_DECODE_MAX_TOKENS + 1);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  m->grouped_min = n;  // the next forward lays the scratch out for it
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_grouped_min_tokens(const hale_moe* m, size_t* n) {
+  if (!m || !n) return fail(m ? m->ctx : nullptr, HALE_EINVAL, "grouped_min_tokens: NULL argument");
+  *n = m->grouped_min;
   return HALE_OK;
 }
 

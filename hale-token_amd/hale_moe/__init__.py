@@ -89,6 +89,8 @@ SIGNATURES = {
     "hale_moe_expert_present": (C.c_int, [_vp, C.c_uint32, _vp]),
     "hale_moe_set_source": (C.c_int, [_vp, _vp]),
     "hale_moe_set_down_fold": (C.c_int, [_vp, C.c_int]),
+    "hale_moe_set_grouped_min_tokens": (C.c_int, [_vp, _sz]),
+    "hale_moe_grouped_min_tokens": (C.c_int, [_vp, C.POINTER(_sz)]),
     "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
     "hale_pack_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "hale_pack_close": (None, [_vp]),
@@ -921,6 +923,17 @@ class MoeLayer:
         if f is None:
             raise ValueError(f"unknown fold {fold!r} (exact or fma)")
         self.ctx.check(lib().hale_moe_set_down_fold(self.handle, f), "set_down_fold")
+
+    def set_grouped_min_tokens(self, n: int):
+        """Fewest tokens per forward that take the expert-grouped path;
+        fewer run the decode kernels in one pass (both exact)."""
+        self.ctx.check(lib().hale_moe_set_grouped_min_tokens(self.handle, n), "set_grouped_min_tokens")
+
+    @property
+    def grouped_min_tokens(self) -> int:
+        n = _sz()
+        self.ctx.check(lib().hale_moe_grouped_min_tokens(self.handle, C.byref(n)), "grouped_min_tokens")
+        return n.value
 
     def set_source(self, pack: "PackExpertSource | None"):
         """Makes the pack this layer's ExpertSource without loading anything:

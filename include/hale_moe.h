@@ -240,8 +240,9 @@ int hale_moe_route(hale_moe *moe, const float *x, uint32_t *index,
 /* Ref: MoeLayer::forward (src/model/moe.rs:56-70) for ntok tokens.  ntok
  * == 1 is decode; ntok > 1 is the reference's token-at-a-time prefill
  * (src/model/transformer.rs:231-239), computed as one decode pass over all
- * tokens below the grouped threshold (8) and as one expert-grouped batch
- * from it: token t's output equals MoeLayer::forward(x_t) either way.  x and out are
+ * tokens below the grouped threshold (hale_moe_set_grouped_min_tokens) and
+ * as one expert-grouped batch from it: token t's output equals
+ * MoeLayer::forward(x_t) either way.  x and out are
  * [ntok][H].  logits: NULL to run the router matvec, else [ntok][E] router
  * outputs used as given.  index/weight: NULL or [ntok][top_k].  The
  * _device form takes device buffers, enqueued on the context's stream:
@@ -253,6 +254,15 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
                             const float *d_logits, float *d_out,
                             uint32_t *d_index, float *d_weight);
 
+/* Fewest tokens per hale_moe_forward* call that take the expert-grouped
+ * path (default 8); fewer tokens run the decode kernels in one pass over
+ * all of them.  Both give the reference's bits; the choice is speed only.
+ * n in 2..HALE_DECODE_MAX_TOKENS + 1.  No counterpart in the reference (its
+ * prefill runs token by token); for callers tuning small batches. */
+#define HALE_DECODE_MAX_TOKENS 256
+int hale_moe_set_grouped_min_tokens(hale_moe *moe, size_t n);
+int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
+
 /* Folds of the expert-grouped down projection (hale_moe_forward with
  * ntok >= the grouped threshold).  HALE_FOLD_EXACT, the default, adds each
  * block term (d_w*d_x)*isum to its row sum as the reference does, product
@@ -261,7 +271,8 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
  * then agrees with the reference to a relative L2 error far below 1e-5,
  * not bit for bit.  No counterpart in the reference; for callers that
  * accept that tolerance in exchange for a faster prefill.  The gate/up
- * projection and the decode path (1..7 tokens) stay exact in both. */
+ * projection and the decode path (below the grouped threshold) stay exact
+ * in both. */
 #define HALE_FOLD_EXACT 0
 #define HALE_FOLD_FMA 1
 int hale_moe_set_down_fold(hale_moe *moe, int fold);

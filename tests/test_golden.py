@@ -113,6 +113,12 @@ def test_gpu_matches_fixture(ctx, g, m, dname, dt):
     assert same_bits(w, want_w)
     assert rel_l2(out, want_out) <= REL_L2
     assert same_bits(out, want_out)
+    # all 12 rows in one decode pass (threshold above 12)
+    moe.set_grouped_min_tokens(13)
+    out, idx, w = moe.forward(x, return_routes=True)
+    assert (np.asarray(idx) == want_idx).all()
+    assert same_bits(w, want_w)
+    assert same_bits(out, want_out)
     # one row at a time: the decode path
     for t in range(x.shape[0]):
         o, i, ww = moe.forward(x[t], return_routes=True)

@@ -247,8 +247,8 @@ def test_moe_multi_token_equals_per_token(ctx, qwen30b_q4):
 
 
 def test_routing_stats_count_decode_selections(ctx):
-    """The decode path (1-7 tokens per call) counts each token's k experts
-    in the gate/up prologue."""
+    """The decode path (below the grouped threshold: 8 tokens for this top-3
+    layer) counts each token's k experts in the gate/up prologue."""
     L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 8, 3, seed=5)
     moe = make_layer(ctx, L, layer_id=3)
     xs = O.normal(6, 10 * 64).reshape(10, 64)
@@ -281,13 +281,18 @@ def test_missing_expert_is_reported(ctx):
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-@pytest.mark.parametrize("T", [7, 8])
-def test_moe_logits_given_zipf_routing(ctx, dtype, T):
-    """Router logits supplied directly (the skewed-routing workloads): 7
-    tokens take the decode path, 8 the grouped path."""
+@pytest.mark.parametrize("T,gmin", [(7, None), (15, None), (16, None), (8, 8)])
+def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin):
+    """Router logits supplied directly (the skewed-routing workloads).  This
+    top-4 layer's grouped threshold is 16 tokens: 7 and 15 take the decode
+    path, 16 the grouped path, and 8 the grouped path once the threshold is
+    set to 8."""
     E, Hd, I, k = 32, 256, 64, 4
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
     moe = make_layer(ctx, L)
+    assert moe.grouped_min_tokens == 16
+    if gmin:
+        moe.set_grouped_min_tokens(gmin)
     rng = np.random.default_rng(1)
     p = np.arange(1, E + 1, dtype=np.float64) ** -1.1
     logits = (np.log(p / p.sum())[rng.permutation(E)] + rng.gumbel(size=(T, E))).astype(np.float32)
@@ -300,9 +305,10 @@ def test_moe_logits_given_zipf_routing(ctx, dtype, T):
 
 
 def _few_tokens_check(L, moe, xs):
-    """The decode path over T < 8 tokens at once (one gate/up and one down
-    launch for all of them) against the oracle's token-at-a-time forward,
-    and against the same layer called one token at a time."""
+    """The decode path over T tokens at once, below the layer's grouped
+    threshold (one gate/up and one down launch for all of them), against the
+    oracle's token-at-a-time forward and against the same layer called one
+    token at a time."""
     out, idx, w = moe.forward(xs, return_routes=True)
     o_out, o_idx, o_w = L.prefill(xs, nthreads=8)
     assert (np.asarray(idx) == np.asarray(o_idx)).all()
@@ -329,12 +335,34 @@ def test_moe_decode_few_tokens(ctx, dtype, hidden, inter, E, k, T):
     moe.close()
 
 
-@pytest.mark.parametrize("T", [2, 7])
+@pytest.mark.parametrize("T", [2, 7, 15])
 def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
-    """Config 1's layer over 2 and 7 tokens: 16-wave gate/up with two tiles
-    per work-group (24 tiles x 8 slots x T > 256)."""
+    """Config 1's layer over 2, 7 and 15 tokens (its grouped threshold is
+    16): 16-wave gate/up with two tiles per work-group (24 tiles x 8 slots x
+    T > 256)."""
     L, moe = qwen30b_q4
+    assert moe.grouped_min_tokens == 16
     _few_tokens_check(L, moe, O.normal(9200 + T, T * 2048).reshape(T, 2048))
+
+
+def test_grouped_threshold_moves_the_path_not_the_bits(ctx):
+    """The grouped threshold only chooses the kernels: the same 12 tokens
+    through the decode path (threshold 13), the grouped path (threshold 2
+    and 12) and one token at a time give the same bits.  Out-of-range
+    thresholds are refused."""
+    L = O.OracleMoe.synthetic(O.Q4_0, 512, 128, 16, 4, normalize_topk=True, seed=41)
+    moe = make_layer(ctx, L)
+    xs = O.normal(42, 12 * 512).reshape(12, 512)
+    o_out, _, _ = L.prefill(xs, nthreads=8)
+    for gmin in (13, 2, 12, 257):
+        moe.set_grouped_min_tokens(gmin)
+        assert moe.grouped_min_tokens == gmin
+        assert_parity(moe.forward(xs), o_out)
+        assert same_bits(moe.forward(xs[:3]), o_out[:3])
+    for bad in (0, 1, 258):
+        with pytest.raises(ValueError):
+            moe.set_grouped_min_tokens(bad)
+    moe.close()
 
 
 def test_moe_top_k_clamped_and_unnormalised(ctx):
