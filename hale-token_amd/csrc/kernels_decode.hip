@@ -669,7 +669,9 @@ __global__ __launch_bounds__(64) void k_route_select(const float* __restrict__ l
 //   EPI_GATE_UP  rows 0-31 gate, 32-63 up of one I-tile; h = silu(g)*u is
 //                quantized to its q8 block for the down projection
 //                (Expert::forward, src/expert/mod.rs:95-102).  With router
-//                logits given, the prologue selects the slot's expert.
+//                logits given, the prologue selects the slot's expert; grid
+//                row y is slot y % k of token y / k when several tokens are
+//                decoded in one launch.
 
 template <int DT>
 __device__ __forceinline__ float block_term(const u32x4* c, uint16_t sc, const ActBlock* ab) {
@@ -1536,7 +1538,7 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   if (T > 1 && (!a.logits || a.x || a.slots != slots || (long)slots * T > 65535))
     return hipErrorInvalidValue;
   const bool many = a.logits && a.E > 256;  // selection state for up to 1024 experts
-  // Gate/up: one work-group per (32-row tile, slot), or per two tiles when
+  // Gate/up: one work-group per (32-row tile, token and slot), or per two tiles when
   // the grid would not be resident at once (at 128 VGPRs and 1024 threads
   // per CU: 256 work-groups of 16 waves, 512 of 8), so that no second round
   // runs on a partly filled GPU.  With routing, one more column of
