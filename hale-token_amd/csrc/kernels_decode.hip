@@ -375,6 +375,95 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
   }
 }
 
+// The router logits of many tokens (T >= ROUTE_TILED_MIN_T): work-group
+// (eg, tg) computes experts 16 eg .. 16 eg + 15 for tokens 8 tg .. 8 tg + 7,
+// 1024 threads.  Lane 8t + l of wave e carries chain l of logit (e, t):
+// acc = acc + w_e[8s + l] * x_t[8s + l] in order of s, each product rounded
+// before it is added (dot_f32's 8-lane order, quant.rs:152-194).  The 24
+// rows (16 router rows, 8 tokens) stream through LDS chain-major in chunks
+// of RT_K steps, two buffers, so chunk c + 1 loads while chunk c is added,
+// and every staged row serves 8 or 16 logits.  The eight chains of a logit
+// are reduced in the one-token kernel's fixed order, so each logit has its
+// bits.  The activation blocks are quantized by k_act_quant.
+constexpr int RT_E = 16, RT_T = 8, RT_K = 64;
+constexpr int RT_STRIDE = RT_K + 4;                 // floats per chain row (16-byte aligned)
+constexpr int RT_BUF = (RT_E + RT_T) * 8 * RT_STRIDE;  // floats per buffer
+constexpr int ROUTE_TILED_MIN_T = 64;
+
+__global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __restrict__ router,
+                                                             const float* __restrict__ x, int H,
+                                                             int E, int T,
+                                                             float* __restrict__ logits) {
+  __shared__ __attribute__((aligned(16))) float buf[2][RT_BUF];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int e0 = blockIdx.x * RT_E, t0 = blockIdx.y * RT_T;
+  const int steps = H / 8;
+  const int nchunk = (steps + RT_K - 1) / RT_K;
+  // Chunk c of row r: elements [8 RT_K c, 8 RT_K (c + 1)), 2 RT_K float4;
+  // thread q moves float4 pieces q, q + 1024, q + 2048 of the 24 rows.  Rows
+  // past E or T repeat the last one and pieces past H the last piece
+  // (in-bounds loads; their chains are not written).
+  constexpr int PPR = 2 * RT_K;                       // float4 pieces per row and chunk
+  constexpr int PPT = (RT_E + RT_T) * PPR / 1024;     // pieces per thread
+  static_assert((RT_E + RT_T) * PPR % 1024 == 0, "whole pieces per thread");
+  auto load_chunk = [&](f32x4* v, int c) {
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+      const int idx = tid + 1024 * j, row = idx / PPR, piece = idx % PPR;
+      const float* src = row < RT_E ? router + (size_t)min(e0 + row, E - 1) * H
+                                    : x + (size_t)min(t0 + row - RT_E, T - 1) * H;
+      const int elem = min(c * 8 * RT_K + 4 * piece, H - 4);
+      v[j] = *(const f32x4*)(src + elem);
+    }
+  };
+  auto store_chunk = [&](const f32x4* v, float* b) {
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+      const int idx = tid + 1024 * j, row = idx / PPR, piece = idx % PPR;
+      float* r = b + (row * 8 + (piece & 1) * 4) * RT_STRIDE + (piece >> 1);
+      r[0] = v[j].x;
+      r[RT_STRIDE] = v[j].y;
+      r[2 * RT_STRIDE] = v[j].z;
+      r[3 * RT_STRIDE] = v[j].w;
+    }
+  };
+  const int t = lane >> 3, l = lane & 7;
+  const int wrow = (wave * 8 + l) * RT_STRIDE, xrow = ((RT_E + t) * 8 + l) * RT_STRIDE;
+  f32x4 v[PPT];
+  load_chunk(v, 0);
+  store_chunk(v, buf[0]);
+  __syncthreads();
+  float acc = 0.0f;
+  for (int c = 0; c < nchunk; c++) {
+    if (c + 1 < nchunk) load_chunk(v, c + 1);  // in flight while chunk c is added
+    const float* b = buf[c & 1];
+    const int kc = min(RT_K, steps - c * RT_K);  // a multiple of 4 (H % 32 == 0)
+    for (int s4 = 0; s4 < kc; s4 += 4) {
+      const f32x4 wv = *(const f32x4*)(b + wrow + s4);
+      const f32x4 xv = *(const f32x4*)(b + xrow + s4);
+      acc = acc + wv.x * xv.x;
+      acc = acc + wv.y * xv.y;
+      acc = acc + wv.z * xv.z;
+      acc = acc + wv.w * xv.w;
+    }
+    if (c + 1 < nchunk) store_chunk(v, buf[(c + 1) & 1]);
+    __syncthreads();  // chunk c + 1 staged; every wave is done with chunk c
+  }
+  const int base = lane & ~7;
+  const float a0 = __shfl(acc, base + 0), a1 = __shfl(acc, base + 1), a2 = __shfl(acc, base + 2),
+              a3 = __shfl(acc, base + 3);
+  const float a4 = __shfl(acc, base + 4), a5 = __shfl(acc, base + 5), a6 = __shfl(acc, base + 6),
+              a7 = __shfl(acc, base + 7);
+  const int e = e0 + wave, tok = t0 + t;
+  if (l == 0 && e < E && tok < T) {
+    const float tail = -0.0f;  // Iterator::sum over the H % 8 leftover products: none (H % 32 == 0)
+    const float s0v = (a0 + a4) + (a1 + a5);
+    const float s1v = (a2 + a6) + (a3 + a7);
+    logits[(size_t)tok * E + e] = (s0v + s1v) + tail;
+  }
+}
+
 // softmax_in_place (src/ops/activation.rs:11-21), top_k (src/ops/topk.rs:
 // 44-61) and the renormalisation of MoeLayer::route, run by one whole wave
 // (all 64 lanes active).  Element i lives in lane i % 64, slot i / 64.
@@ -1515,6 +1604,14 @@ hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipSt
 hipError_t launch_route_logits(const float* router, const float* x, int H, int E, int T,
                                ActBlock* act, float* logits, hipStream_t st) {
   if (H > ROUTE_MAX_H || E > ROUTE_MAX_E || H % QK || E < 1 || T < 1) return hipErrorInvalidValue;
+  if (T >= ROUTE_TILED_MIN_T) {
+    // many tokens: 16 experts x 8 tokens per work-group, then the activation
+    // blocks by the quantization kernel
+    const dim3 grid((E + RT_E - 1) / RT_E, (T + RT_T - 1) / RT_T);
+    hipError_t e = launch(k_route_logits_tiled, grid, 1024, 0, st, router, x, H, E, T, logits);
+    if (e != hipSuccess) return e;
+    return launch_act_quant(x, (size_t)T * (H / QK), act, st);
+  }
   dim3 grid(E, T);
   return launch(k_route_logits, grid, ROUTE_THREADS, 0, st, router, x, H, E, act, logits);
 }

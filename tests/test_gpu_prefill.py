@@ -64,6 +64,23 @@ def test_grouped_small(ctx, dtype, with_router):
     check(moe, L, xs, logits)
 
 
+@pytest.mark.parametrize("dtype,Hd,I,E,k,T", [
+    (H.Q4_0, 2048, 64, 128, 8, 64),    # 64+ tokens: the router's 16-expert x 8-token tiles
+    (H.Q8_0, 2080, 64, 20, 4, 100),    # a partial expert tile, a partial token tile, a partial chunk (260 steps)
+    (H.Q4_0, 4096, 64, 128, 8, 72),    # 512 steps: eight chunks
+])
+def test_grouped_router_many_tokens(ctx, dtype, Hd, I, E, k, T):
+    """The router over many tokens (tiles of router rows and tokens in LDS,
+    products formed in the chains): routes, weights (the softmax over every
+    logit) and outputs have the reference's bits for every token."""
+    L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=Hd + E + T,
+                              with_router=True)
+    moe = make_layer(ctx, L)
+    xs = O.normal(T + Hd, T * Hd).reshape(T, Hd)
+    check(moe, L, xs)
+    moe.close()
+
+
 def test_grouped_empty_and_crowded_experts(ctx):
     """Every token on the same experts (one group of T rows, many tiles) and
     most experts idle."""
