@@ -121,8 +121,10 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
     from hale_moe.synth import zipf_logits
 
     ctx = H.Context(0)
+    # the layer has a router too: the workload's logits are given (Zipf), and
+    # one more timing runs the same forward through the router instead
     moe = build_layers(ctx, 1, seed=4321, dtype=dtype, hid=hid, inter=inter, experts=experts,
-                       topk=topk, router=False)[0]
+                       topk=topk, router=True)[0]
     logits = zipf_logits(tokens, experts, 1.1, seed=7)
     dl = ctx.malloc(logits.nbytes)
     dl.upload(logits)
@@ -142,6 +144,19 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
     for _ in range(reps):
         moe.forward_device(tokens, dx.address, dout.address, dl.address)
     prof = ctx.profile_read()
+    ctx.profile(False)
+    # the same forward with the layer's router computing the logits
+    moe.forward_device(tokens, dx.address, dout.address)
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        moe.forward_device(tokens, dx.address, dout.address)
+    router_ms = ctx.timer_stop() / reps
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(reps):
+        moe.forward_device(tokens, dx.address, dout.address)
+    rprof = ctx.profile_read()
     ctx.profile(False)
     # the opt-in FMA fold of the grouped down projection: its time, and its
     # relative L2 distance from the exact output on the same input
@@ -183,6 +198,9 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
                           "pct_int8_mfma_peak": round(100 * ops / (fma_ms / 1000.0) / INT8_PEAK_OPS, 2),
                           "grouped_down_avg_us": round(1000 * fma_prof["grouped_down"][0] / fma_prof["grouped_down"][1], 2),
                           "rel_l2_vs_exact": float(f"{fma_rel:.3e}")},
+        "with_router": {"ms": round(router_ms, 4), "tokens_per_s": round(tokens / (router_ms / 1000.0), 1),
+                        "route_avg_us": round(1000 * rprof["route"][0] / rprof["route"][1], 2),
+                        "note": "the same forward, logits from the layer's f32 router (routes differ from the Zipf workload's)"},
     }
     # roofline of the dominant grouped kernel: algorithmic weight bytes (every
     # touched expert's planes once) against HBM, or int8 ops against the MFMA
@@ -731,7 +749,7 @@ def main():
             f = prefill[-1]["fma_down_fold"]
             log(f"prefill {name}: {prefill[-1]['ms']} ms, {prefill[-1]['tokens_per_s']} tok/s, "
                 f"{prefill[-1]['pct_int8_mfma_peak']}% int8 MFMA; FMA down fold {f['ms']} ms "
-                f"(rel-L2 {f['rel_l2_vs_exact']:.1e})")
+                f"(rel-L2 {f['rel_l2_vs_exact']:.1e}); with the router {prefill[-1]['with_router']['ms']} ms")
 
     cpu = None
     if not args.no_cpu:
