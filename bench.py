@@ -119,8 +119,9 @@ def build_layers(ctx, nlayers, seed=1234, dtype=DTYPE, hid=HID, inter=INTER, exp
 PREFILL_WARMUP = 30  # untimed forwards before each prefill timing
 
 
-def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfma"):
-    """One MoE layer forward over `tokens` tokens with Zipf-skewed routing."""
+def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfma", router=True):
+    """One MoE layer forward over `tokens` tokens with Zipf-skewed routing
+    (and, with `router`, the same forward through the layer's router)."""
     from hale_moe.synth import zipf_logits
 
     ctx = H.Context(0)
@@ -152,19 +153,21 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
     prof = ctx.profile_read()
     ctx.profile(False)
     # the same forward with the layer's router computing the logits
-    for _ in range(PREFILL_WARMUP // 3):
-        moe.forward_device(tokens, dx.address, dout.address)
-    ctx.synchronize()
-    ctx.timer_start()
-    for _ in range(reps):
-        moe.forward_device(tokens, dx.address, dout.address)
-    router_ms = ctx.timer_stop() / reps
-    ctx.profile(True)
-    ctx.profile_reset()
-    for _ in range(reps):
-        moe.forward_device(tokens, dx.address, dout.address)
-    rprof = ctx.profile_read()
-    ctx.profile(False)
+    router_ms, rprof = None, None
+    if router:
+        for _ in range(PREFILL_WARMUP // 3):
+            moe.forward_device(tokens, dx.address, dout.address)
+        ctx.synchronize()
+        ctx.timer_start()
+        for _ in range(reps):
+            moe.forward_device(tokens, dx.address, dout.address)
+        router_ms = ctx.timer_stop() / reps
+        ctx.profile(True)
+        ctx.profile_reset()
+        for _ in range(reps):
+            moe.forward_device(tokens, dx.address, dout.address)
+        rprof = ctx.profile_read()
+        ctx.profile(False)
     # the opt-in FMA fold of the grouped down projection: its time, and its
     # relative L2 distance from the exact output on the same input
     moe.forward_device(tokens, dx.address, dout.address, dl.address)
@@ -207,9 +210,10 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
                           "pct_int8_mfma_peak": round(100 * ops / (fma_ms / 1000.0) / INT8_PEAK_OPS, 2),
                           "grouped_down_avg_us": round(1000 * fma_prof["grouped_down"][0] / fma_prof["grouped_down"][1], 2),
                           "rel_l2_vs_exact": float(f"{fma_rel:.3e}")},
-        "with_router": {"ms": round(router_ms, 4), "tokens_per_s": round(tokens / (router_ms / 1000.0), 1),
-                        "route_avg_us": round(1000 * rprof["route"][0] / rprof["route"][1], 2),
-                        "note": "the same forward, logits from the layer's f32 router (routes differ from the Zipf workload's)"},
+        "with_router": None if router_ms is None else {
+            "ms": round(router_ms, 4), "tokens_per_s": round(tokens / (router_ms / 1000.0), 1),
+            "route_avg_us": round(1000 * rprof["route"][0] / rprof["route"][1], 2),
+            "note": "the same forward, logits from the layer's f32 router (routes differ from the Zipf workload's)"},
     }
     # roofline of the dominant grouped kernel: algorithmic weight bytes (every
     # touched expert's planes once) against HBM, or int8 ops against the MFMA
@@ -704,7 +708,7 @@ def main():
         print(json.dumps({"decode_eager_steps": decode_eager(args)}), flush=True)
         return
     if args.prefill_only:
-        res = [gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=3, bound=bound)
+        res = [gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=3, bound=bound, router=False)
                for (name, dt, hid, inter, ex, k, tok, bound) in PREFILL]
         print(json.dumps({"prefill": res}), flush=True)
         return
