@@ -1426,6 +1426,17 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
   return HALE_OK;
 }
 
+extern "C" int hale_moe_reserve(hale_moe* m, size_t max_tokens) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m) return fail(c, HALE_EINVAL, "moe_reserve: NULL layer");
+  if (max_tokens == 0) return HALE_OK;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  TokScratch s;
+  void* pws;
+  return moe_forward_scratch(m, max_tokens, &s, &pws);  // the largest call's scratch
+}
+
 extern "C" int hale_moe_set_grouped_min_tokens(hale_moe* m, size_t n) {
   hale_ctx* c = m ? m->ctx : nullptr;
   if (!m) return fail(c, HALE_EINVAL, "set_grouped_min_tokens: NULL layer");

@@ -90,6 +90,7 @@ SIGNATURES = {
     "hale_moe_set_source": (C.c_int, [_vp, _vp]),
     "hale_moe_set_down_fold": (C.c_int, [_vp, C.c_int]),
     "hale_moe_set_grouped_min_tokens": (C.c_int, [_vp, _sz]),
+    "hale_moe_reserve": (C.c_int, [_vp, _sz]),
     "hale_moe_grouped_min_tokens": (C.c_int, [_vp, C.POINTER(_sz)]),
     "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
     "hale_pack_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
@@ -923,6 +924,11 @@ class MoeLayer:
         if f is None:
             raise ValueError(f"unknown fold {fold!r} (exact or fma)")
         self.ctx.check(lib().hale_moe_set_down_fold(self.handle, f), "set_down_fold")
+
+    def reserve(self, max_tokens: int):
+        """Sizes the layer's scratch (and grouped workspace) for forwards of
+        up to max_tokens tokens now, outside any graph capture."""
+        self.ctx.check(lib().hale_moe_reserve(self.handle, max_tokens), "moe_reserve")
 
     def set_grouped_min_tokens(self, n: int):
         """Fewest tokens per forward that take the expert-grouped path;

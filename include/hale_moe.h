@@ -254,6 +254,15 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
                             const float *d_logits, float *d_out,
                             uint32_t *d_index, float *d_weight);
 
+/* Sizes the layer's per-token scratch and, from the grouped threshold on,
+ * its grouped workspace for calls of up to max_tokens tokens, as the first
+ * such call would.  No counterpart in the reference; for callers that
+ * capture graphs (growth is refused during a capture) or want no
+ * allocation, and none of the slower forwards that follow one, in a
+ * serving loop.  Refused (HALE_EINVAL) while the context's stream is being
+ * captured. */
+int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
+
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
  * path (default 8); fewer tokens run the decode kernels in one pass over
  * all of them.  Both give the reference's bits; the choice is speed only.
@@ -499,7 +508,8 @@ const char *hale_kernel_name(int kind);
  *   - Scratch (the context's, a layer's per-token scratch and grouped
  *     workspace) only grows outside a capture.  A call that would have to
  *     grow it while the stream is being captured fails with HALE_EINVAL and
- *     records nothing; make the same call once before the capture.
+ *     records nothing; make the same call once before the capture, or size
+ *     a layer with hale_moe_reserve.
  *   - A graph keeps the addresses it was captured with.  Scratch that a
  *     later call outgrows while any graph of the context exists is kept,
  *     not freed, until the last of those graphs is destroyed, so an older

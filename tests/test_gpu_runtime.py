@@ -56,6 +56,32 @@ def test_capture_refuses_scratch_growth(ctx, layer):
         b.free()
 
 
+@pytest.mark.parametrize("T", [3, 20])
+def test_reserve_sizes_scratch_for_capture(ctx, layer, T):
+    """hale_moe_reserve sizes the layer's scratch (and from the grouped
+    threshold on, 16 tokens for this top-4 layer, its grouped workspace) so
+    that the first forward can be captured; replays are bit-exact.  A
+    reserve that would have to grow scratch during a capture is refused."""
+    L, moe = layer
+    moe.reserve(T)
+    bx, bo = ctx.malloc(T * HID * 4), ctx.malloc(T * HID * 4)
+    xs = O.normal(40 + T, T * HID).reshape(T, HID)
+    bx.upload(xs)
+    g = ctx.capture(lambda: moe.forward_device(T, bx.address, bo.address))
+    want, _, _ = L.prefill(xs)
+    for rep in range(2):
+        g.launch()
+        ctx.synchronize()
+        got = bo.download(np.float32, T * HID).reshape(T, HID)
+        assert (got.view(np.uint32) == want.view(np.uint32)).all(), rep
+    g.close()
+    with pytest.raises(ValueError, match="captured"):
+        ctx.capture(lambda: moe.reserve(64))
+    moe.reserve(64)  # outside a capture it grows
+    for b in (bx, bo):
+        b.free()
+
+
 @pytest.mark.parametrize("big", [5, 24])
 def test_graph_replays_after_scratch_grows(ctx, layer, big):
     """Capture a one-token forward, then grow the layer's scratch with an
