@@ -136,9 +136,9 @@ def gpu_prefill(name, dtype, hid, inter, experts, topk, tokens, reps, bound="mfm
     dx.fill_normal(17, tokens * hid, 0.0, 1.0)
     dout = ctx.malloc(tokens * hid * 4)
     didx = ctx.malloc(tokens * topk * 4)
-    # untimed forwards first: after the layer's workspace is allocated the
-    # first forwards run up to about 10 % slower (2048 tokens q4_0: 1.49 ms
-    # in the first five, 1.33-1.36 ms from about the twenty-fifth on)
+    # untimed forwards first: a GPU that has not been busy runs the first
+    # forwards up to about 10 % slower (2048 tokens q4_0: 1.49 ms in the
+    # first five, 1.32-1.36 ms from about the twenty-fifth on)
     for _ in range(PREFILL_WARMUP):
         moe.forward_device(tokens, dx.address, dout.address, dl.address, didx.address)
     ctx.synchronize()

@@ -258,9 +258,8 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
  * its grouped workspace for calls of up to max_tokens tokens, as the first
  * such call would.  No counterpart in the reference; for callers that
  * capture graphs (growth is refused during a capture) or want no
- * allocation, and none of the slower forwards that follow one, in a
- * serving loop.  Refused (HALE_EINVAL) while the context's stream is being
- * captured. */
+ * allocation inside a serving loop.  Refused (HALE_EINVAL) while the
+ * context's stream is being captured. */
 int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
