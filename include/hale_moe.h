@@ -265,8 +265,11 @@ int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
  * path (default 8); fewer tokens run the decode kernels in one pass over
  * all of them.  Both give the reference's bits; the choice is speed only.
- * n in 2..HALE_DECODE_MAX_TOKENS + 1.  No counterpart in the reference (its
- * prefill runs token by token); for callers tuning small batches. */
+ * n in 2..HALE_DECODE_MAX_TOKENS + 1.  A new threshold re-lays the layer's
+ * per-token scratch on its next call, which must then come outside a graph
+ * capture (or call hale_moe_reserve first).  No counterpart in the
+ * reference (its prefill runs token by token); for callers tuning small
+ * batches. */
 #define HALE_DECODE_MAX_TOKENS 256
 int hale_moe_set_grouped_min_tokens(hale_moe *moe, size_t n);
 int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
