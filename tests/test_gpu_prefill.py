@@ -4,7 +4,8 @@ the oracle's token-at-a-time prefill (src/model/transformer.rs:231-239).
 
 Bar: bit-exact outputs, routes and weights (rel-L2 <= 1e-5 asserted too).
 Tokens are independent, so at the largest shape (2048 tokens) a sample of
-tokens is checked against the oracle while the GPU computes all of them; the
+tokens is checked against the oracle and every token against the decode path
+(one token per call), while the GPU computes all of them; the
 512-token workload is checked token by token in full.
 """
 import numpy as np
@@ -123,7 +124,9 @@ def test_grouped_qwen30b_prefill_512_q8(ctx):
 
 def test_grouped_qwen235b_prefill_2048_q4_sampled(ctx):
     """128 q4_0 experts (H 4096, I 1536), top-8, 2048 tokens, Zipf routing;
-    a sample of tokens is checked against the oracle."""
+    a sample of tokens is checked against the oracle, and every token
+    against the decode path (one token per call, a separate set of kernels
+    that the decode tests check against the oracle at this shape)."""
     E, Hd, I, k, T = 128, 4096, 1536, 8, 2048
     L = O.OracleMoe.synthetic(O.Q4_0, Hd, I, E, k, normalize_topk=True, seed=44, with_router=False)
     moe = make_layer(ctx, L)
@@ -131,7 +134,11 @@ def test_grouped_qwen235b_prefill_2048_q4_sampled(ctx):
     logits = zipf_logits(T, E, 1.1, seed=4)
     rng = np.random.default_rng(1)
     sample = sorted(set(rng.choice(T, 24, replace=False).tolist()) | {0, T - 1})
-    check(moe, L, xs, logits, sample=sample)
+    out, idx = check(moe, L, xs, logits, sample=sample)
+    for t in range(T):
+        o, i, _ = moe.forward(xs[t], logits=logits[t], return_routes=True)
+        assert list(i) == list(idx[t]), t
+        assert same_bits(o, out[t]), t
 
 
 def test_grouped_equals_decode_path(ctx):
