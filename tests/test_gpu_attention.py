@@ -4,7 +4,7 @@ the C ABI.
 Bar: bit-exact.  RMSNorm sums the squares in order (src/ops/norm.rs:25-28);
 attention keeps the reference's in-order score sums, softmax_in_place and
 the position-ordered context (src/model/attention.rs:31-86), so every
-output of every position equals the oracle's bits.  The north-star
+output of every position equals the oracle's bits.  The accumulation-order
 tolerance (rel-L2 <= 1e-5) is asserted as well.
 """
 import numpy as np

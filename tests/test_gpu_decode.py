@@ -3,7 +3,7 @@
 Bar: bit-exact.  Quantization codes and scales, per-block i32 sums and the
 f32 outputs of matvec, Expert::forward and MoeLayer::forward all equal the
 oracle's bits (the kernels keep the reference's left-to-right block order).
-The north-star tolerance for f32 outputs, rel-L2 <= 1e-5, is asserted as
+The accumulation-order tolerance for f32 outputs, rel-L2 <= 1e-5, is asserted as
 well, so a failure reports both.
 """
 import numpy as np

@@ -5,7 +5,7 @@ Bar: bit-exact.  The reference's float dot (src/tensor/quant.rs:146-233)
 sums eight lane accumulators, reduces them in a fixed tree and adds the
 tail of cols % 8 products; every output here equals the oracle's bits,
 including rows whose byte length is not a multiple of 16 (the kernel then
-reads value by value) and rows shorter than one octet.  The north-star
+reads value by value) and rows shorter than one octet.  The accumulation-order
 tolerance (rel-L2 <= 1e-5) is asserted as well.
 """
 import numpy as np
