@@ -136,6 +136,10 @@ hipError_t launch_route_logits(const float* router, const float* x, int H, int E
 hipError_t launch_route_select(const float* logits, int E, int k, int normalize, int T,
                                int* route_idx, float* route_w, unsigned long long* stats,
                                hipStream_t st);
+// launch_route_select (no stats) and launch_act_quant in one launch
+hipError_t launch_route_select_quant(const float* logits, int E, int k, int normalize, int T,
+                                    int* route_idx, float* route_w, const float* x,
+                                    size_t nblocks, ActBlock* act, hipStream_t st);
 hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int slots,
                        hipStream_t st);
 hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,

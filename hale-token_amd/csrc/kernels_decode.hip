@@ -718,14 +718,13 @@ __device__ __forceinline__ int select_slot(const float* lg, int E, int slot, boo
 
 // Standalone routing (MoeLayer::route without the experts, and the grouped
 // path): one wave per token.
-__global__ __launch_bounds__(64) void k_route_select(const float* __restrict__ logits, int E, int k,
-                                                     int normalize, int* __restrict__ route_idx,
-                                                     float* __restrict__ route_w,
-                                                     unsigned long long* __restrict__ stats) {
+__device__ __forceinline__ void route_select_token(const float* __restrict__ logits, int E, int k,
+                                                   int normalize, int t, int* __restrict__ route_idx,
+                                                   float* __restrict__ route_w,
+                                                   unsigned long long* __restrict__ stats) {
   __shared__ int sel_idx[64];
   __shared__ float sel_w[64];
   __shared__ __attribute__((aligned(16))) float rs[RS_SCRATCH];
-  const int t = blockIdx.x;
   ExpTable tab;
   tab.load();
   route_select(logits + (size_t)t * E, E, k, normalize, sel_idx, sel_w, tab, rs);
@@ -736,6 +735,34 @@ __global__ __launch_bounds__(64) void k_route_select(const float* __restrict__ l
     route_w[(size_t)t * k + lane] = sel_w[lane];
     if (stats) atomicAdd(&stats[sel_idx[lane]], 1ull);
   }
+}
+
+__global__ __launch_bounds__(64) void k_route_select(const float* __restrict__ logits, int E, int k,
+                                                     int normalize, int* __restrict__ route_idx,
+                                                     float* __restrict__ route_w,
+                                                     unsigned long long* __restrict__ stats) {
+  route_select_token(logits, E, k, normalize, blockIdx.x, route_idx, route_w, stats);
+}
+
+// The routes of T tokens from given logits and the quantization of their
+// activations in one launch (the two are independent): work-groups 0..T-1
+// select token t's routes as k_route_select does, the others quantize 8
+// activation blocks each as k_act_quant does (x 16-byte aligned).
+__global__ __launch_bounds__(64) void k_route_select_quant(const float* __restrict__ logits, int E,
+                                                           int k, int normalize, int T,
+                                                           int* __restrict__ route_idx,
+                                                           float* __restrict__ route_w,
+                                                           const float* __restrict__ x,
+                                                           size_t nblocks,
+                                                           ActBlock* __restrict__ act) {
+  const int g = blockIdx.x;
+  if (g >= T) {  // work-group-uniform
+    const size_t blk = (size_t)(g - T) * 8 + (threadIdx.x >> 3);
+    const int j = threadIdx.x & 7;
+    if (blk < nblocks) quant_block8(*(const f32x4*)(x + blk * QK + 4 * j), j, act + blk);
+    return;
+  }
+  route_select_token(logits, E, k, normalize, g, route_idx, route_w, nullptr);
 }
 
 // ===========================================================================
@@ -1599,6 +1626,21 @@ hipError_t launch_act_quant(const float* x, size_t nblocks, ActBlock* act, hipSt
   if ((uintptr_t)x % 16)
     return launch(k_act_quant_any, blocks_for(nblocks * 32, 256), 256, 0, st, x, nblocks, act);
   return launch(k_act_quant, blocks_for(nblocks * 8, 256), 256, 0, st, x, nblocks, act);
+}
+
+hipError_t launch_route_select_quant(const float* logits, int E, int k, int normalize, int T,
+                                    int* route_idx, float* route_w, const float* x,
+                                    size_t nblocks, ActBlock* act, hipStream_t st) {
+  if (T < 1 || E < 1 || E > ROUTE_MAX_E || k < 1 || k > E || k > 64) return hipErrorInvalidValue;
+  if ((uintptr_t)x % 16) {  // the quantization share needs 16-byte loads
+    hipError_t e = launch_act_quant(x, nblocks, act, st);
+    if (e != hipSuccess) return e;
+    return launch_route_select(logits, E, k, normalize, T, route_idx, route_w, nullptr, st);
+  }
+  const size_t groups = (size_t)T + (nblocks + 7) / 8;
+  if (groups > 0x7fffffffu) return hipErrorInvalidValue;
+  return launch(k_route_select_quant, (unsigned)groups, 64, 0, st, logits, E, k, normalize, T,
+                route_idx, route_w, x, nblocks, act);
 }
 
 hipError_t launch_route_logits(const float* router, const float* x, int H, int E, int T,

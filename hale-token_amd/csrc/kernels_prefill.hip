@@ -627,15 +627,16 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
     if (e != hipSuccess) return e;  \
   } while (0)
 
-  // 1. route every token and quantize its activations
+  // 1. route every token and quantize its activations (given logits: one
+  // launch for both)
   if (logits) {
-    HALE_STEP(K_ACT_QUANT, launch_act_quant(x, T * nbh, L.act, st));
+    HALE_STEP(K_ROUTE, launch_route_select_quant(logits, L.E, L.k, L.normalize, (int)T,
+                                                 L.route_idx, L.route_w, x, T * nbh, L.act, st));
   } else {
     HALE_STEP(K_ROUTE, launch_route_logits(L.router, x, L.H, L.E, (int)T, L.act, L.logits, st));
-    logits = L.logits;
+    HALE_STEP(K_ROUTE, launch_route_select(L.logits, L.E, L.k, L.normalize, (int)T, L.route_idx,
+                                           L.route_w, nullptr, st));
   }
-  HALE_STEP(K_ROUTE, launch_route_select(logits, L.E, L.k, L.normalize, (int)T, L.route_idx,
-                                         L.route_w, nullptr, st));
   // 2. group assignments by expert
   HALE_STEP(K_GROUP, launch(k_group, 1, 64 * GROUP_WAVES, 0, st, L.route_idx, (int)A, L.E, perm,
                             pos_of, tiles, ntiles, L.stats));
