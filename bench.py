@@ -6,12 +6,13 @@ top-8 renormalised, weighted combine.  One step is one token through one
 MoE layer.  48 such layers (the model's depth, 16.3 GB) stay resident in HBM
 and consecutive steps visit consecutive layers with fresh inputs, so every
 step reads weights that are not in the 256 MB last-level cache.  The steps
-are replayed from a captured HIP graph of one pass over the 48 layers: at
-least 20 replays and at least --steps steps, each replay timed on its own
-(HIP events on the library's stream); `value` and `ms_per_step` come from the
-median replay, `timing` gives the median, min and max per step.  `warmup` is
-the number of eager steps run before the capture (at least one per layer,
-which also sizes each layer's scratch).
+run --warmup eager steps first (each layer's scratch is sized beforehand by
+MoeLayer.reserve, which runs nothing), then exactly --steps steps in one
+region timed with HIP events on the library's stream: replays of a captured
+graph of one pass over the 48 layers, then a graph of the remaining steps
+(graphs are uploaded when captured).  `value` and `ms_per_step` come from
+that region; `timing` gives the median, min and max per step over 20 more
+passes timed one at a time, after it.
 
 value: algorithmic bytes per step (8 routed experts x 2,654,208 B + the
 1,048,576 B router) x steps / time, in GB/s.  roofline: the dominant
@@ -30,6 +31,12 @@ float_matvec: WeightMatrix::matvec over float weights (a bf16 vocabulary
 projection and a dense f32 matrix), GB/s of weight bytes.
 attention: RMSNorm + Attention::forward of one token with 4096 cached
 positions (Qwen3-30B-A3B shape, bf16 projections), per-kernel times.
+reference_kernel_bench: the reference's `hale bench kernels` (a 4096 x 4096
+WeightMatrix::matvec per dtype: f32, bf16, f16, q8_0, q4_0) on the GPU, cold
+(rotated copies) and warm (one matrix, as the reference loops), with the
+oracle at the same shape on the host in cpu_baseline.
+strict_dropin: the decode workload through the unchanged provider surface
+(route, fetch, k x Expert::forward, host combine), microseconds per token.
 prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
 2048 tokens q4_0 H 4096 I 1536; 128 experts, top-8, Zipf-skewed routing)
 with tokens/s, TOPS, the fraction of the int8 MFMA peak and a roofline
@@ -474,6 +481,176 @@ def gpu_float_matvec(name, dtype, rows, cols, copies, reps=20):
             "kernel_GB_per_s": round(nbytes / kus / 1e3, 1) if kus else None}
 
 
+# The reference's own kernel benchmark (`hale bench kernels`,
+# src/cli/bench.rs:73-85 -> matvec_gflops, src/hardware/bench.rs:72-87): a
+# 4096 x 4096 WeightMatrix::matvec for each of f32, bf16, f16, q8_0 and q4_0,
+# values ((i % 97) - 48) / 97 in f32, x = 0.5, GFLOP/s = 2 rows cols / time
+# and GB/s of weights = GFLOP/s / 2 x bits per weight / 8.
+# (name, dtype, bits per weight, distinct copies rotated so the weights stay cold)
+KBENCH = [("f32", H.F32, 32.0, 8), ("bf16", H.BF16, 16.0, 16), ("f16", H.F16, 16.0, 16),
+          ("q8_0", H.Q8_0, 8.5, 32), ("q4_0", H.Q4_0, 4.5, 64)]
+KB_ROWS = KB_COLS = 4096
+
+
+def kbench_values():
+    """The reference benchmark's matrix: ((i % 97) as f32 - 48.0) / 97.0."""
+    i = np.arange(KB_ROWS * KB_COLS, dtype=np.int64)
+    return ((i % 97).astype(np.float32) - np.float32(48.0)) / np.float32(97.0)
+
+
+def gpu_kernel_bench(reps=20):
+    """hale bench kernels on the GPU: per dtype, `copies` matrices holding
+    the benchmark's values, visited in turn (cold weights), and one matrix
+    called repeatedly as the reference's loop does (warm: the matrix stays
+    in the GPU's caches).  Graph-replayed; the outputs are returned for the
+    CPU leg to compare with the oracle's."""
+    ctx = H.Context(0)
+    vals = kbench_values()
+    dv = ctx.malloc(vals.nbytes)
+    dv.upload(vals)
+    x = ctx.malloc(KB_COLS * 4)
+    x.upload(np.full(KB_COLS, 0.5, np.float32))
+    out = ctx.malloc(KB_ROWS * 4)
+    res, outs = [], {}
+    for name, dt, bits, copies in KBENCH:
+        nbytes = KB_ROWS * H.row_bytes(dt, KB_COLS)
+        enc = ctx.malloc(nbytes)
+        ctx.check(H.lib().hale_encode_rows_device(ctx.handle, dt, KB_ROWS, KB_COLS, H._vp(dv.address),
+                                                  H._vp(enc.address)), "encode")
+        mats = []
+        for _ in range(copies):
+            h = H._vp()
+            ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, dt, KB_ROWS, KB_COLS,
+                                                        H._vp(enc.address), nbytes, H.C.byref(h)), "upload")
+            mats.append(H.WeightMatrix(ctx, h, KB_ROWS, KB_COLS, dt))
+        enc.free()
+
+        def call(m):
+            ctx.check(H.lib().hale_matvec_device(ctx.handle, m.handle, H._vp(x.address),
+                                                 H._vp(out.address)), "matvec")
+
+        for m in mats:
+            call(m)
+        ctx.synchronize()
+        outs[name] = out.download(np.float32, KB_ROWS)
+        timed = {}
+        for mode, seq in (("cold", mats), ("warm", [mats[0]] * copies)):
+            g = ctx.capture(lambda: [call(m) for m in seq])
+            g.launch()
+            ctx.synchronize()
+            t = time_replays(ctx, g, reps)
+            g.close()
+            timed[mode] = 1000 * float(np.median(t)) / copies
+        for m in mats:
+            m.close()
+        flops = 2.0 * KB_ROWS * KB_COLS
+        row = {"dtype": name, "bytes_per_call": nbytes, "copies": copies}
+        for mode, us in timed.items():
+            gflops = flops / us / 1e3
+            row[mode] = {"us_per_call": round(us, 3), "GFLOP_per_s": round(gflops, 1),
+                         "GB_per_s": round(gflops / 2 * bits / 8, 1),
+                         "pct_hbm_peak": round(100 * gflops / 2 * bits / 8 / HBM_PEAK_GBS, 2)}
+        res.append(row)
+        log(f"matvec 4096x4096 {name:>5}: cold {row['cold']['GFLOP_per_s']} GFLOP/s "
+            f"({row['cold']['GB_per_s']} GB/s), warm {row['warm']['GFLOP_per_s']} GFLOP/s")
+    for b in (dv, x, out):
+        b.free()
+    ctx.close()
+    return res, outs
+
+
+def cpu_kernel_bench(gpu_outs, nthreads):
+    """The same benchmark on the host through the oracle (the C restatement
+    of WeightMatrix::matvec, row-parallel like the reference's rayon loop):
+    a warm-up call, then 20 timed calls, as matvec_gflops does, on all
+    threads and on one.  Also checks the GPU's outputs against the oracle's,
+    bit for bit."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    vals = kbench_values().reshape(KB_ROWS, KB_COLS)
+    xv = np.full(KB_COLS, 0.5, np.float32)
+    res = {}
+    for name, dt, bits, _ in KBENCH:
+        data = O.encode_matrix(dt, vals)
+        ref = O.matvec(dt, KB_ROWS, KB_COLS, data, xv, nthreads=nthreads)
+        got = gpu_outs.get(name)
+        row = {"bit_exact_gpu_vs_oracle": None if got is None else bool(
+            (got.view(np.uint32) == ref.view(np.uint32)).all())}
+        for nt in (nthreads, 1):
+            O.matvec(dt, KB_ROWS, KB_COLS, data, xv, nthreads=nt)  # warm-up
+            t0 = time.perf_counter()
+            for _ in range(20):
+                O.matvec(dt, KB_ROWS, KB_COLS, data, xv, nthreads=nt)
+            sec = (time.perf_counter() - t0) / 20
+            gflops = 2.0 * KB_ROWS * KB_COLS / sec / 1e9
+            row[f"{nt}_threads"] = {"GFLOP_per_s": round(gflops, 2),
+                                    "GB_per_s": round(gflops / 2 * bits / 8, 2),
+                                    "us_per_call": round(1e6 * sec, 1)}
+        res[name] = row
+        log(f"cpu matvec 4096x4096 {name:>5}: {row[f'{nthreads}_threads']['GFLOP_per_s']} GFLOP/s "
+            f"({nthreads} threads), {row['1_threads']['GFLOP_per_s']} (1); "
+            f"GPU bit-exact: {row['bit_exact_gpu_vs_oracle']}")
+    return res
+
+
+def strict_dropin(layers, xs, ntok=96):
+    """MoeLayer::forward through the provider surface left as the reference
+    has it (src/model/moe.rs:56-70, src/expert/mod.rs:91-103): per token
+    MoeLayer::route (hale_moe_route), ExpertProvider::fetch (hale_moe_fetch),
+    then per route Expert::forward (hale_expert_forward, host slices in and
+    out, synchronous) and the combine out = out + w * y on the host in route
+    order.  Wall-clock per token over the resident layers in turn (cold), with
+    the time of each part, and whether the outputs equal the fused layer
+    forward's bit for bit."""
+    lib = H.lib()
+    L = len(layers)
+    m0 = layers[0]
+    k, hid = m0.top_k, m0.hidden
+    idx = np.zeros(k, np.uint32)
+    w = np.zeros(k, np.float32)
+    g, u, d = ((H._vp * k)() for _ in range(3))
+    tmp = np.zeros((k, hid), np.float32)
+    out = np.zeros(hid, np.float32)
+    ptr = lambda a, t: a.ctypes.data_as(t)  # noqa: E731
+    fp, u32p = H.C.POINTER(H.C.c_float), H.C.POINTER(H.C.c_uint32)
+    parts = {"route": 0.0, "fetch": 0.0, "expert_forward": 0.0, "combine": 0.0}
+    per_tok, exact = [], True
+    for s in range(ntok + L):
+        m = layers[s % L]
+        x = xs[s % xs.shape[0]]
+        t0 = time.perf_counter()
+        m.ctx.check(lib.hale_moe_route(m.handle, ptr(x, fp), ptr(idx, u32p), ptr(w, fp)), "route")
+        t1 = time.perf_counter()
+        m.ctx.check(lib.hale_moe_fetch(m.handle, ptr(idx, u32p), k, g, u, d), "fetch")
+        t2 = time.perf_counter()
+        for r in range(k):
+            m.ctx.check(lib.hale_expert_forward(m.ctx.handle, g[r], u[r], d[r], ptr(x, fp),
+                                                ptr(tmp[r], fp)), "Expert::forward")
+        t3 = time.perf_counter()
+        out[:] = 0.0
+        for r in range(k):
+            out[:] = out + w[r] * tmp[r]  # f32: the product rounded, then the sum
+        t4 = time.perf_counter()
+        if s < L:
+            continue  # first visit of each layer: untimed
+        per_tok.append(t4 - t0)
+        for key, dt_ in zip(parts, (t1 - t0, t2 - t1, t3 - t2, t4 - t3)):
+            parts[key] += dt_
+        if s < L + 8:
+            fused = m.forward(x)
+            exact = exact and bool((fused.view(np.uint32) == out.view(np.uint32)).all())
+    n = len(per_tok)
+    us = 1e6 * float(np.median(per_tok))
+    return {"workload": "the decode workload's layers through route, fetch, k x Expert::forward "
+                        "and a host combine (the reference's provider surface unchanged)",
+            "tokens": n, "us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1),
+            "parts_us_per_token": {k2: round(1e6 * v / n, 1) for k2, v in parts.items()},
+            "same_bits_as_fused_forward": exact,
+            "note": "wall clock including the Python ctypes calls; each Expert::forward copies x in "
+                    "and its output out and synchronizes, as the infallible host-slice API requires"}
+
+
 # (workload, projection dtype, hidden, heads, kv heads, head dim, QK-norm, cached positions)
 ATTENTION = [
     ("qwen3-30b-a3b attention decode bf16, 4096 cached positions", H.BF16, 2048, 32, 4, 128, True, 4096),
@@ -576,21 +753,34 @@ def gpu_decode(args):
     def step(s):
         layers[s % L].forward_device(1, xs.offset((s % nx) * HID * 4), out.address)
 
-    warm = max(args.warmup, L)
-    for s in range(warm):   # eager warm-up (also sizes every layer's scratch)
+    for m in layers:  # size each layer's scratch without running a step
+        m.reserve(1)
+    warm = args.warmup
+    for s in range(warm):   # the eager warm-up steps
         step(s)
     ctx.synchronize()
-    # one graph = one pass over all layers; at least 20 replays and at least
-    # the requested steps, each replay timed on its own
-    graph = ctx.capture(lambda: [step(s) for s in range(L)])
-    graph.launch()
+    # The timed region is exactly `steps` steps (layers s % L for s = warm ..
+    # warm + steps - 1): replays of a graph of one pass over all layers, then
+    # a graph of the remaining steps.  Graphs are uploaded when captured, so
+    # no first-launch work falls inside the region.
+    steps = args.steps
+    s0 = warm % L
+    graph = ctx.capture(lambda: [step(s0 + s) for s in range(L)])
+    full, rest = divmod(steps, L)
+    tail = ctx.capture(lambda: [step(s0 + s) for s in range(rest)]) if rest else None
     ctx.synchronize()
-    reps = max(20, -(-args.steps // L))
-    steps = reps * L
-    times = time_replays(ctx, graph, reps)
-    ms = float(np.median(times)) * reps  # the median replay, scaled to all timed steps
-    log(f"timed {steps} steps in {reps} replays: median {1000 * np.median(times) / L:.2f} us/step "
-        f"(min {1000 * min(times) / L:.2f}, max {1000 * max(times) / L:.2f})")
+    ctx.timer_start()
+    for _ in range(full):
+        graph.launch()
+    if tail is not None:
+        tail.launch()
+    ms = ctx.timer_stop()
+    log(f"timed {steps} steps ({full} passes over {L} layers + {rest}): "
+        f"{1000 * ms / steps:.2f} us/step")
+    # per-pass spread, after the timed region: one pass timed at a time
+    times = time_replays(ctx, graph, 20)
+    if tail is not None:
+        tail.close()
 
     # per-kernel durations: eager pass with events around every launch
     ctx.profile(True)
@@ -620,10 +810,41 @@ def gpu_decode(args):
             few.append({"tokens": T, "us_per_step": round(us, 2), "us_per_token": round(us / T, 2),
                         "tokens_per_s": round(1e6 * T / us, 1), "timing": replay_stats(t, L)})
             log(f"decode {T} tokens per step: {us:.2f} us/step ({us / T:.2f} us/token)")
+    dropin = None
+    if not args.no_prefill:
+        xs_host = np.random.default_rng(99).standard_normal((64, HID), dtype=np.float32)
+        dropin = strict_dropin(layers, xs_host)
+        log(f"strict drop-in (route, fetch, k x Expert::forward, host combine): "
+            f"{dropin['us_per_token']} us/token")
     for m in layers:
         m.close()
     ctx.close()
-    return steps, ms, prof, warm, replay_stats(times, L), few
+    return steps, ms, prof, warm, replay_stats(times, L), few, dropin
+
+
+def cpu_info():
+    """The host CPU as lscpu reports it (model name, sockets, physical cores
+    per socket, threads per core) and the CPUs this process may run on."""
+    import subprocess
+
+    info = {"model": cpu_model()}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, check=True).stdout
+        kv = {a.strip(): b.strip() for a, b in (ln.split(":", 1) for ln in txt.splitlines() if ":" in ln)}
+        info["model"] = kv.get("Model name", info["model"])
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        cps = int(kv.get("Core(s) per socket", "0") or 0)
+        info["sockets"] = sockets
+        info["physical_cores"] = sockets * cps if sockets and cps else None
+        info["threads_per_core"] = int(kv.get("Thread(s) per core", "0") or 0) or None
+        info["logical_cpus"] = int(kv.get("CPU(s)", "0") or 0) or None
+    except (OSError, subprocess.CalledProcessError, ValueError):
+        pass
+    try:
+        info["cpus_available_to_process"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    return info
 
 
 def cpu_model():
@@ -714,7 +935,7 @@ def main():
         return
 
     bytes_step = TOPK * expert_bytes(DTYPE, HID, INTER) + E * HID * 4
-    steps, ms, prof, warm, rstats, few = gpu_decode(args)
+    steps, ms, prof, warm, rstats, few, dropin = gpu_decode(args)
     sec = ms / 1000.0
     gbs = bytes_step * steps / sec / 1e9
 
@@ -749,6 +970,10 @@ def main():
             fmv.append(gpu_float_matvec(name, dt, rows, cols, copies))
             log(f"matvec {name}: {fmv[-1]['us_per_call']} us, {fmv[-1]['GB_per_s']} GB/s")
 
+    kb, kb_outs = [], {}
+    if not args.no_prefill:
+        kb, kb_outs = gpu_kernel_bench()
+
     attn = []
     if not args.no_prefill:
         for (name, dt, hid, nh, nkv, hd, qk, npos) in ATTENTION:
@@ -767,14 +992,19 @@ def main():
     cpu = None
     if not args.no_cpu:
         nall, res = cpu_baseline(args.cpu_seconds)
+        kb_cpu = cpu_kernel_bench(kb_outs, nall) if kb else None
+        host = cpu_info()
         med, n = res[("x86-64", nall)]
         cpu = {"value": round(bytes_step / med / 1e9, 3), "unit": "GB/s", "cores": nall,
                "kind": "port",
                "sample": f"oracle MoeLayer::forward (q4_0, 128 experts, top-8, H 2048, I 768; one "
                          f"340 MB layer, one token per iteration), median of {n} tokens, built "
-                         f"-O3 -march=x86-64, {nall} threads on {cpu_model()}",
+                         f"-O3 -march=x86-64, {nall} threads on {host['model']}",
                "tokens_per_s": round(1.0 / med, 1),
-               "cpu_model": cpu_model(),
+               "cpu_model": host["model"],
+               "host": host,
+               "threads_used": nall,
+               "reference_kernel_bench": kb_cpu,
                "variants": {f"{name} {nt} thread{'s' if nt > 1 else ''}":
                             {"GB_per_s": round(bytes_step / m / 1e9, 3), "ms_per_token": round(1e3 * m, 3),
                              "tokens": c}
@@ -807,6 +1037,10 @@ def main():
         "decode_few_tokens": few,
         "decode_more": more,
         "float_matvec": fmv,
+        "reference_kernel_bench": {"workload": "hale bench kernels: WeightMatrix::matvec 4096 x 4096, "
+                                               "values ((i % 97) - 48) / 97, x = 0.5",
+                                   "gpu": kb},
+        "strict_dropin": dropin,
         "attention": attn,
         "prefill": prefill,
         "cpu_baseline": cpu,

@@ -1337,6 +1337,40 @@ struct ProfPause {
   ~ProfPause() { c->prof_on = was; }
 };
 
+// Bytes of the fixed scratch a no-allocation forward over n tokens uses:
+// the per-token scratch, then (grouped path) the grouped workspace.
+static size_t noalloc_bytes(hale_moe* m, size_t n) {
+  const size_t tb = align_up(tok_scratch_bytes(m, n), 256);
+  if (m->k == 0 || n < m->grouped_min) return tb;
+  return tb + prefill_workspace_bytes(prefill_layer(m, TokScratch{}), n);
+}
+
+// Tokens per chunk of a no-allocation forward over ntok tokens: all of them
+// when they fit the fixed scratch; else the most that fit on the grouped
+// path, if its threshold fits; else decode passes below the threshold.
+// Each size's bytes grow with the token count, so a bisection finds the
+// largest.  0: not even one token fits.
+static size_t noalloc_chunk(hale_moe* m, size_t ntok) {
+  const size_t cap = HALE_NOALLOC_SCRATCH_BYTES;
+  if (noalloc_bytes(m, ntok) <= cap) return ntok;
+  size_t lo, hi;  // noalloc_bytes(lo) fits (or lo == 0), noalloc_bytes(hi) does not
+  const size_t gmin = std::max<size_t>(m->grouped_min, 1);
+  if (m->k > 0 && ntok >= gmin && noalloc_bytes(m, gmin) <= cap) {
+    lo = gmin;
+    hi = ntok;
+  } else {
+    lo = 0;
+    hi = std::min(ntok, gmin);  // decode passes of fewer than gmin tokens
+    if (hi < ntok && noalloc_bytes(m, hi) <= cap) return hi;
+  }
+  while (hi - lo > 1) {
+    const size_t mid = lo + (hi - lo) / 2;
+    if (noalloc_bytes(m, mid) <= cap) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
 extern "C" int hale_moe_forward_device_noalloc(hale_moe* m, size_t ntok, const float* d_x,
                                                const float* d_logits, float* d_out,
                                                uint32_t* d_index, float* d_weight) {
@@ -1348,23 +1382,34 @@ extern "C" int hale_moe_forward_device_noalloc(hale_moe* m, size_t ntok, const f
   if (!c->fixed_scratch) return fail(c, HALE_EHIP, "no fixed scratch on device %d", c->device);
   int rc = moe_forward_check(m, d_x, d_logits);
   if (rc) return rc;
-  char* base = (char*)c->fixed_scratch;
-  const size_t tb = align_up(tok_scratch_bytes(m, ntok), 256);
-  const TokScratch s = tok_scratch_carve(m, base, ntok);
-  const bool grouped = m->k > 0 && ntok >= m->grouped_min;
-  const size_t need = tb + (grouped ? prefill_workspace_bytes(prefill_layer(m, s), ntok) : 0);
-  if (need > (size_t)HALE_NOALLOC_SCRATCH_BYTES)
+  const size_t chunk = noalloc_chunk(m, ntok);
+  if (chunk == 0)
     return fail(c, HALE_EINVAL,
-                "moe_forward_noalloc: %zu tokens need %zu bytes of scratch, the fixed scratch "
+                "moe_forward_noalloc: one token needs %zu bytes of scratch, the fixed scratch "
                 "holds %zu",
-                ntok, need, (size_t)HALE_NOALLOC_SCRATCH_BYTES);
+                noalloc_bytes(m, 1), (size_t)HALE_NOALLOC_SCRATCH_BYTES);
+  char* base = (char*)c->fixed_scratch;
+  const size_t k = m->k;
   ProfPause pause(c);
-  rc = moe_forward_enqueue(m, ntok, d_x, d_logits, d_out, s, grouped ? base + tb : nullptr);
-  if (rc) return rc;
-  if (d_index && m->k)
-    HIPCHK(c, hipMemcpyAsync(d_index, s.route_idx, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
-  if (d_weight && m->k)
-    HIPCHK(c, hipMemcpyAsync(d_weight, s.route_w, ntok * m->k * 4, hipMemcpyDeviceToDevice, c->stream));
+  // Chunks run one after another on the stream, each reusing the array from
+  // its start.  Tokens are independent, so a chunk boundary changes no bits;
+  // a last chunk below the grouped threshold takes the decode path, which
+  // gives the same bits as the grouped one.
+  for (size_t t0 = 0; t0 < ntok; t0 += chunk) {
+    const size_t n = std::min(chunk, ntok - t0);
+    const size_t tb = align_up(tok_scratch_bytes(m, n), 256);
+    const TokScratch s = tok_scratch_carve(m, base, n);
+    const bool grouped = k > 0 && n >= m->grouped_min;
+    rc = moe_forward_enqueue(m, n, d_x + t0 * m->H, d_logits ? d_logits + t0 * m->E : nullptr,
+                             d_out + t0 * m->H, s, grouped ? base + tb : nullptr);
+    if (rc) return rc;
+    if (d_index && k)
+      HIPCHK(c, hipMemcpyAsync(d_index + t0 * k, s.route_idx, n * k * 4, hipMemcpyDeviceToDevice,
+                               c->stream));
+    if (d_weight && k)
+      HIPCHK(c, hipMemcpyAsync(d_weight + t0 * k, s.route_w, n * k * 4, hipMemcpyDeviceToDevice,
+                               c->stream));
+  }
   return HALE_OK;
 }
 
@@ -2201,6 +2246,16 @@ extern "C" int hale_graph_end(hale_ctx* c, hale_graph** out) {
     return fail(c, HALE_EHIP, "instantiate: %s", hipGetErrorString(e));
   }
   std::lock_guard<std::recursive_mutex> lk(c->mu);
+  // the exec's device-side resources are set up now, on the context's
+  // stream, so its first launch costs what every other does
+  e = hipSetDevice(c->device);
+  if (e == hipSuccess) e = hipGraphUpload(g->exec, c->stream);
+  if (e != hipSuccess) {
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(graph);
+    delete g;
+    return fail(c, HALE_EHIP, "graph upload: %s", hipGetErrorString(e));
+  }
   c->live_graphs++;
   *out = g;
   return HALE_OK;

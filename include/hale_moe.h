@@ -259,11 +259,12 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
  * such call would.  No counterpart in the reference; for callers that
  * capture graphs (growth is refused during a capture) or want no
  * allocation inside a serving loop.  Refused (HALE_EINVAL) while the
- * context's stream is being captured. */
+ * context's stream is being captured only when the scratch or workspace
+ * would have to grow; a reserve that fits what is held succeeds. */
 int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
- * path (default 8); fewer tokens run the decode kernels in one pass over
+ * path (default 16 for top_k >= 4, else 8); fewer tokens run the decode kernels in one pass over
  * all of them.  Both give the reference's bits; the choice is speed only.
  * n in 2..HALE_DECODE_MAX_TOKENS + 1.  A new threshold re-lays the layer's
  * per-token scratch on its next call, which must then come outside a graph
@@ -289,7 +290,7 @@ int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
 int hale_moe_set_down_fold(hale_moe *moe, int fold);
 
 /* Bytes of the fixed device scratch of hale_moe_forward_device_noalloc. */
-#define HALE_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define HALE_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 /* No counterpart in the reference: hale_moe_forward_device for callers that
  * cannot allocate device memory (code under HIP graph capture, tight
@@ -297,9 +298,17 @@ int hale_moe_set_down_fold(hale_moe *moe, int fold);
  * and errors, but the per-token scratch and the grouped workspace come from
  * a fixed array of HALE_NOALLOC_SCRATCH_BYTES per device, held until the
  * process ends; the call makes no device or host allocation.  A forward
- * whose scratch would exceed it (about 16 MiB: for H 2048 and top-8, up to
- * roughly 190 tokens on the grouped path) fails with HALE_EINVAL before
- * anything is enqueued.  Every context on one device shares that device's
+ * whose scratch would exceed it runs as consecutive chunks of tokens that
+ * fit, with the same bits (every token's output, routes and routing count
+ * are independent of the others).  A grouped chunk of T tokens needs about
+ * (T*top_k/32 + E) * (H + I)/32 * 1152 bytes of operand tiles plus
+ * T*top_k*H*4 bytes of down outputs and about T*(H/32*48 + E*4) bytes of
+ * per-token scratch: at 64 MiB, chunks of up to about 570 tokens for
+ * E 128, H 2048, I 768, top-8 and about 215 for E 128, H 4096, I 1536.
+ * When not even a chunk of the grouped threshold fits, the tokens run as
+ * decode passes of fewer tokens.  Only a layer whose single token does not
+ * fit is refused (HALE_EINVAL, before anything is enqueued).  Every
+ * context on one device shares that device's
  * array, which keeps the last call's contents (nothing in it must start at
  * zero): calls that overlap in time on one device, from different contexts
  * or streams, race. */

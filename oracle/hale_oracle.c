@@ -690,19 +690,24 @@ int orc_moe_forward(const orc_moe_layer *L, const float *x,
   return 0;
 }
 
-/* Token-at-a-time prefill, src/model/transformer.rs:231-239. */
+/* Token-at-a-time prefill, src/model/transformer.rs:231-239: token t's
+ * output is MoeLayer::forward(x_t), independent of every other token, so
+ * with several threads the tokens are shared among them (each token's own
+ * forward then runs on one thread: the bits do not depend on threads). */
 int orc_moe_prefill(const orc_moe_layer *L, size_t tokens, const float *x,
                     const float *logits, float *out, uint32_t *index,
                     float *weight, int nthreads) {
+  int rc = 0;
+  const int tok_par = nthreads > 1 && tokens > 1;
+#pragma omp parallel for num_threads(tok_par ? nthreads : 1) schedule(dynamic, 1) reduction(|| : rc)
   for (size_t t = 0; t < tokens; t++) {
-    int rc = orc_moe_forward(L, x + t * L->hidden,
-                             logits ? logits + t * L->num_experts : NULL,
-                             out + t * L->hidden,
-                             index ? index + t * L->top_k : NULL,
-                             weight ? weight + t * L->top_k : NULL, nthreads);
-    if (rc) return rc;
+    rc = rc || orc_moe_forward(L, x + t * L->hidden,
+                               logits ? logits + t * L->num_experts : NULL,
+                               out + t * L->hidden,
+                               index ? index + t * L->top_k : NULL,
+                               weight ? weight + t * L->top_k : NULL, tok_par ? 1 : nthreads);
   }
-  return 0;
+  return rc ? -1 : 0;
 }
 
 /* ------------------------------------------------------------------------ */

@@ -56,6 +56,27 @@ def test_float_matvec_lm_head_shape(ctx, dtype):
     check_matvec(ctx, dtype, 151936, 2048, seed=77)
 
 
+@pytest.mark.parametrize("dtype", [O.F16, O.BF16])
+def test_float_matvec_lanes_kept_across_decode_chunks(ctx, dtype):
+    """dot_decoded's 64-value chunks share the eight lane accumulators
+    (src/tensor/quant.rs:166-184): the closed-form row of
+    tests/test_oracle.py gives 2^24 + 4, where a reduce per chunk gives
+    2^24 + 6.  Rows 1 and 2 shift the same products by one octet and hold
+    zeros, to land the terms in other lanes and a zero row."""
+    from test_oracle import decoded_chunk_case
+
+    w, x, kept, reset = decoded_chunk_case()
+    rows = np.stack([w, np.roll(w, 8), np.zeros_like(w)])
+    xs = np.roll(x, 0)
+    data = O.encode_matrix(dtype, rows)
+    m = H.WeightMatrix.new(ctx, 3, w.size, dtype, data)
+    got = m.matvec(xs)
+    want = O.matvec(dtype, 3, w.size, data, xs)
+    assert got[0] == kept and got[0] != reset
+    assert same_bits(got, want)
+    m.close()
+
+
 def test_float_matvec_lane_order_closed_form(ctx):
     # w = [1, 1, 0, 0, 2^24, 0, 0, 0], x = 1: lanes give (1 + 2^24) + 1 -> 2^24
     # with two round-to-even steps; a left-to-right sum would give 2^24 + 2.

@@ -276,6 +276,36 @@ def test_dot_f32_uses_eight_lane_order():
     assert O.dot_f32(w2, np.ones(12, dtype=np.float32)) == 16777218.0
 
 
+def decoded_chunk_case():
+    """A 132-element f16 / bf16 row for dot_decoded (src/tensor/quant.rs:166-184),
+    which decodes 64 values at a time but keeps its eight lane accumulators
+    across the chunks and adds the chunks' tails last.  Products: element 0
+    (chunk 0, lane 0) 256 * 65536 = 2^24; elements 64 and 65 (chunk 1, lanes
+    0 and 1) 1 each; element 128 (the last chunk, a 4-element tail) 1 * 4.
+    Lanes kept: lane 0 = 2^24 + 1 -> 2^24 (ties to even), lane 1 = 1, the
+    reduce (2^24 + 1) -> 2^24, then + 4: 2^24 + 4.  Lanes reset per chunk
+    (a reduce per chunk, summed): 2^24 + 2 + 4.  One sum over the products
+    in order: 2^24 + 1 -> 2^24, + 1 -> 2^24, + 4."""
+    n = 132
+    w = np.zeros(n, np.float32)
+    x = np.zeros(n, np.float32)
+    w[0], x[0] = 256.0, 65536.0
+    w[64] = w[65] = x[64] = x[65] = 1.0
+    w[128], x[128] = 1.0, 4.0
+    return w, x, 16777220.0, 16777222.0
+
+
+def test_dot_decoded_keeps_lanes_across_chunks():
+    w, x, kept, reset = decoded_chunk_case()
+    for dtype in (O.F16, O.BF16):
+        b = O.encode_row(dtype, w)
+        assert (O.decode_row(dtype, b, w.size) == w).all()  # every value exact in both formats
+        got = O.dot(dtype, b, x)
+        assert got == kept and got != reset, dtype
+    # the whole-row f32 dot adds the same lanes in the same order
+    assert O.dot_f32(w, x) == kept
+
+
 # ---------------------------------------------------------------------------
 # matvec (src/tensor/matrix.rs:115-143, tests :150-189)
 # ---------------------------------------------------------------------------
