@@ -117,6 +117,24 @@ struct DownArgs {
 
 hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st);
 
+// WeightMatrix::matvec of one quantized matrix with whole fold chains per
+// wave: out[r] for r < rows.  The activation is x (f32, quantized in the
+// kernel; 16-byte aligned) or act (q8 blocks already made).  Returns
+// hipErrorNotSupported for shapes it does not take (then the caller runs
+// act quantization and launch_gemv).
+struct MatvecArgs {
+  const uint8_t* codes;
+  const uint16_t* scales;
+  int nb;                // blocks per row
+  int rows;
+  const float* x;        // or null
+  const ActBlock* act;   // used when x is null
+  float* out;
+};
+hipError_t launch_matvec(int dtype, const MatvecArgs& a, hipStream_t st);
+constexpr int MATVEC_XQ_MAX_NB = 128;  // blocks per row launch_matvec quantizes x for
+constexpr int MATVEC_MAX_NB = 512;     // blocks per row it takes with act given
+
 hipError_t launch_repack(int dtype, const uint8_t* aos, size_t rows, size_t cols, uint8_t* codes,
                          uint16_t* scales, hipStream_t st);
 hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales, size_t rows,

@@ -11,6 +11,7 @@
 
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "hale_device.h"
 #include "kernels.h"
@@ -1502,6 +1503,175 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   }
 }
 
+// ===========================================================================
+// WeightMatrix::matvec with whole fold chains per wave
+// ===========================================================================
+//
+// out[r] = dot_q8_0 / dot_q4_0 (row r, quantize(x)) (src/tensor/matrix.rs:
+// 115-143, src/tensor/quant.rs:77-144), every row's chain in one wave.  A
+// wave takes RPW consecutive rows (8 or 4) of one 32-row tile with
+// LPR = 64 / RPW lanes per row: lane LPR r + j holds row r and block
+// LPR q + j of block group q, so a wave-load reads, per block, the RPW rows'
+// 16-byte chunks (128 or 64 contiguous bytes of the tile layout).  D groups
+// are in flight per wave; each group's LPR terms join the row's running
+// sum in block order by DPP shifts within the row's lanes (one DPP row of
+// 16 lanes holds one or two rows).  A work-group is NW waves of one tile.
+// With XQ the work-group quantizes x itself (all of it, 8 lanes per block,
+// into LDS; the same expressions as k_act_quant), so no quantization launch
+// comes first; otherwise the q8 blocks are read from act.  MAXNB bounds the
+// blocks per row (the LDS staging and the early loads are sized by it).
+// Four rows per wave give twice the waves of eight for the same matrix: the
+// launcher takes them when eight leave SIMDs without a wave.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// acc + the terms of lanes L + 1 .. L + K of the lane's DPP row, in lane
+// order (a comma fold runs left to right); the _n form adds only lanes
+// L + k with k < n.
+template <int K>
+__device__ __forceinline__ float row_term(float t) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x100 + K, 0xF, 0xF, false));
+}
+template <int... K>
+__device__ __forceinline__ float row_fold(float acc, float t, std::integer_sequence<int, K...>) {
+  ((acc = acc + row_term<K + 1>(t)), ...);
+  return acc;
+}
+template <int... K>
+__device__ __forceinline__ float row_fold_n(float acc, float t, int n, std::integer_sequence<int, K...>) {
+  ((acc = K + 1 < n ? acc + row_term<K + 1>(t) : acc), ...);
+  return acc;
+}
+
+template <int DT, int RPW, int NW, int MAXNB, bool XQ>
+__global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
+  constexpr int CH = Layout<DT>::CH;
+  constexpr int LPR = 64 / RPW;                           // lanes (and blocks of a group) per row
+  static_assert(RPW == 8 || RPW == 4, "a row's lanes lie in one DPP row");
+  static_assert(NW * RPW <= TILE, "a work-group's rows lie in one tile");
+  constexpr int MAXG = (MAXNB + LPR - 1) / LPR;
+  constexpr int D = MAXG < 16 / CH ? (MAXG + 3) / 4 * 4 : 16 / CH;  // groups in flight
+  constexpr int SPL = (MAXNB + 63) / 64;                  // scale pieces per lane
+  constexpr int NT = 64 * NW;
+  constexpr int BPP = NT / 8;                             // x blocks per pass (XQ)
+  constexpr int XP = XQ ? (MAXNB + BPP - 1) / BPP : 1;    // passes
+  constexpr int APT = XQ ? 1 : (MAXNB * 3 + NT - 1) / NT; // activation pieces per thread
+  // a scale piece: the wave's RPW rows' f16 scales of one block
+  typedef typename std::conditional<RPW == 8, u32x4, u32x2>::type Piece;
+  // (unconditional staging stores: room for every thread's pieces or blocks)
+  constexpr int ACT_PIECES = XQ ? XP * BPP * 3 : APT * NT;
+  __shared__ __attribute__((aligned(16))) u32x4 s_actv[(ACT_PIECES + 2) / 3 * 3];
+  __shared__ Piece s_scl[NW][SPL * 64];
+  ActBlock* s_act = (ActBlock*)s_actv;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nb = a.nb, nbg = (nb + LPR - 1) / LPR;
+  const size_t rowg = ((size_t)blockIdx.x * NW + wave) * RPW;  // the wave's first row
+  const size_t tile = rowg / TILE;
+  const int r = lane / LPR, j = lane % LPR;
+  const int rt = (int)(rowg % TILE) + r;
+  const uint8_t* cbase = a.codes + (tile * nb * CH * TILE + rt) * 16;
+  // the RPW rows' scales of block b: one piece at sp + b * TILE * 2 / sizeof(Piece)
+  const Piece* sp = (const Piece*)(a.scales + tile * nb * TILE + rowg % TILE);
+
+  // The loads the staging waits for come first, then the ring; scheduling
+  // barriers keep that order (loads return in order, so the staging's wait
+  // then leaves the ring in flight), and every staging store is
+  // unconditional (clamped values past the row's end, never read), so no
+  // load is sunk into a branch behind the ring.
+  Piece sv[SPL];
+#pragma unroll
+  for (int m = 0; m < SPL; m++)
+    sv[m] = sp[(size_t)min(lane + 64 * m, nb - 1) * (TILE * 2 / sizeof(Piece))];
+  f32x4 xv[XP];
+  u32x4 av[APT];
+  if constexpr (XQ) {
+#pragma unroll
+    for (int p = 0; p < XP; p++) {
+      const int b = min((int)(threadIdx.x >> 3) + BPP * p, nb - 1);
+      xv[p] = *(const f32x4*)(a.x + (size_t)b * QK + 4 * (lane & 7));
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < APT; m++)
+      av[m] = ((const u32x4*)a.act)[min((int)threadIdx.x + NT * m, nb * 3 - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 cw[D][CH];
+  // group q's codes into ring slot d (groups past the end are clamped to
+  // the last: in-bounds loads that are never used)
+  auto load = [&](int d, int q) {
+    const int b = min(min(q, nbg - 1) * LPR + j, nb - 1);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+      cw[d][c] = __builtin_nontemporal_load((const u32x4*)(cbase + ((size_t)b * CH + c) * TILE * 16));
+  };
+#pragma unroll
+  for (int d = 0; d < D; d++) {
+    load(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // staging: the wave's scale pieces, and the activation blocks (all waves)
+#pragma unroll
+  for (int m = 0; m < SPL; m++) s_scl[wave][lane + 64 * m] = sv[m];
+  if constexpr (XQ) {
+#pragma unroll
+    for (int p = 0; p < XP; p++) quant_block8(xv[p], lane & 7, s_act + (threadIdx.x >> 3) + BPP * p);
+  } else {
+#pragma unroll
+    for (int m = 0; m < APT; m++) s_actv[threadIdx.x + NT * m] = av[m];
+  }
+  __syncthreads();
+  const uint16_t* scl16 = (const uint16_t*)s_scl[wave];
+
+  float acc = 0.0f;  // row r's dot product (valid in lane LPR r)
+  // Groups q0 .. q0 + D - 1 from the ring; with RELOAD each batch's ring
+  // slots then take the groups D further on (clamped past the end).
+  auto pass = [&](int q0, auto reload) {
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += 4) {
+      const int qb = q0 + d0;
+      if (qb < nbg) {  // wave-uniform; the batch's four terms, then their sums in order
+        float t[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int b = min((qb + i) * LPR + j, nb - 1);
+          t[i] = block_term<DT>(cw[d0 + i], scl16[b * RPW + r], s_act + b);
+        }
+        if (qb + 4 <= nb / LPR) {  // four whole groups (wave-uniform): plain adds in block order
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc = row_fold(acc + t[i], t[i], std::make_integer_sequence<int, LPR - 1>{});
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            // groups past the row's end have n <= 0 and add nothing
+            const int n = nb - (qb + i) * LPR;  // blocks of the group inside the row
+            acc = n > 0 ? acc + t[i] : acc;
+            acc = row_fold_n(acc, t[i], n, std::make_integer_sequence<int, LPR - 1>{});
+          }
+        }
+      }
+      if constexpr (decltype(reload)::value) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) load(d0 + i, qb + i + D);
+      }
+    }
+  };
+  // One pass when every group fits the ring (the usual case: no refills, so
+  // each batch waits only for its own groups); else unconditional refills,
+  // which keep the wait counts exact across the loop's iterations.
+  if constexpr (MAXG <= D) {
+    pass(0, std::false_type{});
+  } else {
+#pragma unroll 1
+    for (int q0 = 0; q0 < nbg; q0 += D) pass(q0, std::true_type{});
+  }
+  const size_t row = rowg + r;
+  if (j == 0 && row < (size_t)a.rows) a.out[row] = acc;
+}
+
 // Per-block i32 sums of every row (the `isum` of dot_q8_0 / dot_q4_0), one
 // thread per (row, block).  Parity instrumentation, not a hot path.
 template <int DT>
@@ -1735,6 +1905,50 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 8>, groups, 512, 0, st, a);
   if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 8>, groups, 512, 0, st, a);
   return hipErrorInvalidValue;
+}
+
+// Four rows per wave when eight would leave fewer waves than the GPU's
+// 1024 SIMDs; work-groups of one tile (NW = 32 / RPW waves) when that still
+// gives at least 256 work-groups, else half or a quarter of a tile, so
+// small matrices spread over more CUs.
+hipError_t launch_matvec(int dtype, const MatvecArgs& a, hipStream_t st) {
+  if (a.nb < 1 || a.rows < 1) return hipErrorInvalidValue;
+  if (dtype != Q8_0 && dtype != Q4_0) return hipErrorInvalidValue;
+  const bool xq = a.x != nullptr;
+  if (xq && (((uintptr_t)a.x & 15) || a.nb > MATVEC_XQ_MAX_NB)) return hipErrorNotSupported;
+  if (!xq && (!a.act || a.nb > MATVEC_MAX_NB)) return hipErrorNotSupported;
+  const size_t prow = padded_rows((size_t)a.rows);
+  const int rpw = prow / 8 >= 1024 ? 8 : 4;
+  // waves per work-group: a whole tile, half or a quarter (quantizing x in
+  // the kernel takes at least two waves: one leaves too many x loads per lane)
+  int nw = TILE / rpw;
+  while (nw > 2 && prow / (size_t)(rpw * nw) < 256) nw /= 2;
+  const unsigned grid = (unsigned)(prow / (size_t)(rpw * nw));
+#define HALE_MV(D, R, NW, MAXNB, XQ) launch(k_matvec_chain<D, R, NW, MAXNB, XQ>, grid, 64 * NW, 0, st, a)
+#define HALE_MV_NW(D, MAXNB, XQ)                                                           \
+  do {                                                                                     \
+    if (rpw == 8) return nw == 4 ? HALE_MV(D, 8, 4, MAXNB, XQ) : HALE_MV(D, 8, 2, MAXNB, XQ); \
+    return nw == 8 ? HALE_MV(D, 4, 8, MAXNB, XQ)                                            \
+                   : (nw == 4 ? HALE_MV(D, 4, 4, MAXNB, XQ) : HALE_MV(D, 4, 2, MAXNB, XQ)); \
+  } while (0)
+#define HALE_MV_NB(D, XQ)                                                  \
+  do {                                                                     \
+    if (a.nb <= 32) HALE_MV_NW(D, 32, XQ);                                 \
+    if (a.nb <= 64) HALE_MV_NW(D, 64, XQ);                                 \
+    if (a.nb <= MATVEC_XQ_MAX_NB) HALE_MV_NW(D, MATVEC_XQ_MAX_NB, XQ);      \
+  } while (0)
+  if (dtype == Q8_0) {
+    if (xq) HALE_MV_NB(Q8_0, true);
+    HALE_MV_NB(Q8_0, false);
+    HALE_MV_NW(Q8_0, MATVEC_MAX_NB, false);
+  } else {
+    if (xq) HALE_MV_NB(Q4_0, true);
+    HALE_MV_NB(Q4_0, false);
+    HALE_MV_NW(Q4_0, MATVEC_MAX_NB, false);
+  }
+#undef HALE_MV_NB
+#undef HALE_MV_NW
+#undef HALE_MV
 }
 
 hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,

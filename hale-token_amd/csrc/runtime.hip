@@ -743,7 +743,18 @@ static int matvec_enqueue(hale_ctx* c, const hale_matrix* m, const float* dx, fl
     return HALE_OK;
   }
   size_t nb = m->cols / HALE_QK;
+  MatvecArgs mv{m->codes, m->scales, (int)nb, (int)m->rows, nullptr, nullptr, dout};
+  if (((uintptr_t)dx & 15) == 0 && nb <= (size_t)MATVEC_XQ_MAX_NB) {  // one launch
+    mv.x = dx;
+    LAUNCH(c, K_GEMV, launch_matvec(m->dtype, mv, c->stream));
+    return HALE_OK;
+  }
   LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nb, act, c->stream));
+  if (nb <= (size_t)MATVEC_MAX_NB) {
+    mv.act = act;
+    LAUNCH(c, K_GEMV, launch_matvec(m->dtype, mv, c->stream));
+    return HALE_OK;
+  }
   GemvArgs a = plain_args(m, act, dout);
   LAUNCH(c, K_GEMV, launch_gemv(m->dtype, EPI_PLAIN, a, (int)(padded_rows(m->rows) / 64), 1, c->stream));
   return HALE_OK;
@@ -855,8 +866,13 @@ static int expert_enqueue(hale_ctx* c, const hale_matrix* gate, const hale_matri
   a.hact_stride = (int)nbi;
   a.slots = 1;
   LAUNCH(c, K_GATE_UP, launch_gemv(gate->dtype, EPI_GATE_UP, a, (int)nbi, 1, c->stream));
-  GemvArgs d = plain_args(down, hact, dout);
-  LAUNCH(c, K_DOWN, launch_gemv(down->dtype, EPI_PLAIN, d, (int)(padded_rows(H) / 64), 1, c->stream));
+  if (nbi <= (size_t)MATVEC_MAX_NB) {
+    MatvecArgs mv{down->codes, down->scales, (int)nbi, (int)H, nullptr, hact, dout};
+    LAUNCH(c, K_DOWN, launch_matvec(down->dtype, mv, c->stream));
+  } else {
+    GemvArgs d = plain_args(down, hact, dout);
+    LAUNCH(c, K_DOWN, launch_gemv(down->dtype, EPI_PLAIN, d, (int)(padded_rows(H) / 64), 1, c->stream));
+  }
   return HALE_OK;
 }
 

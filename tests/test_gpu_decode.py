@@ -79,7 +79,11 @@ def test_upload_download_round_trip(ctx, dtype):
 # matvec
 # ---------------------------------------------------------------------------
 
-SHAPES = [(768, 2048), (2048, 768), (1536, 4096), (4096, 1536), (32, 64), (100, 96), (4096, 14336)]
+# (4096, 4096) is the reference's kernel benchmark shape; (6000, 4000) has a
+# partial last block group and a partial last tile; (10000, 2048) takes
+# eight rows per wave (8192 rows and more)
+SHAPES = [(768, 2048), (2048, 768), (1536, 4096), (4096, 1536), (32, 64), (100, 96), (4096, 14336),
+          (4096, 4096), (6000, 4000), (10000, 2048)]
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
