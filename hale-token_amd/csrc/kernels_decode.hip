@@ -1503,25 +1503,6 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
   }
 }
 
-// ===========================================================================
-// WeightMatrix::matvec with whole fold chains per wave
-// ===========================================================================
-//
-// out[r] = dot_q8_0 / dot_q4_0 (row r, quantize(x)) (src/tensor/matrix.rs:
-// 115-143, src/tensor/quant.rs:77-144), every row's chain in one wave.  A
-// wave takes RPW consecutive rows (8 or 4) of one 32-row tile with
-// LPR = 64 / RPW lanes per row: lane LPR r + j holds row r and block
-// LPR q + j of block group q, so a wave-load reads, per block, the RPW rows'
-// 16-byte chunks (128 or 64 contiguous bytes of the tile layout).  D groups
-// are in flight per wave; each group's LPR terms join the row's running
-// sum in block order by DPP shifts within the row's lanes (one DPP row of
-// 16 lanes holds one or two rows).  A work-group is NW waves of one tile.
-// With XQ the work-group quantizes x itself (all of it, 8 lanes per block,
-// into LDS; the same expressions as k_act_quant), so no quantization launch
-// comes first; otherwise the q8 blocks are read from act.  MAXNB bounds the
-// blocks per row (the LDS staging and the early loads are sized by it).
-// Four rows per wave give twice the waves of eight for the same matrix: the
-// launcher takes them when eight leave SIMDs without a wave.
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // acc + the terms of lanes L + 1 .. L + K of the lane's DPP row, in lane
@@ -1542,6 +1523,173 @@ __device__ __forceinline__ float row_fold_n(float acc, float t, int n, std::inte
   return acc;
 }
 
+// ===========================================================================
+// Down projection and combine for 4 to 8 routes, whole chains per wave
+// ===========================================================================
+//
+// MoeLayer::forward's combine (src/model/moe.rs:63-68) over down(h_s) of
+// every route s, with a work-group per 8 output rows and one wave per
+// route: wave s folds the chains of slot s for the 8 rows (lane 8r + j:
+// row r, block 8q + j of group q, as k_matvec_chain), all D groups of a
+// short row in flight at once; then the 8 rows' outputs out = out + w_s y_s
+// in route order.  Every slot's activation blocks and each wave's scale
+// pieces are staged in LDS sized by MAXNB, so several work-groups share a
+// CU.  Loads are issued in the order their waits come: the activation
+// pieces (they need no route), then, once the slot's expert is known, the
+// scale pieces and the code ring; every staging store is unconditional.
+template <int DT, int MAXNB>
+__global__ __launch_bounds__(512) void k_down_slots(DownArgs a) {
+  constexpr int CH = Layout<DT>::CH;
+  constexpr int MAXG = (MAXNB + 7) / 8;
+  // groups in flight: every group of a row when they fit (no loads past
+  // the row's end), else a ring of 16 / CH refilled in batches of four
+  constexpr int D = MAXG <= 16 / CH ? MAXG : 16 / CH;
+  static_assert(MAXG <= D || D % 4 == 0, "a refilled ring takes batches of four");
+  constexpr int SPL = (MAXNB + 63) / 64;                  // scale pieces per lane
+  constexpr int APT = (8 * MAXNB * 3 + 511) / 512;        // activation pieces per thread
+  __shared__ __attribute__((aligned(16))) u32x4 s_actv[APT * 512];
+  __shared__ u32x4 s_scl[8][SPL * 64];
+  __shared__ float s_y[8][8];
+  __shared__ float s_w[8];
+
+  const int lane = threadIdx.x & 63;
+  const int sl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's slot
+  const int nt = (int)blockDim.x;                                   // 64 slots
+  const int nb = a.nb, slots = a.slots, nbg = (nb + 7) / 8;
+  if (blockIdx.y > 0) {  // token blockIdx.y of a few-token decode
+    a.route_idx += (size_t)blockIdx.y * slots;
+    a.route_w += (size_t)blockIdx.y * slots;
+    a.hact += (size_t)blockIdx.y * slots * a.hact_stride;
+    a.out += (size_t)blockIdx.y * a.rows;
+  }
+  // the slot's expert first (loads return in order: waiting for it leaves
+  // the activation loads behind it in flight)
+  const int ev = a.route_idx[sl];
+  __builtin_amdgcn_sched_barrier(0);
+  // every slot's activation pieces (slot s's blocks at [s * nb])
+  const int npieces = slots * nb * 3;
+  u32x4 av[APT];
+#pragma unroll
+  for (int m = 0; m < APT; m++) {
+    const int i = min((int)threadIdx.x + nt * m, npieces - 1);
+    const int s2 = i / (nb * 3), rem = i - s2 * nb * 3;
+    av[m] = ((const u32x4*)(a.hact + (size_t)s2 * a.hact_stride))[rem];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int e = __builtin_amdgcn_readfirstlane(ev);
+  // The four 8-row groups of a 32-row tile share its scale lines; work-group
+  // g runs on XCD g % 8, so when the grid is a multiple of 32 the groups of
+  // one tile get ids of one residue class (a permutation of the row groups).
+  const int g = blockIdx.x;
+  size_t row0 = (size_t)g * 8;
+  if ((gridDim.x & 31) == 0) {
+    const int gx = g & 7, gj = g >> 3;
+    row0 = (size_t)(gx + 8 * (gj >> 2)) * TILE + (size_t)(gj & 3) * 8;
+  }
+  const size_t tile = row0 / TILE;
+  const int r = lane >> 3, j = lane & 7;
+  const int rt = (int)(row0 % TILE) + r;
+  const uint8_t* cbase = a.codes + (size_t)e * a.codes_stride + (tile * nb * CH * TILE + rt) * 16;
+  const u32x4* sp = (const u32x4*)(a.scales + (size_t)e * a.scales_stride + tile * nb * TILE + row0 % TILE);
+  u32x4 sv[SPL];
+#pragma unroll
+  for (int m = 0; m < SPL; m++) sv[m] = sp[(size_t)min(lane + 64 * m, nb - 1) * (TILE * 2 / 16)];
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 cw[D][CH];
+  auto load = [&](int d, int q) {
+    const int b = min(min(q, nbg - 1) * 8 + j, nb - 1);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+      cw[d][c] = __builtin_nontemporal_load((const u32x4*)(cbase + ((size_t)b * CH + c) * TILE * 16));
+  };
+#pragma unroll
+  for (int d = 0; d < D; d++) {
+    load(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the route weights, needed only by the combine
+  const float wv = a.route_w[min((int)threadIdx.x & 7, slots - 1)];
+#pragma unroll
+  for (int m = 0; m < SPL; m++) s_scl[sl][lane + 64 * m] = sv[m];
+#pragma unroll
+  for (int m = 0; m < APT; m++) s_actv[threadIdx.x + nt * m] = av[m];
+  __syncthreads();
+  const uint16_t* scl16 = (const uint16_t*)s_scl[sl];
+  const ActBlock* act = (const ActBlock*)s_actv + (size_t)sl * nb;
+
+  float acc = 0.0f;  // row r's dot product for this slot (valid in lane 8 r)
+  auto pass = [&](int q0, auto reload) {
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += 4) {
+      constexpr int NI_MAX = 4;
+      const int ni = D - d0 < NI_MAX ? D - d0 : NI_MAX;  // groups of this batch (compile time)
+      const int qb = q0 + d0;
+      if (qb < nbg) {
+        float t[NI_MAX];
+#pragma unroll
+        for (int i = 0; i < NI_MAX; i++) {
+          if (i < ni) {
+            const int b = min((qb + i) * 8 + j, nb - 1);
+            t[i] = block_term<DT>(cw[d0 + i], scl16[b * 8 + r], act + b);
+          }
+        }
+        if (qb + ni <= nb / 8) {  // whole groups (wave-uniform): plain adds in block order
+#pragma unroll
+          for (int i = 0; i < NI_MAX; i++)
+            if (i < ni) acc = row_fold(acc + t[i], t[i], std::make_integer_sequence<int, 7>{});
+        } else {
+#pragma unroll
+          for (int i = 0; i < NI_MAX; i++) {
+            if (i < ni) {
+              const int n = nb - (qb + i) * 8;  // blocks of the group inside the row
+              acc = n > 0 ? acc + t[i] : acc;
+              acc = row_fold_n(acc, t[i], n, std::make_integer_sequence<int, 7>{});
+            }
+          }
+        }
+      }
+      if constexpr (decltype(reload)::value) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) load(d0 + i, qb + i + D);
+      }
+    }
+  };
+  if constexpr (MAXG <= D) {
+    pass(0, std::false_type{});
+  } else {
+#pragma unroll 1
+    for (int q0 = 0; q0 < nbg; q0 += D) pass(q0, std::true_type{});
+  }
+  if (j == 0) s_y[sl][r] = acc;
+  if (threadIdx.x < 8) s_w[threadIdx.x] = wv;
+  __syncthreads();
+  if ((int)threadIdx.x < 8) {
+    float o = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
+    for (int s2 = 0; s2 < slots; s2++) o = o + s_w[s2] * s_y[s2][threadIdx.x];
+    const size_t row = row0 + threadIdx.x;
+    if (row < (size_t)a.rows) a.out[row] = o;
+  }
+}
+
+// ===========================================================================
+// WeightMatrix::matvec with whole fold chains per wave
+// ===========================================================================
+//
+// out[r] = dot_q8_0 / dot_q4_0 (row r, quantize(x)) (src/tensor/matrix.rs:
+// 115-143, src/tensor/quant.rs:77-144), every row's chain in one wave.  A
+// wave takes RPW consecutive rows (8 or 4) of one 32-row tile with
+// LPR = 64 / RPW lanes per row: lane LPR r + j holds row r and block
+// LPR q + j of block group q, so a wave-load reads, per block, the RPW rows'
+// 16-byte chunks (128 or 64 contiguous bytes of the tile layout).  D groups
+// are in flight per wave; each group's LPR terms join the row's running
+// sum in block order by DPP shifts within the row's lanes (one DPP row of
+// 16 lanes holds one or two rows).  A work-group is NW waves of one tile.
+// With XQ the work-group quantizes x itself (all of it, 8 lanes per block,
+// into LDS; the same expressions as k_act_quant), so no quantization launch
+// comes first; otherwise the q8 blocks are read from act.  MAXNB bounds the
+// blocks per row (the LDS staging and the early loads are sized by it).
+// Four rows per wave give twice the waves of eight for the same matrix: the
+// launcher takes them when eight leave SIMDs without a wave.
 template <int DT, int RPW, int NW, int MAXNB, bool XQ>
 __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
   constexpr int CH = Layout<DT>::CH;
@@ -1549,7 +1697,10 @@ __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
   static_assert(RPW == 8 || RPW == 4, "a row's lanes lie in one DPP row");
   static_assert(NW * RPW <= TILE, "a work-group's rows lie in one tile");
   constexpr int MAXG = (MAXNB + LPR - 1) / LPR;
-  constexpr int D = MAXG < 16 / CH ? (MAXG + 3) / 4 * 4 : 16 / CH;  // groups in flight
+  // groups in flight: every group of a row when they fit (no loads past
+  // the row's end), else a ring of 16 / CH refilled in batches of four
+  constexpr int D = MAXG <= 16 / CH ? MAXG : 16 / CH;
+  static_assert(MAXG <= D || D % 4 == 0, "a refilled ring takes batches of four");
   constexpr int SPL = (MAXNB + 63) / 64;                  // scale pieces per lane
   constexpr int NT = 64 * NW;
   constexpr int BPP = NT / 8;                             // x blocks per pass (XQ)
@@ -1631,25 +1782,30 @@ __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
   auto pass = [&](int q0, auto reload) {
 #pragma unroll
     for (int d0 = 0; d0 < D; d0 += 4) {
+      const int ni = D - d0 < 4 ? D - d0 : 4;  // groups of this batch (compile time)
       const int qb = q0 + d0;
-      if (qb < nbg) {  // wave-uniform; the batch's four terms, then their sums in order
+      if (qb < nbg) {  // wave-uniform; the batch's terms, then their sums in order
         float t[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int b = min((qb + i) * LPR + j, nb - 1);
-          t[i] = block_term<DT>(cw[d0 + i], scl16[b * RPW + r], s_act + b);
+          if (i < ni) {
+            const int b = min((qb + i) * LPR + j, nb - 1);
+            t[i] = block_term<DT>(cw[d0 + i], scl16[b * RPW + r], s_act + b);
+          }
         }
-        if (qb + 4 <= nb / LPR) {  // four whole groups (wave-uniform): plain adds in block order
+        if (qb + ni <= nb / LPR) {  // whole groups (wave-uniform): plain adds in block order
 #pragma unroll
           for (int i = 0; i < 4; i++)
-            acc = row_fold(acc + t[i], t[i], std::make_integer_sequence<int, LPR - 1>{});
+            if (i < ni) acc = row_fold(acc + t[i], t[i], std::make_integer_sequence<int, LPR - 1>{});
         } else {
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            // groups past the row's end have n <= 0 and add nothing
-            const int n = nb - (qb + i) * LPR;  // blocks of the group inside the row
-            acc = n > 0 ? acc + t[i] : acc;
-            acc = row_fold_n(acc, t[i], n, std::make_integer_sequence<int, LPR - 1>{});
+            if (i < ni) {
+              // groups past the row's end have n <= 0 and add nothing
+              const int n = nb - (qb + i) * LPR;  // blocks of the group inside the row
+              acc = n > 0 ? acc + t[i] : acc;
+              acc = row_fold_n(acc, t[i], n, std::make_integer_sequence<int, LPR - 1>{});
+            }
           }
         }
       }
@@ -1901,6 +2057,21 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
     if (nbg <= 8 || dtype == Q8_0) HALE_DOWN_CHAIN(8);
     HALE_DOWN_CHAIN(16);
 #undef HALE_DOWN_CHAIN
+  }
+  // 4 to 8 routes over rows of at most 128 blocks: a wave per route
+  if (a.slots >= 4 && a.slots <= 8 && a.nb <= 128) {
+    const unsigned threads = 64u * (unsigned)a.slots;
+#define HALE_DOWN_SLOTS(N)                                                                  \
+  do {                                                                                      \
+    if (dtype == Q8_0) return launch(k_down_slots<Q8_0, N>, groups, threads, 0, st, a);     \
+    if (dtype == Q4_0) return launch(k_down_slots<Q4_0, N>, groups, threads, 0, st, a);     \
+  } while (0)
+    if (a.nb <= 24) HALE_DOWN_SLOTS(24);
+    if (a.nb <= 32) HALE_DOWN_SLOTS(32);
+    if (a.nb <= 48) HALE_DOWN_SLOTS(48);
+    if (a.nb <= 64) HALE_DOWN_SLOTS(64);
+    HALE_DOWN_SLOTS(128);
+#undef HALE_DOWN_SLOTS
   }
   if (dtype == Q8_0) return launch(k_down_combine<Q8_0, 8>, groups, 512, 0, st, a);
   if (dtype == Q4_0) return launch(k_down_combine<Q4_0, 8>, groups, 512, 0, st, a);

@@ -339,6 +339,28 @@ def test_moe_decode_few_tokens(ctx, dtype, hidden, inter, E, k, T):
     moe.close()
 
 
+@pytest.mark.parametrize("dtype,hidden,inter,k,T", [
+    (H.Q4_0, 256, 32, 4, 1),      # one block per row: a partial first group
+    (H.Q8_0, 512, 224, 5, 2),     # 7 blocks
+    (H.Q4_0, 2048, 768, 6, 1),    # 24 blocks: three whole groups
+    (H.Q8_0, 1024, 1280, 7, 3),   # 40 blocks, rows up to 64 blocks staged
+    (H.Q4_0, 4096, 2048, 8, 1),   # 64 blocks, the XCD row permutation (512 row groups)
+    (H.Q8_0, 256, 2080, 8, 2),    # 65 blocks: the 128-block variant, refilled ring (q8_0)
+    (H.Q4_0, 1024, 3200, 4, 4),   # 100 blocks
+    (H.Q8_0, 2080, 4096, 8, 1),   # 128 blocks, rows not a multiple of 32 row groups
+])
+def test_moe_decode_down_one_wave_per_route(ctx, dtype, hidden, inter, k, T):
+    """The down projection and combine of 4 to 8 routes over rows of up to
+    128 blocks: one work-group per 8 rows, one wave per route folding its
+    chains, then the route-order combine; every token bit-exact."""
+    E = 16
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=bool(k % 2),
+                              seed=hidden + inter + k + T)
+    moe = make_layer(ctx, L)
+    _few_tokens_check(L, moe, O.normal(9300 + T, T * hidden).reshape(T, hidden))
+    moe.close()
+
+
 @pytest.mark.parametrize("T", [2, 7, 15])
 def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
     """Config 1's layer over 2, 7 and 15 tokens (its grouped threshold is
