@@ -1329,178 +1329,29 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
 }
 
 // The same projection and combine with whole fold chains per wave, used
-// when every slot's activation blocks fit in LDS.  A work-group owns RG
-// output rows for every slot; wave w takes the chains (8 rows, slot) of row
-// subgroup w / SW and slots w % SW, w % SW + SW, ... (SW = min(slots, 8)).
-// A wave walks its slot's blocks in groups of eight: lane 8 r + j holds row
-// r, block 8 q + j of group q, so one wave-load is 8 cache lines of the tile
-// layout.  D groups are in flight; each group's terms fold into the row's
-// running sum as soon as they are computed, in block order, by DPP adds
-// within the row's 8 lanes, so no other wave or barrier is waited for until
-// the combine.  The chain's scales are staged in LDS first, in 16-byte
-// pieces (a block's scales for the wave's 8 rows).  RG = 16 for 2 or 3 slots (4 or 6 waves), 32 for 1 (4
-// waves); the launcher takes it for 1 to 3 slots.
+// for 1 to 3 routes when every slot's activation blocks fit in LDS.  A
+// work-group owns RG output rows for every slot (RG = 16 for 2 or 3 slots,
+// 32 for 1); wave w takes the chain (RPW rows, slot) of row subgroup
+// w / slots and slot w % slots.  Lane LPR r + j (LPR = 64 / RPW) holds row
+// r and block LPR q + j of group q, so a wave-load reads, per block, the
+// RPW rows' 16-byte chunks of the tile layout.  D groups are in flight; each
+// group's terms join the row's running sum in block order by DPP shifts
+// within the row's lanes, so no other wave or barrier is waited for until
+// the combine.  (The launcher takes eight rows per wave.)  The chain's scales are
+// staged in LDS first, one piece per block (its RPW rows' scales), loaded
+// before the ring (loads return in order, so the staging barrier waits for
+// them and the activations, not for the ring).
 constexpr int DOWN_ACT_MAX = 1024;  // activation blocks staged in LDS (48 KB)
 constexpr int DOWN_SCL_MAX = 4096;  // 16-byte scale pieces staged in LDS (64 KB): waves x blocks
 constexpr int DOWN_CHAIN_MAX_NB = 512;  // blocks per row: one scale piece per lane and 64 blocks
 
 __host__ __device__ inline int down_chain_rows(int slots) { return slots >= 4 ? 8 : (slots >= 2 ? 16 : 32); }
-__host__ __device__ inline int down_chain_waves(int slots) {
-  return down_chain_rows(slots) / 8 * (slots < 8 ? slots : 8);
+__host__ __device__ inline int down_chain_waves(int slots, int rpw) {
+  return down_chain_rows(slots) / rpw * (slots < 8 ? slots : 8);
 }
-
-template <int DT, int D>  // D: groups in flight per wave, a multiple of 4
-__global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
-  constexpr int CH = Layout<DT>::CH;
-  static_assert(D % 4 == 0, "groups go in batches of four");
-  __shared__ ActBlock s_act[DOWN_ACT_MAX];
-  // each wave's scales: one 16-byte piece (its 8 rows) per block, wave w at
-  // [w * nb, (w + 1) * nb)
-  __shared__ u32x4 s_scl[DOWN_SCL_MAX];
-  __shared__ float s_tot[DOWN_MAX_SLOTS][32];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x;
-  const int nb = a.nb, slots = a.slots;  // slots <= 3: one chain per wave
-  if (blockIdx.y > 0) {  // token blockIdx.y of a few-token decode
-    a.route_idx += (size_t)blockIdx.y * slots;
-    a.route_w += (size_t)blockIdx.y * slots;
-    a.hact += (size_t)blockIdx.y * slots * a.hact_stride;
-    a.out += (size_t)blockIdx.y * a.rows;
-  }
-  const int nbg = (nb + 7) / 8;
-  const int rg = down_chain_rows(slots);
-  const int sub = wave / slots, sl = wave % slots;
-  // every slot's activation blocks (independent of the routes): loads
-  // issued first, stored after the first weight loads.  The launcher takes
-  // D = 4 only for rows of at most 32 blocks and q4_0 D = 8 for at most 64,
-  // so those variants hold at most 3 x 8 D blocks; the others up to
-  // DOWN_ACT_MAX.  (Sizing them all for DOWN_ACT_MAX spilled the pieces.)
-  constexpr int MAXB = (D == 4 || (DT == Q4_0 && D == 8)) ? 3 * 8 * D : DOWN_ACT_MAX;
-  constexpr int APT = (MAXB * 3 + 255) / 256;  // pieces per thread, at most (256+ threads)
-  const int npieces = slots * nb * 3;
-  u32x4 av[APT];
-#pragma unroll
-  for (int m = 0; m < APT; m++) {
-    const int i = threadIdx.x + m * blockDim.x;
-    if (i < npieces) {
-      const int sl = i / (nb * 3), rem = i - sl * nb * 3;
-      av[m] = ((const u32x4*)(a.hact + (size_t)sl * a.hact_stride))[rem];
-    }
-  }
-  // The row groups of a 32-row tile share its scale lines; work-group g runs
-  // on XCD g % 8, so when the grid allows the groups of one tile get ids of
-  // one residue class (a permutation of the row groups).
-  const int per_tile = 32 / rg;
-  size_t row0 = (size_t)g * rg;
-  if (per_tile > 1 && gridDim.x % (8 * per_tile) == 0) {
-    const int gx = g & 7, gj = g >> 3;
-    row0 = (size_t)(gx + 8 * (gj / per_tile)) * TILE + (size_t)(gj % per_tile) * rg;
-  }
-  const int r = lane >> 3, j = lane & 7;
-  const size_t rowg = row0 + (size_t)sub * 8;
-  const size_t tile = rowg / TILE;
-  const int rt = (int)(rowg % TILE) + r;
-  const size_t row_off = (tile * nb * CH * TILE + rt) * 16;
-
-  u32x4 cw[D][CH];
-  const size_t e = (size_t)__builtin_amdgcn_readfirstlane(a.route_idx[sl]);
-  const uint8_t* cbase = a.codes + e * a.codes_stride + row_off;
-  // group q's codes into ring slot d (groups past the end are clamped to
-  // the last: in-bounds loads that are never used)
-  auto load = [&](int d, int q) {
-    const int b = min(min(q, nbg - 1) * 8 + j, nb - 1);
-#pragma unroll
-    for (int c = 0; c < CH; c++)
-      cw[d][c] = __builtin_nontemporal_load((const u32x4*)(cbase + ((size_t)b * CH + c) * TILE * 16));
-  };
-  // The chain's scales: the 8 rows' scales of a block are 16 contiguous bytes
-  // of the tile's scale line, so a lane loads whole pieces (blocks lane,
-  // lane + 64, ...) and parks them in LDS; a per-block 2-byte load per lane
-  // would touch 8 lines per group for 128 useful bytes.  The pieces (at
-  // most 512: the launcher keeps nb <= 512) are loaded before the ring's
-  // codes: loads return in order, so they and the activation pieces can be
-  // parked while the codes are still in flight, and the staging barrier
-  // does not wait for the ring.
-  u32x4* scl = s_scl + wave * nb;
-  const u32x4* sp = (const u32x4*)(a.scales + e * a.scales_stride + tile * nb * TILE + (rowg % TILE));
-  {
-    u32x4 v[8];
-#pragma unroll
-    for (int m = 0; m < 8; m++)
-      if (lane + 64 * m < nb) v[m] = sp[(size_t)(lane + 64 * m) * (TILE * 2 / 16)];
-#pragma unroll
-    for (int d = 0; d < D; d++) load(d, d);
-#pragma unroll
-    for (int m = 0; m < 8; m++)
-      if (lane + 64 * m < nb) scl[lane + 64 * m] = v[m];
-  }
-#pragma unroll
-  for (int m = 0; m < APT; m++) {
-    const int i = threadIdx.x + m * blockDim.x;
-    if (i < npieces) ((u32x4*)s_act)[i] = av[m];
-  }
-  const uint16_t* scl16 = (const uint16_t*)scl;
-  __syncthreads();  // s_act, s_scl
-
-  {
-    const ActBlock* act = s_act + (size_t)sl * nb;
-    float acc = 0.0f;  // row r's dot product (valid in lane 8 r)
-#pragma unroll 1
-    for (int q0 = 0; q0 < nbg; q0 += D) {
-#pragma unroll
-      for (int d0 = 0; d0 < D; d0 += 4) {
-        const int qb = q0 + d0;
-        if (qb < nbg) {  // wave-uniform; the batch's four terms, then their sums in order
-          float t[4];
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int b = min((qb + i) * 8 + j, nb - 1);
-            t[i] = block_term<DT>(cw[d0 + i], scl16[b * 8 + r], act + b);
-          }
-#define HALE_ROW_TERM(k) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ti), 0x100 + (k), 0xF, 0xF, false))
-          if (qb + 4 <= nb / 8) {  // four whole groups (wave-uniform): plain adds in block order
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const float ti = t[i];
-              acc = acc + ti;
-              acc = acc + HALE_ROW_TERM(1);
-              acc = acc + HALE_ROW_TERM(2);
-              acc = acc + HALE_ROW_TERM(3);
-              acc = acc + HALE_ROW_TERM(4);
-              acc = acc + HALE_ROW_TERM(5);
-              acc = acc + HALE_ROW_TERM(6);
-              acc = acc + HALE_ROW_TERM(7);
-            }
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              // groups past the row's end have n <= 0 and add nothing
-              const int n = nb - (qb + i) * 8;  // blocks of the group inside the row
-              const float ti = t[i];
-              acc = n > 0 ? acc + ti : acc;
-#define HALE_ROW_TERM_IF(k) acc = (k) < n ? acc + HALE_ROW_TERM(k) : acc;
-              HALE_ROW_TERM_IF(1) HALE_ROW_TERM_IF(2) HALE_ROW_TERM_IF(3) HALE_ROW_TERM_IF(4)
-              HALE_ROW_TERM_IF(5) HALE_ROW_TERM_IF(6) HALE_ROW_TERM_IF(7)
-#undef HALE_ROW_TERM_IF
-            }
-          }
-#undef HALE_ROW_TERM
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) load(d0 + i, qb + i + D);
-      }
-    }
-    if (j == 0) s_tot[sl][sub * 8 + r] = acc;
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < rg) {
-    float acc = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
-    for (int s2 = 0; s2 < slots; s2++) acc = acc + a.route_w[s2] * s_tot[s2][threadIdx.x];
-    const size_t row = row0 + threadIdx.x;
-    if (row < (size_t)a.rows) a.out[row] = acc;
-  }
+// bytes of k_down_chain's staging (its dynamic LDS)
+static inline size_t down_chain_lds(int slots, int nb, int rpw) {
+  return (size_t)slots * nb * 48 + (size_t)down_chain_waves(slots, rpw) * nb * 2 * rpw;
 }
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -1521,6 +1372,150 @@ template <int... K>
 __device__ __forceinline__ float row_fold_n(float acc, float t, int n, std::integer_sequence<int, K...>) {
   ((acc = K + 1 < n ? acc + row_term<K + 1>(t) : acc), ...);
   return acc;
+}
+
+template <int DT, int RPW, int D>  // D: groups in flight per wave, a multiple of 4
+__global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
+  constexpr int CH = Layout<DT>::CH;
+  constexpr int LPR = 64 / RPW;
+  static_assert(D % 4 == 0, "groups go in batches of four");
+  static_assert(RPW == 8 || RPW == 4, "a row's lanes lie in one DPP row");
+  typedef typename std::conditional<RPW == 8, u32x4, u32x2>::type Piece;
+  // LDS sized at launch (down_chain_lds): every slot's activation blocks
+  // (slot s at [s * nb]), then each wave's scale pieces, one per block,
+  // wave w at [w * nb, (w + 1) * nb)
+  extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn_chain[];
+  ActBlock* s_act = (ActBlock*)s_dyn_chain;
+  Piece* s_scl = (Piece*)(s_dyn_chain + (size_t)a.slots * a.nb * 3);
+  __shared__ float s_tot[3][32];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x;
+  const int nb = a.nb, slots = a.slots;  // slots <= 3: one chain per wave
+  if (blockIdx.y > 0) {  // token blockIdx.y of a few-token decode
+    a.route_idx += (size_t)blockIdx.y * slots;
+    a.route_w += (size_t)blockIdx.y * slots;
+    a.hact += (size_t)blockIdx.y * slots * a.hact_stride;
+    a.out += (size_t)blockIdx.y * a.rows;
+  }
+  const int nbg = (nb + LPR - 1) / LPR;
+  const int rg = down_chain_rows(slots);
+  const int sub = wave / slots, sl = wave % slots;
+  // every slot's activation blocks (independent of the routes): loads
+  // issued first, stored after the first weight loads.  The launcher takes
+  // D = 4 only for rows of at most 4 LPR blocks and q4_0 D = 8 for at most
+  // 8 LPR, so those variants hold at most 3 x LPR D blocks; the others up
+  // to DOWN_ACT_MAX.  (Sizing them all for DOWN_ACT_MAX spilled the pieces.)
+  constexpr int MAXB = (D == 4 || (DT == Q4_0 && D == 8)) ? 3 * LPR * D : DOWN_ACT_MAX;
+  constexpr int APT = (MAXB * 3 + 255) / 256;  // pieces per thread, at most (256+ threads)
+  const int npieces = slots * nb * 3;
+  u32x4 av[APT];
+#pragma unroll
+  for (int m = 0; m < APT; m++) {
+    const int i = threadIdx.x + m * blockDim.x;
+    if (i < npieces) {
+      const int sl = i / (nb * 3), rem = i - sl * nb * 3;
+      av[m] = ((const u32x4*)(a.hact + (size_t)sl * a.hact_stride))[rem];
+    }
+  }
+  // The row groups of a 32-row tile share its scale lines; work-group g runs
+  // on XCD g % 8, so when the grid allows the groups of one tile get ids of
+  // one residue class (a permutation of the row groups).
+  const int per_tile = 32 / rg;
+  size_t row0 = (size_t)g * rg;
+  if (per_tile > 1 && gridDim.x % (8 * per_tile) == 0) {
+    const int gx = g & 7, gj = g >> 3;
+    row0 = (size_t)(gx + 8 * (gj / per_tile)) * TILE + (size_t)(gj % per_tile) * rg;
+  }
+  const int r = lane / LPR, j = lane % LPR;
+  const size_t rowg = row0 + (size_t)sub * RPW;
+  const size_t tile = rowg / TILE;
+  const int rt = (int)(rowg % TILE) + r;
+  const size_t row_off = (tile * nb * CH * TILE + rt) * 16;
+
+  u32x4 cw[D][CH];
+  const size_t e = (size_t)__builtin_amdgcn_readfirstlane(a.route_idx[sl]);
+  const uint8_t* cbase = a.codes + e * a.codes_stride + row_off;
+  // group q's codes into ring slot d (groups past the end are clamped to
+  // the last: in-bounds loads that are never used)
+  auto load = [&](int d, int q) {
+    const int b = min(min(q, nbg - 1) * LPR + j, nb - 1);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+      cw[d][c] = __builtin_nontemporal_load((const u32x4*)(cbase + ((size_t)b * CH + c) * TILE * 16));
+  };
+  // The chain's scales: the RPW rows' scales of a block are contiguous in
+  // the tile's scale line, so a lane loads whole pieces (blocks lane,
+  // lane + 64, ...) and parks them in LDS; a per-block 2-byte load per lane
+  // would touch a line per row group for a few useful bytes.  The pieces
+  // (at most 512: the launcher keeps nb <= 512) are loaded before the
+  // ring's codes: loads return in order, so they and the activation pieces
+  // can be parked while the codes are still in flight, and the staging
+  // barrier does not wait for the ring.
+  Piece* scl = s_scl + wave * nb;
+  const Piece* sp = (const Piece*)(a.scales + e * a.scales_stride + tile * nb * TILE + (rowg % TILE));
+  {
+    Piece v[8];
+#pragma unroll
+    for (int m = 0; m < 8; m++)
+      if (lane + 64 * m < nb) v[m] = sp[(size_t)(lane + 64 * m) * (TILE * 2 / sizeof(Piece))];
+#pragma unroll
+    for (int d = 0; d < D; d++) load(d, d);
+#pragma unroll
+    for (int m = 0; m < 8; m++)
+      if (lane + 64 * m < nb) scl[lane + 64 * m] = v[m];
+  }
+#pragma unroll
+  for (int m = 0; m < APT; m++) {
+    const int i = threadIdx.x + m * blockDim.x;
+    if (i < npieces) ((u32x4*)s_act)[i] = av[m];
+  }
+  const uint16_t* scl16 = (const uint16_t*)scl;
+  __syncthreads();  // s_act, s_scl
+
+  {
+    const ActBlock* act = s_act + (size_t)sl * nb;
+    float acc = 0.0f;  // row r's dot product (valid in lane LPR r)
+#pragma unroll 1
+    for (int q0 = 0; q0 < nbg; q0 += D) {
+#pragma unroll
+      for (int d0 = 0; d0 < D; d0 += 4) {
+        const int qb = q0 + d0;
+        if (qb < nbg) {  // wave-uniform; the batch's four terms, then their sums in order
+          float t[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int b = min((qb + i) * LPR + j, nb - 1);
+            t[i] = block_term<DT>(cw[d0 + i], scl16[b * RPW + r], act + b);
+          }
+          if (qb + 4 <= nb / LPR) {  // four whole groups (wave-uniform): plain adds in block order
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc = row_fold(acc + t[i], t[i], std::make_integer_sequence<int, LPR - 1>{});
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              // groups past the row's end have n <= 0 and add nothing
+              const int n = nb - (qb + i) * LPR;  // blocks of the group inside the row
+              acc = n > 0 ? acc + t[i] : acc;
+              acc = row_fold_n(acc, t[i], n, std::make_integer_sequence<int, LPR - 1>{});
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) load(d0 + i, qb + i + D);
+      }
+    }
+    if (j == 0) s_tot[sl][sub * RPW + r] = acc;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < rg) {
+    float acc = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
+    for (int s2 = 0; s2 < slots; s2++) acc = acc + a.route_w[s2] * s_tot[s2][threadIdx.x];
+    const size_t row = row0 + threadIdx.x;
+    if (row < (size_t)a.rows) a.out[row] = acc;
+  }
 }
 
 // ===========================================================================
@@ -2042,15 +2037,20 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   // A wave per (slot, 8 rows) pays off when few routes leave many rows per
   // work-group (top-1..3); top-4 and wider use the block-group pipeline.
   if (a.slots <= 3 && a.nb <= DOWN_CHAIN_MAX_NB && a.slots * a.nb <= DOWN_ACT_MAX &&
-      down_chain_waves(a.slots) * a.nb <= DOWN_SCL_MAX) {
+      down_chain_waves(a.slots, 8) * a.nb <= DOWN_SCL_MAX) {
     const int rg = down_chain_rows(a.slots);
     const dim3 grid((unsigned)(padded_rows((size_t)a.rows) / rg), T);
-    const unsigned threads = 64 * down_chain_waves(a.slots);
+    // eight rows per wave: four (twice the waves, each row's chunks in
+    // 64-byte halves of the tile layout's lines) measured slower on every
+    // top-1 and top-2 shape tried, the small ones included
+    const int rpw = 8;
+    const unsigned threads = 64 * down_chain_waves(a.slots, rpw);
+    const uint32_t lds = (uint32_t)down_chain_lds(a.slots, a.nb, rpw);
     const int nbg = (a.nb + 7) / 8;
-#define HALE_DOWN_CHAIN(D)                                                                  \
-  do {                                                                                      \
-    if (dtype == Q8_0) return launch(k_down_chain<Q8_0, D>, grid, threads, 0, st, a);       \
-    if (dtype == Q4_0) return launch(k_down_chain<Q4_0, D>, grid, threads, 0, st, a);       \
+#define HALE_DOWN_CHAIN(D)                                                                     \
+  do {                                                                                         \
+    if (dtype == Q8_0) return launch(k_down_chain<Q8_0, 8, D>, grid, threads, lds, st, a);     \
+    if (dtype == Q4_0) return launch(k_down_chain<Q4_0, 8, D>, grid, threads, lds, st, a);     \
   } while (0)
     // (k_down_chain sizes its activation staging by these bounds)
     if (nbg <= 4) HALE_DOWN_CHAIN(4);
