@@ -45,6 +45,7 @@ int8 MFMA for the 2048-token one).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--prefill-only] [--decode-eager]
+                       [--eager-leg kernels|float|expert|attention]
                        [--copy-calibration BYTES]
 """
 import argparse
@@ -291,6 +292,90 @@ def decode_eager(args):
         m.close()
     ctx.close()
     return 2 * L
+
+
+def eager_leg(name, passes=3):
+    """One secondary workload launched eagerly (no graph), for kernel traces
+    and counter runs: `kernels` (the reference's 4096 x 4096 matvec per
+    dtype, rotated copies), `float` (the bf16 vocabulary projection and the
+    dense f32 matrix), `expert` (the q8_0 Qwen3-30B expert, 128 copies in
+    turn) or `attention` (RMSNorm + attention decode).  Returns the number
+    of calls."""
+    ctx = H.Context(0)
+    calls = 0
+    if name in ("kernels", "float"):
+        specs = ([(n, dt, KB_ROWS, KB_COLS, c) for n, dt, _, c in KBENCH] if name == "kernels"
+                 else [(n, dt, r, c, k) for n, dt, r, c, k in FLOAT_MATVEC])
+        for label, dt, rows, cols, copies in specs:
+            nbytes = rows * H.row_bytes(dt, cols)
+            vals = ctx.malloc(rows * cols * 4)
+            if name == "kernels":
+                vals.upload(kbench_values())
+            else:
+                vals.fill_normal(900, rows * cols, 0.0, 0.02)
+            enc = ctx.malloc(nbytes)
+            ctx.check(H.lib().hale_encode_rows_device(ctx.handle, dt, rows, cols, H._vp(vals.address),
+                                                      H._vp(enc.address)), "encode")
+            vals.free()
+            mats = []
+            for _ in range(copies):
+                h = H._vp()
+                ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, dt, rows, cols, H._vp(enc.address),
+                                                            nbytes, H.C.byref(h)), "upload")
+                mats.append(H.WeightMatrix(ctx, h, rows, cols, dt))
+            enc.free()
+            x = ctx.malloc(cols * 4)
+            x.upload(np.full(cols, 0.5, np.float32))
+            out = ctx.malloc(rows * 4)
+            for _ in range(passes):
+                for m in mats:
+                    ctx.check(H.lib().hale_matvec_device(ctx.handle, m.handle, H._vp(x.address),
+                                                         H._vp(out.address)), "matvec")
+                    calls += 1
+            ctx.synchronize()
+            for m in mats:
+                m.close()
+            x.free()
+            out.free()
+            log(f"eager {name}: {label} done")
+    elif name == "expert":
+        hid, inter, dt = 2048, 768, H.Q8_0
+        vals = ctx.malloc(inter * hid * 4)
+        enc = ctx.malloc(inter * H.row_bytes(dt, hid))
+        experts = []
+        for c in range(128):
+            mats = []
+            for j, (rows, cols) in enumerate(((inter, hid), (inter, hid), (hid, inter))):
+                vals.fill_normal(31 + 3 * c + j, rows * cols, 0.0, 0.02)
+                ctx.check(H.lib().hale_encode_rows_device(ctx.handle, dt, rows, cols, H._vp(vals.address),
+                                                          H._vp(enc.address)), "encode")
+                h = H._vp()
+                ctx.check(H.lib().hale_matrix_upload_device(ctx.handle, dt, rows, cols, H._vp(enc.address),
+                                                            rows * H.row_bytes(dt, cols), H.C.byref(h)), "upload")
+                mats.append(H.WeightMatrix(ctx, h, rows, cols, dt))
+            experts.append(H.Expert(*mats))
+        vals.free()
+        enc.free()
+        xs = ctx.malloc(16 * hid * 4)
+        xs.fill_normal(8, 16 * hid, 0.0, 1.0)
+        out = ctx.malloc(hid * 4)
+        for s in range(passes * 128):
+            experts[s % 128].forward_device(xs.offset((s % 16) * hid * 4), out.address)
+            calls += 1
+        ctx.synchronize()
+        for e in experts:
+            for m in (e.gate, e.up, e.down):
+                m.close()
+    elif name == "attention":
+        ctx.close()
+        for spec in ATTENTION:
+            r = gpu_attention(*spec)
+            calls += r.get("calls", 64)
+        return calls
+    else:
+        raise SystemExit(f"unknown eager leg {name!r}: kernels, float, expert or attention")
+    ctx.close()
+    return calls
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode_q4_qwen3_30b.txt")
@@ -915,6 +1000,9 @@ def main():
                     help="only two eager decode passes over the layers (for counter runs)")
     ap.add_argument("--decode-workload", default="", metavar="NAME",
                     help="with --decode-eager: one of the larger decode layers")
+    ap.add_argument("--eager-leg", default="", metavar="NAME",
+                    help="only one secondary workload, launched eagerly (for counter and trace runs): "
+                         "kernels, float, expert or attention")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only time the plain copy kernel over BYTES (counter yardstick)")
     args = ap.parse_args()
@@ -927,6 +1015,9 @@ def main():
         return
     if args.decode_eager:
         print(json.dumps({"decode_eager_steps": decode_eager(args)}), flush=True)
+        return
+    if args.eager_leg:
+        print(json.dumps({"eager_leg": args.eager_leg, "calls": eager_leg(args.eager_leg)}), flush=True)
         return
     if args.prefill_only:
         res = [gpu_prefill(name, dt, hid, inter, ex, k, tok, reps=3, bound=bound, router=False)

@@ -130,8 +130,16 @@ struct MatvecArgs {
   const float* x;        // or null
   const ActBlock* act;   // used when x is null
   float* out;
+  // launch_matvec_pair: a second matrix of the same shape and input
+  // (Expert::forward's gate and up); out then receives silu(first row's
+  // dot) * (second row's dot) per row, the f32 h of the SwiGLU
+  const uint8_t* codes2;
+  const uint16_t* scales2;
 };
 hipError_t launch_matvec(int dtype, const MatvecArgs& a, hipStream_t st);
+// both matrices of a in one launch, x quantized in the kernel:
+// out[r] = silu(dot(codes row r, x)) * dot(codes2 row r, x)
+hipError_t launch_matvec_pair(int dtype, const MatvecArgs& a, hipStream_t st);
 constexpr int MATVEC_XQ_MAX_NB = 128;  // blocks per row launch_matvec quantizes x for
 constexpr int MATVEC_MAX_NB = 512;     // blocks per row it takes with act given
 

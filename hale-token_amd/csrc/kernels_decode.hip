@@ -1685,12 +1685,14 @@ __global__ __launch_bounds__(512) void k_down_slots(DownArgs a) {
 // blocks per row (the LDS staging and the early loads are sized by it).
 // Four rows per wave give twice the waves of eight for the same matrix: the
 // launcher takes them when eight leave SIMDs without a wave.
-template <int DT, int RPW, int NW, int MAXNB, bool XQ>
+template <int DT, int RPW, int NW, int MAXNB, bool XQ, bool PAIR = false>
 __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
+  static_assert(XQ || !PAIR, "the pair form quantizes its input");
+  static_assert(!PAIR || NW % 2 == 0, "the pair form splits the waves between the matrices");
   constexpr int CH = Layout<DT>::CH;
   constexpr int LPR = 64 / RPW;                           // lanes (and blocks of a group) per row
   static_assert(RPW == 8 || RPW == 4, "a row's lanes lie in one DPP row");
-  static_assert(NW * RPW <= TILE, "a work-group's rows lie in one tile");
+  static_assert((PAIR ? NW / 2 : NW) * RPW <= TILE, "a work-group's rows lie in one tile");
   constexpr int MAXG = (MAXNB + LPR - 1) / LPR;
   // groups in flight: every group of a row when they fit (no loads past
   // the row's end), else a ring of 16 / CH refilled in batches of four
@@ -1712,7 +1714,17 @@ __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nb = a.nb, nbg = (nb + LPR - 1) / LPR;
-  const size_t rowg = ((size_t)blockIdx.x * NW + wave) * RPW;  // the wave's first row
+  // PAIR (Expert::forward's gate and up): waves NW/2 .. NW - 1 take the
+  // second matrix's rows of the same row range as waves 0 .. NW/2 - 1 take
+  // the first's, and the work-group writes silu(first) * second
+  constexpr int RW = PAIR ? NW / 2 : NW;  // row chains per matrix
+  const int half = PAIR ? wave / RW : 0;
+  const int wv = wave - half * RW;
+  if (PAIR && half) {
+    a.codes = a.codes2;
+    a.scales = a.scales2;
+  }
+  const size_t rowg = ((size_t)blockIdx.x * RW + wv) * RPW;  // the wave's first row
   const size_t tile = rowg / TILE;
   const int r = lane / LPR, j = lane % LPR;
   const int rt = (int)(rowg % TILE) + r;
@@ -1820,7 +1832,23 @@ __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
     for (int q0 = 0; q0 < nbg; q0 += D) pass(q0, std::true_type{});
   }
   const size_t row = rowg + r;
-  if (j == 0 && row < (size_t)a.rows) a.out[row] = acc;
+  if constexpr (PAIR) {
+    // h = silu(g) * u of the work-group's rows (the gate/up epilogue's
+    // expression), by wave 0 with every lane taking part in the exp table
+    __shared__ float s_gu[2][RW * RPW];
+    if (j == 0) s_gu[half][wv * RPW + r] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      ExpTable tab;
+      tab.load();
+      const int i = lane % (RW * RPW);
+      const float h = wave_silu(s_gu[0][i], tab) * s_gu[1][i];
+      const size_t hrow = (size_t)blockIdx.x * RW * RPW + lane;
+      if (lane < RW * RPW && hrow < (size_t)a.rows) a.out[hrow] = h;
+    }
+  } else {
+    if (j == 0 && row < (size_t)a.rows) a.out[row] = acc;
+  }
 }
 
 // Per-block i32 sums of every row (the `isum` of dot_q8_0 / dot_q4_0), one
@@ -2108,6 +2136,8 @@ hipError_t launch_matvec(int dtype, const MatvecArgs& a, hipStream_t st) {
     if (a.nb <= 64) HALE_MV_NW(D, 64, XQ);                                 \
     if (a.nb <= MATVEC_XQ_MAX_NB) HALE_MV_NW(D, MATVEC_XQ_MAX_NB, XQ);      \
   } while (0)
+#undef HALE_MV
+#define HALE_MV(D, R, NW, MAXNB, XQ) launch(k_matvec_chain<D, R, NW, MAXNB, XQ>, grid, 64 * NW, 0, st, a)
   if (dtype == Q8_0) {
     if (xq) HALE_MV_NB(Q8_0, true);
     HALE_MV_NB(Q8_0, false);
@@ -2117,6 +2147,41 @@ hipError_t launch_matvec(int dtype, const MatvecArgs& a, hipStream_t st) {
     HALE_MV_NB(Q4_0, false);
     HALE_MV_NW(Q4_0, MATVEC_MAX_NB, false);
   }
+#undef HALE_MV_NB
+#undef HALE_MV_NW
+#undef HALE_MV
+}
+
+// Both matrices in one launch: a work-group's first half of waves folds the
+// first matrix's rows, its second half the same rows of the second, and it
+// writes silu(first) * second; rows per wave and waves chosen as for one
+// matrix of twice the rows.
+hipError_t launch_matvec_pair(int dtype, const MatvecArgs& a, hipStream_t st) {
+  if (a.nb < 1 || a.rows < 1 || !a.x || !a.codes2 || !a.scales2) return hipErrorInvalidValue;
+  if (dtype != Q8_0 && dtype != Q4_0) return hipErrorInvalidValue;
+  if (((uintptr_t)a.x & 15) || a.nb > MATVEC_XQ_MAX_NB) return hipErrorNotSupported;
+  const size_t prow = padded_rows((size_t)a.rows);
+  const int rpw = 2 * prow / 8 >= 1024 ? 8 : 4;
+  int nw = 2 * TILE / rpw;  // waves per work-group, both matrices
+  while (nw > 2 && 2 * prow / (size_t)(rpw * nw) < 256) nw /= 2;
+  const unsigned grid = (unsigned)(2 * prow / (size_t)(rpw * nw));
+#define HALE_MV(D, R, NW, MAXNB) launch(k_matvec_chain<D, R, NW, MAXNB, true, true>, grid, 64 * NW, 0, st, a)
+#define HALE_MV_NW(D, MAXNB)                                                                   \
+  do {                                                                                         \
+    if (rpw == 8)                                                                              \
+      return nw == 8 ? HALE_MV(D, 8, 8, MAXNB) : (nw == 4 ? HALE_MV(D, 8, 4, MAXNB) : HALE_MV(D, 8, 2, MAXNB)); \
+    return nw == 16 ? HALE_MV(D, 4, 16, MAXNB)                                                 \
+                    : (nw == 8 ? HALE_MV(D, 4, 8, MAXNB)                                       \
+                               : (nw == 4 ? HALE_MV(D, 4, 4, MAXNB) : HALE_MV(D, 4, 2, MAXNB))); \
+  } while (0)
+#define HALE_MV_NB(D)                                                  \
+  do {                                                                 \
+    if (a.nb <= 32) HALE_MV_NW(D, 32);                                 \
+    if (a.nb <= 64) HALE_MV_NW(D, 64);                                 \
+    HALE_MV_NW(D, MATVEC_XQ_MAX_NB);                                   \
+  } while (0)
+  if (dtype == Q8_0) HALE_MV_NB(Q8_0);
+  else HALE_MV_NB(Q4_0);
 #undef HALE_MV_NB
 #undef HALE_MV_NW
 #undef HALE_MV

@@ -832,10 +832,12 @@ static int expert_check(hale_ctx* c, const hale_matrix* gate, const hale_matrix*
   return HALE_OK;
 }
 
-// Bytes of scratch expert_enqueue needs after `lead` bytes of the caller's.
+// Bytes of scratch expert_enqueue needs after `lead` bytes of the caller's:
+// x's q8 blocks, h's q8 blocks, then h in f32.
 static size_t expert_scratch_bytes(const hale_matrix* gate, size_t lead) {
   const size_t nbh = gate->cols / HALE_QK, nbi = gate->rows / HALE_QK;
-  return lead + align_up(nbh * sizeof(ActBlock), 256) + nbi * sizeof(ActBlock);
+  return lead + align_up(nbh * sizeof(ActBlock), 256) + align_up(nbi * sizeof(ActBlock), 256) +
+         align_up(gate->rows * 4, 256);
 }
 
 // Enqueues Expert::forward for device x/out: q8 activation blocks of x, the
@@ -850,6 +852,34 @@ static int expert_enqueue(hale_ctx* c, const hale_matrix* gate, const hale_matri
   if (rc) return rc;
   ActBlock* act = (ActBlock*)((char*)s + lead);
   ActBlock* hact = (ActBlock*)((char*)s + lead + align_up(nbh * sizeof(ActBlock), 256));
+  float* gv = (float*)((char*)hact + align_up(nbi * sizeof(ActBlock), 256));  // f32 h
+  // An aligned x of up to 128 blocks, with h of up to 128: gate and up rows
+  // in one launch of row chains (x quantized in the kernel), a work-group's
+  // gate and up chains of the same rows writing their f32 h = silu(g) * u;
+  // then down, which quantizes h while staging its input (the same
+  // expressions as requantizing h in the gate/up epilogue, so the same
+  // bits), each launch spread over rows rather than over h's 32-row blocks.
+  if (((uintptr_t)dx & 15) == 0 && nbh <= (size_t)MATVEC_XQ_MAX_NB && nbi <= (size_t)MATVEC_XQ_MAX_NB) {
+    MatvecArgs p{};
+    p.codes = gate->codes;
+    p.scales = gate->scales;
+    p.codes2 = up->codes;
+    p.scales2 = up->scales;
+    p.nb = (int)nbh;
+    p.rows = (int)I;
+    p.x = dx;
+    p.out = gv;
+    LAUNCH(c, K_GATE_UP, launch_matvec_pair(gate->dtype, p, c->stream));
+    MatvecArgs d{};
+    d.codes = down->codes;
+    d.scales = down->scales;
+    d.nb = (int)nbi;
+    d.rows = (int)H;
+    d.x = gv;
+    d.out = dout;
+    LAUNCH(c, K_DOWN, launch_matvec(down->dtype, d, c->stream));
+    return HALE_OK;
+  }
   // the gate/up kernel quantizes an aligned x of up to 128 blocks itself
   const bool fuse = ((uintptr_t)dx & 15) == 0 && nbh <= (size_t)GEMV_X_MAX_NB;
   if (!fuse) LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nbh, act, c->stream));
