@@ -1724,7 +1724,17 @@ __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
     a.codes = a.codes2;
     a.scales = a.scales2;
   }
-  const size_t rowg = ((size_t)blockIdx.x * RW + wv) * RPW;  // the wave's first row
+  // The row groups of a 32-row tile share its lines (codes when a wave
+  // takes 4 rows, scales always); work-group g runs on XCD g % 8, so when
+  // the grid allows, the groups of one tile get ids of one residue class (a
+  // permutation of the row groups)
+  constexpr int PER_TILE = TILE / (RW * RPW);
+  size_t grp = blockIdx.x;
+  if (PER_TILE > 1 && gridDim.x % (8 * PER_TILE) == 0) {
+    const size_t gx = grp & 7, gj = grp >> 3;
+    grp = (gx + 8 * (gj / PER_TILE)) * PER_TILE + gj % PER_TILE;
+  }
+  const size_t rowg = (grp * RW + wv) * RPW;  // the wave's first row
   const size_t tile = rowg / TILE;
   const int r = lane / LPR, j = lane % LPR;
   const int rt = (int)(rowg % TILE) + r;
@@ -1843,7 +1853,7 @@ __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
       tab.load();
       const int i = lane % (RW * RPW);
       const float h = wave_silu(s_gu[0][i], tab) * s_gu[1][i];
-      const size_t hrow = (size_t)blockIdx.x * RW * RPW + lane;
+      const size_t hrow = grp * RW * RPW + lane;
       if (lane < RW * RPW && hrow < (size_t)a.rows) a.out[hrow] = h;
     }
   } else {
