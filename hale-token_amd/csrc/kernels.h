@@ -143,6 +143,40 @@ hipError_t launch_matvec_pair(int dtype, const MatvecArgs& a, hipStream_t st);
 constexpr int MATVEC_XQ_MAX_NB = 128;  // blocks per row launch_matvec quantizes x for
 constexpr int MATVEC_MAX_NB = 512;     // blocks per row it takes with act given
 
+// Shapes the fast decode and grouped kernels take; a layer beyond any of
+// them runs the general path below (any number of experts, top_k, hidden
+// and intermediate sizes).
+constexpr size_t FAST_MAX_E = 1024, FAST_MAX_H = 8192, FAST_MAX_K = 64, FAST_MAX_NB = 512;
+
+// General-shape matvec: lane per row, every block of the row in order, any
+// row length.  Grid row y (of ny) reads the q8 blocks act + (y / act_div) *
+// nb, uses expert route[y] (planes at codes + e * codes_stride; expert 0
+// without route) and writes out + y * out_stride.
+struct RowsArgs {
+  const uint8_t* codes;
+  const uint16_t* scales;
+  size_t codes_stride, scales_stride;
+  const int* route;
+  int nb, rows;
+  const ActBlock* act;
+  int act_div;
+  float* out;
+  size_t out_stride;
+};
+hipError_t launch_matvec_rows(int dtype, const RowsArgs& a, int ny, hipStream_t st);
+// h = silu(g) * u elementwise, quantized to q8 blocks (nblocks blocks of 32)
+hipError_t launch_swiglu_quant(const float* g, const float* u, size_t nblocks, ActBlock* h,
+                               hipStream_t st);
+// MoeLayer::route for any E and k <= E from T tokens' logits: softmax,
+// top-k, renormalisation; ebuf holds T * E floats of scratch
+hipError_t launch_route_select_wide(const float* logits, int E, int k, int normalize, int T,
+                                    float* ebuf, int* route_idx, float* route_w,
+                                    unsigned long long* stats, hipStream_t st);
+// out[t] = 0, then out[t] = out[t] + w[t][s] * y[t * k + s] for s in route
+// order (kernels_prefill.hip's combine with the rows in (token, slot) order)
+hipError_t launch_combine_rows(const float* y, const float* route_w, int k, int H, int T,
+                               float* out, hipStream_t st);
+
 hipError_t launch_repack(int dtype, const uint8_t* aos, size_t rows, size_t cols, uint8_t* codes,
                          uint16_t* scales, hipStream_t st);
 hipError_t launch_unpack(int dtype, const uint8_t* codes, const uint16_t* scales, size_t rows,

@@ -1861,6 +1861,163 @@ __global__ __launch_bounds__(64 * NW) void k_matvec_chain(MatvecArgs a) {
   }
 }
 
+// ===========================================================================
+// General shapes
+// ===========================================================================
+//
+// WeightMatrix::matvec for rows of any length, one lane per row: each lane
+// folds its row's block terms (d_w * d_x) * isum left to right from +0.0
+// (src/tensor/quant.rs:115-144), the 32 rows of a tile reading 512 or
+// 1024 contiguous bytes per block.  The activation blocks go through LDS in
+// chunks of 64.  The path for shapes the chain kernels do not take.
+template <int DT>
+__global__ __launch_bounds__(64) void k_matvec_rows(RowsArgs a) {
+  constexpr int CH = Layout<DT>::CH;
+  __shared__ __attribute__((aligned(16))) u32x4 s_act[64 * 3];
+  const int lane = threadIdx.x;
+  const int y = blockIdx.y;
+  const size_t row = (size_t)blockIdx.x * 64 + lane;  // < padded rows
+  const int nb = a.nb;
+  const size_t e = a.route ? (size_t)a.route[y] : 0;
+  const uint8_t* cbase = a.codes + e * a.codes_stride + ((row / TILE) * nb * CH * TILE + row % TILE) * 16;
+  const uint16_t* sbase = a.scales + e * a.scales_stride + (row / TILE) * nb * TILE + row % TILE;
+  const u32x4* act = (const u32x4*)(a.act + (size_t)(y / a.act_div) * nb);
+  float acc = 0.0f;
+  for (int b0 = 0; b0 < nb; b0 += 64) {
+    const int n = min(64, nb - b0);
+    __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+    for (int m = 0; m < 3; m++) {
+      const int i = lane + 64 * m;
+      if (i < n * 3) s_act[i] = act[(size_t)b0 * 3 + i];
+    }
+    __syncthreads();
+    const ActBlock* sa = (const ActBlock*)s_act;
+    int b = 0;
+    for (; b + 4 <= n; b += 4) {  // four blocks' loads, then their terms in order
+      u32x4 c[4][CH];
+      uint16_t sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int q = 0; q < CH; q++)
+          c[i][q] = *(const u32x4*)(cbase + ((size_t)(b0 + b + i) * CH + q) * TILE * 16);
+        sc[i] = sbase[(size_t)(b0 + b + i) * TILE];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc = acc + block_term<DT>(c[i], sc[i], sa + b + i);
+    }
+    for (; b < n; b++) {
+      u32x4 c[CH];
+#pragma unroll
+      for (int q = 0; q < CH; q++) c[q] = *(const u32x4*)(cbase + ((size_t)(b0 + b) * CH + q) * TILE * 16);
+      acc = acc + block_term<DT>(c, sbase[(size_t)(b0 + b) * TILE], sa + b);
+    }
+  }
+  if (row < (size_t)a.rows) a.out[(size_t)y * a.out_stride + row] = acc;
+}
+
+// h = silu(g) * u (src/expert/mod.rs:99-101, src/ops/activation.rs:5-7),
+// quantized as Q8Activations::quantize does, 8 lanes per block.
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ g,
+                                                      const float* __restrict__ u, size_t nblocks,
+                                                      ActBlock* __restrict__ h) {
+  const size_t blk = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) / 8;
+  const int j = threadIdx.x & 7;
+  if (blk >= nblocks) return;  // uniform across the 8-lane group
+  const f32x4 gv = *(const f32x4*)(g + blk * QK + 4 * j);
+  const f32x4 uv = *(const f32x4*)(u + blk * QK + 4 * j);
+  f32x4 hv;
+  hv.x = silu(gv.x) * uv.x;
+  hv.y = silu(gv.y) * uv.y;
+  hv.z = silu(gv.z) * uv.z;
+  hv.w = silu(gv.w) * uv.w;
+  quant_block8(hv, j, h + blk);
+}
+
+// MoeLayer::route (src/model/moe.rs:36-53) for any number of experts, one
+// work-group per token: softmax_in_place (src/ops/activation.rs:11-21: the
+// maximum, exp(v - max) with glibc's expf, the sum in index order, each
+// value divided by it), top_k (src/ops/topk.rs:27-61: k rounds, each
+// taking the largest probability by total order, the lower index on ties)
+// and the renormalisation (the chosen scores summed best first from -0.0).
+constexpr int RW_THREADS = 256;
+__global__ __launch_bounds__(RW_THREADS) void k_route_select_wide(
+    const float* __restrict__ logits, int E, int k, int normalize, float* __restrict__ ebuf,
+    int* __restrict__ route_idx, float* __restrict__ route_w, unsigned long long* __restrict__ stats) {
+  __shared__ float s_red[RW_THREADS];
+  __shared__ unsigned s_key[RW_THREADS];
+  __shared__ int s_idx[RW_THREADS];
+  __shared__ float s_sum;
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float* lg = logits + (size_t)t * E;
+  float* ev = ebuf + (size_t)t * E;
+  // the maximum (order-free)
+  float mx = -__builtin_huge_valf();
+  for (int i = tid; i < E; i += RW_THREADS) mx = fmaxf(mx, lg[i]);
+  s_red[tid] = mx;
+  __syncthreads();
+  for (int w = RW_THREADS / 2; w > 0; w >>= 1) {
+    if (tid < w) s_red[tid] = fmaxf(s_red[tid], s_red[tid + w]);
+    __syncthreads();
+  }
+  mx = s_red[0];
+  for (int i = tid; i < E; i += RW_THREADS) ev[i] = hale_expf(lg[i] - mx);
+  __syncthreads();  // ebuf is written by this work-group only
+  if (tid == 0) {
+    float sum = 0.0f;
+    for (int i = 0; i < E; i++) sum = sum + ev[i];
+    s_sum = sum;
+  }
+  __syncthreads();
+  const float sum = s_sum;
+  // probabilities, kept as their total-order keys (0: taken)
+  unsigned* key = (unsigned*)ev;
+  for (int i = tid; i < E; i += RW_THREADS) key[i] = order_key(ev[i] / sum);
+  __syncthreads();
+  float norm = normalize ? -0.0f : 1.0f;  // thread 0's
+  for (int r = 0; r < k; r++) {
+    unsigned bk = 0u;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < E; i += RW_THREADS) {
+      const unsigned ki = key[i];
+      if (ki > bk) {  // indices ascend per thread: the first of equal keys stays
+        bk = ki;
+        bi = i;
+      }
+    }
+    s_key[tid] = bk;
+    s_idx[tid] = bi;
+    __syncthreads();
+    for (int w = RW_THREADS / 2; w > 0; w >>= 1) {
+      if (tid < w) {
+        const unsigned k2 = s_key[tid + w];
+        const int i2 = s_idx[tid + w];
+        if (k2 > s_key[tid] || (k2 == s_key[tid] && i2 < s_idx[tid])) {
+          s_key[tid] = k2;
+          s_idx[tid] = i2;
+        }
+      }
+      __syncthreads();
+    }
+    // (a key of 0 marks a taken element; a probability with that key, the
+    // negative NaN of all-ones bits, cannot come out of the division)
+    const int win = s_idx[0] < E ? s_idx[0] : 0;
+    const float pw = key_value(s_key[0]);
+    __syncthreads();
+    if (tid == 0) {
+      key[win] = 0u;
+      route_idx[(size_t)t * k + r] = win;
+      route_w[(size_t)t * k + r] = pw;
+      if (normalize) norm = norm + pw;
+      if (stats) atomicAdd(&stats[win], 1ull);
+    }
+    __syncthreads();
+  }
+  if (tid == 0)
+    for (int r = 0; r < k; r++) route_w[(size_t)t * k + r] = route_w[(size_t)t * k + r] / norm;
+}
+
 // Per-block i32 sums of every row (the `isum` of dot_q8_0 / dot_q4_0), one
 // thread per (row, block).  Parity instrumentation, not a hot path.
 template <int DT>
@@ -2195,6 +2352,29 @@ hipError_t launch_matvec_pair(int dtype, const MatvecArgs& a, hipStream_t st) {
 #undef HALE_MV_NB
 #undef HALE_MV_NW
 #undef HALE_MV
+}
+
+hipError_t launch_matvec_rows(int dtype, const RowsArgs& a, int ny, hipStream_t st) {
+  if (a.nb < 1 || a.rows < 1 || ny < 1 || ny > 65535 || a.act_div < 1) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(padded_rows((size_t)a.rows) / 64), (unsigned)ny);
+  if (dtype == Q8_0) return launch(k_matvec_rows<Q8_0>, grid, 64, 0, st, a);
+  if (dtype == Q4_0) return launch(k_matvec_rows<Q4_0>, grid, 64, 0, st, a);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_swiglu_quant(const float* g, const float* u, size_t nblocks, ActBlock* h,
+                               hipStream_t st) {
+  if (nblocks == 0) return hipSuccess;
+  if (((uintptr_t)g & 15) || ((uintptr_t)u & 15)) return hipErrorInvalidValue;
+  return launch(k_swiglu_quant, blocks_for(nblocks * 8, 256), 256, 0, st, g, u, nblocks, h);
+}
+
+hipError_t launch_route_select_wide(const float* logits, int E, int k, int normalize, int T,
+                                    float* ebuf, int* route_idx, float* route_w,
+                                    unsigned long long* stats, hipStream_t st) {
+  if (T < 1 || E < 1 || k < 1 || k > E) return hipErrorInvalidValue;
+  return launch(k_route_select_wide, T, RW_THREADS, 0, st, logits, E, k, normalize, ebuf, route_idx,
+                route_w, stats);
 }
 
 hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* act, size_t rows,

@@ -537,7 +537,8 @@ __global__ __launch_bounds__(256) void k_gather_tiles(const ActBlock* __restrict
 }
 
 // out[t] = 0, then out[t] = out[t] + w[t][s] * y[pos(t, s)] for s in route
-// order (MoeLayer::forward's combine, src/model/moe.rs:63-68).  Thread i of
+// order (MoeLayer::forward's combine, src/model/moe.rs:63-68); pos_of null:
+// the rows are in (token, slot) order.  Thread i of
 // work-group (c, t) owns columns 4i..4i+3 of column chunk c; the rows of 8
 // slots are loaded together before they are added in slot order.
 constexpr int COMBINE_COLS = 1024;
@@ -556,7 +557,8 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y,
     for (int j = 0; j < 8; j++) {
       const int s = min(s0 + j, k - 1);
       w[j] = route_w[(size_t)t * k + s];
-      v[j] = *(const f32x4*)(y + (size_t)pos_of[(size_t)t * k + s] * H + i);
+      const size_t pos = pos_of ? (size_t)pos_of[(size_t)t * k + s] : (size_t)t * k + s;
+      v[j] = *(const f32x4*)(y + pos * H + i);
     }
 #pragma unroll
     for (int j = 0; j < 8; j++)
@@ -568,6 +570,13 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y,
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
+
+hipError_t launch_combine_rows(const float* y, const float* route_w, int k, int H, int T,
+                               float* out, hipStream_t st) {
+  if (T < 1 || k < 1 || H % 4 || T > 65535) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((H + COMBINE_COLS - 1) / COMBINE_COLS), (unsigned)T);
+  return launch(k_combine, grid, 256, 0, st, y, (const int*)nullptr, route_w, k, H, out);
+}
 
 size_t prefill_min_tokens(size_t) { return 8; }
 

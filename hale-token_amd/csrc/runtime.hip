@@ -85,6 +85,9 @@ struct hale_moe {
   size_t E = 0, H = 0, I = 0, k = 0;
   int dtype = 0;
   int normalize = 0;
+  // a shape beyond the fast kernels (FAST_MAX_*): every forward and route
+  // runs the general path (moe_wide_enqueue)
+  bool wide = false;
   float* router = nullptr;  // [E][H] f32, or null
   // resident experts, [E][plane]
   uint8_t *gate_c = nullptr, *up_c = nullptr, *down_c = nullptr;
@@ -755,8 +758,16 @@ static int matvec_enqueue(hale_ctx* c, const hale_matrix* m, const float* dx, fl
     LAUNCH(c, K_GEMV, launch_matvec(m->dtype, mv, c->stream));
     return HALE_OK;
   }
-  GemvArgs a = plain_args(m, act, dout);
-  LAUNCH(c, K_GEMV, launch_gemv(m->dtype, EPI_PLAIN, a, (int)(padded_rows(m->rows) / 64), 1, c->stream));
+  // longer rows: lane-per-row chains over every block
+  RowsArgs r{};
+  r.codes = m->codes;
+  r.scales = m->scales;
+  r.nb = (int)nb;
+  r.rows = (int)m->rows;
+  r.act = act;
+  r.act_div = 1;
+  r.out = dout;
+  LAUNCH(c, K_GEMV, launch_matvec_rows(m->dtype, r, 1, c->stream));
   return HALE_OK;
 }
 
@@ -833,11 +844,11 @@ static int expert_check(hale_ctx* c, const hale_matrix* gate, const hale_matrix*
 }
 
 // Bytes of scratch expert_enqueue needs after `lead` bytes of the caller's:
-// x's q8 blocks, h's q8 blocks, then h in f32.
+// x's q8 blocks, h's q8 blocks, then the f32 h (or g) and u.
 static size_t expert_scratch_bytes(const hale_matrix* gate, size_t lead) {
   const size_t nbh = gate->cols / HALE_QK, nbi = gate->rows / HALE_QK;
   return lead + align_up(nbh * sizeof(ActBlock), 256) + align_up(nbi * sizeof(ActBlock), 256) +
-         align_up(gate->rows * 4, 256);
+         2 * align_up(gate->rows * 4, 256);
 }
 
 // Enqueues Expert::forward for device x/out: q8 activation blocks of x, the
@@ -878,6 +889,36 @@ static int expert_enqueue(hale_ctx* c, const hale_matrix* gate, const hale_matri
     d.x = gv;
     d.out = dout;
     LAUNCH(c, K_DOWN, launch_matvec(down->dtype, d, c->stream));
+    return HALE_OK;
+  }
+  if (nbh > FAST_MAX_NB || nbi > (size_t)MATVEC_MAX_NB) {
+    // rows longer than the tile kernels take: lane-per-row chains for gate
+    // and up, h = silu(g) * u requantized, lane-per-row chains for down
+    float* uv = gv + align_up(I * 4, 256) / 4;
+    LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, nbh, act, c->stream));
+    RowsArgs r{};
+    r.nb = (int)nbh;
+    r.rows = (int)I;
+    r.act = act;
+    r.act_div = 1;
+    r.codes = gate->codes;
+    r.scales = gate->scales;
+    r.out = gv;
+    LAUNCH(c, K_GATE_UP, launch_matvec_rows(gate->dtype, r, 1, c->stream));
+    r.codes = up->codes;
+    r.scales = up->scales;
+    r.out = uv;
+    LAUNCH(c, K_GATE_UP, launch_matvec_rows(up->dtype, r, 1, c->stream));
+    LAUNCH(c, K_GATE_UP, launch_swiglu_quant(gv, uv, nbi, hact, c->stream));
+    RowsArgs d{};
+    d.codes = down->codes;
+    d.scales = down->scales;
+    d.nb = (int)nbi;
+    d.rows = (int)H;
+    d.act = hact;
+    d.act_div = 1;
+    d.out = dout;
+    LAUNCH(c, K_DOWN, launch_matvec_rows(down->dtype, d, 1, c->stream));
     return HALE_OK;
   }
   // the gate/up kernel quantizes an aligned x of up to 128 blocks itself
@@ -957,7 +998,7 @@ struct TokScratch {
 // h blocks are kept for the tokens a decode pass can take: min(ntok,
 // grouped_min - 1), so scratch laid out for more tokens holds at least as many
 static size_t hact_tokens(const hale_moe* m, size_t ntok) {
-  return std::min(ntok, m->grouped_min - 1);
+  return m->wide ? 0 : std::min(ntok, m->grouped_min - 1);
 }
 
 static size_t tok_scratch_bytes(const hale_moe* m, size_t ntok) {
@@ -1007,19 +1048,19 @@ static int moe_reserve(hale_moe* m, size_t ntok, TokScratch* out) {
   return HALE_OK;
 }
 
-// The layer's grouped-path workspace for at least T tokens.
-static int moe_prefill_ws(hale_moe* m, const PrefillLayer& L, size_t T, void** out) {
+// The layer's workspace (the grouped path's, or the general path's) of at
+// least `need` bytes.
+static int moe_ws(hale_moe* m, size_t need, void** out) {
   hale_ctx* c = m->ctx;
-  const size_t need = prefill_workspace_bytes(L, T);
   if (m->pw.bytes < need) {
-    int rc = growth_allowed(c, "grouped prefill workspace", need);
+    int rc = growth_allowed(c, "MoE layer workspace", need);
     if (rc) return rc;
     HIPCHK(c, hipStreamSynchronize(c->stream));
     scratch_release(c, m->pw.base);
     m->pw.base = nullptr;
     m->pw.bytes = 0;
     if (hipMalloc(&m->pw.base, need) != hipSuccess)
-      return fail(c, HALE_ENOMEM, "grouped prefill workspace of %zu bytes", need);
+      return fail(c, HALE_ENOMEM, "MoE layer workspace of %zu bytes", need);
     m->pw.bytes = need;
   }
   *out = m->pw.base;
@@ -1047,11 +1088,11 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   if (!c || !out) return fail(c, HALE_EINVAL, "moe_create: NULL argument");
   *out = nullptr;
   if (!quantized(dtype)) return fail(c, HALE_EINVAL, "expert dtype %d is not q8_0/q4_0", dtype);
-  if (E == 0 || E > 1024) return fail(c, HALE_EINVAL, "num_experts %zu outside 1..1024", E);
+  if (E == 0 || E > (size_t)INT32_MAX) return fail(c, HALE_EINVAL, "num_experts %zu outside 1..2^31-1", E);
   if (H == 0 || I == 0 || H % HALE_QK || I % HALE_QK)
     return fail(c, HALE_EINVAL, "hidden %zu / inter %zu must be non-zero multiples of 32", H, I);
-  if (H > 8192) return fail(c, HALE_EINVAL, "hidden %zu above 8192", H);
-  if (std::min(top_k, E) > 64) return fail(c, HALE_EINVAL, "top_k %zu above 64", top_k);
+  if (H > (size_t)INT32_MAX / 4 || I > (size_t)INT32_MAX / 4)
+    return fail(c, HALE_EINVAL, "hidden %zu / inter %zu too large", H, I);
   if (router && (router->dtype != HALE_F32 || router->rows != E || router->cols != H))
     return fail(c, HALE_EINVAL, "router must be f32 [%zu x %zu]", E, H);
   std::lock_guard<std::recursive_mutex> g(c->mu);
@@ -1064,7 +1105,9 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   m->H = H;
   m->I = I;
   m->k = std::min(top_k, E);  // top_k clamps k to the number of scores
-  m->grouped_min = default_grouped_min(dtype, E, H, I, m->k);
+  m->wide = E > FAST_MAX_E || H > FAST_MAX_H || m->k > FAST_MAX_K || I / HALE_QK > FAST_MAX_NB;
+  // (a wide layer never takes the grouped path)
+  m->grouped_min = m->wide ? SIZE_MAX : default_grouped_min(dtype, E, H, I, m->k);
   m->dtype = dtype;
   m->normalize = normalize;
   m->gc_bytes = code_plane_bytes(dtype, I, H);
@@ -1304,6 +1347,101 @@ static PrefillLayer prefill_layer(hale_moe* m, const TokScratch& s) {
   return L;
 }
 
+// ---------------------------------------------------------------------------
+// the general path: layers beyond the fast kernels' shapes
+// ---------------------------------------------------------------------------
+
+// The general path's workspace over T tokens: the routing kernel's exp
+// values [T][E], then per (token, slot) the gate and up outputs [T k][I],
+// h's q8 blocks [T k][I/32] and the down outputs [T k][H].  base null: the
+// layout only.
+struct WideWs {
+  float* ebuf;
+  float* g;
+  float* u;
+  ActBlock* hact;
+  float* y;
+  size_t total;
+};
+
+static WideWs wide_layout(const hale_moe* m, size_t T, char* base) {
+  WideWs w{};
+  const size_t A = T * m->k;
+  size_t o = 0;
+  auto take = [&](size_t bytes) -> char* {
+    const size_t at = o;
+    o += align_up(bytes, 256);
+    return base ? base + at : nullptr;
+  };
+  w.ebuf = (float*)take(T * m->E * 4);
+  w.g = (float*)take(A * m->I * 4);
+  w.u = (float*)take(A * m->I * 4);
+  w.hact = (ActBlock*)take(A * (m->I / HALE_QK) * sizeof(ActBlock));
+  w.y = (float*)take(A * m->H * 4);
+  w.total = o;
+  return w;
+}
+
+// MoeLayer::forward over ntok tokens for any E, top_k, H and I: the router
+// logits by the f32 GEMV (dot_f32's lane order), the routes by the general
+// routing kernel, then per (token, slot) the gate and up matvecs, h =
+// silu(g) * u requantized, the down matvec (lane-per-row chains, the
+// expert read from the route on the device) and the route-order combine.
+// Every step has the reference's arithmetic, so the outputs are its bits.
+static int moe_wide_enqueue(hale_moe* m, size_t ntok, const float* dx, const float* dlogits,
+                            float* dout, const TokScratch& s, void* ws) {
+  hale_ctx* c = m->ctx;
+  const size_t E = m->E, H = m->H, I = m->I, k = m->k, nbh = H / HALE_QK, nbi = I / HALE_QK;
+  const WideWs w = wide_layout(m, ntok, (char*)ws);
+  const float* lg = dlogits;
+  if (!lg) {
+    for (size_t t = 0; t < ntok; t++)
+      LAUNCH(c, K_ROUTE, launch_gemv_float(HALE_F32, m->router, dx + t * H, E, H, s.logits + t * E, c->stream));
+    lg = s.logits;
+  }
+  LAUNCH(c, K_ROUTE, launch_route_select_wide(lg, (int)E, (int)k, m->normalize, (int)ntok, w.ebuf,
+                                              s.route_idx, s.route_w, m->stats, c->stream));
+  LAUNCH(c, K_ACT_QUANT, launch_act_quant(dx, ntok * nbh, s.act, c->stream));
+  const size_t tc = std::max<size_t>(1, 65535 / k);  // tokens per pass: grid rows (token, slot)
+  for (size_t t0 = 0; t0 < ntok; t0 += tc) {
+    const size_t nt = std::min(tc, ntok - t0), A0 = t0 * k, ny = nt * k;
+    RowsArgs r{};
+    r.route = s.route_idx + A0;
+    r.nb = (int)nbh;
+    r.rows = (int)I;
+    r.act = s.act + t0 * nbh;
+    r.act_div = (int)k;
+    r.out_stride = I;
+    r.codes_stride = m->gc_bytes;
+    r.scales_stride = m->gs_elems;
+    r.codes = m->gate_c;
+    r.scales = m->gate_s;
+    r.out = w.g + A0 * I;
+    LAUNCH(c, K_GATE_UP, launch_matvec_rows(m->dtype, r, (int)ny, c->stream));
+    r.codes = m->up_c;
+    r.scales = m->up_s;
+    r.out = w.u + A0 * I;
+    LAUNCH(c, K_GATE_UP, launch_matvec_rows(m->dtype, r, (int)ny, c->stream));
+    LAUNCH(c, K_GATE_UP, launch_swiglu_quant(w.g + A0 * I, w.u + A0 * I, ny * nbi, w.hact + A0 * nbi, c->stream));
+    RowsArgs d{};
+    d.codes = m->down_c;
+    d.scales = m->down_s;
+    d.codes_stride = m->dc_bytes;
+    d.scales_stride = m->ds_elems;
+    d.route = s.route_idx + A0;
+    d.nb = (int)nbi;
+    d.rows = (int)H;
+    d.act = w.hact + A0 * nbi;
+    d.act_div = 1;
+    d.out = w.y + A0 * H;
+    d.out_stride = H;
+    LAUNCH(c, K_DOWN, launch_matvec_rows(m->dtype, d, (int)ny, c->stream));
+    LAUNCH(c, K_COMBINE, launch_combine_rows(w.y + A0 * H, s.route_w + A0, (int)k, (int)H, (int)nt,
+                                             dout + t0 * H, c->stream));
+  }
+  return HALE_OK;
+}
+
 // Checks that apply to every forward: device x 16-byte aligned (the router
 // reads it as float4) and device logits float-aligned (host buffers are
 // staged, dx NULL), a pending pack load, every expert present, a router or
@@ -1330,6 +1468,7 @@ static int moe_forward_enqueue(hale_moe* m, size_t ntok, const float* dx, const 
     LAUNCH(c, K_FILL, launch_fill(dout, ntok * m->H, 0.0f, c->stream));
     return HALE_OK;
   }
+  if (m->wide) return moe_wide_enqueue(m, ntok, dx, dlogits, dout, s, pws);
   if (ntok >= m->grouped_min) {
     PrefillLayer L = prefill_layer(m, s);
     hipError_t e = prefill_enqueue(L, pws, ntok, dx, dlogits, dout, c->stream, ctx_hook(c));
@@ -1344,9 +1483,10 @@ static int moe_forward_scratch(hale_moe* m, size_t ntok, TokScratch* s, void** p
   int rc = moe_reserve(m, ntok, s);
   if (rc) return rc;
   *pws = nullptr;
+  if (m->k > 0 && m->wide) return moe_ws(m, wide_layout(m, ntok, nullptr).total, pws);
   if (m->k > 0 && ntok >= m->grouped_min) {
     PrefillLayer L = prefill_layer(m, *s);
-    rc = moe_prefill_ws(m, L, ntok, pws);
+    rc = moe_ws(m, prefill_workspace_bytes(L, ntok), pws);
   }
   return rc;
 }
@@ -1387,6 +1527,7 @@ struct ProfPause {
 // the per-token scratch, then (grouped path) the grouped workspace.
 static size_t noalloc_bytes(hale_moe* m, size_t n) {
   const size_t tb = align_up(tok_scratch_bytes(m, n), 256);
+  if (m->k > 0 && m->wide) return tb + wide_layout(m, n, nullptr).total;
   if (m->k == 0 || n < m->grouped_min) return tb;
   return tb + prefill_workspace_bytes(prefill_layer(m, TokScratch{}), n);
 }
@@ -1445,9 +1586,9 @@ extern "C" int hale_moe_forward_device_noalloc(hale_moe* m, size_t ntok, const f
     const size_t n = std::min(chunk, ntok - t0);
     const size_t tb = align_up(tok_scratch_bytes(m, n), 256);
     const TokScratch s = tok_scratch_carve(m, base, n);
-    const bool grouped = k > 0 && n >= m->grouped_min;
+    const bool ws = k > 0 && (m->wide || n >= m->grouped_min);
     rc = moe_forward_enqueue(m, n, d_x + t0 * m->H, d_logits ? d_logits + t0 * m->E : nullptr,
-                             d_out + t0 * m->H, s, grouped ? base + tb : nullptr);
+                             d_out + t0 * m->H, s, ws ? base + tb : nullptr);
     if (rc) return rc;
     if (d_index && k)
       HIPCHK(c, hipMemcpyAsync(d_index + t0 * k, s.route_idx, n * k * 4, hipMemcpyDeviceToDevice,
@@ -1504,13 +1645,20 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
   int rc = moe_reserve(m, 1, &s);
   if (rc) return rc;
   void* sp;
-  rc = ctx_scratch(c, m->H * 4, &sp);
+  rc = ctx_scratch(c, align_up(m->H * 4, 256) + (m->wide ? m->E * 4 : 0), &sp);
   if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync(sp, x, m->H * 4, hipMemcpyHostToDevice, c->stream));
-  LAUNCH(c, K_ROUTE, launch_route_logits(m->router, (const float*)sp, (int)m->H, (int)m->E, 1,
-                                         s.act, s.logits, c->stream));
-  LAUNCH(c, K_ROUTE, launch_route_select(s.logits, (int)m->E, (int)m->k, m->normalize, 1,
-                                         s.route_idx, s.route_w, nullptr, c->stream));
+  if (m->wide) {  // the general path's routing, its exp values after x
+    float* ebuf = (float*)((char*)sp + align_up(m->H * 4, 256));
+    LAUNCH(c, K_ROUTE, launch_gemv_float(HALE_F32, m->router, (const float*)sp, m->E, m->H, s.logits, c->stream));
+    LAUNCH(c, K_ROUTE, launch_route_select_wide(s.logits, (int)m->E, (int)m->k, m->normalize, 1, ebuf,
+                                                s.route_idx, s.route_w, nullptr, c->stream));
+  } else {
+    LAUNCH(c, K_ROUTE, launch_route_logits(m->router, (const float*)sp, (int)m->H, (int)m->E, 1,
+                                           s.act, s.logits, c->stream));
+    LAUNCH(c, K_ROUTE, launch_route_select(s.logits, (int)m->E, (int)m->k, m->normalize, 1,
+                                           s.route_idx, s.route_w, nullptr, c->stream));
+  }
   HIPCHK(c, hipMemcpyAsync(index, s.route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipMemcpyAsync(weight, s.route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -1535,6 +1683,7 @@ extern "C" int hale_moe_set_grouped_min_tokens(hale_moe* m, size_t n) {
     return fail(c, HALE_EINVAL, "set_grouped_min_tokens: %zu is outside 2..%d", n,
                 HALE_DECODE_MAX_TOKENS + 1);
   std::lock_guard<std::recursive_mutex> g(c->mu);
+  if (m->wide) return HALE_OK;  // the general path has no grouped form
   m->grouped_min = n;  // the next forward lays the scratch out for it
   return HALE_OK;
 }

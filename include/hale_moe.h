@@ -173,7 +173,8 @@ int hale_matrix_convert(hale_ctx *ctx, const hale_matrix *m, int dtype,
  * cols and outlen rows (the reference asserts both).  Quantized matrices:
  * x is quantized once, then dot_q8_0 / dot_q4_0 per row (quant.rs:
  * 115-144).  Float matrices: dot_f32 / dot_decoded per row (quant.rs:
- * 146-233: eight lane accumulators, the fixed reduce, then the tail). */
+ * 146-233: eight lane accumulators, the fixed reduce, then the tail).
+ * Any row length (a multiple of 32 for q8_0 / q4_0). */
 int hale_matvec(hale_ctx *ctx, const hale_matrix *m, const float *x,
                 size_t xlen, float *out, size_t outlen);
 /* Same on device buffers (d_x 16-byte aligned for float matrices),
@@ -207,7 +208,13 @@ int hale_expert_forward_device(hale_ctx *ctx, const hale_matrix *gate,
  * layer whose router logits are supplied to hale_moe_forward.
  * normalize_topk: ModelConfig::normalize_topk (src/config.rs:205-208).
  * top_k is clamped to num_experts (top_k, src/ops/topk.rs:45); top_k = 0
- * routes every token nowhere, so forward leaves out at zero. */
+ * routes every token nowhere, so forward leaves out at zero.  Any
+ * num_experts, top_k, hidden and inter (multiples of 32) are taken, as in
+ * the reference.  Layers within 1024 experts, top-64, hidden 8192 and down
+ * rows of 512 blocks run the decode and expert-grouped kernels; larger ones
+ * run a general path (router logits by the f32 GEMV, a routing kernel for
+ * any expert count, row-chain matvecs per route, the route-order combine)
+ * with the same bits, and never take the grouped path. */
 int hale_moe_create(hale_ctx *ctx, uint32_t layer, size_t num_experts,
                     size_t hidden, size_t inter, int dtype, size_t top_k,
                     int normalize_topk, const hale_matrix *router,
