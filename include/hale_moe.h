@@ -277,7 +277,9 @@ int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
  * per-token scratch on its next call, which must then come outside a graph
  * capture (or call hale_moe_reserve first).  No counterpart in the
  * reference (its prefill runs token by token); for callers tuning small
- * batches. */
+ * batches.  A layer on the general path (see hale_moe_create) has no
+ * grouped form: the setting is accepted and ignored, and the threshold
+ * reads SIZE_MAX. */
 #define HALE_DECODE_MAX_TOKENS 256
 int hale_moe_set_grouped_min_tokens(hale_moe *moe, size_t n);
 int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
