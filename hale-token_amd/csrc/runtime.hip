@@ -61,6 +61,12 @@ struct hale_ctx {
   std::vector<void*> retired;
   // this device's copy of the fixed scratch array (forward without allocation)
   void* fixed_scratch = nullptr;
+  // pinned host staging of the synchronous host-slice entry points: inputs
+  // are copied in and outputs out of it by the CPU, the GPU copies from and
+  // to it (every such call ends with a stream synchronize, so the next one
+  // may reuse it)
+  void* pinned = nullptr;
+  size_t pinned_bytes = 0;
 };
 
 struct hale_graph {
@@ -224,6 +230,7 @@ extern "C" void hale_ctx_destroy(hale_ctx* c) {
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
+  if (c->pinned) (void)hipHostFree(c->pinned);
   for (void* p : c->retired) (void)hipFree(p);
   for (auto& r : c->recs) {
     (void)hipEventDestroy(r.start);
@@ -291,6 +298,62 @@ static int ctx_scratch(hale_ctx* c, size_t bytes, void** p) {
 }
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// The context's pinned staging of at least `bytes` (grown; not while the
+// stream is captured, where host-slice calls cannot run anyway).
+static int ctx_pinned(hale_ctx* c, size_t bytes, char** out) {
+  if (c->pinned_bytes < bytes) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (c->pinned) (void)hipHostFree(c->pinned);
+    c->pinned = nullptr;
+    c->pinned_bytes = 0;
+    const size_t want = std::max<size_t>(bytes, 1 << 20);
+    if (hipHostMalloc(&c->pinned, want, hipHostMallocDefault) != hipSuccess) {
+      c->pinned = nullptr;
+      return fail(c, HALE_ENOMEM, "pinned staging of %zu bytes", want);
+    }
+    c->pinned_bytes = want;
+  }
+  *out = (char*)c->pinned;
+  return HALE_OK;
+}
+
+// Host-slice staging of one synchronous call: inputs are copied into the
+// pinned buffer and sent to the device; outputs come back into it and are
+// copied out after the call's synchronize (finish).
+struct HostStage {
+  hale_ctx* c;
+  char* base = nullptr;
+  size_t used = 0;
+  struct Out {
+    void* host;
+    size_t off, n;
+  };
+  Out outs[4];
+  int nouts = 0;
+  explicit HostStage(hale_ctx* ctx) : c(ctx) {}
+  // room for every input and output of the call (before any in/out)
+  int reserve(size_t bytes) { return ctx_pinned(c, bytes, &base); }
+  int in(void* dev, const void* host, size_t n) {
+    std::memcpy(base + used, host, n);
+    const hipError_t e = hipMemcpyAsync(dev, base + used, n, hipMemcpyHostToDevice, c->stream);
+    used += align_up(n, 256);
+    return e == hipSuccess ? HALE_OK : fail(c, HALE_EHIP, "copy to device: %s", hipGetErrorString(e));
+  }
+  int out(void* host, const void* dev, size_t n) {
+    const hipError_t e = hipMemcpyAsync(base + used, dev, n, hipMemcpyDeviceToHost, c->stream);
+    if (e != hipSuccess) return fail(c, HALE_EHIP, "copy to host: %s", hipGetErrorString(e));
+    outs[nouts++] = {host, used, n};
+    used += align_up(n, 256);
+    return HALE_OK;
+  }
+  int finish() {
+    const hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return fail(c, HALE_EHIP, "synchronize: %s", hipGetErrorString(e));
+    for (int i = 0; i < nouts; i++) std::memcpy(outs[i].host, base + outs[i].off, outs[i].n);
+    return HALE_OK;
+  }
+};
 
 // ---------------------------------------------------------------------------
 // per-kernel profiler (events on the context's stream around each launch)
@@ -786,12 +849,11 @@ extern "C" int hale_matvec(hale_ctx* c, const hale_matrix* m, const float* x, si
   float* dx = (float*)s;
   float* dout = (float*)((char*)s + o1);
   ActBlock* act = (ActBlock*)((char*)s + o2);
-  HIPCHK(c, hipMemcpyAsync(dx, x, xlen * 4, hipMemcpyHostToDevice, c->stream));
+  HostStage st(c);
+  if ((rc = st.reserve(o2)) || (rc = st.in(dx, x, xlen * 4))) return rc;
   rc = matvec_enqueue(c, m, dx, dout, act);
-  if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync(out, dout, outlen * 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  return HALE_OK;
+  if (rc || (rc = st.out(out, dout, outlen * 4))) return rc;
+  return st.finish();
 }
 
 extern "C" int hale_matvec_device(hale_ctx* c, const hale_matrix* m, const float* d_x, float* d_out) {
@@ -960,12 +1022,11 @@ extern "C" int hale_expert_forward(hale_ctx* c, const hale_matrix* gate, const h
   if (rc) return rc;
   float* dx = (float*)s;
   float* dout = (float*)((char*)s + io);
-  HIPCHK(c, hipMemcpyAsync(dx, x, H * 4, hipMemcpyHostToDevice, c->stream));
+  HostStage st(c);
+  if ((rc = st.reserve(2 * io)) || (rc = st.in(dx, x, H * 4))) return rc;
   rc = expert_enqueue(c, gate, up, down, dx, dout, 2 * io);
-  if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync(out, dout, H * 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  return HALE_OK;
+  if (rc || (rc = st.out(out, dout, H * 4))) return rc;
+  return st.finish();
 }
 
 extern "C" int hale_expert_forward_device(hale_ctx* c, const hale_matrix* gate,
@@ -1621,17 +1682,16 @@ extern "C" int hale_moe_forward(hale_moe* m, size_t ntok, const float* x, const 
   void* pws;
   rc = moe_forward_scratch(m, ntok, &s, &pws);
   if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream));
-  if (logits) HIPCHK(c, hipMemcpyAsync(dl, logits, lb, hipMemcpyHostToDevice, c->stream));
+  HostStage st(c);
+  const size_t rb = align_up(ntok * m->k * 4, 256);
+  if ((rc = st.reserve(2 * align_up(xb, 256) + align_up(lb, 256) + 2 * rb))) return rc;
+  if ((rc = st.in(dx, x, xb))) return rc;
+  if (logits && (rc = st.in(dl, logits, lb))) return rc;
   rc = moe_forward_enqueue(m, ntok, dx, dl, dout, s, pws);
-  if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync(out, dout, xb, hipMemcpyDeviceToHost, c->stream));
-  if (index && m->k)
-    HIPCHK(c, hipMemcpyAsync(index, s.route_idx, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
-  if (weight && m->k)
-    HIPCHK(c, hipMemcpyAsync(weight, s.route_w, ntok * m->k * 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  return HALE_OK;
+  if (rc || (rc = st.out(out, dout, xb))) return rc;
+  if (index && m->k && (rc = st.out(index, s.route_idx, ntok * m->k * 4))) return rc;
+  if (weight && m->k && (rc = st.out(weight, s.route_w, ntok * m->k * 4))) return rc;
+  return st.finish();
 }
 
 extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, float* weight) {
@@ -1647,7 +1707,10 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
   void* sp;
   rc = ctx_scratch(c, align_up(m->H * 4, 256) + (m->wide ? m->E * 4 : 0), &sp);
   if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync(sp, x, m->H * 4, hipMemcpyHostToDevice, c->stream));
+  HostStage st(c);
+  if ((rc = st.reserve(align_up(m->H * 4, 256) + 2 * align_up(m->k * 4, 256))) ||
+      (rc = st.in(sp, x, m->H * 4)))
+    return rc;
   if (m->wide) {  // the general path's routing, its exp values after x
     float* ebuf = (float*)((char*)sp + align_up(m->H * 4, 256));
     LAUNCH(c, K_ROUTE, launch_gemv_float(HALE_F32, m->router, (const float*)sp, m->E, m->H, s.logits, c->stream));
@@ -1659,10 +1722,8 @@ extern "C" int hale_moe_route(hale_moe* m, const float* x, uint32_t* index, floa
     LAUNCH(c, K_ROUTE, launch_route_select(s.logits, (int)m->E, (int)m->k, m->normalize, 1,
                                            s.route_idx, s.route_w, nullptr, c->stream));
   }
-  HIPCHK(c, hipMemcpyAsync(index, s.route_idx, m->k * 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipMemcpyAsync(weight, s.route_w, m->k * 4, hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  return HALE_OK;
+  if ((rc = st.out(index, s.route_idx, m->k * 4)) || (rc = st.out(weight, s.route_w, m->k * 4))) return rc;
+  return st.finish();
 }
 
 extern "C" int hale_moe_reserve(hale_moe* m, size_t max_tokens) {
