@@ -24,6 +24,15 @@ enum DType : int { F32 = 0, F16 = 1, BF16 = 2, Q8_0 = 3, Q4_0 = 4 };
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// A weight load: non-temporal when each weight byte is read once (one
+// token's routes), ordinary when other tokens of the same pass read it
+// again from the caches.
+template <bool NT>
+__device__ __forceinline__ u32x4 load_weights(const u32x4* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  return *p;
+}
+
 // One q8 activation block as the kernels read it: the 32 codes and f32
 // scale of Q8Activations (src/tensor/quant.rs:69-93) plus the code sum used
 // by the q4 kernels (sum_j (n_j - 8) x_j = sum_j n_j x_j - 8 sum_j x_j).

@@ -1132,15 +1132,15 @@ static int moe_ws(hale_moe* m, size_t need, void** out) {
 // grouped path costs about 60 us (Qwen3-30B shape) to 190 us (Mixtral) more
 // than the decode path before its first token, and then adds little per
 // token; the decode path adds each token's k experts' bytes.  Measured
-// crossovers (graph replay, one MI355X): Qwen3-30B q4_0 and q8_0 and
-// Qwen3-235B q4_0 (top-8 of 128) between 12 and 16 tokens, Mixtral (top-2 of
-// 8) between 6 and 8.
+// crossovers (graph replay over layers visited in turn, one MI355X):
+// Qwen3-30B q4_0 and q8_0 and Qwen3-235B q4_0 (top-8 of 128) between 20
+// and 24 tokens, Mixtral (top-2 of 8) between 6 and 8.
 static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_t k) {
   (void)dtype;
   (void)E;
   (void)H;
   (void)I;
-  return k >= 4 ? 16 : 8;
+  return k >= 4 ? 22 : 8;
 }
 
 extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, size_t I, int dtype,

@@ -271,7 +271,7 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
 int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
- * path (default 16 for top_k >= 4, else 8); fewer tokens run the decode kernels in one pass over
+ * path (default 22 for top_k >= 4, else 8); fewer tokens run the decode kernels in one pass over
  * all of them.  Both give the reference's bits; the choice is speed only.
  * n in 2..HALE_DECODE_MAX_TOKENS + 1.  A new threshold re-lays the layer's
  * per-token scratch on its next call, which must then come outside a graph

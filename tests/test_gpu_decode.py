@@ -285,16 +285,16 @@ def test_missing_expert_is_reported(ctx):
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-@pytest.mark.parametrize("T,gmin", [(7, None), (15, None), (16, None), (8, 8)])
+@pytest.mark.parametrize("T,gmin", [(7, None), (21, None), (22, None), (8, 8)])
 def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin):
     """Router logits supplied directly (the skewed-routing workloads).  This
-    top-4 layer's grouped threshold is 16 tokens: 7 and 15 take the decode
-    path, 16 the grouped path, and 8 the grouped path once the threshold is
-    set to 8."""
+    top-4 layer's grouped threshold is 22 tokens: 7 and 21 take the decode
+    path (21 with cached weight loads), 22 the grouped path, and 8 the
+    grouped path once the threshold is set to 8."""
     E, Hd, I, k = 32, 256, 64, 4
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
     moe = make_layer(ctx, L)
-    assert moe.grouped_min_tokens == 16
+    assert moe.grouped_min_tokens == 22
     if gmin:
         moe.set_grouped_min_tokens(gmin)
     rng = np.random.default_rng(1)
@@ -361,13 +361,14 @@ def test_moe_decode_down_one_wave_per_route(ctx, dtype, hidden, inter, k, T):
     moe.close()
 
 
-@pytest.mark.parametrize("T", [2, 7, 15])
+@pytest.mark.parametrize("T", [2, 7, 15, 21])
 def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
-    """Config 1's layer over 2, 7 and 15 tokens (its grouped threshold is
-    16): 16-wave gate/up with two tiles per work-group (24 tiles x 8 slots x
-    T > 256)."""
+    """Config 1's layer over 2, 7, 15 and 21 tokens (its grouped threshold
+    is 22): 16-wave gate/up with two tiles per work-group (24 tiles x 8
+    slots x T > 256); from 12 tokens on the weights load through the
+    caches."""
     L, moe = qwen30b_q4
-    assert moe.grouped_min_tokens == 16
+    assert moe.grouped_min_tokens == 22
     _few_tokens_check(L, moe, O.normal(9200 + T, T * 2048).reshape(T, 2048))
 
 

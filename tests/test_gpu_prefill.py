@@ -1,5 +1,5 @@
 """GPU parity of the expert-grouped multi-token path (ntok at or above the
-layer's grouped threshold: 16 tokens for top-4 and wider, 8 below) against
+layer's grouped threshold: 22 tokens for top-4 and wider, 8 below) against
 the oracle's token-at-a-time prefill (src/model/transformer.rs:231-239).
 
 Bar: bit-exact outputs, routes and weights (rel-L2 <= 1e-5 asserted too).
@@ -145,7 +145,7 @@ def test_grouped_qwen235b_prefill_2048_q4(ctx):
 
 
 def test_grouped_equals_decode_path(ctx):
-    """The grouped path (24 tokens, above this top-6 layer's threshold of 16)
+    """The grouped path (24 tokens, above this top-6 layer's threshold of 22)
     and the decode path (one token at a time) give the same bits."""
     E, Hd, I, k, T = 64, 512, 128, 6, 24
     L = O.OracleMoe.synthetic(O.Q4_0, Hd, I, E, k, normalize_topk=True, seed=12, with_router=True)

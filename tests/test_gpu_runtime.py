@@ -56,10 +56,10 @@ def test_capture_refuses_scratch_growth(ctx, layer):
         b.free()
 
 
-@pytest.mark.parametrize("T", [3, 20])
+@pytest.mark.parametrize("T", [3, 24])
 def test_reserve_sizes_scratch_for_capture(ctx, layer, T):
     """hale_moe_reserve sizes the layer's scratch (and from the grouped
-    threshold on, 16 tokens for this top-4 layer, its grouped workspace) so
+    threshold on, 22 tokens for this top-4 layer, its grouped workspace) so
     that the first forward can be captured; replays are bit-exact.  A
     reserve that would have to grow scratch during a capture is refused."""
     L, moe = layer
@@ -121,7 +121,7 @@ def test_graph_of_grouped_forward_replays(ctx, layer):
     """A captured grouped (multi-token) forward replays bit-exact, several
     times, with different inputs uploaded between the replays."""
     L, moe = layer
-    T = 16
+    T = 24
     bx, bo = ctx.malloc(T * HID * 4), ctx.malloc(T * HID * 4)
     bx.upload(O.normal(4, T * HID))
     moe.forward_device(T, bx.address, bo.address)
