@@ -266,6 +266,47 @@ def copy_calibration(nbytes, reps=5):
             "GB_per_s": round(2 * nbytes / ms / 1e6, 1)}
 
 
+STREAM_POOL = 768 << 20          # three times the 256 MB last-level cache: every read is cold
+STREAM_WORKGROUPS = (512, 1024, 2048)
+
+
+def stream_ceiling(named_bytes, reps=12):
+    """What one launch can stream from HBM: the library's plain read kernel
+    over each kernel's bytes, each launch timed like the decode kernels'
+    (events around the launch, eager), cold (consecutive reads walk a pool
+    three times the last-level cache); the best of three work-group counts.
+    {name: {"bytes", "us", "GB_per_s", "workgroups"}}."""
+    ctx = H.Context(0)
+    pool = ctx.malloc(STREAM_POOL)
+    pool.fill_normal(5, STREAM_POOL // 4)
+    out = ctx.malloc(4 * max(STREAM_WORKGROUPS))
+    pool.stream_read(1 << 20, 512, out)  # first launch of the kernel, untimed
+    ctx.synchronize()
+    res, off = {}, 0
+    for name, nbytes in named_bytes.items():
+        n = (nbytes + 4095) // 4096 * 4096
+        best = None
+        for wg in STREAM_WORKGROUPS:
+            ctx.profile(True)
+            ctx.profile_reset()
+            for _ in range(reps):
+                if off + n > STREAM_POOL:
+                    off = 0
+                pool.stream_read(n, wg, out, offset=off)
+                off += n
+            tot_ms, cnt = ctx.profile_read()["stream_read"]
+            ctx.profile(False)
+            us = 1000 * tot_ms / cnt
+            if best is None or us < best[0]:
+                best = (us, wg)
+        res[name] = {"bytes": n, "us": round(best[0], 2), "GB_per_s": round(n / best[0] / 1e3, 1),
+                     "workgroups": best[1]}
+    pool.free()
+    out.free()
+    ctx.close()
+    return res
+
+
 def decode_eager(args):
     """Two eager passes over the resident layers (no graph): the run the
     per-dispatch counter passes profile.  --decode-workload picks one of the
@@ -1071,6 +1112,27 @@ def main():
             attn.append(gpu_attention(name, dt, hid, nh, nkv, hd, qk, npos))
             log(f"attention {name}: {attn[-1]['us_per_token']} us/token, {attn[-1]['GB_per_s']} GB/s")
 
+    ceiling = None
+    if not args.no_prefill:
+        # each decode kernel beside a plain read of its bytes in one launch
+        sizes, kernel_us = {}, {}
+        for (name, dt, hid, inter, ex, k, nl), r in [(("qwen3-30b-a3b decode q4_0", DTYPE, HID, INTER, E,
+                                                        TOPK, args.layers), {"kernels": kernels})] + \
+                [(spec, m) for spec, m in zip(DECODE_MORE, more)]:
+            short = name.split(" decode")[0]
+            per = {"route": ex * hid * 4, "gate_up": k * 2 * inter * H.row_bytes(dt, hid),
+                   "down": k * hid * H.row_bytes(dt, inter)}
+            for kern, nbytes in per.items():
+                if kern in r["kernels"]:
+                    sizes[f"{short} {kern}"] = nbytes
+                    kernel_us[f"{short} {kern}"] = r["kernels"][kern]["avg_us"]
+        ceiling = stream_ceiling(sizes)
+        for key, c in ceiling.items():
+            c["kernel_us"] = kernel_us[key]
+            c["kernel_over_ceiling"] = round(kernel_us[key] / c["us"], 3)
+            log(f"{key}: {kernel_us[key]} us vs one-launch read of {c['bytes'] / 1e6:.1f} MB "
+                f"{c['us']} us ({c['GB_per_s']} GB/s)")
+
     prefill = []
     if not args.no_prefill:
         for (name, dt, hid, inter, ex, k, tok, bound) in PREFILL:
@@ -1127,6 +1189,7 @@ def main():
         "expert": expert,
         "decode_few_tokens": few,
         "decode_more": more,
+        "stream_read_ceiling": ceiling,
         "float_matvec": fmv,
         "reference_kernel_bench": {"workload": "hale bench kernels: WeightMatrix::matvec 4096 x 4096, "
                                                "values ((i % 97) - 48) / 97, x = 0.5",

@@ -206,6 +206,10 @@ hipError_t launch_block_sums(int dtype, const uint8_t* codes, const ActBlock* ac
                              size_t cols, int32_t* isums, hipStream_t st);
 hipError_t launch_fill(float* p, size_t n, float v, hipStream_t st);
 hipError_t launch_copy(void* dst, const void* src, size_t n16, hipStream_t st);
+// out[g] = XOR of the 32-bit words of work-group g's contiguous chunk of
+// src[n16] (workgroups in 1..65535)
+hipError_t launch_stream_read(const void* src, size_t n16, unsigned workgroups, unsigned* out,
+                              hipStream_t st);
 // out[rows] = W x for row-major f32 / f16 / bf16 W [rows][cols] (x 16-byte
 // aligned), in the reference's 8-lane dot order.
 hipError_t launch_gemv_float(int dtype, const void* w, const float* x, size_t rows, size_t cols,
@@ -262,6 +266,7 @@ enum KernelKind : int {
   K_ATTENTION,
   K_GATHER,
   K_DECODE,
+  K_STREAM_READ,
   K_KINDS
 };
 

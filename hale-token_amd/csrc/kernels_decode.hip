@@ -2077,6 +2077,36 @@ __global__ __launch_bounds__(256) void k_copy(u32x4* __restrict__ dst, const u32
     __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
+// Plain streaming read, the calibration for what one launch can stream from
+// HBM: work-group g reads a contiguous chunk of src with sixteen 16-byte
+// loads in flight per thread and writes the XOR of every 32-bit word it
+// read to out[g] (0 for a work-group whose chunk is empty).
+__global__ __launch_bounds__(256) void k_stream_read(const u32x4* __restrict__ src, size_t n16,
+                                                     unsigned* __restrict__ out) {
+  constexpr int U = 16;
+  const size_t chunk = (n16 + gridDim.x - 1) / gridDim.x;
+  const size_t b0 = min(n16, (size_t)blockIdx.x * chunk), b1 = min(n16, b0 + chunk);
+  unsigned acc = 0;
+  size_t i = b0 + threadIdx.x;
+  for (; i + (size_t)(U - 1) * 256 < b1; i += (size_t)U * 256) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] = __builtin_nontemporal_load(src + i + u * 256);
+#pragma unroll
+    for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < b1; i += 256) {
+    const u32x4 v = src[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc ^= (unsigned)__shfl_xor((int)acc, o);
+  __shared__ unsigned s_w[4];
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = s_w[0] ^ s_w[1] ^ s_w[2] ^ s_w[3];
+}
+
 // ===========================================================================
 // Launchers
 // ===========================================================================
@@ -2417,6 +2447,12 @@ hipError_t launch_fill_normal(float* p, size_t n, uint64_t seed, float mean, flo
 hipError_t launch_fill(float* p, size_t n, float v, hipStream_t st) {
   if (n == 0) return hipSuccess;
   return launch(k_fill, blocks_for(n, 256), 256, 0, st, p, n, v);
+}
+
+hipError_t launch_stream_read(const void* src, size_t n16, unsigned workgroups, unsigned* out,
+                              hipStream_t st) {
+  if (workgroups < 1 || workgroups > 65535) return hipErrorInvalidValue;
+  return launch(k_stream_read, workgroups, 256, 0, st, (const u32x4*)src, n16, out);
 }
 
 hipError_t launch_copy(void* dst, const void* src, size_t n16, hipStream_t st) {

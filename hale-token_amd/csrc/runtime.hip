@@ -2386,6 +2386,19 @@ extern "C" int hale_copy_device(hale_ctx* c, void* d_dst, const void* d_src, siz
   return HALE_OK;
 }
 
+extern "C" int hale_stream_read_device(hale_ctx* c, const void* d_src, size_t n, unsigned workgroups,
+                                       uint32_t* d_out) {
+  if (!c || !d_out || (n && !d_src)) return fail(c, HALE_EINVAL, "stream_read_device: NULL argument");
+  if (n % 16 || (uintptr_t)d_src % 16)
+    return fail(c, HALE_EINVAL, "stream_read_device: size and address must be multiples of 16");
+  if (workgroups < 1 || workgroups > 65535)
+    return fail(c, HALE_EINVAL, "stream_read_device: %u work-groups outside 1..65535", workgroups);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  HIPCHK(c, hipSetDevice(c->device));
+  LAUNCH(c, K_STREAM_READ, launch_stream_read(d_src, n / 16, workgroups, d_out, c->stream));
+  return HALE_OK;
+}
+
 extern "C" int hale_timer_start(hale_ctx* c) {
   if (!c) return HALE_EINVAL;
   std::lock_guard<std::recursive_mutex> g(c->mu);
@@ -2462,7 +2475,7 @@ extern "C" const char* hale_kernel_name(int kind) {
   static const char* names[K_KINDS] = {"route", "gate_up", "down", "act_quant", "gemv", "encode",
                                        "repack", "fill", "group", "grouped_gate_up",
                                        "grouped_down", "combine", "copy", "rms_norm",
-                                       "attention", "gather", "decode"};
+                                       "attention", "gather", "decode", "stream_read"};
   return kind >= 0 && kind < K_KINDS ? names[kind] : "";
 }
 

@@ -118,6 +118,7 @@ SIGNATURES = {
     "hale_memcpy_dtoh": (C.c_int, [_vp, _vp, _vp, _sz]),
     "hale_fill_normal_device": (C.c_int, [_vp, C.c_uint64, C.c_float, C.c_float, _vp, _sz]),
     "hale_copy_device": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "hale_stream_read_device": (C.c_int, [_vp, _vp, _sz, C.c_uint, _vp]),
     "hale_timer_start": (C.c_int, [_vp]),
     "hale_timer_stop": (C.c_int, [_vp, C.POINTER(C.c_double)]),
     "hale_profile_enable": (C.c_int, [_vp, C.c_int]),
@@ -335,6 +336,15 @@ class DeviceBuffer:
             raise ValueError("copy past the end of a buffer")
         self.ctx.check(lib().hale_copy_device(self.ctx.handle, _vp(self.address), _vp(src.address),
                                               nbytes), "copy")
+
+    def stream_read(self, nbytes: int, workgroups: int, out: "DeviceBuffer", offset: int = 0):
+        """Reads self[offset, offset + nbytes) once with the library's
+        streaming-read kernel; out[g] (uint32) = XOR of the words of
+        work-group g's contiguous chunk."""
+        if offset < 0 or offset + nbytes > self.nbytes or 4 * workgroups > out.nbytes:
+            raise ValueError("stream_read past the end of a buffer")
+        self.ctx.check(lib().hale_stream_read_device(self.ctx.handle, _vp(self.address + offset), nbytes,
+                                                     workgroups, _vp(out.address)), "stream_read")
 
     def free(self):
         if self.ptr and self.ctx.alive:

@@ -504,6 +504,13 @@ int hale_fill_normal_device(hale_ctx *ctx, uint64_t seed, float mean,
  * addresses multiples of 16), enqueued on the context's stream: one read and
  * one write per byte, the calibration for HBM traffic counters. */
 int hale_copy_device(hale_ctx *ctx, void *d_dst, const void *d_src, size_t n);
+/* Reads d_src[0, n) once by a plain streaming kernel of `workgroups`
+ * work-groups (1..65535), each over a contiguous chunk, and writes the XOR
+ * of the 32-bit words of chunk g to d_out[g] (n and d_src multiples of 16).
+ * No counterpart in the reference: the yardstick for what one launch of n
+ * bytes can stream from HBM, timed beside the decode kernels. */
+int hale_stream_read_device(hale_ctx *ctx, const void *d_src, size_t n, unsigned workgroups,
+                            uint32_t *d_out);
 
 /* Wall time of the work enqueued between start and stop, from HIP events
  * recorded on the context's stream; stop waits for that work. */
