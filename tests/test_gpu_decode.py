@@ -339,6 +339,26 @@ def test_moe_decode_few_tokens(ctx, dtype, hidden, inter, E, k, T):
     moe.close()
 
 
+@pytest.mark.parametrize("dtype,hidden,inter,E,k,T", [
+    (H.Q4_0, 256, 768, 16, 8, 12),     # q4_0 16-wave gate/up; down rows of 24 blocks
+    (H.Q8_0, 512, 1024, 16, 6, 13),    # q8_0 8-wave gate/up; 32 blocks
+    (H.Q4_0, 2080, 1536, 16, 8, 14),   # q4_0 rows of 65 blocks: 8-wave gate/up; 48 blocks
+    (H.Q8_0, 256, 2048, 16, 5, 17),    # 64 blocks
+    (H.Q4_0, 256, 4096, 16, 4, 21),    # 128 blocks, one token below the grouped threshold
+    (H.Q4_0, 256, 64, 300, 8, 12),     # more than 256 experts: the 1024-expert selection
+])
+def test_moe_decode_cached_weight_loads(ctx, dtype, hidden, inter, E, k, T):
+    """Decode passes of 12 to 21 tokens (top-4 and wider, below the grouped
+    threshold of 22) load the weights through the caches: every gate/up
+    form and every down row class of that path, bit-exact per token."""
+    L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=True,
+                              seed=hidden + inter + E + k + T)
+    moe = make_layer(ctx, L)
+    assert moe.grouped_min_tokens == 22
+    _few_tokens_check(L, moe, O.normal(9200 + T, T * hidden).reshape(T, hidden))
+    moe.close()
+
+
 @pytest.mark.parametrize("dtype,hidden,inter,k,T", [
     (H.Q4_0, 256, 32, 4, 1),      # one block per row: a partial first group
     (H.Q8_0, 512, 224, 5, 2),     # 7 blocks
