@@ -389,7 +389,10 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
 constexpr int RT_E = 16, RT_T = 8, RT_K = 64;
 constexpr int RT_STRIDE = RT_K + 4;                 // floats per chain row (16-byte aligned)
 constexpr int RT_BUF = (RT_E + RT_T) * 8 * RT_STRIDE;  // floats per buffer
-constexpr int ROUTE_TILED_MIN_T = 64;
+// From 32 tokens (Qwen3-30B-A3B layer, graph replay: 48 tokens 125 -> 121 us
+// per step, equal at 32, slower below 24, where the separate quantization
+// launch costs more than the tiling saves).
+constexpr int ROUTE_TILED_MIN_T = 32;
 
 __global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __restrict__ router,
                                                              const float* __restrict__ x, int H,

@@ -65,7 +65,8 @@ def test_grouped_small(ctx, dtype, with_router):
 
 
 @pytest.mark.parametrize("dtype,Hd,I,E,k,T", [
-    (H.Q4_0, 2048, 64, 128, 8, 64),    # 64+ tokens: the router's 16-expert x 8-token tiles
+    (H.Q4_0, 2048, 64, 128, 8, 64),    # 32+ tokens: the router's 16-expert x 8-token tiles
+    (H.Q8_0, 1024, 64, 32, 6, 33),     # ... from 32 tokens: a partial token tile of one
     (H.Q8_0, 2080, 64, 20, 4, 100),    # a partial expert tile, a partial token tile, a partial chunk (260 steps)
     (H.Q4_0, 4096, 64, 128, 8, 72),    # 512 steps: eight chunks
 ])
