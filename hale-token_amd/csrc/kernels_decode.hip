@@ -385,19 +385,22 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
 // of RT_K steps, two buffers, so chunk c + 1 loads while chunk c is added,
 // and every staged row serves 8 or 16 logits.  The eight chains of a logit
 // are reduced in the one-token kernel's fixed order, so each logit has its
-// bits.  The activation blocks are quantized by k_act_quant.
+// bits.  Then the work-groups quantize the token tile's activation blocks
+// (as k_act_quant does), each taking its share: block q of the tile goes to
+// the work-group of expert column q % gridDim.x.
 constexpr int RT_E = 16, RT_T = 8, RT_K = 64;
 constexpr int RT_STRIDE = RT_K + 4;                 // floats per chain row (16-byte aligned)
 constexpr int RT_BUF = (RT_E + RT_T) * 8 * RT_STRIDE;  // floats per buffer
-// From 32 tokens (Qwen3-30B-A3B layer, graph replay: 48 tokens 125 -> 121 us
-// per step, equal at 32, slower below 24, where the separate quantization
-// launch costs more than the tiling saves).
+// From 32 tokens (Qwen3-30B-A3B layer, graph replay: 48 tokens 125 -> 118.5
+// us per step and 32 tokens 116 -> 113.6 us against one work-group per
+// (expert, token); at 8 and 16 tokens the tiles were 5-10 % slower).
 constexpr int ROUTE_TILED_MIN_T = 32;
 
 __global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __restrict__ router,
                                                              const float* __restrict__ x, int H,
                                                              int E, int T,
-                                                             float* __restrict__ logits) {
+                                                             float* __restrict__ logits,
+                                                             ActBlock* __restrict__ act) {
   __shared__ __attribute__((aligned(16))) float buf[2][RT_BUF];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -465,6 +468,15 @@ __global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __rest
     const float s0v = (a0 + a4) + (a1 + a5);
     const float s1v = (a2 + a6) + (a3 + a7);
     logits[(size_t)tok * E + e] = (s0v + s1v) + tail;
+  }
+  // this work-group's share of the tile's activation blocks, 8 lanes per
+  // block, 128 blocks per pass (the bound is uniform per 8-lane group)
+  const int nb = H / QK;
+  const int nq = min(RT_T, T - t0) * nb;
+  for (int q = blockIdx.x + gridDim.x * (tid >> 3); q < nq; q += gridDim.x * 128) {
+    const int tk = q / nb, b = q - tk * nb;
+    const size_t blk = (size_t)(t0 + tk) * nb + b;
+    quant_block8(*(const f32x4*)(x + blk * QK + 4 * (tid & 7)), tid & 7, act + blk);
   }
 }
 
@@ -2198,12 +2210,10 @@ hipError_t launch_route_logits(const float* router, const float* x, int H, int E
                                ActBlock* act, float* logits, hipStream_t st) {
   if (H > ROUTE_MAX_H || E > ROUTE_MAX_E || H % QK || E < 1 || T < 1) return hipErrorInvalidValue;
   if (T >= ROUTE_TILED_MIN_T) {
-    // many tokens: 16 experts x 8 tokens per work-group, then the activation
-    // blocks by the quantization kernel
+    // many tokens: 16 experts x 8 tokens per work-group, the activation
+    // blocks quantized by the same launch
     const dim3 grid((E + RT_E - 1) / RT_E, (T + RT_T - 1) / RT_T);
-    hipError_t e = launch(k_route_logits_tiled, grid, 1024, 0, st, router, x, H, E, T, logits);
-    if (e != hipSuccess) return e;
-    return launch_act_quant(x, (size_t)T * (H / QK), act, st);
+    return launch(k_route_logits_tiled, grid, 1024, 0, st, router, x, H, E, T, logits, act);
   }
   dim3 grid(E, T);
   return launch(k_route_logits, grid, ROUTE_THREADS, 0, st, router, x, H, E, act, logits);
