@@ -37,6 +37,12 @@ WeightMatrix::matvec per dtype: f32, bf16, f16, q8_0, q4_0) on the GPU, cold
 oracle at the same shape on the host in cpu_baseline.
 strict_dropin: the decode workload through the unchanged provider surface
 (route, fetch, k x Expert::forward, host combine), microseconds per token.
+decode_few_tokens / decode_band: the same layers with 2 to 64 tokens per
+step (graph replay): the default path (one decode pass below the layer's
+grouped threshold, the expert-grouped path from it) and, at 16, 24 and 32
+tokens, both paths forced.
+stream_read_ceiling: each decode kernel beside the library's plain read of
+the same bytes in one launch.
 prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
 2048 tokens q4_0 H 4096 I 1536; 128 experts, top-8, Zipf-skewed routing)
 with tokens/s, TOPS, the fraction of the int8 MFMA peak and a roofline
@@ -936,6 +942,45 @@ def gpu_decode(args):
             few.append({"tokens": T, "us_per_step": round(us, 2), "us_per_token": round(us / T, 2),
                         "tokens_per_s": round(1e6 * T / us, 1), "timing": replay_stats(t, L)})
             log(f"decode {T} tokens per step: {us:.2f} us/step ({us / T:.2f} us/token)")
+    # 8 to 64 tokens per step: the default path (the decode pass below the
+    # layer's grouped threshold, the grouped path from it) and, around the
+    # threshold, both paths forced
+    band = []
+    if not args.no_prefill:
+        band_t = (8, 16, 24, 32, 64)
+        xb = ctx.malloc((max(band_t) + 8) * HID * 4)  # step inputs start up to 7 rows in
+        xb.fill_normal(98, (max(band_t) + 8) * HID, 0.0, 1.0)
+        ob = ctx.malloc(max(band_t) * HID * 4)
+        gmin0 = layers[0].grouped_min_tokens
+
+        def time_band(T):
+            def step_b(s):
+                layers[s % L].forward_device(T, xb.offset((s % 8) * HID * 4), ob.address)
+            for s in range(L):  # sizes each layer's scratch for T tokens
+                step_b(s)
+            ctx.synchronize()
+            g = ctx.capture(lambda: [step_b(s) for s in range(L)])
+            g.launch()
+            ctx.synchronize()
+            t = time_replays(ctx, g, 10)
+            g.close()
+            return round(1000 * float(np.median(t)) / L, 2)
+
+        for T in band_t:
+            row = {"tokens": T, "path": "decode pass" if T < gmin0 else "grouped", "us_per_step": time_band(T)}
+            if T in (16, 24, 32):
+                for m in layers:
+                    m.set_grouped_min_tokens(T + 1)
+                row["decode_pass_us"] = time_band(T)
+                for m in layers:
+                    m.set_grouped_min_tokens(2)
+                row["grouped_us"] = time_band(T)
+                for m in layers:
+                    m.set_grouped_min_tokens(gmin0)
+            band.append(row)
+            log(f"band {T} tokens: {row}")
+        xb.free()
+        ob.free()
     dropin = None
     if not args.no_prefill:
         xs_host = np.random.default_rng(99).standard_normal((64, HID), dtype=np.float32)
@@ -945,7 +990,7 @@ def gpu_decode(args):
     for m in layers:
         m.close()
     ctx.close()
-    return steps, ms, prof, warm, replay_stats(times, L), few, dropin
+    return steps, ms, prof, warm, replay_stats(times, L), few, dropin, band
 
 
 def cpu_info():
@@ -1067,7 +1112,7 @@ def main():
         return
 
     bytes_step = TOPK * expert_bytes(DTYPE, HID, INTER) + E * HID * 4
-    steps, ms, prof, warm, rstats, few, dropin = gpu_decode(args)
+    steps, ms, prof, warm, rstats, few, dropin, band = gpu_decode(args)
     sec = ms / 1000.0
     gbs = bytes_step * steps / sec / 1e9
 
@@ -1188,6 +1233,7 @@ def main():
         "kernels": kernels,
         "expert": expert,
         "decode_few_tokens": few,
+        "decode_band": band,
         "decode_more": more,
         "stream_read_ceiling": ceiling,
         "float_matvec": fmv,
