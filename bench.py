@@ -39,8 +39,9 @@ strict_dropin: the decode workload through the unchanged provider surface
 (route, fetch, k x Expert::forward, host combine), microseconds per token.
 decode_few_tokens / decode_band: the same layers with 2 to 64 tokens per
 step (graph replay): the default path (one decode pass below the layer's
-grouped threshold, the expert-grouped path from it) and, at 16, 24 and 32
-tokens, both paths forced.
+grouped threshold, from it the expert-grouped row-chain kernels up to the
+band threshold, the grouped int8 matrix products above) and, from 16
+tokens, each of the three forced.
 stream_read_ceiling: each decode kernel beside the library's plain read of
 the same bytes in one launch.
 prefill: the two multi-token workloads (512 tokens q8_0 H 2048 I 768, and
@@ -943,15 +944,17 @@ def gpu_decode(args):
                         "tokens_per_s": round(1e6 * T / us, 1), "timing": replay_stats(t, L)})
             log(f"decode {T} tokens per step: {us:.2f} us/step ({us / T:.2f} us/token)")
     # 8 to 64 tokens per step: the default path (the decode pass below the
-    # layer's grouped threshold, the grouped path from it) and, around the
-    # threshold, both paths forced
+    # layer's grouped threshold, from it the grouped row-chain kernels up to
+    # the band threshold, the grouped matrix products above) and, from 16
+    # tokens, each path forced
     band = []
     if not args.no_prefill:
-        band_t = (8, 16, 24, 32, 64)
+        band_t = (8, 12, 16, 24, 32, 48, 64)
         xb = ctx.malloc((max(band_t) + 8) * HID * 4)  # step inputs start up to 7 rows in
         xb.fill_normal(98, (max(band_t) + 8) * HID, 0.0, 1.0)
         ob = ctx.malloc(max(band_t) * HID * 4)
         gmin0 = layers[0].grouped_min_tokens
+        bmax0 = layers[0].band_max_tokens
 
         def time_band(T):
             def step_b(s):
@@ -966,17 +969,22 @@ def gpu_decode(args):
             g.close()
             return round(1000 * float(np.median(t)) / L, 2)
 
+        def forced(gmin, bmax):
+            for m in layers:
+                m.set_grouped_min_tokens(gmin)
+                m.set_band_max_tokens(bmax)
+
         for T in band_t:
-            row = {"tokens": T, "path": "decode pass" if T < gmin0 else "grouped", "us_per_step": time_band(T)}
-            if T in (16, 24, 32):
-                for m in layers:
-                    m.set_grouped_min_tokens(T + 1)
+            path = "decode pass" if T < gmin0 else ("row chains" if T <= bmax0 else "matrix products")
+            row = {"tokens": T, "path": path, "us_per_step": time_band(T)}
+            if T >= 16:
+                forced(T + 1, bmax0)
                 row["decode_pass_us"] = time_band(T)
-                for m in layers:
-                    m.set_grouped_min_tokens(2)
-                row["grouped_us"] = time_band(T)
-                for m in layers:
-                    m.set_grouped_min_tokens(gmin0)
+                forced(2, 1 << 20)
+                row["row_chains_us"] = time_band(T)
+                forced(2, 0)
+                row["matrix_products_us"] = time_band(T)
+                forced(gmin0, bmax0)
             band.append(row)
             log(f"band {T} tokens: {row}")
         xb.free()

@@ -15,7 +15,9 @@
 //     routing itself are the decode path's exact formulas.
 //
 // Pipeline: route (per token) -> group (counts, prefix sums, stable scatter,
-// tile list) -> grouped gate/up -> grouped down -> combine.
+// tile list) -> grouped gate/up -> grouped down -> combine.  Calls of few
+// tokens per expert run the same pipeline with row-chain kernels in place
+// of the matrix products (and no gather).
 #pragma clang fp contract(off)
 
 #include "hale_device.h"
@@ -46,7 +48,7 @@ constexpr int TACT_BLOCK = TACT_CODES + TM * 4;
 struct Tile {
   int expert;
   int row0;  // first sorted position
-  int rows;  // 1..TM
+  int rows;  // 1..tile rows (TM; BAND_ROWS for the row-chain kernels)
   int pad;
 };
 
@@ -61,7 +63,8 @@ struct Tile {
 // with equal experts in a 64-wide chunk are found with ballots over the
 // expert's bits.  The layer's routing counts (stats, optional) grow by each
 // expert's group size here rather than by one atomic per assignment, which
-// would serialize on the popular experts' counters.
+// would serialize on the popular experts' counters.  Each expert's group is
+// cut into tiles of at most tm rows.
 
 __device__ __forceinline__ unsigned long long match_mask(int e, int nbits, bool valid) {
   unsigned long long m = __ballot(valid);
@@ -77,7 +80,8 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
                                                             int* __restrict__ pos_of,
                                                             Tile* __restrict__ tiles,
                                                             int* __restrict__ ntiles,
-                                                            unsigned long long* __restrict__ stats) {
+                                                            unsigned long long* __restrict__ stats,
+                                                            int tm) {
   __shared__ int cnt[GROUP_WAVES][GROUP_MAX_E];
   __shared__ int scan_a[GROUP_MAX_E];
   __shared__ int scan_t[GROUP_MAX_E];
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
     int tot = 0;
     if (tid < E)
       for (int q = 0; q < GROUP_WAVES; q++) tot += cnt[q][tid];
-    int va = tot, vt = (tot + TM - 1) / TM;
+    int va = tot, vt = (tot + tm - 1) / tm;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const int ua = __shfl_up(va, off), ut = __shfl_up(vt, off);
@@ -171,11 +175,11 @@ __global__ __launch_bounds__(64 * GROUP_WAVES) void k_group(const int* __restric
       run += c;
     }
     const int t0 = e ? scan_t[e - 1] : 0;
-    for (int i = 0; i * TM < tot_e; i++) {
+    for (int i = 0; i * tm < tot_e; i++) {
       Tile tl;
       tl.expert = e;
-      tl.row0 = base + i * TM;
-      tl.rows = min(TM, tot_e - i * TM);
+      tl.row0 = base + i * tm;
+      tl.rows = min(tm, tot_e - i * tm);
       tl.pad = 0;
       tiles[t0 + i] = tl;
     }
@@ -504,6 +508,280 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   }
 }
 
+// ---------------------------------------------------------------------------
+// row-chain grouped products (few assignments per expert)
+// ---------------------------------------------------------------------------
+//
+// A call of tens of tokens gives most experts one to a few assignments, so
+// the 32-row products above are mostly padding and each wave's chain of K
+// blocks is bound by its own latency.  Here a band tile holds at most
+// BAND_ROWS assignments of one expert, and lane l of a wave owns one weight
+// row (gate/up: lanes 0-31 the gate rows, 32-63 the up rows of one 32-row
+// I-tile; down: two 32-row H-tiles).  The lane walks its row's K blocks
+// with a ring of D blocks in flight and adds each block's term
+// (d_w * d_x) * isum to every assignment's sum, block after block: the
+// reference's dot_q8_0 / dot_q4_0 and its left-to-right fold
+// (src/tensor/quant.rs:115-144).  An assignment's activation block is the
+// same for every lane of the wave: it comes with the block's weights in the
+// ring, spread over the lanes, and enters the dot products as scalar
+// operands; the gate/up input is read in place (token-major, through perm),
+// with no gather.
+// Assignments per band tile: two.  Tiles of four or eight (more terms per
+// weight block, fewer re-reads of an expert's weights) measured slower at
+// every size where this path is the faster one: their longer per-block
+// chains leave the ring's loads waiting.
+constexpr int BAND_ROWS = 2;
+constexpr int BAND_WAVES = 4;
+
+struct BandArgs {
+  const uint8_t* codes;  // gate (gate/up) or down weights, expert e at + e * stride
+  const uint16_t* scales;
+  const uint8_t* codes2;  // up (gate/up)
+  const uint16_t* scales2;
+  size_t codes_stride, scales_stride;
+  int nb;   // K blocks
+  int ntc;  // 32-row output tiles: I / 32 (gate/up), H / 32 (down)
+  int rows;  // output rows (down stores rows below it)
+  int wpt;   // waves per band tile: ntc (gate/up), ceil(ntc / 2) (down)
+  const Tile* tiles;
+  const int* ntiles;
+  const int* perm;  // gate/up: sorted position p is assignment perm[p], token perm[p] / k
+  int k;
+  const ActBlock* act;  // gate/up: [T][nb] by token; down: [A][nb] by sorted position
+  ActBlock* hout;       // gate/up output: [A][I / 32] by sorted position
+  float* y;             // down output: [A][H] by sorted position
+};
+
+// LDS of a band work-group: the tile's activation blocks [BAND_ROWS][nb]
+// (48 bytes each), then per wave the double-buffered scales of its ring
+// cycle, [2][2 halves][D blocks][32 rows] f16.
+constexpr int BAND_MAX_NB = 256;  // K blocks per row (24 KB of activations)
+static size_t band_lds(int nb, int d) {
+  return (size_t)BAND_ROWS * nb * sizeof(ActBlock) + (size_t)BAND_WAVES * 2 * 2 * d * TILE * 2;
+}
+
+// Work-group: BAND_WAVES waves of one band tile (gpt work-groups per tile,
+// waves past the tile's wpt only help stage).  The XCDs take work-groups in
+// turn (linear id % 8), so work-group L runs item (L % 8) * per + L / 8:
+// the work-groups of one tile run on one XCD.  Both assignments of a tile
+// are computed; a tile of one repeats it, and the copy is never stored.
+//
+// Each lane's row streams through a ring of D code blocks; per ring cycle
+// (D blocks) the wave loads the cycle after next's scales as whole 16-byte
+// pieces (8 rows of one block) and parks them in LDS, so a block costs one
+// load per lane.  The activation words of block b come from LDS, one word
+// per lane (word i of assignment j in lane 12 j + i), and enter the dot
+// products through readlane as scalar operands.
+template <int DT, bool GATE_UP, int D>
+__global__ __launch_bounds__(64 * BAND_WAVES) void k_band(BandArgs a) {
+  extern __shared__ __attribute__((aligned(16))) u32x4 s_band[];
+  constexpr int CH = Layout<DT>::CH;
+  constexpr int NR = BAND_ROWS;
+  constexpr int LPA = 12;      // lanes per assignment: one ActBlock word each
+  constexpr int SPL = D / 8;   // scale pieces per lane per cycle
+  constexpr int APT = (NR * BAND_MAX_NB * 3 + 64 * BAND_WAVES - 1) / (64 * BAND_WAVES);  // activation pieces per thread
+  static_assert(D % 8 == 0, "a ring cycle's scales are whole pieces per lane");
+  static_assert(NR * LPA <= 64, "one word per lane");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nt = *a.ntiles;
+  const int gpt = (a.wpt + BAND_WAVES - 1) / BAND_WAVES;
+  const int wgs = nt * gpt;
+  const int per = (wgs + 7) >> 3;
+  const int wg = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= per || wg >= wgs) return;  // the whole work-group
+  const int ti = wg / gpt;
+  const int wt = min((wg - ti * gpt) * BAND_WAVES + wave, a.wpt - 1);  // spare waves repeat the last
+  const Tile tl = a.tiles[ti];
+  const int nb = a.nb, n = tl.rows;
+  const size_t e = (size_t)tl.expert;
+
+  // the tile's activation blocks: loads first, stored once the ring is in
+  // flight.  Threads past the last piece load and store it again (the same
+  // bytes to the same place), so the loads need no branches.
+  const int np = NR * nb * 3;
+  u32x4 av[APT];
+  {
+    int src[APT];
+#pragma unroll
+    for (int m = 0; m < APT; m++) {
+      const int q = min((int)threadIdx.x + m * 64 * BAND_WAVES, np - 1);
+      const int j = q / (nb * 3);
+      const int p = tl.row0 + min(j, n - 1);
+      src[m] = GATE_UP ? a.perm[p] : p;
+    }
+#pragma unroll
+    for (int m = 0; m < APT; m++) {
+      const int q = min((int)threadIdx.x + m * 64 * BAND_WAVES, np - 1);
+      const int rem = q - q / (nb * 3) * (nb * 3);
+      const size_t row = GATE_UP ? (size_t)(src[m] / a.k) : (size_t)src[m];
+      av[m] = ((const u32x4*)(a.act + row * nb))[rem];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int half = lane >> 5, r = lane & 31;
+  const size_t tile = GATE_UP ? (size_t)wt : 2 * (size_t)wt + half;
+  const uint8_t* crow = (GATE_UP && half ? a.codes2 : a.codes) + e * a.codes_stride +
+                        (tile * nb * CH * TILE + r) * 16;
+  const uint16_t* splane = (GATE_UP && half ? a.scales2 : a.scales) + e * a.scales_stride +
+                           tile * nb * TILE;
+  uint16_t* s_scl = (uint16_t*)((char*)s_band + (size_t)NR * nb * sizeof(ActBlock)) +
+                    wave * (2 * 2 * D * TILE);
+  // scale pieces of ring cycle c: piece m of lane r is block c D + q / 4,
+  // rows 8 (q % 4) .. + 7, q = r + 32 m (blocks past the end: the last)
+  u32x4 sp[SPL];
+  auto scale_load = [&](int c) {
+#pragma unroll
+    for (int m = 0; m < SPL; m++) {
+      const int q = r + 32 * m;
+      const int b = min(c * D + q / 4, nb - 1);
+      sp[m] = *(const u32x4*)(splane + (size_t)b * TILE + 8 * (q % 4));
+    }
+  };
+  auto scale_store = [&](int c) {
+    uint16_t* dst = s_scl + ((c & 1) * 2 + half) * D * TILE;
+#pragma unroll
+    for (int m = 0; m < SPL; m++) {
+      const int q = r + 32 * m;
+      *(u32x4*)(dst + (q / 4) * TILE + 8 * (q % 4)) = sp[m];
+    }
+  };
+  u32x4 cw[D][CH];
+  // blocks past the row's end load the last block (in bounds; unused)
+  auto load = [&](int d, int b) {
+    b = min(b, nb - 1);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+      cw[d][c] = __builtin_nontemporal_load((const u32x4*)(crow + ((size_t)b * CH + c) * TILE * 16));
+  };
+  scale_load(0);
+  __builtin_amdgcn_sched_barrier(0);
+  // the ring's first loads in slot order, as the refills come: the loop
+  // head then waits for slot 0 alone on every pass, the first included
+  // (reordered here, it would wait for all of them on every pass)
+#pragma unroll
+  for (int d = 0; d < D; d++) {
+    load(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int m = 0; m < APT; m++) s_band[min((int)threadIdx.x + m * 64 * BAND_WAVES, np - 1)] = av[m];
+  scale_store(0);
+  __builtin_amdgcn_sched_barrier(0);
+  scale_load(1);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // the activation blocks
+
+  const ActBlock* s_act = (const ActBlock*)s_band;
+  const int jl = min(lane / LPA, NR - 1);  // the lane's assignment and word
+  const unsigned* aword = (const unsigned*)(s_act + (size_t)jl * nb) + lane % LPA;
+  // word i of assignment j's block in slot d, as a scalar
+  unsigned aw[D];
+  auto word = [&](int d, int j, int i) -> unsigned {
+    return (unsigned)__builtin_amdgcn_readlane((int)aw[d], LPA * j + i);
+  };
+  // sums start at +0.0 like the reference's `let mut total = 0.0`
+  float acc[NR];
+#pragma unroll
+  for (int j = 0; j < NR; j++) acc[j] = 0.0f;
+  uint16_t sw[D];
+#pragma unroll 1
+  for (int b0 = 0, c = 0; b0 < nb; b0 += D, c++) {
+    const uint16_t* scl = s_scl + ((c & 1) * 2 + half) * D * TILE + r;
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      sw[d] = scl[d * TILE];
+      aw[d] = aword[(size_t)min(b0 + d, nb - 1) * (sizeof(ActBlock) / 4)];
+    }
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      // terms of blocks past the row's end become +0.0 (the sums never
+      // hold -0.0, so adding it changes nothing)
+      const unsigned keep = b0 + d < nb ? ~0u : 0u;
+      // weight codes as the dot products take them: q8_0 the signed bytes;
+      // q4_0 the low nibbles (elements 0-15) then the high (16-31), raw
+      // 0..15, with 8 * sum(x) taken off the sum
+      unsigned w[8];
+      if constexpr (DT == Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          w[i] = cw[d][0][i];
+          w[4 + i] = cw[d][1][i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          w[i] = cw[d][0][i] & 0x0f0f0f0fu;
+          w[4 + i] = (cw[d][0][i] >> 4) & 0x0f0f0f0fu;
+        }
+      }
+      const float dw = h2f(sw[d]);
+#pragma unroll
+      for (int j = 0; j < NR; j++) {
+        // ActBlock words: codes 0-7, scale 8, code sum 9, all read into
+        // scalar registers before the products (one register reused for
+        // each would stall every product on the read before it)
+        int x[10];
+#pragma unroll
+        for (int i = 0; i < 10; i++) x[i] = (int)word(d, j, i);
+        asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]), "s"(x[5]),
+                     "s"(x[6]), "s"(x[7]), "s"(x[8]), "s"(x[9]));
+        // two chains of four dot products (integer sums: any order)
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          s0 = __builtin_amdgcn_sdot4((int)w[i], x[i], s0, false);
+          s1 = __builtin_amdgcn_sdot4((int)w[4 + i], x[4 + i], s1, false);
+        }
+        int isum = s0 + s1;
+        if constexpr (DT == Q4_0) isum -= 8 * x[9];
+        const float t = (dw * __builtin_bit_cast(float, x[8])) * (float)isum;
+        acc[j] = acc[j] + __builtin_bit_cast(float, __builtin_bit_cast(unsigned, t) & keep);
+      }
+      // the ring slot refills right after its block (left free, the
+      // scheduler hoists the refills and holds two rings of registers)
+      __builtin_amdgcn_sched_barrier(0);
+      load(d, b0 + d + D);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    scale_store(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    scale_load(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if ((wg - ti * gpt) * BAND_WAVES + wave >= a.wpt) return;  // a spare wave
+  if constexpr (GATE_UP) {
+    // h = silu(g) * u of each assignment, quantized to its q8 block of 32
+    // rows (lanes 0-31) for the down projection
+    ExpTable tab;
+    tab.load();
+#pragma unroll
+    for (int j = 0; j < NR; j++) {
+      if (j < n) {  // wave-uniform
+        const float u = __shfl(acc[j], lane + 32);
+        const float h = wave_silu(acc[j], tab) * u;
+        float scale;
+        int qsum;
+        const int q = quant_block_lane(h, &scale, &qsum);
+        if (lane < 32) {
+          ActBlock* hb = a.hout + (size_t)(tl.row0 + j) * a.ntc + wt;
+          hb->q[lane] = (int8_t)q;
+          if (lane == 0) {
+            hb->scale = scale;
+            hb->qsum = qsum;
+          }
+        }
+      }
+    }
+  } else {
+    const int row = (int)tile * TILE + r;
+#pragma unroll
+    for (int j = 0; j < NR; j++)
+      if (j < n && row < a.rows) a.y[(size_t)(tl.row0 + j) * a.rows + row] = acc[j];
+  }
+}
+
 // Gather of the gate/up input into the tile layout: work-group (tile, 8
 // blocks), thread (block, row): row r of tile ti is token perm[row0 + r] / k
 // (rows past the tile's end repeat its last row).  Grid: max_tiles x
@@ -587,10 +865,20 @@ struct WsLayout {
   size_t max_tiles;
 };
 
+// Calls of at most band_max tokens take the row-chain kernels when the
+// tiles' activation blocks fit their LDS staging.
+static bool band_on(const PrefillLayer& L, size_t T) {
+  return T <= L.band_max && std::max(L.H, L.I) / QK <= BAND_MAX_NB;
+}
+
+// The row-chain kernels' layout has tiles of BAND_ROWS rows, no gathered
+// input and the SiLU output as [A][I / 32] activation blocks in `tact`.
 static WsLayout ws_layout(const PrefillLayer& L, size_t T) {
   WsLayout w{};
   const size_t A = T * (size_t)L.k;
-  w.max_tiles = (A + TM - 1) / TM + (size_t)L.E;
+  const bool band = band_on(L, T);
+  const size_t tm = band ? (size_t)BAND_ROWS : TM;
+  w.max_tiles = (A + tm - 1) / tm + (size_t)L.E;
   size_t o = 0;
   w.perm = o;
   o += align256(A * 4);
@@ -601,9 +889,10 @@ static WsLayout ws_layout(const PrefillLayer& L, size_t T) {
   w.ntiles = o;
   o += 256;
   w.tin = o;
-  o += align256(w.max_tiles * (size_t)(L.H / QK) * TACT_BLOCK);
+  if (!band) o += align256(w.max_tiles * (size_t)(L.H / QK) * TACT_BLOCK);
   w.tact = o;
-  o += align256(w.max_tiles * (size_t)(L.I / QK) * TACT_BLOCK);
+  o += band ? align256(A * (size_t)(L.I / QK) * sizeof(ActBlock))
+            : align256(w.max_tiles * (size_t)(L.I / QK) * TACT_BLOCK);
   w.y = o;
   o += align256(A * (size_t)L.H * 4);
   w.total = o;
@@ -647,8 +936,64 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
                                            L.route_w, nullptr, st));
   }
   // 2. group assignments by expert
+  const bool band = band_on(L, T);
   HALE_STEP(K_GROUP, launch(k_group, 1, 64 * GROUP_WAVES, 0, st, L.route_idx, (int)A, L.E, perm,
-                            pos_of, tiles, ntiles, L.stats));
+                            pos_of, tiles, ntiles, L.stats, band ? BAND_ROWS : TM));
+  if (band) {
+    // 3-4. row-chain gate/up (input read in place) and down
+    BandArgs g{};
+    g.codes = L.gate_c;
+    g.scales = L.gate_s;
+    g.codes2 = L.up_c;
+    g.scales2 = L.up_s;
+    g.codes_stride = L.gc_bytes;
+    g.scales_stride = L.gs_elems;
+    g.nb = nbh;
+    g.ntc = nbi;
+    g.rows = L.I;
+    g.wpt = nbi;
+    g.tiles = tiles;
+    g.ntiles = ntiles;
+    g.perm = perm;
+    g.k = L.k;
+    g.act = L.act;
+    g.hout = (ActBlock*)tact;
+    auto grid = [&](int wpt) {
+      const size_t wgs = w.max_tiles * (size_t)((wpt + BAND_WAVES - 1) / BAND_WAVES);
+      return (unsigned)((wgs + 7) / 8 * 8);
+    };
+#define HALE_BAND(DT_, GU_, D_, args)                                                     \
+  HALE_STEP(GU_ ? K_GROUPED_GATE_UP : K_GROUPED_DOWN,                                     \
+            (launch(k_band<DT_, GU_, D_>, grid(args.wpt), 64 * BAND_WAVES,                  \
+                    (uint32_t)band_lds(args.nb, D_), st, args)))
+    if (L.dtype == Q8_0)
+      HALE_BAND(Q8_0, true, 8, g);
+    else
+      HALE_BAND(Q4_0, true, 8, g);
+    BandArgs d{};
+    d.codes = L.down_c;
+    d.scales = L.down_s;
+    d.codes_stride = L.dc_bytes;
+    d.scales_stride = L.ds_elems;
+    d.nb = nbi;
+    d.ntc = nbh;
+    d.rows = L.H;
+    d.wpt = (nbh + 1) / 2;
+    d.tiles = tiles;
+    d.ntiles = ntiles;
+    d.act = (const ActBlock*)tact;
+    d.y = y;
+    if (L.dtype == Q8_0)
+      HALE_BAND(Q8_0, false, 8, d);
+    else if (nbi >= 32)
+      HALE_BAND(Q4_0, false, 16, d);
+    else
+      HALE_BAND(Q4_0, false, 8, d);
+#undef HALE_BAND
+    dim3 gc((unsigned)((L.H + COMBINE_COLS - 1) / COMBINE_COLS), (unsigned)T);
+    HALE_STEP(K_COMBINE, launch(k_combine, gc, 256, 0, st, y, pos_of, L.route_w, L.k, L.H, out));
+    return hipSuccess;
+  }
   // 3. gather the activations into tiles, then the grouped gate/up with SiLU
   // and requantization
   const dim3 ggr((unsigned)w.max_tiles, (unsigned)((nbh + 7) / 8));

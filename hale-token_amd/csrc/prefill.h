@@ -29,6 +29,7 @@ struct PrefillLayer {
   float* route_w;        // [T][k]
   unsigned long long* stats;  // [E]
   int down_fold;         // DOWN_FOLD_EXACT or DOWN_FOLD_FMA (grouped down projection)
+  size_t band_max;       // calls of at most this many tokens take the row-chain kernels
 };
 
 // Folds of the grouped down projection: the reference's product then sum,

@@ -108,6 +108,8 @@ struct hale_moe {
   // forwards of at least grouped_min tokens take the expert-grouped path,
   // fewer the decode path (one pass over all of them)
   size_t grouped_min = 0;
+  // grouped forwards of at most band_max tokens take the row-chain kernels
+  size_t band_max = 0;
   // grouped prefill workspace
   PrefillWorkspace pw;
   // load from an expert pack: pending until the layer's next use waits for
@@ -1129,18 +1131,32 @@ static int moe_ws(hale_moe* m, size_t need, void** out) {
 }
 
 // Fewest tokens per forward that take the expert-grouped path.  The
-// grouped path costs about 60 us (Qwen3-30B shape) to 190 us (Mixtral) more
-// than the decode path before its first token, and then adds little per
-// token; the decode path adds each token's k experts' bytes.  Measured
-// crossovers (graph replay over layers visited in turn, one MI355X):
-// Qwen3-30B q4_0 and q8_0 and Qwen3-235B q4_0 (top-8 of 128) between 20
-// and 24 tokens, Mixtral (top-2 of 8) between 6 and 8.
+// grouped path has a fixed cost (routing, grouping, combine launches) and
+// then reads each touched expert once; the decode path adds each token's k
+// experts' bytes.  Measured crossovers against the row-chain grouped
+// kernels (graph replay over layers visited in turn, one MI355X): Qwen3-30B
+// q4_0 and q8_0 and Qwen3-235B q4_0 (top-8 of 128) between 8 and 12
+// tokens (at 12: 62 against 64, 83 against 85 and 161 against 178 us per
+// layer); Mixtral (top-2 of 8, no row-chain form) between 6 and 8.
 static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_t k) {
   (void)dtype;
   (void)E;
   (void)H;
   (void)I;
-  return k >= 4 ? 22 : 8;
+  return k >= 4 ? 12 : 8;
+}
+
+// Most tokens per grouped forward that take the row-chain kernels rather
+// than the matrix products.  The row-chain kernels read an expert's weights
+// once per two assignments, so they lose once experts hold several: the
+// crossovers (same measurement) sit at about 3.5 E / k tokens for Qwen3-30B
+// q4_0 (56 tokens: 119.0 against 120.6 us, 127 against 121 at 64) and
+// 2.75 E / k for q8_0 and for Qwen3-235B q4_0 (44 tokens; at 48 q8_0 172
+// against 160 us).
+static size_t default_band_max(int dtype, size_t E, size_t H, size_t I, size_t k) {
+  (void)I;
+  const size_t c4 = dtype == HALE_Q4_0 && H <= 2048 ? 14 : 11;  // quarter-assignments per expert
+  return c4 * E / (4 * std::max<size_t>(k, 1));
 }
 
 extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, size_t I, int dtype,
@@ -1169,6 +1185,7 @@ extern "C" int hale_moe_create(hale_ctx* c, uint32_t layer, size_t E, size_t H, 
   m->wide = E > FAST_MAX_E || H > FAST_MAX_H || m->k > FAST_MAX_K || I / HALE_QK > FAST_MAX_NB;
   // (a wide layer never takes the grouped path)
   m->grouped_min = m->wide ? SIZE_MAX : default_grouped_min(dtype, E, H, I, m->k);
+  m->band_max = default_band_max(dtype, E, H, I, m->k);
   m->dtype = dtype;
   m->normalize = normalize;
   m->gc_bytes = code_plane_bytes(dtype, I, H);
@@ -1405,6 +1422,7 @@ static PrefillLayer prefill_layer(hale_moe* m, const TokScratch& s) {
   L.route_w = s.route_w;
   L.stats = m->stats;
   L.down_fold = m->down_fold == HALE_FOLD_FMA ? DOWN_FOLD_FMA : DOWN_FOLD_EXACT;
+  L.band_max = m->band_max;
   return L;
 }
 
@@ -1752,6 +1770,22 @@ extern "C" int hale_moe_set_grouped_min_tokens(hale_moe* m, size_t n) {
 extern "C" int hale_moe_grouped_min_tokens(const hale_moe* m, size_t* n) {
   if (!m || !n) return fail(m ? m->ctx : nullptr, HALE_EINVAL, "grouped_min_tokens: NULL argument");
   *n = m->grouped_min;
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_set_band_max_tokens(hale_moe* m, size_t n) {
+  hale_ctx* c = m ? m->ctx : nullptr;
+  if (!m) return fail(c, HALE_EINVAL, "set_band_max_tokens: NULL layer");
+  if (n > (size_t)INT32_MAX / 64)
+    return fail(c, HALE_EINVAL, "set_band_max_tokens: %zu is above %d", n, INT32_MAX / 64);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  m->band_max = n;  // the next grouped forward sizes its workspace for it
+  return HALE_OK;
+}
+
+extern "C" int hale_moe_band_max_tokens(const hale_moe* m, size_t* n) {
+  if (!m || !n) return fail(m ? m->ctx : nullptr, HALE_EINVAL, "band_max_tokens: NULL argument");
+  *n = m->band_max;
   return HALE_OK;
 }
 

@@ -92,6 +92,8 @@ SIGNATURES = {
     "hale_moe_set_grouped_min_tokens": (C.c_int, [_vp, _sz]),
     "hale_moe_reserve": (C.c_int, [_vp, _sz]),
     "hale_moe_grouped_min_tokens": (C.c_int, [_vp, C.POINTER(_sz)]),
+    "hale_moe_set_band_max_tokens": (C.c_int, [_vp, _sz]),
+    "hale_moe_band_max_tokens": (C.c_int, [_vp, C.POINTER(_sz)]),
     "hale_moe_routing_counts": (C.c_int, [_vp, _u64p]),
     "hale_pack_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "hale_pack_close": (None, [_vp]),
@@ -949,6 +951,17 @@ class MoeLayer:
     def grouped_min_tokens(self) -> int:
         n = _sz()
         self.ctx.check(lib().hale_moe_grouped_min_tokens(self.handle, C.byref(n)), "grouped_min_tokens")
+        return n.value
+
+    def set_band_max_tokens(self, n: int):
+        """Most tokens per expert-grouped forward that run the row-chain
+        kernels instead of the matrix products (0: never; both exact)."""
+        self.ctx.check(lib().hale_moe_set_band_max_tokens(self.handle, n), "set_band_max_tokens")
+
+    @property
+    def band_max_tokens(self) -> int:
+        n = _sz()
+        self.ctx.check(lib().hale_moe_band_max_tokens(self.handle, C.byref(n)), "band_max_tokens")
         return n.value
 
     def set_source(self, pack: "PackExpertSource | None"):

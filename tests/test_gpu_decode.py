@@ -285,18 +285,28 @@ def test_missing_expert_is_reported(ctx):
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-@pytest.mark.parametrize("T,gmin", [(7, None), (21, None), (22, None), (8, 8)])
-def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin):
+@pytest.mark.parametrize("T,gmin,bmax", [(7, None, None), (11, None, None), (12, None, None),
+                                         (21, None, None), (24, None, None), (40, None, None),
+                                         (8, 8, None), (12, None, 0), (16, 17, None)])
+def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin, bmax):
     """Router logits supplied directly (the skewed-routing workloads).  This
-    top-4 layer's grouped threshold is 22 tokens: 7 and 21 take the decode
-    path (21 with cached weight loads), 22 the grouped path, and 8 the
-    grouped path once the threshold is set to 8."""
+    top-4 layer of 32 experts takes the decode path below 12 tokens, the
+    row-chain grouped kernels up to 3.5 * 32 / 4 = 28 tokens (q4_0) or
+    2.75 * 32 / 4 = 22 (q8_0) and the grouped matrix products above: 7 and
+    11 decode, 12 and 21 row-chain, 24 row-chain (q4_0) or matrix products
+    (q8_0), 40 the matrix products; then 8 tokens with the threshold set to
+    8 (row chains), 12 with the row chains off (matrix products) and 16
+    with the threshold above them (a decode pass with cached weight
+    loads)."""
     E, Hd, I, k = 32, 256, 64, 4
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
     moe = make_layer(ctx, L)
-    assert moe.grouped_min_tokens == 22
+    assert moe.grouped_min_tokens == 12
+    assert moe.band_max_tokens == (28 if dtype == H.Q4_0 else 22)
     if gmin:
         moe.set_grouped_min_tokens(gmin)
+    if bmax is not None:
+        moe.set_band_max_tokens(bmax)
     rng = np.random.default_rng(1)
     p = np.arange(1, E + 1, dtype=np.float64) ** -1.1
     logits = (np.log(p / p.sum())[rng.permutation(E)] + rng.gumbel(size=(T, E))).astype(np.float32)
@@ -344,17 +354,18 @@ def test_moe_decode_few_tokens(ctx, dtype, hidden, inter, E, k, T):
     (H.Q8_0, 512, 1024, 16, 6, 13),    # q8_0 8-wave gate/up; 32 blocks
     (H.Q4_0, 2080, 1536, 16, 8, 14),   # q4_0 rows of 65 blocks: 8-wave gate/up; 48 blocks
     (H.Q8_0, 256, 2048, 16, 5, 17),    # 64 blocks
-    (H.Q4_0, 256, 4096, 16, 4, 21),    # 128 blocks, one token below the grouped threshold
+    (H.Q4_0, 256, 4096, 16, 4, 21),    # 128 blocks
     (H.Q4_0, 256, 64, 300, 8, 12),     # more than 256 experts: the 1024-expert selection
 ])
 def test_moe_decode_cached_weight_loads(ctx, dtype, hidden, inter, E, k, T):
-    """Decode passes of 12 to 21 tokens (top-4 and wider, below the grouped
-    threshold of 22) load the weights through the caches: every gate/up
-    form and every down row class of that path, bit-exact per token."""
+    """Decode passes of 12 to 21 tokens (the grouped threshold raised above
+    them; by default these take the grouped path) load the weights through
+    the caches: every gate/up form and every down row class of that path,
+    bit-exact per token."""
     L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=True,
                               seed=hidden + inter + E + k + T)
     moe = make_layer(ctx, L)
-    assert moe.grouped_min_tokens == 22
+    moe.set_grouped_min_tokens(T + 1)
     _few_tokens_check(L, moe, O.normal(9200 + T, T * hidden).reshape(T, hidden))
     moe.close()
 
@@ -381,34 +392,43 @@ def test_moe_decode_down_one_wave_per_route(ctx, dtype, hidden, inter, k, T):
     moe.close()
 
 
-@pytest.mark.parametrize("T", [2, 7, 15, 21])
+@pytest.mark.parametrize("T", [2, 7, 11, 15, 21])
 def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
-    """Config 1's layer over 2, 7, 15 and 21 tokens (its grouped threshold
-    is 22): 16-wave gate/up with two tiles per work-group (24 tiles x 8
-    slots x T > 256); from 12 tokens on the weights load through the
-    caches."""
+    """Config 1's layer over 2, 7 and 11 tokens (below its grouped threshold
+    of 12) and, with the threshold raised, 15 and 21: 16-wave gate/up with
+    two tiles per work-group (24 tiles x 8 slots x T > 256); from 12 tokens
+    on the weights load through the caches."""
     L, moe = qwen30b_q4
-    assert moe.grouped_min_tokens == 22
-    _few_tokens_check(L, moe, O.normal(9200 + T, T * 2048).reshape(T, 2048))
+    assert moe.grouped_min_tokens == 12
+    moe.set_grouped_min_tokens(max(12, T + 1))
+    try:
+        _few_tokens_check(L, moe, O.normal(9200 + T, T * 2048).reshape(T, 2048))
+    finally:
+        moe.set_grouped_min_tokens(12)
 
 
 def test_grouped_threshold_moves_the_path_not_the_bits(ctx):
-    """The grouped threshold only chooses the kernels: the same 12 tokens
-    through the decode path (threshold 13), the grouped path (threshold 2
-    and 12) and one token at a time give the same bits.  Out-of-range
-    thresholds are refused."""
+    """The thresholds only choose the kernels: the same 12 tokens through
+    the decode path (threshold 13), the row-chain grouped kernels (threshold
+    2 and 12) and the grouped matrix products (row chains off) and one
+    token at a time give the same bits.  Out-of-range thresholds are
+    refused."""
     L = O.OracleMoe.synthetic(O.Q4_0, 512, 128, 16, 4, normalize_topk=True, seed=41)
     moe = make_layer(ctx, L)
     xs = O.normal(42, 12 * 512).reshape(12, 512)
     o_out, _, _ = L.prefill(xs, nthreads=8)
-    for gmin in (13, 2, 12, 257):
+    assert moe.band_max_tokens == 14
+    for gmin, bmax in ((13, 14), (2, 14), (12, 14), (12, 0), (2, 0), (257, 14)):
         moe.set_grouped_min_tokens(gmin)
-        assert moe.grouped_min_tokens == gmin
+        moe.set_band_max_tokens(bmax)
+        assert moe.grouped_min_tokens == gmin and moe.band_max_tokens == bmax
         assert_parity(moe.forward(xs), o_out)
         assert same_bits(moe.forward(xs[:3]), o_out[:3])
     for bad in (0, 1, 258):
         with pytest.raises(ValueError):
             moe.set_grouped_min_tokens(bad)
+    with pytest.raises(ValueError):
+        moe.set_band_max_tokens(1 << 40)
     moe.close()
 
 

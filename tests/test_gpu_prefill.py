@@ -1,6 +1,8 @@
 """GPU parity of the expert-grouped multi-token path (ntok at or above the
-layer's grouped threshold: 22 tokens for top-4 and wider, 8 below) against
-the oracle's token-at-a-time prefill (src/model/transformer.rs:231-239).
+layer's grouped threshold: 12 tokens for top-4 and wider, 8 below; the
+row-chain kernels up to the layer's band threshold, the int8 matrix
+products above it) against the oracle's token-at-a-time prefill
+(src/model/transformer.rs:231-239).
 
 Bar: bit-exact outputs, routes and weights (rel-L2 <= 1e-5 asserted too).
 Both model-shaped workloads (512 tokens of Qwen3-30B-A3B q8_0 and 2048 of
@@ -82,6 +84,68 @@ def test_grouped_router_many_tokens(ctx, dtype, Hd, I, E, k, T):
     moe.close()
 
 
+@pytest.mark.parametrize("dtype,Hd,I,E,k,T,with_router", [
+    (H.Q4_0, 256, 96, 32, 4, 40, True),     # 8-block gate/up rows; down rows of 3 blocks (a partial ring cycle)
+    (H.Q8_0, 256, 96, 32, 4, 40, False),
+    (H.Q4_0, 2048, 64, 128, 8, 64, True),   # the tiled router feeding the row chains
+    (H.Q8_0, 1024, 64, 32, 6, 33, True),
+    (H.Q4_0, 2080, 96, 20, 4, 100, True),   # 65-block rows; 65 down tiles (a spare wave per tile)
+    (H.Q8_0, 4096, 64, 128, 8, 16, True),   # 128-block rows
+    (H.Q4_0, 8192, 64, 8, 2, 5, False),     # 256-block rows: the most activation blocks staged
+    (H.Q4_0, 512, 1024, 8, 2, 9, False),    # top-2, 32-block down rows (a ring of 16)
+    (H.Q8_0, 256, 160, 4, 4, 30, False),    # 4 experts: every expert in many two-row tiles
+])
+def test_band_row_chains(ctx, dtype, Hd, I, E, k, T, with_router):
+    """The row-chain grouped kernels (two assignments of an expert per tile,
+    a lane per weight row, the activations as scalar operands), forced for
+    every call: routes, weights and outputs bit-exact per token against the
+    oracle, and the same bits as the grouped matrix products."""
+    L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=Hd + I + T,
+                              with_router=with_router)
+    moe = make_layer(ctx, L)
+    moe.set_grouped_min_tokens(2)
+    moe.set_band_max_tokens(1 << 20)
+    xs = O.normal(T + 7, T * Hd).reshape(T, Hd)
+    logits = None if with_router else zipf_logits(T, E, 1.1, seed=3)
+    out, _ = check(moe, L, xs, logits)
+    moe.set_band_max_tokens(0)
+    assert same_bits(moe.forward(xs, logits=logits), out)
+    moe.close()
+
+
+@pytest.mark.parametrize("T,bmax", [(16, None), (24, None), (48, None), (64, 1 << 20)])
+def test_band_qwen30b_q4(ctx, T, bmax):
+    """Qwen3-30B-A3B's layer shape (128 q4_0 experts, H 2048, I 768, top-8)
+    at 16, 24 and 48 tokens (its default row-chain range: 12 to 56) and at
+    64 with the row chains forced: every token against the oracle."""
+    E, Hd, I, k = 128, 2048, 768, 8
+    L = O.OracleMoe.synthetic(H.Q4_0, Hd, I, E, k, normalize_topk=True, seed=50 + T, with_router=True)
+    moe = make_layer(ctx, L)
+    assert moe.grouped_min_tokens == 12 and moe.band_max_tokens == 56
+    if bmax is not None:
+        moe.set_band_max_tokens(bmax)
+    xs = O.normal(60 + T, T * Hd).reshape(T, Hd)
+    check(moe, L, xs)
+    moe.close()
+
+
+def test_band_crowded_experts(ctx):
+    """The row chains with every token on the same two experts (ten two-row
+    tiles each) and the others idle."""
+    E, Hd, I, k, T = 16, 128, 64, 2, 20
+    L = O.OracleMoe.synthetic(O.Q8_0, Hd, I, E, k, normalize_topk=False, seed=19, with_router=False)
+    moe = make_layer(ctx, L)
+    moe.set_grouped_min_tokens(2)
+    moe.set_band_max_tokens(T)
+    xs = O.normal(14, T * Hd).reshape(T, Hd)
+    logits = np.full((T, E), -5.0, np.float32)
+    logits[:, 5] = 2.0
+    logits[:, 9] = 1.0
+    out, idx = check(moe, L, xs, logits)
+    assert (idx[:, 0] == 5).all() and (idx[:, 1] == 9).all()
+    moe.close()
+
+
 def test_grouped_empty_and_crowded_experts(ctx):
     """Every token on the same experts (one group of T rows, many tiles) and
     most experts idle."""
@@ -145,12 +209,17 @@ def test_grouped_qwen235b_prefill_2048_q4(ctx):
         assert same_bits(o, out[t]), t
 
 
-def test_grouped_equals_decode_path(ctx):
-    """The grouped path (24 tokens, above this top-6 layer's threshold of 22)
-    and the decode path (one token at a time) give the same bits."""
+@pytest.mark.parametrize("bmax", [None, 0])
+def test_grouped_equals_decode_path(ctx, bmax):
+    """The grouped path over 24 tokens (this top-6 layer's row-chain kernels,
+    up to 37 tokens; with them off, the matrix products) and the decode
+    path (one token at a time) give the same bits."""
     E, Hd, I, k, T = 64, 512, 128, 6, 24
     L = O.OracleMoe.synthetic(O.Q4_0, Hd, I, E, k, normalize_topk=True, seed=12, with_router=True)
     moe = make_layer(ctx, L)
+    assert moe.band_max_tokens == 37
+    if bmax is not None:
+        moe.set_band_max_tokens(bmax)
     xs = O.normal(9, T * Hd).reshape(T, Hd)
     batch = moe.forward(xs)
     for t in range(T):

@@ -59,7 +59,7 @@ def test_capture_refuses_scratch_growth(ctx, layer):
 @pytest.mark.parametrize("T", [3, 24])
 def test_reserve_sizes_scratch_for_capture(ctx, layer, T):
     """hale_moe_reserve sizes the layer's scratch (and from the grouped
-    threshold on, 22 tokens for this top-4 layer, its grouped workspace) so
+    threshold on, 12 tokens for this top-4 layer, its grouped workspace) so
     that the first forward can be captured; replays are bit-exact.  A
     reserve that would have to grow scratch during a capture is refused."""
     L, moe = layer
@@ -117,11 +117,13 @@ def test_graph_replays_after_scratch_grows(ctx, layer, big):
         b.free()
 
 
-def test_graph_of_grouped_forward_replays(ctx, layer):
+@pytest.mark.parametrize("T", [12, 24])
+def test_graph_of_grouped_forward_replays(ctx, layer, T):
     """A captured grouped (multi-token) forward replays bit-exact, several
-    times, with different inputs uploaded between the replays."""
+    times, with different inputs uploaded between the replays: 12 tokens
+    on the row-chain kernels (up to 14 tokens for this layer), 24 on the
+    matrix products."""
     L, moe = layer
-    T = 24
     bx, bo = ctx.malloc(T * HID * 4), ctx.malloc(T * HID * 4)
     bx.upload(O.normal(4, T * HID))
     moe.forward_device(T, bx.address, bo.address)
