@@ -52,7 +52,7 @@ int8 MFMA for the 2048-token one).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--prefill-only] [--decode-eager]
-                       [--eager-leg kernels|float|expert|attention]
+                       [--eager-leg kernels|float|expert|band|attention]
                        [--copy-calibration BYTES]
 """
 import argparse
@@ -342,13 +342,19 @@ def decode_eager(args):
     return 2 * L
 
 
+# token counts of the eager `band` leg (the headline layers on their default
+# grouped row-chain path)
+BAND_EAGER_T = (16, 48)
+
+
 def eager_leg(name, passes=3):
     """One secondary workload launched eagerly (no graph), for kernel traces
     and counter runs: `kernels` (the reference's 4096 x 4096 matvec per
     dtype, rotated copies), `float` (the bf16 vocabulary projection and the
     dense f32 matrix), `expert` (the q8_0 Qwen3-30B expert, 128 copies in
-    turn) or `attention` (RMSNorm + attention decode).  Returns the number
-    of calls."""
+    turn), `band` (the 48 headline layers in turn, two passes at 16 and at
+    48 tokens per call: the grouped row-chain kernels) or `attention`
+    (RMSNorm + attention decode).  Returns the number of calls."""
     ctx = H.Context(0)
     calls = 0
     if name in ("kernels", "float"):
@@ -414,6 +420,21 @@ def eager_leg(name, passes=3):
         for e in experts:
             for m in (e.gate, e.up, e.down):
                 m.close()
+    elif name == "band":
+        layers = build_layers(ctx, 48)
+        xs = ctx.malloc((max(BAND_EAGER_T) + 8) * HID * 4)
+        xs.fill_normal(98, (max(BAND_EAGER_T) + 8) * HID, 0.0, 1.0)
+        out = ctx.malloc(max(BAND_EAGER_T) * HID * 4)
+        for T in BAND_EAGER_T:
+            for s in range(2 * len(layers)):
+                layers[s % len(layers)].forward_device(T, xs.offset((s % 8) * HID * 4), out.address)
+                calls += 1
+            ctx.synchronize()
+            log(f"eager band: {T} tokens done")
+        for m in layers:
+            m.close()
+        xs.free()
+        out.free()
     elif name == "attention":
         ctx.close()
         for spec in ATTENTION:
@@ -1096,7 +1117,7 @@ def main():
                     help="with --decode-eager: one of the larger decode layers")
     ap.add_argument("--eager-leg", default="", metavar="NAME",
                     help="only one secondary workload, launched eagerly (for counter and trace runs): "
-                         "kernels, float, expert or attention")
+                         "kernels, float, expert, band or attention")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only time the plain copy kernel over BYTES (counter yardstick)")
     args = ap.parse_args()
