@@ -94,6 +94,8 @@ def test_grouped_router_many_tokens(ctx, dtype, Hd, I, E, k, T):
     (H.Q4_0, 8192, 64, 8, 2, 5, False),     # 256-block rows: the most activation blocks staged
     (H.Q4_0, 512, 1024, 8, 2, 9, False),    # top-2, 32-block down rows (a ring of 16)
     (H.Q8_0, 256, 160, 4, 4, 30, False),    # 4 experts: every expert in many two-row tiles
+    (H.Q8_0, 32, 32, 4, 2, 6, False),       # one block per row, one output tile: spare waves
+    (H.Q4_0, 64, 32, 1024, 1, 40, True),    # 1024 experts, top-1
 ])
 def test_band_row_chains(ctx, dtype, Hd, I, E, k, T, with_router):
     """The row-chain grouped kernels (two assignments of an expert per tile,
