@@ -1148,14 +1148,17 @@ static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_
 
 // Most tokens per grouped forward that take the row-chain kernels rather
 // than the matrix products.  The row-chain kernels read an expert's weights
-// once per two assignments, so they lose once experts hold several: the
-// crossovers (same measurement) sit at about 3.5 E / k tokens for Qwen3-30B
-// q4_0 (56 tokens: 119.0 against 120.6 us, 127 against 121 at 64) and
-// 2.75 E / k for q8_0 and for Qwen3-235B q4_0 (44 tokens; at 48 q8_0 172
-// against 160 us).
+// once per two assignments (from L2 for an expert's later tiles, with
+// ordinary loads above two assignments per expert), so they lose once
+// experts hold several.  The crossovers (same measurement): Qwen3-30B q4_0
+// at about 3.75 E / k tokens (56 tokens: 114.4 against 120.8 us, 64 a tie at
+// 121.3, 80: 140.5 against 122.6), Qwen3-30B q8_0 at 3.5 E / k (56 tokens
+// 160.5 against 161.7 us, 64: 169.4 against 162.9) and Qwen3-235B q4_0 at
+// 3.25 E / k (48 tokens 325.7 against 347.6 us, 56: 355.2 against 350.8).
 static size_t default_band_max(int dtype, size_t E, size_t H, size_t I, size_t k) {
   (void)I;
-  const size_t c4 = dtype == HALE_Q4_0 && H <= 2048 ? 14 : 11;  // quarter-assignments per expert
+  // quarter-assignments per expert
+  const size_t c4 = H <= 2048 ? (dtype == HALE_Q4_0 ? 15 : 14) : 13;
   return c4 * E / (4 * std::max<size_t>(k, 1));
 }
 

@@ -287,9 +287,10 @@ int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
 /* Most tokens per expert-grouped call that run the row-chain kernels
  * (each lane one weight row, each expert's assignments two at a time as
  * scalar operands) in place of the int8 matrix products; larger grouped
- * calls take the matrix products.  Default 3.5 * num_experts / top_k for
- * q4_0 layers with hidden <= 2048, else 2.75 * num_experts / top_k (56 and
- * 44 tokens at 128 experts, top-8); layers whose hidden or inter exceeds
+ * calls take the matrix products.  Default 3.75 * num_experts / top_k for
+ * q4_0 layers with hidden <= 2048, 3.5 * num_experts / top_k for q8_0 ones
+ * and 3.25 * num_experts / top_k above (60, 56 and 52 tokens at 128
+ * experts, top-8); layers whose hidden or inter exceeds
  * 8192 never take them.  Both give the reference's bits; the choice is
  * speed only.  0 never takes them.  No counterpart in the reference; for
  * callers tuning batched decode and small prefill chunks. */
