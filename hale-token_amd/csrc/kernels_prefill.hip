@@ -555,7 +555,7 @@ struct BandArgs {
 // LDS of a band work-group: the tile's activation blocks [BAND_ROWS][nb]
 // (48 bytes each), then per wave the double-buffered scales of its ring
 // cycle, [2][2 halves][D blocks][32 rows] f16.
-constexpr int BAND_MAX_NB = 256;  // K blocks per row (24 KB of activations)
+constexpr int BAND_MAX_NB = 512;  // K blocks per row (48 KB of activations)
 static size_t band_lds(int nb, int d) {
   return (size_t)BAND_ROWS * nb * sizeof(ActBlock) + (size_t)BAND_WAVES * 2 * 2 * d * TILE * 2;
 }
@@ -575,14 +575,17 @@ static size_t band_lds(int nb, int d) {
 // loads, when experts hold about two assignments or fewer (each expert's
 // weights read once); with more, ordinary loads let an expert's later tiles
 // find its weights in L2.
-template <int DT, bool GATE_UP, int D, bool NT>
+// MAXNB: the K blocks the activation staging is sized for (256, or 512 for
+// longer rows: its loads need registers that cost the others occupancy).
+template <int DT, bool GATE_UP, int D, bool NT, int MAXNB>
 __global__ __launch_bounds__(64 * BAND_WAVES) void k_band(BandArgs a) {
   extern __shared__ __attribute__((aligned(16))) u32x4 s_band[];
   constexpr int CH = Layout<DT>::CH;
   constexpr int NR = BAND_ROWS;
   constexpr int LPA = 12;      // lanes per assignment: one ActBlock word each
   constexpr int SPL = D / 8;   // scale pieces per lane per cycle
-  constexpr int APT = (NR * BAND_MAX_NB * 3 + 64 * BAND_WAVES - 1) / (64 * BAND_WAVES);  // activation pieces per thread
+  constexpr int APT = (NR * MAXNB * 3 + 64 * BAND_WAVES - 1) / (64 * BAND_WAVES);  // activation pieces per thread
+  static_assert(MAXNB <= BAND_MAX_NB, "the staging fits its bound");
   static_assert(D % 8 == 0, "a ring cycle's scales are whole pieces per lane");
   static_assert(NR * LPA <= 64, "one word per lane");
   const int lane = threadIdx.x & 63;
@@ -969,16 +972,23 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
     // (Qwen3-30B q4_0 layer, per layer: 72.9 against 75.2 us at 16 tokens;
     // cached from there: 121 against 125.7 at 64, 153.8 against 161.8 at 96)
     const bool nt = A <= 2 * (size_t)L.E;
-#define HALE_BAND(DT_, GU_, D_, args)                                                     \
+#define HALE_BAND_NB(DT_, GU_, D_, NT_, args)                                             \
   do {                                                                                    \
-    if (nt)                                                                               \
+    if (args.nb <= 256)                                                                   \
       HALE_STEP(GU_ ? K_GROUPED_GATE_UP : K_GROUPED_DOWN,                                 \
-                (launch(k_band<DT_, GU_, D_, true>, grid(args.wpt), 64 * BAND_WAVES,        \
+                (launch(k_band<DT_, GU_, D_, NT_, 256>, grid(args.wpt), 64 * BAND_WAVES,    \
                         (uint32_t)band_lds(args.nb, D_), st, args)));                       \
     else                                                                                  \
       HALE_STEP(GU_ ? K_GROUPED_GATE_UP : K_GROUPED_DOWN,                                 \
-                (launch(k_band<DT_, GU_, D_, false>, grid(args.wpt), 64 * BAND_WAVES,       \
-                        (uint32_t)band_lds(args.nb, D_), st, args)));                       \
+                (launch(k_band<DT_, GU_, D_, NT_, BAND_MAX_NB>, grid(args.wpt),             \
+                        64 * BAND_WAVES, (uint32_t)band_lds(args.nb, D_), st, args)));      \
+  } while (0)
+#define HALE_BAND(DT_, GU_, D_, args)        \
+  do {                                       \
+    if (nt)                                  \
+      HALE_BAND_NB(DT_, GU_, D_, true, args); \
+    else                                     \
+      HALE_BAND_NB(DT_, GU_, D_, false, args); \
   } while (0)
     if (L.dtype == Q8_0)
       HALE_BAND(Q8_0, true, 8, g);
@@ -1004,6 +1014,7 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
     else
       HALE_BAND(Q4_0, false, 8, d);
 #undef HALE_BAND
+#undef HALE_BAND_NB
     dim3 gc((unsigned)((L.H + COMBINE_COLS - 1) / COMBINE_COLS), (unsigned)T);
     HALE_STEP(K_COMBINE, launch(k_combine, gc, 256, 0, st, y, pos_of, L.route_w, L.k, L.H, out));
     return hipSuccess;

@@ -1137,13 +1137,14 @@ static int moe_ws(hale_moe* m, size_t need, void** out) {
 // kernels (graph replay over layers visited in turn, one MI355X): Qwen3-30B
 // q4_0 and q8_0 and Qwen3-235B q4_0 (top-8 of 128) between 8 and 12
 // tokens (at 12: 62 against 64, 83 against 85 and 161 against 178 us per
-// layer); Mixtral (top-2 of 8, no row-chain form) between 6 and 8.
+// layer); Mixtral (top-2 of 8) between 4 and 6 (136 against 166 us at 4,
+// 198 against 184 at 6).
 static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_t k) {
   (void)dtype;
   (void)E;
   (void)H;
   (void)I;
-  return k >= 4 ? 12 : 8;
+  return k >= 4 ? 12 : 6;
 }
 
 // Most tokens per grouped forward that take the row-chain kernels rather

@@ -271,7 +271,7 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
 int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
- * path (default 12 for top_k >= 4, else 8); fewer tokens run the decode kernels in one pass over
+ * path (default 12 for top_k >= 4, else 6); fewer tokens run the decode kernels in one pass over
  * all of them.  Both give the reference's bits; the choice is speed only.
  * n in 2..HALE_DECODE_MAX_TOKENS + 1.  A new threshold re-lays the layer's
  * per-token scratch on its next call, which must then come outside a graph
@@ -290,8 +290,8 @@ int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
  * calls take the matrix products.  Default 3.75 * num_experts / top_k for
  * q4_0 layers with hidden <= 2048, 3.5 * num_experts / top_k for q8_0 ones
  * and 3.25 * num_experts / top_k above (60, 56 and 52 tokens at 128
- * experts, top-8); layers whose hidden or inter exceeds
- * 8192 never take them.  Both give the reference's bits; the choice is
+ * experts, top-8); layers whose intermediate size exceeds 16384 never
+ * take them.  Both give the reference's bits; the choice is
  * speed only.  0 never takes them.  No counterpart in the reference; for
  * callers tuning batched decode and small prefill chunks. */
 int hale_moe_set_band_max_tokens(hale_moe *moe, size_t n);

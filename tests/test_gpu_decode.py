@@ -251,7 +251,7 @@ def test_moe_multi_token_equals_per_token(ctx, qwen30b_q4):
 
 
 def test_routing_stats_count_decode_selections(ctx):
-    """The decode path (below the grouped threshold: 8 tokens for this top-3
+    """The decode path (below the grouped threshold: 6 tokens for this top-3
     layer) counts each token's k experts in the gate/up prologue."""
     L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 8, 3, seed=5)
     moe = make_layer(ctx, L, layer_id=3)
@@ -268,7 +268,7 @@ def test_routing_stats_count_decode_selections(ctx):
 
 
 def test_routing_stats_count_grouped_selections(ctx):
-    """The grouped path (8+ tokens) adds each expert's group size once."""
+    """The grouped path (6+ tokens) adds each expert's group size once."""
     L = O.OracleMoe.synthetic(O.Q8_0, 64, 32, 8, 3, seed=5)
     moe = make_layer(ctx, L, layer_id=3)
     xs = O.normal(6, 10 * 64).reshape(10, 64)
@@ -337,7 +337,7 @@ def _few_tokens_check(L, moe, xs):
     (H.Q8_0, 2048, 768, 32, 8, 5),     # 24 x 40 = 960 > 512: two tiles per work-group
     (H.Q4_0, 2080, 2080, 6, 2, 5),     # top-2: whole-chain down per token, 65 blocks
     (H.Q8_0, 1024, 1024, 8, 3, 4),     # top-3 whole chain, q8_0
-    (H.Q4_0, 1024, 256, 8, 1, 6),      # top-1 (32-row chain groups)
+    (H.Q4_0, 1024, 256, 8, 1, 5),      # top-1 (32-row chain groups)
     (H.Q4_0, 256, 64, 300, 16, 3),     # more than 256 experts: eight-wave selection, 16 slots
     (H.Q4_0, 4160, 64, 16, 4, 2),      # pipelined down at H 4160 (no XCD permutation)
 ])

@@ -1,5 +1,5 @@
 """GPU parity of the expert-grouped multi-token path (ntok at or above the
-layer's grouped threshold: 12 tokens for top-4 and wider, 8 below; the
+layer's grouped threshold: 12 tokens for top-4 and wider, 6 below; the
 row-chain kernels up to the layer's band threshold, the int8 matrix
 products above it) against the oracle's token-at-a-time prefill
 (src/model/transformer.rs:231-239).
@@ -96,6 +96,7 @@ def test_grouped_router_many_tokens(ctx, dtype, Hd, I, E, k, T):
     (H.Q8_0, 256, 160, 4, 4, 30, False),    # 4 experts: every expert in many two-row tiles
     (H.Q8_0, 32, 32, 4, 2, 6, False),       # one block per row, one output tile: spare waves
     (H.Q4_0, 64, 32, 1024, 1, 40, True),    # 1024 experts, top-1
+    (H.Q8_0, 256, 9216, 4, 2, 6, False),    # 288-block down rows: the 512-block staging
 ])
 def test_band_row_chains(ctx, dtype, Hd, I, E, k, T, with_router):
     """The row-chain grouped kernels (two assignments of an expert per tile,
@@ -129,6 +130,18 @@ def test_band_qwen30b_q4(ctx, T, bmax):
         moe.set_band_max_tokens(bmax)
     xs = O.normal(60 + T, T * Hd).reshape(T, Hd)
     check(moe, L, xs)
+    moe.close()
+
+
+def test_band_mixtral_8_tokens(ctx):
+    """Mixtral-8x7B's layer shape (8 q4_0 experts, H 4096, I 14336, top-2)
+    at 8 tokens, its default path (grouped from 6 tokens, row chains up to
+    13; 448-block down rows): every token against the oracle."""
+    E, Hd, I, k, T = 8, 4096, 14336, 2, 8
+    L = O.OracleMoe.synthetic(H.Q4_0, Hd, I, E, k, normalize_topk=True, seed=88, with_router=True)
+    moe = make_layer(ctx, L)
+    assert moe.grouped_min_tokens == 6 and moe.band_max_tokens == 13
+    check(moe, L, O.normal(89, T * Hd).reshape(T, Hd))
     moe.close()
 
 
