@@ -26,7 +26,8 @@ on one layer of the same shape on this host, built -march=x86-64 and
 -march=native, each on all threads and on one; medians of at least 20 tokens.
 expert: one q8_0 Qwen3-30B expert (Expert::forward, 1 token), 128 distinct
 experts in turn (cold weights).
-decode_more: Mixtral-8x7B- and Qwen3-235B-shaped decode layers, same timing.
+decode_more: Mixtral-8x7B- and Qwen3-235B-shaped decode layers, same timing,
+and 8 (Mixtral) or 16 (Qwen3-235B) tokens per step on each path.
 float_matvec: WeightMatrix::matvec over float weights (a bf16 vocabulary
 projection and a dense f32 matrix), GB/s of weight bytes.
 attention: RMSNorm + Attention::forward of one token with 4096 cached
@@ -75,6 +76,8 @@ E, HID, INTER, TOPK = 128, 2048, 768, 8
 DTYPE = H.Q4_0
 INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA
 
+# tokens per step of the batched decode_more measurement
+MORE_BATCH = {"mixtral-8x7b decode q4_0": 8, "qwen3-235b-a22b decode q4_0": 16}
 # further decode workloads: (name, dtype, hidden, inter, experts, top_k, layers)
 DECODE_MORE = [
     ("mixtral-8x7b decode q4_0", H.Q4_0, 4096, 14336, 8, 2, 4),
@@ -469,16 +472,19 @@ def measured_traffic(path=TRAFFIC_FILE):
     return out
 
 
-def gpu_decode_more(name, dtype, hid, inter, experts, topk, nlayers, reps=20):
+def gpu_decode_more(name, dtype, hid, inter, experts, topk, nlayers, reps=20, batch=0):
     """One-token MoE layer decode over nlayers resident layers visited in
     turn (cold weights), replayed from a graph; GB/s of routed expert bytes
-    plus router bytes."""
+    plus router bytes.  batch > 0: also `batch` tokens per step, on the
+    default path and with each of the decode pass, the grouped row chains
+    and the grouped matrix products forced (graph replay, us per step)."""
     ctx = H.Context(0)
     layers = build_layers(ctx, nlayers, seed=555, dtype=dtype, hid=hid, inter=inter,
                           experts=experts, topk=topk)
-    xs = ctx.malloc(16 * hid * 4)
-    xs.fill_normal(7, 16 * hid, 0.0, 1.0)
-    out = ctx.malloc(hid * 4)
+    nx = 16 + batch
+    xs = ctx.malloc(nx * hid * 4)
+    xs.fill_normal(7, nx * hid, 0.0, 1.0)
+    out = ctx.malloc(max(batch, 1) * hid * 4)
 
     def step(s):
         layers[s % nlayers].forward_device(1, xs.offset((s % 16) * hid * 4), out.address)
@@ -501,16 +507,45 @@ def gpu_decode_more(name, dtype, hid, inter, experts, topk, nlayers, reps=20):
     prof = ctx.profile_read()
     ctx.profile(False)
     graph.close()
+    batched = None
+    if batch:
+        gmin0, bmax0 = layers[0].grouped_min_tokens, layers[0].band_max_tokens
+
+        def time_t(gmin, bmax):
+            for m in layers:
+                m.set_grouped_min_tokens(gmin)
+                m.set_band_max_tokens(bmax)
+
+            def step_t(s):
+                layers[s % nlayers].forward_device(batch, xs.offset((s % 16) * hid * 4), out.address)
+            for s in range(nlayers):
+                step_t(s)
+            ctx.synchronize()
+            g = ctx.capture(lambda: [step_t(s) for s in range(nlayers)])
+            g.launch()
+            ctx.synchronize()
+            t = time_replays(ctx, g, 10)
+            g.close()
+            return round(1000 * float(np.median(t)) / nlayers, 2)
+
+        path = "decode pass" if batch < gmin0 else ("row chains" if batch <= bmax0 else "matrix products")
+        batched = {"tokens": batch, "path": path, "us_per_step": time_t(gmin0, bmax0),
+                   "decode_pass_us": time_t(min(batch + 1, 257), bmax0),
+                   "row_chains_us": time_t(2, 1 << 20), "matrix_products_us": time_t(2, 0)}
+        log(f"{name} at {batch} tokens per step: {batched}")
     for m in layers:
         m.close()
     ctx.close()
     bytes_step = topk * expert_bytes(dtype, hid, inter) + experts * hid * 4
     us = 1000 * ms / steps
-    return {"workload": name, "bytes_per_step": bytes_step, "us_per_step": round(us, 2),
-            "GB_per_s": round(bytes_step / us / 1e3, 1),
-            "pct_hbm_peak": round(100 * bytes_step / us / 1e3 / HBM_PEAK_GBS, 2),
-            "layers_resident": nlayers,
-            "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
+    r = {"workload": name, "bytes_per_step": bytes_step, "us_per_step": round(us, 2),
+         "GB_per_s": round(bytes_step / us / 1e3, 1),
+         "pct_hbm_peak": round(100 * bytes_step / us / 1e3 / HBM_PEAK_GBS, 2),
+         "layers_resident": nlayers,
+         "kernels": {k: {"avg_us": round(1000 * v[0] / v[1], 2), "launches": v[1]} for k, v in prof.items()}}
+    if batched:
+        r["batched"] = batched
+    return r
 
 
 def gpu_expert(copies=128, reps=20):
@@ -1167,7 +1202,7 @@ def main():
     more = []
     if not args.no_prefill:
         for (name, dt, hid, inter, ex, k, nl) in DECODE_MORE:
-            more.append(gpu_decode_more(name, dt, hid, inter, ex, k, nl))
+            more.append(gpu_decode_more(name, dt, hid, inter, ex, k, nl, batch=MORE_BATCH.get(name, 0)))
             log(f"decode {name}: {more[-1]['us_per_step']} us/step, {more[-1]['GB_per_s']} GB/s")
 
     fmv = []
