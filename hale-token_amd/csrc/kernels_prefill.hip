@@ -522,10 +522,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // (d_w * d_x) * isum to every assignment's sum, block after block: the
 // reference's dot_q8_0 / dot_q4_0 and its left-to-right fold
 // (src/tensor/quant.rs:115-144).  An assignment's activation block is the
-// same for every lane of the wave: it comes with the block's weights in the
-// ring, spread over the lanes, and enters the dot products as scalar
-// operands; the gate/up input is read in place (token-major, through perm),
-// with no gather.
+// same for every lane of the wave, so it enters the dot products as scalar
+// operands (staged in LDS by the work-group, read into scalar registers);
+// the gate/up input is read in place (token-major, through perm), with no
+// gather.
+//
 // Assignments per band tile: two.  Tiles of four or eight (more terms per
 // weight block, fewer re-reads of an expert's weights) measured slower at
 // every size where this path is the faster one: their longer per-block
