@@ -522,10 +522,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // (d_w * d_x) * isum to every assignment's sum, block after block: the
 // reference's dot_q8_0 / dot_q4_0 and its left-to-right fold
 // (src/tensor/quant.rs:115-144).  An assignment's activation block is the
-// same for every lane of the wave, so it enters the dot products as scalar
-// operands (staged in LDS by the work-group, read into scalar registers);
-// the gate/up input is read in place (token-major, through perm), with no
-// gather.
+// same for every lane of the wave (staged in LDS by the work-group, read by
+// all lanes at once); the gate/up input is read in place (token-major,
+// through perm), with no gather.
 //
 // Assignments per band tile: two.  Tiles of four or eight (more terms per
 // weight block, fewer re-reads of an expert's weights) measured slower at
@@ -570,9 +569,12 @@ static size_t band_lds(int nb, int d) {
 // Each lane's row streams through a ring of D code blocks; per ring cycle
 // (D blocks) the wave loads the cycle after next's scales as whole 16-byte
 // pieces (8 rows of one block) and parks them in LDS, so a block costs one
-// load per lane.  The activation words of block b come from LDS, one word
-// per lane (word i of assignment j in lane 12 j + i), and enter the dot
-// products through readlane as scalar operands.  NT: non-temporal weight
+// load per lane.  The activation blocks of block b come from LDS: for q4_0
+// rows of up to 256 blocks every lane reads the same words (a broadcast:
+// Qwen3-30B q4_0 layer 109.4 -> 102.7 us at 48 tokens, Qwen3-235B 326 ->
+// 319); for q8_0 and longer rows, where the broadcast measured 1-2 %
+// slower, each lane reads one word (word i of assignment j in lane 12 j +
+// i) and readlane moves it to a scalar register.  NT: non-temporal weight
 // loads, when experts hold about two assignments or fewer (each expert's
 // weights read once); with more, ordinary loads let an expert's later tiles
 // find its weights in L2.
@@ -583,12 +585,14 @@ __global__ __launch_bounds__(64 * BAND_WAVES) void k_band(BandArgs a) {
   extern __shared__ __attribute__((aligned(16))) u32x4 s_band[];
   constexpr int CH = Layout<DT>::CH;
   constexpr int NR = BAND_ROWS;
-  constexpr int LPA = 12;      // lanes per assignment: one ActBlock word each
   constexpr int SPL = D / 8;   // scale pieces per lane per cycle
   constexpr int APT = (NR * MAXNB * 3 + 64 * BAND_WAVES - 1) / (64 * BAND_WAVES);  // activation pieces per thread
   static_assert(MAXNB <= BAND_MAX_NB, "the staging fits its bound");
+  // activation words by broadcast LDS reads (q4_0 rows of up to 256 blocks)
+  // or one word per lane moved to scalar registers (q8_0, longer rows)
+  constexpr bool BCAST = DT == Q4_0 && MAXNB <= 256;
+  static_assert(NR * 12 <= 64, "one word per lane");
   static_assert(D % 8 == 0, "a ring cycle's scales are whole pieces per lane");
-  static_assert(NR * LPA <= 64, "one word per lane");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nt = *a.ntiles;
@@ -681,13 +685,11 @@ __global__ __launch_bounds__(64 * BAND_WAVES) void k_band(BandArgs a) {
   __syncthreads();  // the activation blocks
 
   const ActBlock* s_act = (const ActBlock*)s_band;
-  const int jl = min(lane / LPA, NR - 1);  // the lane's assignment and word
-  const unsigned* aword = (const unsigned*)(s_act + (size_t)jl * nb) + lane % LPA;
-  // word i of assignment j's block in slot d, as a scalar
+  // (readlane form) the lane's word of block b: word i of assignment j in
+  // lane 12 j + i
+  const unsigned* aword =
+      (const unsigned*)(s_act + (size_t)min(lane / 12, NR - 1) * nb) + lane % 12;
   unsigned aw[D];
-  auto word = [&](int d, int j, int i) -> unsigned {
-    return (unsigned)__builtin_amdgcn_readlane((int)aw[d], LPA * j + i);
-  };
   // sums start at +0.0 like the reference's `let mut total = 0.0`
   float acc[NR];
 #pragma unroll
@@ -699,7 +701,7 @@ __global__ __launch_bounds__(64 * BAND_WAVES) void k_band(BandArgs a) {
 #pragma unroll
     for (int d = 0; d < D; d++) {
       sw[d] = scl[d * TILE];
-      aw[d] = aword[(size_t)min(b0 + d, nb - 1) * (sizeof(ActBlock) / 4)];
+      if constexpr (!BCAST) aw[d] = aword[(size_t)min(b0 + d, nb - 1) * (sizeof(ActBlock) / 4)];
     }
 #pragma unroll
     for (int d = 0; d < D; d++) {
@@ -726,14 +728,27 @@ __global__ __launch_bounds__(64 * BAND_WAVES) void k_band(BandArgs a) {
       const float dw = h2f(sw[d]);
 #pragma unroll
       for (int j = 0; j < NR; j++) {
-        // ActBlock words: codes 0-7, scale 8, code sum 9, all read into
-        // scalar registers before the products (one register reused for
-        // each would stall every product on the read before it)
+        // assignment j's block words: codes 0-7, scale 8, code sum 9
         int x[10];
+        if constexpr (BCAST) {  // every lane reads the same LDS words
+          const ActBlock* xb = s_act + (size_t)j * nb + min(b0 + d, nb - 1);
+          const u32x4 xa0 = *(const u32x4*)xb->q, xa1 = *(const u32x4*)(xb->q + 16);
+          const u32x2 xs = *(const u32x2*)&xb->scale;
 #pragma unroll
-        for (int i = 0; i < 10; i++) x[i] = (int)word(d, j, i);
-        asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]), "s"(x[5]),
-                     "s"(x[6]), "s"(x[7]), "s"(x[8]), "s"(x[9]));
+          for (int i = 0; i < 4; i++) {
+            x[i] = (int)xa0[i];
+            x[4 + i] = (int)xa1[i];
+          }
+          x[8] = (int)xs[0];
+          x[9] = (int)xs[1];
+        } else {
+          // each word into a scalar register, all before the products (one
+          // register reused for each would stall every product on its read)
+#pragma unroll
+          for (int i = 0; i < 10; i++) x[i] = __builtin_amdgcn_readlane((int)aw[d], 12 * j + i);
+          asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]), "s"(x[5]),
+                       "s"(x[6]), "s"(x[7]), "s"(x[8]), "s"(x[9]));
+        }
         // two chains of four dot products (integer sums: any order)
         int s0 = 0, s1 = 0;
 #pragma unroll

@@ -1152,14 +1152,16 @@ static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_
 // once per two assignments (from L2 for an expert's later tiles, with
 // ordinary loads above two assignments per expert), so they lose once
 // experts hold several.  The crossovers (same measurement): Qwen3-30B q4_0
-// at about 3.75 E / k tokens (56 tokens: 114.4 against 120.8 us, 64 a tie at
-// 121.3, 80: 140.5 against 122.6), Qwen3-30B q8_0 at 3.5 E / k (56 tokens
-// 160.5 against 161.7 us, 64: 169.4 against 162.9) and Qwen3-235B q4_0 at
-// 3.25 E / k (48 tokens 325.7 against 347.6 us, 56: 355.2 against 350.8).
+// at about 4.75 E / k tokens (72 tokens: 118.4 against 121.7 us, 80: 124.4
+// against 122.1), Qwen3-235B q4_0 at 3.75 E / k (56 tokens 343 against
+// 351 us, 64: 368 against 353), Qwen3-30B q8_0 at 3.5 E / k (48 tokens
+// 153.7 against 160.1 us, 64: 171 against 163) and Mixtral (448-block down
+// rows) at 3.25 E / k (12 tokens 244.5 against 252 us, 14: 261 against 252).
 static size_t default_band_max(int dtype, size_t E, size_t H, size_t I, size_t k) {
-  (void)I;
-  // quarter-assignments per expert
-  const size_t c4 = H <= 2048 ? (dtype == HALE_Q4_0 ? 15 : 14) : 13;
+  size_t c4;  // quarter-assignments per expert
+  if (I / HALE_QK > 256) c4 = 13;
+  else if (dtype == HALE_Q4_0) c4 = H <= 2048 ? 19 : 15;
+  else c4 = H <= 2048 ? 14 : 13;
   return c4 * E / (4 * std::max<size_t>(k, 1));
 }
 

@@ -287,11 +287,12 @@ int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
 /* Most tokens per expert-grouped call that run the row-chain kernels
  * (each lane one weight row, each expert's assignments two at a time as
  * scalar operands) in place of the int8 matrix products; larger grouped
- * calls take the matrix products.  Default 3.75 * num_experts / top_k for
- * q4_0 layers with hidden <= 2048, 3.5 * num_experts / top_k for q8_0 ones
- * and 3.25 * num_experts / top_k above (60, 56 and 52 tokens at 128
- * experts, top-8); layers whose intermediate size exceeds 16384 never
- * take them.  Both give the reference's bits; the choice is
+ * calls take the matrix products.  Default c * num_experts / top_k with
+ * c = 4.75 for q4_0 layers with hidden <= 2048, 3.75 for larger q4_0
+ * ones, 3.5 for q8_0 ones with hidden <= 2048 and 3.25 for the rest and for
+ * layers whose intermediate size exceeds 8192 (76, 60 and 56 tokens at
+ * 128 experts, top-8; 13 at 8 experts, top-2); layers whose intermediate
+ * size exceeds 16384 never take them.  Both give the reference's bits; the choice is
  * speed only.  0 never takes them.  No counterpart in the reference; for
  * callers tuning batched decode and small prefill chunks. */
 int hale_moe_set_band_max_tokens(hale_moe *moe, size_t n);

@@ -291,7 +291,7 @@ def test_missing_expert_is_reported(ctx):
 def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin, bmax):
     """Router logits supplied directly (the skewed-routing workloads).  This
     top-4 layer of 32 experts takes the decode path below 12 tokens, the
-    row-chain grouped kernels up to 3.75 * 32 / 4 = 30 tokens (q4_0) or
+    row-chain grouped kernels up to 4.75 * 32 / 4 = 38 tokens (q4_0) or
     3.5 * 32 / 4 = 28 (q8_0) and the grouped matrix products above: 7 and
     11 decode, 12 and 21 row chains (non-temporal weight loads), 24 row
     chains (cached loads: more than two assignments per expert), 40 the
@@ -302,7 +302,7 @@ def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin, bmax):
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
     moe = make_layer(ctx, L)
     assert moe.grouped_min_tokens == 12
-    assert moe.band_max_tokens == (30 if dtype == H.Q4_0 else 28)
+    assert moe.band_max_tokens == (38 if dtype == H.Q4_0 else 28)
     if gmin:
         moe.set_grouped_min_tokens(gmin)
     if bmax is not None:
@@ -417,8 +417,8 @@ def test_grouped_threshold_moves_the_path_not_the_bits(ctx):
     moe = make_layer(ctx, L)
     xs = O.normal(42, 12 * 512).reshape(12, 512)
     o_out, _, _ = L.prefill(xs, nthreads=8)
-    assert moe.band_max_tokens == 15
-    for gmin, bmax in ((13, 15), (2, 15), (12, 15), (12, 0), (2, 0), (257, 15)):
+    assert moe.band_max_tokens == 19
+    for gmin, bmax in ((13, 19), (2, 19), (12, 19), (12, 0), (2, 0), (257, 19)):
         moe.set_grouped_min_tokens(gmin)
         moe.set_band_max_tokens(bmax)
         assert moe.grouped_min_tokens == gmin and moe.band_max_tokens == bmax

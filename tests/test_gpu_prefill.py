@@ -120,12 +120,12 @@ def test_band_row_chains(ctx, dtype, Hd, I, E, k, T, with_router):
 def test_band_qwen30b_q4(ctx, T, bmax):
     """Qwen3-30B-A3B's layer shape (128 q4_0 experts, H 2048, I 768, top-8)
     at 16, 24 (non-temporal weight loads) and 48 tokens (cached loads; the
-    default row-chain range is 12 to 60) and at 80 with the row chains
+    default row-chain range is 12 to 76) and at 80 with the row chains
     forced: every token against the oracle."""
     E, Hd, I, k = 128, 2048, 768, 8
     L = O.OracleMoe.synthetic(H.Q4_0, Hd, I, E, k, normalize_topk=True, seed=50 + T, with_router=True)
     moe = make_layer(ctx, L)
-    assert moe.grouped_min_tokens == 12 and moe.band_max_tokens == 60
+    assert moe.grouped_min_tokens == 12 and moe.band_max_tokens == 76
     if bmax is not None:
         moe.set_band_max_tokens(bmax)
     xs = O.normal(60 + T, T * Hd).reshape(T, Hd)
@@ -228,12 +228,12 @@ def test_grouped_qwen235b_prefill_2048_q4(ctx):
 @pytest.mark.parametrize("bmax", [None, 0])
 def test_grouped_equals_decode_path(ctx, bmax):
     """The grouped path over 24 tokens (this top-6 layer's row-chain kernels,
-    up to 40 tokens; with them off, the matrix products) and the decode
+    up to 50 tokens; with them off, the matrix products) and the decode
     path (one token at a time) give the same bits."""
     E, Hd, I, k, T = 64, 512, 128, 6, 24
     L = O.OracleMoe.synthetic(O.Q4_0, Hd, I, E, k, normalize_topk=True, seed=12, with_router=True)
     moe = make_layer(ctx, L)
-    assert moe.band_max_tokens == 40
+    assert moe.band_max_tokens == 50
     if bmax is not None:
         moe.set_band_max_tokens(bmax)
     xs = O.normal(9, T * Hd).reshape(T, Hd)
