@@ -1134,17 +1134,18 @@ static int moe_ws(hale_moe* m, size_t need, void** out) {
 // grouped path has a fixed cost (routing, grouping, combine launches) and
 // then reads each touched expert once; the decode path adds each token's k
 // experts' bytes.  Measured crossovers against the row-chain grouped
-// kernels (graph replay over layers visited in turn, one MI355X): Qwen3-30B
-// q4_0 and q8_0 and Qwen3-235B q4_0 (top-8 of 128) between 8 and 12
-// tokens (at 12: 62 against 64, 83 against 85 and 161 against 178 us per
-// layer); Mixtral (top-2 of 8) between 4 and 6 (136 against 166 us at 4,
-// 198 against 184 at 6).
+// kernels (graph replay over layers visited in turn, one MI355X):
+// Qwen3-30B q4_0 (top-8 of 128) between 10 and 11 tokens (55.6 against
+// 56.8 us at 10, 62.2 against 59.9 at 11), Qwen3-235B q4_0 at 8 (125.8
+// both; 153 against 136 at 10), Qwen3-30B q8_0 between 10 and 12 (73.4
+// against 75.7 at 10, 85.1 against 83.1 at 12); Mixtral (top-2 of 8)
+// between 4 and 6 (136 against 166 us at 4, 198 against 184 at 6).
 static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_t k) {
-  (void)dtype;
   (void)E;
-  (void)H;
   (void)I;
-  return k >= 4 ? 12 : 6;
+  if (k < 4) return 6;
+  if (dtype == HALE_Q4_0) return H <= 2048 ? 11 : 9;
+  return 12;
 }
 
 // Most tokens per grouped forward that take the row-chain kernels rather

@@ -271,8 +271,9 @@ int hale_moe_forward_device(hale_moe *moe, size_t ntok, const float *d_x,
 int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
- * path (default 12 for top_k >= 4, else 6); fewer tokens run the decode kernels in one pass over
- * all of them.  Both give the reference's bits; the choice is speed only.
+ * path (default for top_k >= 4: 11 for q4_0 with hidden <= 2048, 9 for
+ * wider q4_0, 12 for q8_0; 6 for top_k < 4); fewer tokens run the decode
+ * kernels in one pass over all of them.  Both give the reference's bits; the choice is speed only.
  * n in 2..HALE_DECODE_MAX_TOKENS + 1.  A new threshold re-lays the layer's
  * per-token scratch on its next call, which must then come outside a graph
  * capture (or call hale_moe_reserve first).  No counterpart in the

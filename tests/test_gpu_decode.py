@@ -285,15 +285,17 @@ def test_missing_expert_is_reported(ctx):
 
 
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
-@pytest.mark.parametrize("T,gmin,bmax", [(7, None, None), (11, None, None), (12, None, None),
-                                         (21, None, None), (24, None, None), (40, None, None),
+@pytest.mark.parametrize("T,gmin,bmax", [(7, None, None), (10, None, None), (11, None, None),
+                                         (12, None, None), (21, None, None), (24, None, None),
+                                         (40, None, None),
                                          (8, 8, None), (12, None, 0), (16, 17, None)])
 def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin, bmax):
     """Router logits supplied directly (the skewed-routing workloads).  This
-    top-4 layer of 32 experts takes the decode path below 12 tokens, the
-    row-chain grouped kernels up to 4.75 * 32 / 4 = 38 tokens (q4_0) or
-    3.5 * 32 / 4 = 28 (q8_0) and the grouped matrix products above: 7 and
-    11 decode, 12 and 21 row chains (non-temporal weight loads), 24 row
+    top-4 layer of 32 experts takes the decode path below 11 tokens (q4_0)
+    or 12 (q8_0), the row-chain grouped kernels up to 4.75 * 32 / 4 = 38
+    tokens (q4_0) or 3.5 * 32 / 4 = 28 (q8_0) and the grouped matrix
+    products above: 7 and 10 decode, 11 row chains (q4_0) or decode (q8_0),
+    12 and 21 row chains (non-temporal weight loads), 24 row
     chains (cached loads: more than two assignments per expert), 40 the
     matrix products; then 8 tokens with the threshold set to 8 (row
     chains), 12 with the row chains off (matrix products) and 16 with the
@@ -301,7 +303,7 @@ def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin, bmax):
     E, Hd, I, k = 32, 256, 64, 4
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
     moe = make_layer(ctx, L)
-    assert moe.grouped_min_tokens == 12
+    assert moe.grouped_min_tokens == (11 if dtype == H.Q4_0 else 12)
     assert moe.band_max_tokens == (38 if dtype == H.Q4_0 else 28)
     if gmin:
         moe.set_grouped_min_tokens(gmin)
@@ -392,19 +394,19 @@ def test_moe_decode_down_one_wave_per_route(ctx, dtype, hidden, inter, k, T):
     moe.close()
 
 
-@pytest.mark.parametrize("T", [2, 7, 11, 15, 21])
+@pytest.mark.parametrize("T", [2, 7, 10, 11, 15, 21])
 def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
-    """Config 1's layer over 2, 7 and 11 tokens (below its grouped threshold
-    of 12) and, with the threshold raised, 15 and 21: 16-wave gate/up with
-    two tiles per work-group (24 tiles x 8 slots x T > 256); from 12 tokens
-    on the weights load through the caches."""
+    """Config 1's layer over 2, 7 and 10 tokens (below its grouped threshold
+    of 11) and, with the threshold raised, 11, 15 and 21: 16-wave gate/up
+    with two tiles per work-group (24 tiles x 8 slots x T > 256); from 12
+    tokens on the weights load through the caches."""
     L, moe = qwen30b_q4
-    assert moe.grouped_min_tokens == 12
-    moe.set_grouped_min_tokens(max(12, T + 1))
+    assert moe.grouped_min_tokens == 11
+    moe.set_grouped_min_tokens(max(11, T + 1))
     try:
         _few_tokens_check(L, moe, O.normal(9200 + T, T * 2048).reshape(T, 2048))
     finally:
-        moe.set_grouped_min_tokens(12)
+        moe.set_grouped_min_tokens(11)
 
 
 def test_grouped_threshold_moves_the_path_not_the_bits(ctx):

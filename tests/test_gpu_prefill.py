@@ -1,5 +1,6 @@
 """GPU parity of the expert-grouped multi-token path (ntok at or above the
-layer's grouped threshold: 12 tokens for top-4 and wider, 6 below; the
+layer's grouped threshold: for top-4 and wider 11 tokens (q4_0, hidden
+size up to 2048), 9 (q4_0, wider) or 12 (q8_0), 6 below; the
 row-chain kernels up to the layer's band threshold, the int8 matrix
 products above it) against the oracle's token-at-a-time prefill
 (src/model/transformer.rs:231-239).
@@ -120,12 +121,12 @@ def test_band_row_chains(ctx, dtype, Hd, I, E, k, T, with_router):
 def test_band_qwen30b_q4(ctx, T, bmax):
     """Qwen3-30B-A3B's layer shape (128 q4_0 experts, H 2048, I 768, top-8)
     at 16, 24 (non-temporal weight loads) and 48 tokens (cached loads; the
-    default row-chain range is 12 to 76) and at 80 with the row chains
+    default row-chain range is 11 to 76) and at 80 with the row chains
     forced: every token against the oracle."""
     E, Hd, I, k = 128, 2048, 768, 8
     L = O.OracleMoe.synthetic(H.Q4_0, Hd, I, E, k, normalize_topk=True, seed=50 + T, with_router=True)
     moe = make_layer(ctx, L)
-    assert moe.grouped_min_tokens == 12 and moe.band_max_tokens == 76
+    assert moe.grouped_min_tokens == 11 and moe.band_max_tokens == 76
     if bmax is not None:
         moe.set_band_max_tokens(bmax)
     xs = O.normal(60 + T, T * Hd).reshape(T, Hd)

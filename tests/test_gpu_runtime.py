@@ -59,7 +59,7 @@ def test_capture_refuses_scratch_growth(ctx, layer):
 @pytest.mark.parametrize("T", [3, 24])
 def test_reserve_sizes_scratch_for_capture(ctx, layer, T):
     """hale_moe_reserve sizes the layer's scratch (and from the grouped
-    threshold on, 12 tokens for this top-4 layer, its grouped workspace) so
+    threshold on, 11 tokens for this top-4 q4_0 layer, its grouped workspace) so
     that the first forward can be captured; replays are bit-exact.  A
     reserve that would have to grow scratch during a capture is refused."""
     L, moe = layer
