@@ -337,7 +337,9 @@ def _few_tokens_check(L, moe, xs):
 @pytest.mark.parametrize("dtype,hidden,inter,E,k,T", [
     (H.Q8_0, 2048, 768, 32, 8, 3),     # q8_0 gate/up at 8 waves: 24 x 24 tile-slots, one tile per work-group
     (H.Q8_0, 2048, 768, 32, 8, 5),     # 24 x 40 = 960 > 512: two tiles per work-group
-    (H.Q4_0, 2080, 2080, 6, 2, 5),     # top-2: whole-chain down per token, 65 blocks
+    (H.Q4_0, 2080, 2080, 6, 2, 5),     # top-2: spread-term down, 65 blocks, 132 x 5 16-row groups (no XCD permutation)
+    (H.Q8_0, 1024, 16384, 4, 2, 2),    # top-2, down rows of 512 blocks (the most the spread-term kernel stages)
+    (H.Q4_0, 512, 16416, 4, 2, 2),     # top-2, 513 blocks: the pipelined down kernel
     (H.Q8_0, 1024, 1024, 8, 3, 4),     # top-3 whole chain, q8_0
     (H.Q4_0, 1024, 256, 8, 1, 5),      # top-1 (32-row chain groups)
     (H.Q4_0, 256, 64, 300, 16, 3),     # more than 256 experts: eight-wave selection, 16 slots
@@ -457,6 +459,10 @@ def test_moe_decode_mixtral_q4_bit_exact(ctx):
         assert list(idx) == list(o_idx)
         assert same_bits(w, o_w)
         assert_parity(out, o_out)
+    # two and three tokens in one decode pass: the down kernel's 32-row and
+    # 16-row work-groups (one token took the 16-row ones)
+    for T in (2, 3):
+        _few_tokens_check(L, moe, O.normal(4100 + T, T * 4096).reshape(T, 4096))
     moe.close()
 
 
@@ -465,9 +471,10 @@ def test_moe_decode_mixtral_q4_bit_exact(ctx):
                                         (2080, 8, 4)])
 def test_moe_decode_wide_hidden(ctx, dtype, hidden, E, k):
     # wide hidden sizes for both dtypes; 2, 3, 4 and 8 slots per token.
-    # 2 and 3 slots run the whole-chain down kernel (16-row groups: H 4160
-    # gives 260 work-groups, not a multiple of 16, so its XCD permutation is
-    # off), 4 and 8 the pipelined one (8-row groups: H 2080 gives 260, its
+    # 2 slots run the spread-term down kernel (H 4160: 130 groups of 32
+    # rows), 3 the whole-chain one (16-row groups: H 4160 gives 260
+    # work-groups, not a multiple of 16, so its XCD permutation is off), 4
+    # and 8 a wave per route (8-row groups: H 2080 gives 260, its
     # permutation off too).  Gate/up: H 2048 is one chunk per row (16 waves
     # for q4_0), H 2080 is 65 blocks (8 waves, two chunks)
     L = O.OracleMoe.synthetic(dtype, hidden, 256, E, k, normalize_topk=True, seed=hidden + E + k)

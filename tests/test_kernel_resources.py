@@ -24,6 +24,7 @@ OCCUPANCY = [
     (r"k_grouped", 4),           # grouped prefill: four waves per SIMD (128 VGPRs)
     (r"k_gemvILi\d+ELi1ELi16E", 4),  # sixteen-wave gate/up: one work-group of 1024 threads per CU
     (r"k_down_combine", 2),      # eight-wave down + combine
+    (r"k_down_tile", 4),         # sixteen-wave top-2 down: one work-group of 1024 threads per CU
 ]
 
 REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|"
@@ -64,7 +65,7 @@ def report():
 
 def test_every_unit_reports_its_kernels(report):
     names = [k for u in UNITS for k in report[u]]
-    for kernel in ("k_gemv", "k_down_combine", "k_down_chain", "k_route_logits", "k_grouped",
+    for kernel in ("k_gemv", "k_down_combine", "k_down_chain", "k_down_tile", "k_route_logits", "k_grouped",
                    "k_group", "k_combine"):
         assert any(kernel in n for n in names), kernel
 
