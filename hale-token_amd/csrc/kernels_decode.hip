@@ -1537,42 +1537,55 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
 }
 
 // ===========================================================================
-// Down projection and combine for two routes over long rows
+// Down projection and combine with block terms spread over the waves
 // ===========================================================================
 //
-// MoeLayer::forward's combine (src/model/moe.rs:63-68) for top-2 layers whose
-// down rows hold hundreds of blocks, with each row's block terms spread over
-// the work-group's waves (the k_gemv scheme) instead of one wave per chain.
-// A work-group owns RW output rows (32: one tile; 16: half of one) of both
-// slots.  Lane l works for slot l / 32; within the half, lane RW p + r holds
-// row r and, for RW = 16, block parity p.  So one wave-load reads, for each
-// slot, RW rows of 32 / RW consecutive blocks: 512 contiguous bytes of the
-// tile layout per 16-byte chunk (two 256-byte pieces for RW = 16), where the
-// chain kernel reads eight 128-byte lines spread over 4 KB.  The blocks go
-// to the waves in chunks of CB: wave w takes UPW wave-loads of each chunk,
-// and the next chunk's loads are issued while a chunk's terms are formed.
-// Terms go to LDS; wave 0 adds them to its running sums (lane 32 s + r:
-// slot s, row r) in block order, the reference's left-to-right sum, and
-// finally forms out = (0 + w_0 y_0) + w_1 y_1.  The launcher takes sixteen
-// waves, each with two 16-byte code loads per lane in flight per chunk
-// (q4_0; one 32-byte block for q8_0): on a Mixtral-8x7B-shaped layer at one
-// token, 11.8 us against 11.8-12.0 with eight waves and four loads, 13.5
-// with eight waves and two, 15.1 with four waves, 14.5-17.7 for 32-row
-// groups at one token.
-constexpr int DOWN_TILE_MAX_NB = 512;  // blocks per row: both slots' activations in 48 KB of LDS
+// MoeLayer::forward's combine (src/model/moe.rs:63-68) for S = 2, 4 or 8
+// routes, with each row's block terms spread over the work-group's waves
+// (the k_gemv scheme) instead of one wave per chain.  A work-group owns RW
+// output rows (32: one tile; 16 or 8: part of one) of every slot.  The
+// slots go in pairs: lane l of a wave works for slot 2 q + l / 32 of the
+// wave's pair q (waves w of one pair: w / (NW / (S / 2)) = q); within the
+// half, lane RW p + r holds row r and block p of each group of 32 / RW
+// consecutive blocks.  So one wave-load reads, per slot, RW rows of 32 / RW
+// consecutive blocks: 512 contiguous bytes of the tile layout per 16-byte
+// chunk for RW = 32 (two 256-byte pieces for 16), where a wave per chain
+// reads eight 128-byte lines spread over 4 KB.  Blocks go to the waves in
+// chunks of CB per slot; the next chunk's loads are issued while a chunk's
+// terms are formed.  Terms go to LDS; the first S RW / 64 waves add them to
+// the running sums of the S x RW chains (chain RW s + r: slot s, row r) in
+// block order, the reference's left-to-right sum; then
+// out = (((0 + w_0 y_0) + w_1 y_1) + ...) in route order.  The launcher takes
+// sixteen waves with two 16-byte code loads per lane in flight per chunk
+// (q4_0; one 32-byte block for q8_0).  Measured (q4_0, one token): Mixtral-
+// 8x7B-shaped down 11.8 us against 11.8-12.0 with eight waves and four
+// loads, 13.5 with eight waves and two, 15.1 with four waves and four;
+// Qwen3-235B-shaped, 16-row groups: 6.4-7.5 us with two loads, 6.6-6.7
+// with three, 7.7 with four.
+constexpr int DOWN_TILE_MAX_NB = 512;  // blocks per row: two slots' activations in 48 KB of LDS
 
-static inline size_t down_tile_lds(int nb) { return (size_t)2 * nb * sizeof(ActBlock); }
+static inline size_t down_tile_lds(int slots, int nb) { return (size_t)slots * nb * sizeof(ActBlock); }
 
-template <int DT, int NW, int RW, int UPW>
+template <int DT, int S, int NW, int RW, int UPW>
 __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
   constexpr int BPL = 32 / RW;        // blocks per slot and wave-load
-  constexpr int CB = UPW * NW * BPL;  // blocks per chunk
-  constexpr int GS = UPW < 4 ? UPW : 4;  // terms per group; the next chunk's loads follow each group
-  static_assert(RW == 32 || RW == 16, "a half-wave covers one or two blocks of RW rows");
+  constexpr int SP = S / 2;           // slot pairs
+  constexpr int WPP = NW / SP;        // waves per slot pair
+  constexpr int CB = WPP * UPW * BPL; // blocks per chunk
+  constexpr int NCH = S * RW;         // fold chains
+  constexpr int FW = (NCH + 63) / 64; // folding waves
+  // terms per group (the largest of 4, 3, 2, 1 that divides UPW); the next
+  // chunk's loads follow each group
+  constexpr int GS = UPW % 4 == 0 ? 4 : (UPW % 3 == 0 ? 3 : (UPW % 2 == 0 ? 2 : 1));
+  static_assert(S == 2 || S == 4 || S == 8, "slots go in pairs over whole waves");
+  static_assert(NW % SP == 0, "whole waves per slot pair");
+  static_assert(RW == 32 || RW == 16 || RW == 8, "a half-wave covers 1, 2 or 4 blocks of RW rows");
   static_assert(UPW % GS == 0, "wave-loads go in whole groups");
-  __shared__ float terms[2][CB][64];
-  // both slots' activation blocks, sized at launch (down_tile_lds): slot s at [s * nb]
+  static_assert(FW <= NW, "enough waves to fold");
+  __shared__ float terms[2][CB][NCH];
+  __shared__ float s_tot[NCH];
+  // every slot's activation blocks, sized at launch (down_tile_lds): slot s at [s * nb]
   extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn_tile[];
   ActBlock* s_act = (ActBlock*)s_dyn_tile;
 
@@ -1580,51 +1593,53 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nb = a.nb;
   if (blockIdx.y > 0) {  // token blockIdx.y of a few-token decode
-    a.route_idx += (size_t)blockIdx.y * 2;
-    a.route_w += (size_t)blockIdx.y * 2;
-    a.hact += (size_t)blockIdx.y * 2 * a.hact_stride;
+    a.route_idx += (size_t)blockIdx.y * S;
+    a.route_w += (size_t)blockIdx.y * S;
+    a.hact += (size_t)blockIdx.y * S * a.hact_stride;
     a.out += (size_t)blockIdx.y * a.rows;
   }
-  const int hs = lane >> 5;           // slot
-  const int p = (lane & 31) / RW;     // block parity (RW = 16)
-  const int r = lane & (RW - 1);      // row of the work-group's rows
-  // the experts first (loads return in order: waiting for them leaves the
-  // activation loads behind them in flight)
-  const int e0 = __builtin_amdgcn_readfirstlane(a.route_idx[0]);
-  const int e1 = __builtin_amdgcn_readfirstlane(a.route_idx[1]);
+  const int sl = 2 * (wave / WPP) + (lane >> 5);  // this lane's slot
+  const int wq = wave % WPP;                      // the wave's place among its pair's waves
+  const int p = (lane & 31) / RW;                 // block within a group of BPL
+  const int r = lane & (RW - 1);                  // row of the work-group's rows
+  // the lane's expert first (loads return in order: waiting for it leaves
+  // the activation loads behind it in flight)
+  const int ev = a.route_idx[sl];
   __builtin_amdgcn_sched_barrier(0);
-  // both slots' activation pieces, clamped to the last (no branches, so the
-  // waits stay counted)
+  // every slot's activation pieces, clamped to the last (no branches, so
+  // the waits stay counted)
   constexpr int NT = 64 * NW;
-  constexpr int APT = (2 * DOWN_TILE_MAX_NB * 3 + NT - 1) / NT;
-  const int npieces = 2 * nb * 3;
+  constexpr int MAXP = S == 2 ? 2 * DOWN_TILE_MAX_NB * 3 : S * 128 * 3;  // launcher: nb <= 128 for S > 2
+  constexpr int APT = (MAXP + NT - 1) / NT;
+  const int npieces = S * nb * 3;
   u32x4 av[APT];
 #pragma unroll
   for (int m = 0; m < APT; m++) {
     const int i = min((int)threadIdx.x + NT * m, npieces - 1);
-    const int s2 = i >= nb * 3 ? 1 : 0, rem = i - s2 * nb * 3;
+    const int s2 = i / (nb * 3), rem = i - s2 * nb * 3;
     av[m] = ((const u32x4*)(a.hact + (size_t)s2 * a.hact_stride))[rem];
   }
   __builtin_amdgcn_sched_barrier(0);
-  // Work-group g runs on XCD g % 8; for RW = 16 the two halves of a tile
+  // Work-group g runs on XCD g % 8; for RW < 32 the row groups of one tile
   // get ids of one residue class when the grid allows (they share the
   // tile's scale lines).
+  constexpr int PER_TILE = 32 / RW;
   const int g = blockIdx.x;
   size_t row0 = (size_t)g * RW;
-  if (RW == 16 && (gridDim.x & 15) == 0) {
+  if (PER_TILE > 1 && gridDim.x % (8 * PER_TILE) == 0) {
     const int gx = g & 7, gj = g >> 3;
-    row0 = (size_t)(gx + 8 * (gj >> 1)) * TILE + (size_t)(gj & 1) * 16;
+    row0 = (size_t)(gx + 8 * (gj / PER_TILE)) * TILE + (size_t)(gj % PER_TILE) * RW;
   }
   const size_t tile = row0 / TILE;
   const int rt = (int)(row0 % TILE) + r;
-  const size_t e = (size_t)(hs ? e1 : e0);
+  const size_t e = (size_t)ev;
   const uint8_t* cbase = a.codes + e * a.codes_stride + (tile * nb * CH * TILE + rt) * 16;
   const uint16_t* sbase = a.scales + e * a.scales_stride + tile * nb * TILE + rt;
   u32x4 cw[UPW][CH];
   uint16_t sw[UPW];
   // blocks past the end of the row are clamped to the last block (in-bounds
   // loads whose terms are never folded)
-  auto block_of = [&](int ch, int s) { return min(ch * CB + (wave * UPW + s) * BPL + p, nb - 1); };
+  auto block_of = [&](int ch, int s) { return min(ch * CB + (wq * UPW + s) * BPL + p, nb - 1); };
   auto load_block = [&](int ch, int s) {
     const int b = block_of(ch, s);
 #pragma unroll
@@ -1637,7 +1652,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
     load_block(0, s);
     __builtin_amdgcn_sched_barrier(0);
   }
-  const float w0 = a.route_w[0], w1 = a.route_w[1];
+  const float wv = a.route_w[min(lane, S - 1)];
 #pragma unroll
   for (int m = 0; m < APT; m++) {
     const int i = (int)threadIdx.x + NT * m;
@@ -1645,13 +1660,14 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   }
   __syncthreads();  // s_act
 
-  const ActBlock* act = s_act + (size_t)hs * nb;
-  float total = 0.0f;  // wave 0: slot lane / 32, row lane % 32
+  const ActBlock* act = s_act + (size_t)sl * nb;
+  const int chain = wave * 64 + lane;  // folding waves: chain RW s + r
+  float total = 0.0f;
   const int nchunks = (nb + CB - 1) / CB;
   for (int c = 0; c < nchunks; c++) {
     const int b0 = c * CB;
     const int bend = min(nb, b0 + CB);
-    float(*tb)[64] = terms[c & 1];
+    float(*tb)[NCH] = terms[c & 1];
     float tv[UPW];
     const bool more = c + 1 < nchunks;
 #pragma unroll
@@ -1668,23 +1684,25 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int s = 0; s < UPW; s++) tb[(wave * UPW + s) * BPL + p][32 * hs + r] = tv[s];
+    for (int s = 0; s < UPW; s++) tb[(wq * UPW + s) * BPL + p][sl * RW + r] = tv[s];
     __syncthreads();
-    if (wave == 0) {  // the fold chains first when the SIMD has several ready waves
+    if (wave < FW && chain < NCH) {  // the fold chains first when the SIMD has several ready waves
       __builtin_amdgcn_s_setprio(3);
-      total = lds_sum_strided<64>(&tb[0][lane], bend - b0, total);
+      total = lds_sum_strided<NCH>(&tb[0][chain], bend - b0, total);
       __builtin_amdgcn_s_setprio(0);
     }
   }
-  if (wave == 0) {
-    const float y1 = __shfl(total, lane + 32);  // lanes 0-31: slot 1's sum of the same row
-    if (lane < RW) {
-      float o = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
-      o = o + w0 * total;
-      o = o + w1 * y1;
-      const size_t row = row0 + lane;
-      if (row < (size_t)a.rows) a.out[row] = o;
-    }
+  if (wave < FW && chain < NCH) s_tot[chain] = total;
+  float wts[S];  // the route weights, lane s's wv
+#pragma unroll
+  for (int s2 = 0; s2 < S; s2++) wts[s2] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), s2));
+  __syncthreads();
+  if (wave == 0 && lane < RW) {
+    float o = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
+#pragma unroll
+    for (int s2 = 0; s2 < S; s2++) o = o + wts[s2] * s_tot[s2 * RW + lane];
+    const size_t row = row0 + lane;
+    if (row < (size_t)a.rows) a.out[row] = o;
   }
 }
 
@@ -2444,28 +2462,43 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   const dim3 groups((unsigned)(padded_rows((size_t)a.rows) / DR), T);
   if (groups.x == 0) return hipSuccess;
   if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS || T > 65535) return hipErrorInvalidValue;
-  // Two routes: the rows' block terms spread over sixteen waves per
-  // work-group (k_down_tile), faster than a wave per chain on every top-2
-  // shape measured (H 2048-4096, down rows of 32-448 blocks, 1-3 tokens;
-  // Mixtral-8x7B-shaped q4_0 layer: 15.2-16.9 -> 11.8 us at one token).
+  // Block terms spread over sixteen waves per work-group (k_down_tile):
+  // for two routes on every shape measured (H 2048-4096, down rows of
+  // 32-448 blocks, 1-3 tokens; Mixtral-8x7B-shaped q4_0 layer: 15.2-16.9 ->
+  // 11.8 us at one token); for four and eight routes over rows of at most
+  // 128 blocks when its 16-row groups give every CU one (Qwen3-235B-shaped
+  // layer, 48-block rows: 8.0 -> 6.4-7.5 us at one token, 23.2 -> 17.3 at
+  // four; H 2048 at one token has 128 such groups, and there the
+  // wave-per-route kernel's 8-row groups are as fast or faster), and only
+  // for calls below CACHED_LOAD_TOKENS (its weight loads are non-temporal).
   // Work-groups of 16 rows (half a tile) or 32: the size whose busiest CU
   // gets fewer rows, ceil(groups / 256 CUs) x rows per group, 32 on a tie
   // (one token of H 4096: 256 groups of 16 against 128 of 32 that would
   // leave half the CUs idle; two tokens: 256 of 32).
-  if (a.slots == 2 && a.nb <= DOWN_TILE_MAX_NB) {
-    const uint32_t lds = (uint32_t)down_tile_lds(a.nb);
+  {
     const size_t prow = padded_rows((size_t)a.rows);
-    auto busiest = [&](size_t rw) { return (prow / rw * T + 255) / 256 * rw; };
-    if (busiest(16) < busiest(32)) {
-      const dim3 grid((unsigned)(prow / 16), T);
-      if (dtype == Q8_0) return launch(k_down_tile<Q8_0, 16, 16, 1>, grid, 1024, lds, st, a);
-      if (dtype == Q4_0) return launch(k_down_tile<Q4_0, 16, 16, 2>, grid, 1024, lds, st, a);
-    } else {
-      const dim3 grid((unsigned)(prow / 32), T);
-      if (dtype == Q8_0) return launch(k_down_tile<Q8_0, 16, 32, 1>, grid, 1024, lds, st, a);
-      if (dtype == Q4_0) return launch(k_down_tile<Q4_0, 16, 32, 2>, grid, 1024, lds, st, a);
+    const bool spread =
+        (a.slots == 2 && a.nb <= DOWN_TILE_MAX_NB) ||
+        ((a.slots == 4 || a.slots == 8) && a.nb <= 128 && (int)T < CACHED_LOAD_TOKENS &&
+         prow / 16 * T >= 256);
+    if (spread) {
+      const uint32_t lds = (uint32_t)down_tile_lds(a.slots, a.nb);
+      auto busiest = [&](size_t rw) { return (prow / rw * T + 255) / 256 * rw; };
+      const bool half = busiest(16) < busiest(32);
+      const dim3 grid((unsigned)(prow / (half ? 16 : 32)), T);
+#define HALE_DOWN_TILE(S_)                                                                          \
+  do {                                                                                              \
+    if (half && dtype == Q8_0) return launch(k_down_tile<Q8_0, S_, 16, 16, 1>, grid, 1024, lds, st, a); \
+    if (half && dtype == Q4_0) return launch(k_down_tile<Q4_0, S_, 16, 16, 2>, grid, 1024, lds, st, a); \
+    if (dtype == Q8_0) return launch(k_down_tile<Q8_0, S_, 16, 32, 1>, grid, 1024, lds, st, a);         \
+    if (dtype == Q4_0) return launch(k_down_tile<Q4_0, S_, 16, 32, 2>, grid, 1024, lds, st, a);         \
+  } while (0)
+      if (a.slots == 2) HALE_DOWN_TILE(2);
+      if (a.slots == 4) HALE_DOWN_TILE(4);
+      if (a.slots == 8) HALE_DOWN_TILE(8);
+#undef HALE_DOWN_TILE
+      return hipErrorInvalidValue;
     }
-    return hipErrorInvalidValue;
   }
   // A wave per (slot, 8 rows) pays off when few routes leave many rows per
   // work-group (top-1 and top-3); top-4 and wider use the block-group pipeline.
