@@ -293,13 +293,17 @@ constexpr int ROUTE_MAX_E = 1024;
 constexpr int GEMV_MAX_NB = 512;  // blocks per row the GEMV stages in LDS
 
 constexpr int ROUTE_THREADS = 256;
-constexpr int ROUTE_VPT = ROUTE_MAX_H / 4 / ROUTE_THREADS;  // float4 of w (and of x) per thread
 
+// VPT: float4 of w (and of x) per thread, so H <= 4 VPT ROUTE_THREADS.  The
+// launcher takes the smallest of 2, 4 and 8 that covers H: registers and
+// LDS sized for H = 8192 held four work-groups per CU, and a 16-token call
+// of a 128-expert layer (2,048 work-groups) then ran in two rounds.
+template <int VPT>
 __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __restrict__ router,
                                                                 const float* __restrict__ x, int H,
                                                                 int E, ActBlock* __restrict__ act,
                                                                 float* __restrict__ logits) {
-  __shared__ __attribute__((aligned(16))) float prod[ROUTE_MAX_H + 32];  // chain-major
+  __shared__ __attribute__((aligned(16))) float prod[4 * VPT * ROUTE_THREADS + 32];  // chain-major
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int t = blockIdx.y;
@@ -312,9 +316,9 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
   const int nvec = steps * 2;  // float4 chunks covering the 8-lane part
 
   // every load of the row and of x first
-  f32x4 wv[ROUTE_VPT], xv[ROUTE_VPT];
+  f32x4 wv[VPT], xv[VPT];
 #pragma unroll
-  for (int j = 0; j < ROUTE_VPT; j++) {
+  for (int j = 0; j < VPT; j++) {
     const int c = tid + j * ROUTE_THREADS;
     if (c < nvec) {
       wv[j] = *(const f32x4*)(w + 4 * c);
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
   // chain l holds i = 8s + l at prod[l * stride + s]
   const int stride = steps + 4;  // 16 B aligned rows, chains on distinct banks
 #pragma unroll
-  for (int j = 0; j < ROUTE_VPT; j++) {
+  for (int j = 0; j < VPT; j++) {
     const int c = tid + j * ROUTE_THREADS;
     if (c < nvec) {
       const int sidx = c >> 1, l0 = (c & 1) * 4;
@@ -2387,7 +2391,11 @@ hipError_t launch_route_logits(const float* router, const float* x, int H, int E
     return launch(k_route_logits_tiled, grid, 1024, 0, st, router, x, H, E, T, logits, act);
   }
   dim3 grid(E, T);
-  return launch(k_route_logits, grid, ROUTE_THREADS, 0, st, router, x, H, E, act, logits);
+  if (H <= 8 * ROUTE_THREADS)
+    return launch(k_route_logits<2>, grid, ROUTE_THREADS, 0, st, router, x, H, E, act, logits);
+  if (H <= 16 * ROUTE_THREADS)
+    return launch(k_route_logits<4>, grid, ROUTE_THREADS, 0, st, router, x, H, E, act, logits);
+  return launch(k_route_logits<8>, grid, ROUTE_THREADS, 0, st, router, x, H, E, act, logits);
 }
 
 hipError_t launch_route_select(const float* logits, int E, int k, int normalize, int T,
