@@ -395,10 +395,13 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
 constexpr int RT_E = 16, RT_T = 8, RT_K = 64;
 constexpr int RT_STRIDE = RT_K + 4;                 // floats per chain row (16-byte aligned)
 constexpr int RT_BUF = (RT_E + RT_T) * 8 * RT_STRIDE;  // floats per buffer
-// From 32 tokens (Qwen3-30B-A3B layer, graph replay: 48 tokens 125 -> 118.5
-// us per step and 32 tokens 116 -> 113.6 us against one work-group per
-// (expert, token); at 8 and 16 tokens the tiles were 5-10 % slower).
-constexpr int ROUTE_TILED_MIN_T = 32;
+// From 48 tokens.  Against one work-group per (expert, token) sized for
+// the row length (eight per CU), per layer, graph replay, row-chain
+// grouped path: Qwen3-30B-A3B q4_0 at 32 / 40 / 48 / 64 / 76 tokens 89.1 /
+// 95.6 / 102.7 / 112.5 / 120 us with the tiles against 87.0 / 93.9 / 101.9 /
+// 114.1 / 122.7 without; Qwen3-235B-A22B at 32 / 48 / 60: 294 / 315 / 352
+// against 289 / 316 / 356.
+constexpr int ROUTE_TILED_MIN_T = 48;
 
 __global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __restrict__ router,
                                                              const float* __restrict__ x, int H,

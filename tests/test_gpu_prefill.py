@@ -68,8 +68,10 @@ def test_grouped_small(ctx, dtype, with_router):
 
 
 @pytest.mark.parametrize("dtype,Hd,I,E,k,T", [
-    (H.Q4_0, 2048, 64, 128, 8, 64),    # 32+ tokens: the router's 16-expert x 8-token tiles
-    (H.Q8_0, 1024, 64, 32, 6, 33),     # ... from 32 tokens: a partial token tile of one
+    (H.Q4_0, 2048, 64, 128, 8, 64),    # 48+ tokens: the router's 16-expert x 8-token tiles
+    (H.Q8_0, 1024, 64, 32, 6, 49),     # ... from 48 tokens: a partial token tile of one
+    (H.Q4_0, 2048, 64, 128, 8, 47),    # one work-group per (expert, token): 6016 of them
+    (H.Q8_0, 4160, 64, 16, 4, 40),     # ... rows of 4160 (registers and LDS sized for 8192)
     (H.Q8_0, 2080, 64, 20, 4, 100),    # a partial expert tile, a partial token tile, a partial chunk (260 steps)
     (H.Q4_0, 4096, 64, 128, 8, 72),    # 512 steps: eight chunks
 ])
