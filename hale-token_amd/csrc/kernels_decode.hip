@@ -2433,10 +2433,21 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   // per CU: 256 work-groups of 16 waves, 512 of 8), so that no second round
   // runs on a partly filled GPU.  With routing, one more column of
   // work-groups holds the selector.
+  // q4_0 gate/up rows of more than one 64-block chunk with 257 to 512
+  // tile-slots (eight-wave work-groups of one tile would put two on some
+  // CUs and one on the rest): sixteen waves and two tiles of one slot per
+  // work-group, at most one per CU, each running one selection and four
+  // chunks of loads (Qwen3-235B-shaped layer at one token, 384 tile-slots:
+  // 14.1-14.4 -> 13.2-13.8 us; at two tokens, 768, the eight-wave form
+  // stays faster)
+  const long tslots = (long)groups * slots * T;
+  const bool pair16 = dtype == Q4_0 && epi == EPI_GATE_UP && a.nb > 64 && tslots > 256 &&
+                      tslots <= 512 && !(a.logits && a.E > 256);
   auto grid_of = [&](int nw) {
     GemvArgs b = a;
     b.tiles = groups;
     b.ipw = epi == EPI_GATE_UP && (long)groups * slots * T > 256L * (16 / nw) ? 2 : 1;
+    if (pair16) b.ipw = 2;
     return std::make_pair(dim3((groups + b.ipw - 1) / b.ipw + (a.logits ? 1 : 0), slots * T), b);
   };
   const bool cached = T >= CACHED_LOAD_TOKENS;
@@ -2457,7 +2468,7 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   HALE_GEMV_CASE(Q4_0, EPI_PLAIN, 4)
   // sixteen waves leave 128 VGPRs, too few for the selection state of more
   // than 256 experts: those layers take the eight-wave form
-  if (dtype == Q4_0 && epi == EPI_GATE_UP && a.nb <= 64 && !many) {
+  if (dtype == Q4_0 && epi == EPI_GATE_UP && (a.nb <= 64 || pair16) && !many) {
     const auto gb = grid_of(16);
     if (cached) HALE_GEMV_LAUNCH(Q4_0, EPI_GATE_UP, 16, 256, false);
     HALE_GEMV_LAUNCH(Q4_0, EPI_GATE_UP, 16, 256, true);
