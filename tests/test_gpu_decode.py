@@ -343,7 +343,10 @@ def _few_tokens_check(L, moe, xs):
     (H.Q8_0, 1024, 1024, 8, 3, 4),     # top-3 whole chain, q8_0
     (H.Q4_0, 1024, 256, 8, 1, 5),      # top-1 (32-row chain groups)
     (H.Q4_0, 256, 64, 300, 16, 3),     # more than 256 experts: eight-wave selection, 16 slots
-    (H.Q4_0, 4160, 64, 16, 4, 2),      # pipelined down at H 4160 (no XCD permutation)
+    (H.Q4_0, 4160, 64, 16, 4, 2),      # spread-term down, top-4, 520 16-row groups (no XCD permutation)
+    (H.Q8_0, 4096, 512, 16, 4, 3),     # spread-term down, top-4 q8_0, 16-row groups
+    (H.Q4_0, 4096, 1536, 16, 8, 2),    # spread-term down, top-8, 32-row groups (two tokens of H 4096)
+    (H.Q8_0, 4096, 512, 16, 4, 2),     # ... q8_0, 32-row groups
 ])
 def test_moe_decode_few_tokens(ctx, dtype, hidden, inter, E, k, T):
     L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=True,
