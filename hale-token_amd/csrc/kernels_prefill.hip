@@ -48,7 +48,7 @@ constexpr int TACT_BLOCK = TACT_CODES + TM * 4;
 struct Tile {
   int expert;
   int row0;  // first sorted position
-  int rows;  // 1..tile rows (TM; BAND_ROWS for the row-chain kernels)
+  int rows;  // 1..tile rows (TM; band_rows for the row-chain kernels)
   int pad;
 };
 
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // A call of tens of tokens gives most experts one to a few assignments, so
 // the 32-row products above are mostly padding and each wave's chain of K
 // blocks is bound by its own latency.  Here a band tile holds at most
-// BAND_ROWS assignments of one expert, and lane l of a wave owns one weight
+// NR assignments of one expert, and lane l of a wave owns one weight
 // row (gate/up: lanes 0-31 the gate rows, 32-63 the up rows of one 32-row
 // I-tile; down: two 32-row H-tiles).  The lane walks its row's K blocks
 // with a ring of D blocks in flight and adds each block's term
@@ -526,11 +526,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // all lanes at once); the gate/up input is read in place (token-major,
 // through perm), with no gather.
 //
-// Assignments per band tile: two.  Tiles of four or eight (more terms per
-// weight block, fewer re-reads of an expert's weights) measured slower at
-// every size where this path is the faster one: their longer per-block
-// chains leave the ring's loads waiting.
-constexpr int BAND_ROWS = 2;
+// Assignments per band tile (band_rows): two, or four when a call gives the
+// experts two or more assignments each on average and a gate/up row holds
+// at least 2 KB (q8_0 from H 2048, q4_0 from H 4096) over rows of at most
+// 256 blocks.  Four terms per weight block then outweigh the longer
+// per-block chains; with shorter rows or fewer assignments per expert the
+// ring's loads wait on those chains and two per tile are faster.  Measured
+// per layer, graph replay: Qwen3-235B-A22B q4_0 at 32 / 48 / 60 / 72 tokens
+// 283.7 / 317.5 / 352.4 / 388.8 us with two, 261.6 / 306 / 333.9 / 369.2
+// with four (at 9 / 16 tokens 129.3 / 188.1 against 149.0 / 197.4);
+// Qwen3-30B-A3B q8_0 at 32 / 48 / 64 / 72: 136.7 / 157 / 169.5 / 179.2
+// against 122.6 / 150.7 / 159.2 / 159.5; Qwen3-30B-A3B q4_0 (1,152-byte
+// rows) slower with four at every size (64 tokens 111.7 against 118.2);
+// Mixtral-8x7B (448-block down rows) at 8 / 12 tokens 198.4 / 243.6
+// against 234.7 / 254.2.
 constexpr int BAND_WAVES = 4;
 
 struct BandArgs {
@@ -552,19 +561,20 @@ struct BandArgs {
   float* y;             // down output: [A][H] by sorted position
 };
 
-// LDS of a band work-group: the tile's activation blocks [BAND_ROWS][nb]
-// (48 bytes each), then per wave the double-buffered scales of its ring
-// cycle, [2][2 halves][D blocks][32 rows] f16.
-constexpr int BAND_MAX_NB = 512;  // K blocks per row (48 KB of activations)
-static size_t band_lds(int nb, int d) {
-  return (size_t)BAND_ROWS * nb * sizeof(ActBlock) + (size_t)BAND_WAVES * 2 * 2 * d * TILE * 2;
+// LDS of a band work-group: the tile's activation blocks [nr][nb] (48
+// bytes each), then per wave the double-buffered scales of its ring cycle,
+// [2][2 halves][D blocks][32 rows] f16.
+constexpr int BAND_MAX_NB = 512;  // K blocks per row (48 KB of activations at two rows)
+static size_t band_lds(int nr, int nb, int d) {
+  return (size_t)nr * nb * sizeof(ActBlock) + (size_t)BAND_WAVES * 2 * 2 * d * TILE * 2;
 }
 
 // Work-group: BAND_WAVES waves of one band tile (gpt work-groups per tile,
 // waves past the tile's wpt only help stage).  The XCDs take work-groups in
 // turn (linear id % 8), so work-group L runs item (L % 8) * per + L / 8:
-// the work-groups of one tile run on one XCD.  Both assignments of a tile
-// are computed; a tile of one repeats it, and the copy is never stored.
+// the work-groups of one tile run on one XCD.  All NR assignments of a
+// tile are computed; a shorter tile repeats its last, whose copies are
+// never stored.
 //
 // Each lane's row streams through a ring of D code blocks; per ring cycle
 // (D blocks) the wave loads the cycle after next's scales as whole 16-byte
@@ -580,11 +590,11 @@ static size_t band_lds(int nb, int d) {
 // find its weights in L2.
 // MAXNB: the K blocks the activation staging is sized for (256, or 512 for
 // longer rows: its loads need registers that cost the others occupancy).
-template <int DT, bool GATE_UP, int D, bool NT, int MAXNB>
+template <int DT, bool GATE_UP, int D, bool NT, int MAXNB, int NR>
 __global__ __launch_bounds__(64 * BAND_WAVES) void k_band(BandArgs a) {
   extern __shared__ __attribute__((aligned(16))) u32x4 s_band[];
   constexpr int CH = Layout<DT>::CH;
-  constexpr int NR = BAND_ROWS;
+  static_assert(NR == 2 || (NR == 4 && MAXNB <= 256), "tiles of two, or of four over rows of at most 256 blocks");
   constexpr int SPL = D / 8;   // scale pieces per lane per cycle
   constexpr int APT = (NR * MAXNB * 3 + 64 * BAND_WAVES - 1) / (64 * BAND_WAVES);  // activation pieces per thread
   static_assert(MAXNB <= BAND_MAX_NB, "the staging fits its bound");
@@ -893,13 +903,22 @@ static bool band_on(const PrefillLayer& L, size_t T) {
   return T <= L.band_max && std::max(L.H, L.I) / QK <= BAND_MAX_NB;
 }
 
-// The row-chain kernels' layout has tiles of BAND_ROWS rows, no gathered
+// Assignments per row-chain tile (see k_band): four when the call gives
+// the experts two or more each on average and a gate/up row holds at least
+// 2 KB over rows of at most 256 blocks, else two.
+static int band_rows(const PrefillLayer& L, size_t T) {
+  const size_t A = T * (size_t)L.k;
+  const size_t row_bytes = (size_t)(L.H / QK) * (L.dtype == Q8_0 ? 34 : 18);
+  return A >= 2 * (size_t)L.E && row_bytes >= 2048 && std::max(L.H, L.I) / QK <= 256 ? 4 : 2;
+}
+
+// The row-chain kernels' layout has tiles of band_rows rows, no gathered
 // input and the SiLU output as [A][I / 32] activation blocks in `tact`.
 static WsLayout ws_layout(const PrefillLayer& L, size_t T) {
   WsLayout w{};
   const size_t A = T * (size_t)L.k;
   const bool band = band_on(L, T);
-  const size_t tm = band ? (size_t)BAND_ROWS : TM;
+  const size_t tm = band ? (size_t)band_rows(L, T) : TM;
   w.max_tiles = (A + tm - 1) / tm + (size_t)L.E;
   size_t o = 0;
   w.perm = o;
@@ -960,7 +979,7 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
   // 2. group assignments by expert
   const bool band = band_on(L, T);
   HALE_STEP(K_GROUP, launch(k_group, 1, 64 * GROUP_WAVES, 0, st, L.route_idx, (int)A, L.E, perm,
-                            pos_of, tiles, ntiles, L.stats, band ? BAND_ROWS : TM));
+                            pos_of, tiles, ntiles, L.stats, band ? band_rows(L, T) : TM));
   if (band) {
     // 3-4. row-chain gate/up (input read in place) and down
     BandArgs g{};
@@ -988,16 +1007,21 @@ hipError_t prefill_enqueue(const PrefillLayer& L, void* ws, size_t T, const floa
     // (Qwen3-30B q4_0 layer, per layer: 72.9 against 75.2 us at 16 tokens;
     // cached from there: 121 against 125.7 at 64, 153.8 against 161.8 at 96)
     const bool nt = A <= 2 * (size_t)L.E;
+    const int nr = band_rows(L, T);  // four only over rows of at most 256 blocks
 #define HALE_BAND_NB(DT_, GU_, D_, NT_, args)                                             \
   do {                                                                                    \
-    if (args.nb <= 256)                                                                   \
+    if (nr == 4)                                                                          \
       HALE_STEP(GU_ ? K_GROUPED_GATE_UP : K_GROUPED_DOWN,                                 \
-                (launch(k_band<DT_, GU_, D_, NT_, 256>, grid(args.wpt), 64 * BAND_WAVES,    \
-                        (uint32_t)band_lds(args.nb, D_), st, args)));                       \
+                (launch(k_band<DT_, GU_, D_, NT_, 256, 4>, grid(args.wpt), 64 * BAND_WAVES, \
+                        (uint32_t)band_lds(4, args.nb, D_), st, args)));                    \
+    else if (args.nb <= 256)                                                              \
+      HALE_STEP(GU_ ? K_GROUPED_GATE_UP : K_GROUPED_DOWN,                                 \
+                (launch(k_band<DT_, GU_, D_, NT_, 256, 2>, grid(args.wpt), 64 * BAND_WAVES, \
+                        (uint32_t)band_lds(2, args.nb, D_), st, args)));                    \
     else                                                                                  \
       HALE_STEP(GU_ ? K_GROUPED_GATE_UP : K_GROUPED_DOWN,                                 \
-                (launch(k_band<DT_, GU_, D_, NT_, BAND_MAX_NB>, grid(args.wpt),             \
-                        64 * BAND_WAVES, (uint32_t)band_lds(args.nb, D_), st, args)));      \
+                (launch(k_band<DT_, GU_, D_, NT_, BAND_MAX_NB, 2>, grid(args.wpt),          \
+                        64 * BAND_WAVES, (uint32_t)band_lds(2, args.nb, D_), st, args)));   \
   } while (0)
 #define HALE_BAND(DT_, GU_, D_, args)        \
   do {                                       \

@@ -1150,19 +1150,20 @@ static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_
 
 // Most tokens per grouped forward that take the row-chain kernels rather
 // than the matrix products.  The row-chain kernels read an expert's weights
-// once per two assignments (from L2 for an expert's later tiles, with
-// ordinary loads above two assignments per expert), so they lose once
-// experts hold several.  The crossovers (same measurement): Qwen3-30B q4_0
-// at about 4.75 E / k tokens (72 tokens: 118.4 against 121.7 us, 80: 124.4
-// against 122.1), Qwen3-235B q4_0 at 3.75 E / k (56 tokens 343 against
-// 351 us, 64: 368 against 353), Qwen3-30B q8_0 at 3.5 E / k (48 tokens
-// 153.7 against 160.1 us, 64: 171 against 163) and Mixtral (448-block down
-// rows) at 3.25 E / k (12 tokens 244.5 against 252 us, 14: 261 against 252).
+// once per tile of two or four assignments (from L2 for an expert's later
+// tiles, with ordinary loads above two assignments per expert), so they
+// lose once experts hold several.  The crossovers (same measurement):
+// Qwen3-30B q4_0 at about 4.75 E / k tokens (72 tokens: 118.4 against 121.7
+// us, 80: 124.4 against 122.1), Qwen3-235B q4_0 with tiles of four at 4.25
+// E / k (68 tokens 355.1 against 356.9 us, 72: 367.6 against 357.6),
+// Qwen3-30B q8_0 with tiles of four at 5 E / k (80 tokens 160.9 against
+// 164.9 us, 88: 171.9 against 165.1) and Mixtral (448-block down rows) at
+// 3.25 E / k (12 tokens 244.5 against 252 us, 14: 261 against 252).
 static size_t default_band_max(int dtype, size_t E, size_t H, size_t I, size_t k) {
   size_t c4;  // quarter-assignments per expert
   if (I / HALE_QK > 256) c4 = 13;
-  else if (dtype == HALE_Q4_0) c4 = H <= 2048 ? 19 : 15;
-  else c4 = H <= 2048 ? 14 : 13;
+  else if (dtype == HALE_Q4_0) c4 = H <= 2048 ? 19 : 17;
+  else c4 = H <= 2048 ? 20 : 13;
   return c4 * E / (4 * std::max<size_t>(k, 1));
 }
 

@@ -286,12 +286,12 @@ int hale_moe_set_grouped_min_tokens(hale_moe *moe, size_t n);
 int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
 
 /* Most tokens per expert-grouped call that run the row-chain kernels
- * (each lane one weight row, each expert's assignments two at a time as
- * scalar operands) in place of the int8 matrix products; larger grouped
- * calls take the matrix products.  Default c * num_experts / top_k with
- * c = 4.75 for q4_0 layers with hidden <= 2048, 3.75 for larger q4_0
- * ones, 3.5 for q8_0 ones with hidden <= 2048 and 3.25 for the rest and for
- * layers whose intermediate size exceeds 8192 (76, 60 and 56 tokens at
+ * (each lane one weight row, each expert's assignments two or four at a
+ * time as scalar operands) in place of the int8 matrix products; larger
+ * grouped calls take the matrix products.  Default c * num_experts / top_k
+ * with c = 4.75 for q4_0 layers with hidden <= 2048, 4.25 for larger q4_0
+ * ones, 5 for q8_0 ones with hidden <= 2048 and 3.25 for the rest and for
+ * layers whose intermediate size exceeds 8192 (76, 68 and 80 tokens at
  * 128 experts, top-8; 13 at 8 experts, top-2); layers whose intermediate
  * size exceeds 16384 never take them.  Both give the reference's bits; the choice is
  * speed only.  0 never takes them.  No counterpart in the reference; for

@@ -287,24 +287,25 @@ def test_missing_expert_is_reported(ctx):
 @pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_0])
 @pytest.mark.parametrize("T,gmin,bmax", [(7, None, None), (10, None, None), (11, None, None),
                                          (12, None, None), (21, None, None), (24, None, None),
-                                         (40, None, None),
+                                         (40, None, None), (44, None, None),
                                          (8, 8, None), (12, None, 0), (16, 17, None)])
 def test_moe_logits_given_zipf_routing(ctx, dtype, T, gmin, bmax):
     """Router logits supplied directly (the skewed-routing workloads).  This
     top-4 layer of 32 experts takes the decode path below 11 tokens (q4_0)
     or 12 (q8_0), the row-chain grouped kernels up to 4.75 * 32 / 4 = 38
-    tokens (q4_0) or 3.5 * 32 / 4 = 28 (q8_0) and the grouped matrix
+    tokens (q4_0) or 5 * 32 / 4 = 40 (q8_0) and the grouped matrix
     products above: 7 and 10 decode, 11 row chains (q4_0) or decode (q8_0),
     12 and 21 row chains (non-temporal weight loads), 24 row
     chains (cached loads: more than two assignments per expert), 40 the
-    matrix products; then 8 tokens with the threshold set to 8 (row
+    matrix products (q4_0) or row chains (q8_0), 44 the matrix products;
+    then 8 tokens with the threshold set to 8 (row
     chains), 12 with the row chains off (matrix products) and 16 with the
     threshold above them (a decode pass with cached weight loads)."""
     E, Hd, I, k = 32, 256, 64, 4
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=77, with_router=False)
     moe = make_layer(ctx, L)
     assert moe.grouped_min_tokens == (11 if dtype == H.Q4_0 else 12)
-    assert moe.band_max_tokens == (38 if dtype == H.Q4_0 else 28)
+    assert moe.band_max_tokens == (38 if dtype == H.Q4_0 else 40)
     if gmin:
         moe.set_grouped_min_tokens(gmin)
     if bmax is not None:

@@ -100,12 +100,18 @@ def test_grouped_router_many_tokens(ctx, dtype, Hd, I, E, k, T):
     (H.Q8_0, 32, 32, 4, 2, 6, False),       # one block per row, one output tile: spare waves
     (H.Q4_0, 64, 32, 1024, 1, 40, True),    # 1024 experts, top-1
     (H.Q8_0, 256, 9216, 4, 2, 6, False),    # 288-block down rows: the 512-block staging
+    # tiles of four (two or more assignments per expert, gate/up rows of 2 KB or more)
+    (H.Q8_0, 2048, 96, 16, 4, 8, True),     # exactly two per expert: tiles of four, non-temporal loads
+    (H.Q8_0, 2048, 96, 16, 4, 20, False),   # Zipf: tiles of 1-4 rows, ordinary loads
+    (H.Q4_0, 4096, 64, 16, 4, 12, True),    # q4_0 (broadcast activation reads)
+    (H.Q4_0, 4096, 1056, 8, 2, 13, False),  # q4_0 down rows of 33 blocks (a ring of 16)
+    (H.Q4_0, 8192, 64, 8, 2, 9, False),     # 256-block rows: four rows' activations staged
 ])
 def test_band_row_chains(ctx, dtype, Hd, I, E, k, T, with_router):
-    """The row-chain grouped kernels (two assignments of an expert per tile,
-    a lane per weight row, the activations as scalar operands), forced for
-    every call: routes, weights and outputs bit-exact per token against the
-    oracle, and the same bits as the grouped matrix products."""
+    """The row-chain grouped kernels (two or four assignments of an expert
+    per tile, a lane per weight row, the activations as scalar operands),
+    forced for every call: routes, weights and outputs bit-exact per token
+    against the oracle, and the same bits as the grouped matrix products."""
     L = O.OracleMoe.synthetic(dtype, Hd, I, E, k, normalize_topk=True, seed=Hd + I + T,
                               with_router=with_router)
     moe = make_layer(ctx, L)
