@@ -1138,14 +1138,16 @@ static int moe_ws(hale_moe* m, size_t need, void** out) {
 // Qwen3-30B q4_0 (top-8 of 128) between 10 and 11 tokens (55.6 against
 // 56.8 us at 10, 62.2 against 59.9 at 11), Qwen3-235B q4_0 at 8 (125.8
 // both; 153 against 136 at 10), Qwen3-30B q8_0 between 10 and 12 (73.4
-// against 75.7 at 10, 85.1 against 83.1 at 12); Mixtral (top-2 of 8)
+// against 75.7 at 10, 85.1 against 83.1 at 12), a Qwen3-235B-shaped q8_0
+// layer between 7 and 8 (175.6 against 177.4 us at 7, 196.3 against 188.8
+// at 8); Mixtral (top-2 of 8)
 // between 4 and 6 (136 against 166 us at 4, 198 against 184 at 6).
 static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_t k) {
   (void)E;
   (void)I;
   if (k < 4) return 6;
   if (dtype == HALE_Q4_0) return H <= 2048 ? 11 : 9;
-  return 12;
+  return H <= 2048 ? 12 : 8;
 }
 
 // Most tokens per grouped forward that take the row-chain kernels rather
@@ -1157,13 +1159,15 @@ static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_
 // us, 80: 124.4 against 122.1), Qwen3-235B q4_0 with tiles of four at 4.25
 // E / k (68 tokens 355.1 against 356.9 us, 72: 367.6 against 357.6),
 // Qwen3-30B q8_0 with tiles of four at 5 E / k (80 tokens 160.9 against
-// 164.9 us, 88: 171.9 against 165.1) and Mixtral (448-block down rows) at
-// 3.25 E / k (12 tokens 244.5 against 252 us, 14: 261 against 252).
+// 164.9 us, 88: 171.9 against 165.1), a Qwen3-235B-shaped q8_0 layer with
+// tiles of four at 3.75 E / k (60 tokens 498.8 against 511.9 us, 64: 517.5
+// against 515.1) and Mixtral (448-block down rows) at 3.25 E / k (12
+// tokens 244.5 against 252 us, 14: 261 against 252).
 static size_t default_band_max(int dtype, size_t E, size_t H, size_t I, size_t k) {
   size_t c4;  // quarter-assignments per expert
   if (I / HALE_QK > 256) c4 = 13;
   else if (dtype == HALE_Q4_0) c4 = H <= 2048 ? 19 : 17;
-  else c4 = H <= 2048 ? 20 : 13;
+  else c4 = H <= 2048 ? 20 : 15;
   return c4 * E / (4 * std::max<size_t>(k, 1));
 }
 

@@ -272,7 +272,8 @@ int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
  * path (default for top_k >= 4: 11 for q4_0 with hidden <= 2048, 9 for
- * wider q4_0, 12 for q8_0; 6 for top_k < 4); fewer tokens run the decode
+ * wider q4_0, 12 for q8_0 with hidden <= 2048, 8 for wider q8_0; 6 for
+ * top_k < 4); fewer tokens run the decode
  * kernels in one pass over all of them.  Both give the reference's bits; the choice is speed only.
  * n in 2..HALE_DECODE_MAX_TOKENS + 1.  A new threshold re-lays the layer's
  * per-token scratch on its next call, which must then come outside a graph
@@ -290,9 +291,9 @@ int hale_moe_grouped_min_tokens(const hale_moe *moe, size_t *n);
  * time as scalar operands) in place of the int8 matrix products; larger
  * grouped calls take the matrix products.  Default c * num_experts / top_k
  * with c = 4.75 for q4_0 layers with hidden <= 2048, 4.25 for larger q4_0
- * ones, 5 for q8_0 ones with hidden <= 2048 and 3.25 for the rest and for
- * layers whose intermediate size exceeds 8192 (76, 68 and 80 tokens at
- * 128 experts, top-8; 13 at 8 experts, top-2); layers whose intermediate
+ * ones, 5 for q8_0 ones with hidden <= 2048, 3.75 for larger q8_0 ones
+ * and 3.25 for layers whose intermediate size exceeds 8192 (76, 68, 80 and
+ * 60 tokens at 128 experts, top-8; 13 at 8 experts, top-2); layers whose intermediate
  * size exceeds 16384 never take them.  Both give the reference's bits; the choice is
  * speed only.  0 never takes them.  No counterpart in the reference; for
  * callers tuning batched decode and small prefill chunks. */

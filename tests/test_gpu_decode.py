@@ -415,6 +415,21 @@ def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
         moe.set_grouped_min_tokens(11)
 
 
+@pytest.mark.parametrize("dtype,hidden,inter,E,k,gmin,bmax", [
+    (H.Q4_0, 2048, 768, 128, 8, 11, 76),    # Qwen3-30B-A3B q4_0: 4.75 E / k
+    (H.Q4_0, 4096, 1536, 128, 8, 9, 68),    # Qwen3-235B-A22B q4_0: 4.25 E / k
+    (H.Q8_0, 2048, 768, 128, 8, 12, 80),    # Qwen3-30B-A3B q8_0: 5 E / k
+    (H.Q8_0, 4096, 1536, 128, 8, 8, 60),    # Qwen3-235B-A22B q8_0: 3.75 E / k
+    (H.Q4_0, 4096, 14336, 8, 2, 6, 13),     # Mixtral-8x7B: 3.25 E / k (448-block down rows)
+])
+def test_default_thresholds_by_layer_type(ctx, dtype, hidden, inter, E, k, gmin, bmax):
+    """A new layer's grouped and row-chain thresholds follow its type and
+    shape (the measured crossovers)."""
+    moe = H.MoeLayer(ctx, 0, E, hidden, inter, dtype, k, True, None)
+    assert (moe.grouped_min_tokens, moe.band_max_tokens) == (gmin, bmax)
+    moe.close()
+
+
 def test_grouped_threshold_moves_the_path_not_the_bits(ctx):
     """The thresholds only choose the kernels: the same 12 tokens through
     the decode path (threshold 13), the row-chain grouped kernels (threshold
