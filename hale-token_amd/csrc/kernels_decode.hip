@@ -381,20 +381,20 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_logits(const float* __r
 }
 
 // The router logits of many tokens (T >= ROUTE_TILED_MIN_T): work-group
-// (eg, tg) computes experts 16 eg .. 16 eg + 15 for tokens 8 tg .. 8 tg + 7,
-// 1024 threads.  Lane 8t + l of wave e carries chain l of logit (e, t):
+// (eg, tg) computes experts RT_E eg .. RT_E eg + RT_E - 1 (RT_E = 16 or 8)
+// for tokens 8 tg .. 8 tg + 7, one wave per expert.  Lane 8t + l of wave e
+// carries chain l of logit (e, t):
 // acc = acc + w_e[8s + l] * x_t[8s + l] in order of s, each product rounded
-// before it is added (dot_f32's 8-lane order, quant.rs:152-194).  The 24
-// rows (16 router rows, 8 tokens) stream through LDS chain-major in chunks
+// before it is added (dot_f32's 8-lane order, quant.rs:152-194).  The
+// RT_E + 8 rows (router rows, then tokens) stream through LDS chain-major in chunks
 // of RT_K steps, two buffers, so chunk c + 1 loads while chunk c is added,
-// and every staged row serves 8 or 16 logits.  The eight chains of a logit
+// and every staged row serves 8 or RT_E logits.  The eight chains of a logit
 // are reduced in the one-token kernel's fixed order, so each logit has its
 // bits.  Then the work-groups quantize the token tile's activation blocks
 // (as k_act_quant does), each taking its share: block q of the tile goes to
 // the work-group of expert column q % gridDim.x.
-constexpr int RT_E = 16, RT_T = 8, RT_K = 64;
+constexpr int RT_T = 8, RT_K = 64;
 constexpr int RT_STRIDE = RT_K + 4;                 // floats per chain row (16-byte aligned)
-constexpr int RT_BUF = (RT_E + RT_T) * 8 * RT_STRIDE;  // floats per buffer
 // From 48 tokens.  Against one work-group per (expert, token) sized for
 // the row length (eight per CU), per layer, graph replay, row-chain
 // grouped path: Qwen3-30B-A3B q4_0 at 32 / 40 / 48 / 64 / 76 tokens 89.1 /
@@ -403,11 +403,14 @@ constexpr int RT_BUF = (RT_E + RT_T) * 8 * RT_STRIDE;  // floats per buffer
 // against 289 / 316 / 356.
 constexpr int ROUTE_TILED_MIN_T = 48;
 
-__global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __restrict__ router,
-                                                             const float* __restrict__ x, int H,
-                                                             int E, int T,
-                                                             float* __restrict__ logits,
-                                                             ActBlock* __restrict__ act) {
+template <int RT_E>  // experts per work-group: one wave each
+__global__ __launch_bounds__(64 * RT_E) void k_route_logits_tiled(const float* __restrict__ router,
+                                                                  const float* __restrict__ x, int H,
+                                                                  int E, int T,
+                                                                  float* __restrict__ logits,
+                                                                  ActBlock* __restrict__ act) {
+  constexpr int NT = 64 * RT_E;                          // threads
+  constexpr int RT_BUF = (RT_E + RT_T) * 8 * RT_STRIDE;  // floats per buffer
   __shared__ __attribute__((aligned(16))) float buf[2][RT_BUF];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -415,16 +418,16 @@ __global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __rest
   const int steps = H / 8;
   const int nchunk = (steps + RT_K - 1) / RT_K;
   // Chunk c of row r: elements [8 RT_K c, 8 RT_K (c + 1)), 2 RT_K float4;
-  // thread q moves float4 pieces q, q + 1024, q + 2048 of the 24 rows.  Rows
+  // thread q moves float4 pieces q, q + NT, q + 2 NT, ... of the rows.  Rows
   // past E or T repeat the last one and pieces past H the last piece
   // (in-bounds loads; their chains are not written).
   constexpr int PPR = 2 * RT_K;                       // float4 pieces per row and chunk
-  constexpr int PPT = (RT_E + RT_T) * PPR / 1024;     // pieces per thread
-  static_assert((RT_E + RT_T) * PPR % 1024 == 0, "whole pieces per thread");
+  constexpr int PPT = (RT_E + RT_T) * PPR / NT;       // pieces per thread
+  static_assert((RT_E + RT_T) * PPR % NT == 0, "whole pieces per thread");
   auto load_chunk = [&](f32x4* v, int c) {
 #pragma unroll
     for (int j = 0; j < PPT; j++) {
-      const int idx = tid + 1024 * j, row = idx / PPR, piece = idx % PPR;
+      const int idx = tid + NT * j, row = idx / PPR, piece = idx % PPR;
       const float* src = row < RT_E ? router + (size_t)min(e0 + row, E - 1) * H
                                     : x + (size_t)min(t0 + row - RT_E, T - 1) * H;
       const int elem = min(c * 8 * RT_K + 4 * piece, H - 4);
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __rest
   auto store_chunk = [&](const f32x4* v, float* b) {
 #pragma unroll
     for (int j = 0; j < PPT; j++) {
-      const int idx = tid + 1024 * j, row = idx / PPR, piece = idx % PPR;
+      const int idx = tid + NT * j, row = idx / PPR, piece = idx % PPR;
       float* r = b + (row * 8 + (piece & 1) * 4) * RT_STRIDE + (piece >> 1);
       r[0] = v[j].x;
       r[RT_STRIDE] = v[j].y;
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(1024) void k_route_logits_tiled(const float* __rest
   // block, 128 blocks per pass (the bound is uniform per 8-lane group)
   const int nb = H / QK;
   const int nq = min(RT_T, T - t0) * nb;
-  for (int q = blockIdx.x + gridDim.x * (tid >> 3); q < nq; q += gridDim.x * 128) {
+  for (int q = blockIdx.x + gridDim.x * (tid >> 3); q < nq; q += gridDim.x * (NT / 8)) {
     const int tk = q / nb, b = q - tk * nb;
     const size_t blk = (size_t)(t0 + tk) * nb + b;
     quant_block8(*(const f32x4*)(x + blk * QK + 4 * (tid & 7)), tid & 7, act + blk);
@@ -2390,8 +2393,17 @@ hipError_t launch_route_logits(const float* router, const float* x, int H, int E
   if (T >= ROUTE_TILED_MIN_T) {
     // many tokens: 16 experts x 8 tokens per work-group, the activation
     // blocks quantized by the same launch
-    const dim3 grid((E + RT_E - 1) / RT_E, (T + RT_T - 1) / RT_T);
-    return launch(k_route_logits_tiled, grid, 1024, 0, st, router, x, H, E, T, logits, act);
+    // 16 experts per work-group, or 8 when 16 would leave CUs without one
+    // (Qwen3-30B-A3B layer on the row chains at 48 / 64 / 76 tokens: 103.2-
+    // 103.6 / 112.7-113.2 / 120.3-120.6 -> 101.8-101.9 / 112.3-112.7 /
+    // 118.9-119.3 us per step; Qwen3-235B-A22B at 48: 315-317 -> 310-313)
+    const int tt = (T + RT_T - 1) / RT_T;
+    if ((E + 15) / 16 * tt < 256) {
+      const dim3 grid8((E + 7) / 8, tt);
+      return launch(k_route_logits_tiled<8>, grid8, 512, 0, st, router, x, H, E, T, logits, act);
+    }
+    const dim3 grid((E + 15) / 16, tt);
+    return launch(k_route_logits_tiled<16>, grid, 1024, 0, st, router, x, H, E, T, logits, act);
   }
   dim3 grid(E, T);
   if (H <= 8 * ROUTE_THREADS)

@@ -68,7 +68,9 @@ def test_grouped_small(ctx, dtype, with_router):
 
 
 @pytest.mark.parametrize("dtype,Hd,I,E,k,T", [
-    (H.Q4_0, 2048, 64, 128, 8, 64),    # 48+ tokens: the router's 16-expert x 8-token tiles
+    (H.Q4_0, 2048, 64, 128, 8, 64),    # 48+ tokens: the router's 8-expert x 8-token tiles (64 of 16 would leave CUs idle)
+    (H.Q4_0, 256, 64, 256, 8, 128),    # 16-expert tiles (256 of them)
+    (H.Q8_0, 512, 64, 264, 4, 129),    # 16-expert tiles, a partial expert and a partial token tile
     (H.Q8_0, 1024, 64, 32, 6, 49),     # ... from 48 tokens: a partial token tile of one
     (H.Q4_0, 2048, 64, 128, 8, 47),    # one work-group per (expert, token): 6016 of them
     (H.Q8_0, 4160, 64, 16, 4, 40),     # ... rows of 4160 (registers and LDS sized for 8192)
