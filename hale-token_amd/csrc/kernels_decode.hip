@@ -1356,7 +1356,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
 }
 
 // The same projection and combine with whole fold chains per wave, used
-// for 1 or 3 routes when every slot's activation blocks fit in LDS (two
+// for 3 routes when every slot's activation blocks fit in LDS (one and two
 // routes take k_down_tile below).  A
 // work-group owns RG output rows for every slot (RG = 16 for 2 or 3 slots,
 // 32 for 1); wave w takes the chain (RPW rows, slot) of row subgroup
@@ -1550,15 +1550,16 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
 // Down projection and combine with block terms spread over the waves
 // ===========================================================================
 //
-// MoeLayer::forward's combine (src/model/moe.rs:63-68) for S = 2, 4 or 8
-// routes, with each row's block terms spread over the work-group's waves
+// MoeLayer::forward's combine (src/model/moe.rs:63-68) for S = 1, 2, 4 or
+// 8 routes, with each row's block terms spread over the work-group's waves
 // (the k_gemv scheme) instead of one wave per chain.  A work-group owns RW
 // output rows (32: one tile; 16 or 8: part of one) of every slot.  The
 // slots go in pairs: lane l of a wave works for slot 2 q + l / 32 of the
 // wave's pair q (waves w of one pair: w / (NW / (S / 2)) = q); within the
 // half, lane RW p + r holds row r and block p of each group of 32 / RW
-// consecutive blocks.  So one wave-load reads, per slot, RW rows of 32 / RW
-// consecutive blocks: 512 contiguous bytes of the tile layout per 16-byte
+// consecutive blocks (one route: the whole wave works for it, lane RW p + r
+// holding block p of each group of 64 / RW).  So one wave-load reads, per
+// slot, RW rows of consecutive blocks: 512 contiguous bytes of the tile layout per 16-byte
 // chunk for RW = 32 (two 256-byte pieces for 16), where a wave per chain
 // reads eight 128-byte lines spread over 4 KB.  Blocks go to the waves in
 // chunks of CB per slot; the next chunk's loads are issued while a chunk's
@@ -1579,8 +1580,9 @@ static inline size_t down_tile_lds(int slots, int nb) { return (size_t)slots * n
 template <int DT, int S, int NW, int RW, int UPW>
 __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
-  constexpr int BPL = 32 / RW;        // blocks per slot and wave-load
-  constexpr int SP = S / 2;           // slot pairs
+  constexpr int LPS = S == 1 ? 64 : 32;  // lanes per slot
+  constexpr int BPL = LPS / RW;       // blocks per slot and wave-load
+  constexpr int SP = S == 1 ? 1 : S / 2;  // slot pairs (one route: one slot)
   constexpr int WPP = NW / SP;        // waves per slot pair
   constexpr int CB = WPP * UPW * BPL; // blocks per chunk
   constexpr int NCH = S * RW;         // fold chains
@@ -1588,7 +1590,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   // terms per group (the largest of 4, 3, 2, 1 that divides UPW); the next
   // chunk's loads follow each group
   constexpr int GS = UPW % 4 == 0 ? 4 : (UPW % 3 == 0 ? 3 : (UPW % 2 == 0 ? 2 : 1));
-  static_assert(S == 2 || S == 4 || S == 8, "slots go in pairs over whole waves");
+  static_assert(S == 1 || S == 2 || S == 4 || S == 8, "slots go in pairs over whole waves");
   static_assert(NW % SP == 0, "whole waves per slot pair");
   static_assert(RW == 32 || RW == 16 || RW == 8, "a half-wave covers 1, 2 or 4 blocks of RW rows");
   static_assert(UPW % GS == 0, "wave-loads go in whole groups");
@@ -1608,9 +1610,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
     a.hact += (size_t)blockIdx.y * S * a.hact_stride;
     a.out += (size_t)blockIdx.y * a.rows;
   }
-  const int sl = 2 * (wave / WPP) + (lane >> 5);  // this lane's slot
+  const int sl = S == 1 ? 0 : 2 * (wave / WPP) + (lane >> 5);  // this lane's slot
   const int wq = wave % WPP;                      // the wave's place among its pair's waves
-  const int p = (lane & 31) / RW;                 // block within a group of BPL
+  const int p = (lane % LPS) / RW;                // block within a group of BPL
   const int r = lane & (RW - 1);                  // row of the work-group's rows
   // the lane's expert first (loads return in order: waiting for it leaves
   // the activation loads behind it in flight)
@@ -1619,7 +1621,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   // every slot's activation pieces, clamped to the last (no branches, so
   // the waits stay counted)
   constexpr int NT = 64 * NW;
-  constexpr int MAXP = S == 2 ? 2 * DOWN_TILE_MAX_NB * 3 : S * 128 * 3;  // launcher: nb <= 128 for S > 2
+  constexpr int MAXP = S <= 2 ? S * DOWN_TILE_MAX_NB * 3 : S * 128 * 3;  // launcher: nb <= 128 for S > 2
   constexpr int APT = (MAXP + NT - 1) / NT;
   const int npieces = S * nb * 3;
   u32x4 av[APT];
@@ -2497,9 +2499,10 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   if (groups.x == 0) return hipSuccess;
   if (a.nb < 1 || a.slots < 1 || a.slots > DOWN_MAX_SLOTS || T > 65535) return hipErrorInvalidValue;
   // Block terms spread over sixteen waves per work-group (k_down_tile):
-  // for two routes on every shape measured (H 2048-4096, down rows of
-  // 32-448 blocks, 1-3 tokens; Mixtral-8x7B-shaped q4_0 layer: 15.2-16.9 ->
-  // 11.8 us at one token); for four and eight routes over rows of at most
+  // for one and two routes on every shape measured (H 1024-5120, down rows
+  // of 8-448 blocks, 1-3 tokens; Mixtral-8x7B-shaped q4_0 layer: 15.2-16.9
+  // -> 11.8 us at one token; top-1, H 5120, I 8192: 9.6 -> 7.2 us, H 4096,
+  // I 14336: 14.1 -> 8.3 us); for four and eight routes over rows of at most
   // 128 blocks when its 16-row groups give every CU one (Qwen3-235B-shaped
   // layer, 48-block rows: 8.0 -> 6.4-7.5 us at one token, 23.2 -> 17.3 at
   // four; H 2048 at one token has 128 such groups, and there the
@@ -2512,7 +2515,7 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   {
     const size_t prow = padded_rows((size_t)a.rows);
     const bool spread =
-        (a.slots == 2 && a.nb <= DOWN_TILE_MAX_NB) ||
+        ((a.slots == 1 || a.slots == 2) && a.nb <= DOWN_TILE_MAX_NB) ||
         ((a.slots == 4 || a.slots == 8) && a.nb <= 128 && (int)T < CACHED_LOAD_TOKENS &&
          prow / 16 * T >= 256);
     if (spread) {
@@ -2527,6 +2530,7 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
     if (dtype == Q8_0) return launch(k_down_tile<Q8_0, S_, 16, 32, 1>, grid, 1024, lds, st, a);         \
     if (dtype == Q4_0) return launch(k_down_tile<Q4_0, S_, 16, 32, 2>, grid, 1024, lds, st, a);         \
   } while (0)
+      if (a.slots == 1) HALE_DOWN_TILE(1);
       if (a.slots == 2) HALE_DOWN_TILE(2);
       if (a.slots == 4) HALE_DOWN_TILE(4);
       if (a.slots == 8) HALE_DOWN_TILE(8);

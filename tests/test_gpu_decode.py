@@ -342,7 +342,9 @@ def _few_tokens_check(L, moe, xs):
     (H.Q8_0, 1024, 16384, 4, 2, 2),    # top-2, down rows of 512 blocks (the most the spread-term kernel stages)
     (H.Q4_0, 512, 16416, 4, 2, 2),     # top-2, 513 blocks: the pipelined down kernel
     (H.Q8_0, 1024, 1024, 8, 3, 4),     # top-3 whole chain, q8_0
-    (H.Q4_0, 1024, 256, 8, 1, 5),      # top-1 (32-row chain groups)
+    (H.Q4_0, 1024, 256, 8, 1, 5),      # top-1: spread-term down, 16-row groups of 4 consecutive blocks per wave-load
+    (H.Q8_0, 2048, 4096, 4, 1, 1),     # top-1 q8_0, 128-block down rows, one token
+    (H.Q4_0, 5120, 2048, 4, 1, 3),     # top-1, H 5120 (160 tiles): 16-row groups, no XCD permutation
     (H.Q4_0, 256, 64, 300, 16, 3),     # more than 256 experts: eight-wave selection, 16 slots
     (H.Q4_0, 4160, 64, 16, 4, 2),      # spread-term down, top-4, 520 16-row groups (no XCD permutation)
     (H.Q8_0, 4096, 512, 16, 4, 3),     # spread-term down, top-4 q8_0, 16-row groups
