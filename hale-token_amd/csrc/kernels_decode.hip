@@ -1356,8 +1356,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_combine(DownArgs a) {
 }
 
 // The same projection and combine with whole fold chains per wave, used
-// for 3 routes when every slot's activation blocks fit in LDS (one and two
-// routes take k_down_tile below).  A
+// for 3 routes over rows of 129-512 blocks, or in calls of CACHED_LOAD_TOKENS
+// tokens or more, when every slot's activation blocks fit in LDS (the rest
+// of one to three routes take k_down_tile below).  A
 // work-group owns RG output rows for every slot (RG = 16 for 2 or 3 slots,
 // 32 for 1); wave w takes the chain (RPW rows, slot) of row subgroup
 // w / slots and slot w % slots.  Lane LPR r + j (LPR = 64 / RPW) holds row
@@ -1550,16 +1551,18 @@ __global__ __launch_bounds__(512) void k_down_chain(DownArgs a) {
 // Down projection and combine with block terms spread over the waves
 // ===========================================================================
 //
-// MoeLayer::forward's combine (src/model/moe.rs:63-68) for S = 1, 2, 4 or
-// 8 routes, with each row's block terms spread over the work-group's waves
+// MoeLayer::forward's combine (src/model/moe.rs:63-68) for S = 1 to 8
+// routes, with each row's block terms spread over the work-group's waves
 // (the k_gemv scheme) instead of one wave per chain.  A work-group owns RW
 // output rows (32: one tile; 16 or 8: part of one) of every slot.  The
 // slots go in pairs: lane l of a wave works for slot 2 q + l / 32 of the
 // wave's pair q (waves w of one pair: w / (NW / (S / 2)) = q); within the
 // half, lane RW p + r holds row r and block p of each group of 32 / RW
 // consecutive blocks (one route: the whole wave works for it, lane RW p + r
-// holding block p of each group of 64 / RW).  So one wave-load reads, per
-// slot, RW rows of consecutive blocks: 512 contiguous bytes of the tile layout per 16-byte
+// holding block p of each group of 64 / RW; for odd S the last pair's second
+// half repeats the last slot's loads, the same lines in the same wave-load,
+// and its chains are never combined).  So one wave-load reads, per slot, RW
+// rows of consecutive blocks: 512 contiguous bytes of the tile layout per 16-byte
 // chunk for RW = 32 (two 256-byte pieces for 16), where a wave per chain
 // reads eight 128-byte lines spread over 4 KB.  Blocks go to the waves in
 // chunks of CB per slot; the next chunk's loads are issued while a chunk's
@@ -1582,15 +1585,15 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
   constexpr int LPS = S == 1 ? 64 : 32;  // lanes per slot
   constexpr int BPL = LPS / RW;       // blocks per slot and wave-load
-  constexpr int SP = S == 1 ? 1 : S / 2;  // slot pairs (one route: one slot)
+  constexpr int SP = S == 1 ? 1 : (S + 1) / 2;  // slot pairs (one route: one slot; odd S: a ghost)
   constexpr int WPP = NW / SP;        // waves per slot pair
   constexpr int CB = WPP * UPW * BPL; // blocks per chunk
-  constexpr int NCH = S * RW;         // fold chains
+  constexpr int NCH = (S == 1 ? 1 : 2 * SP) * RW;  // fold chains (a ghost slot's are never combined)
   constexpr int FW = (NCH + 63) / 64; // folding waves
   // terms per group (the largest of 4, 3, 2, 1 that divides UPW); the next
   // chunk's loads follow each group
   constexpr int GS = UPW % 4 == 0 ? 4 : (UPW % 3 == 0 ? 3 : (UPW % 2 == 0 ? 2 : 1));
-  static_assert(S == 1 || S == 2 || S == 4 || S == 8, "slots go in pairs over whole waves");
+  static_assert(S >= 1 && S <= 8, "at most eight routes");
   static_assert(NW % SP == 0, "whole waves per slot pair");
   static_assert(RW == 32 || RW == 16 || RW == 8, "a half-wave covers 1, 2 or 4 blocks of RW rows");
   static_assert(UPW % GS == 0, "wave-loads go in whole groups");
@@ -1610,13 +1613,15 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
     a.hact += (size_t)blockIdx.y * S * a.hact_stride;
     a.out += (size_t)blockIdx.y * a.rows;
   }
-  const int sl = S == 1 ? 0 : 2 * (wave / WPP) + (lane >> 5);  // this lane's slot
+  const int sl = S == 1 ? 0 : 2 * (wave / WPP) + (lane >> 5);  // this lane's slot (S: the ghost)
+  const int slc = min(sl, S - 1);  // the slot it loads for: a ghost repeats the last one's
+                                   // addresses (the same wave-load, the same lines)
   const int wq = wave % WPP;                      // the wave's place among its pair's waves
   const int p = (lane % LPS) / RW;                // block within a group of BPL
   const int r = lane & (RW - 1);                  // row of the work-group's rows
   // the lane's expert first (loads return in order: waiting for it leaves
   // the activation loads behind it in flight)
-  const int ev = a.route_idx[sl];
+  const int ev = a.route_idx[slc];
   __builtin_amdgcn_sched_barrier(0);
   // every slot's activation pieces, clamped to the last (no branches, so
   // the waits stay counted)
@@ -1672,7 +1677,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   }
   __syncthreads();  // s_act
 
-  const ActBlock* act = s_act + (size_t)sl * nb;
+  const ActBlock* act = s_act + (size_t)slc * nb;
   const int chain = wave * 64 + lane;  // folding waves: chain RW s + r
   float total = 0.0f;
   const int nchunks = (nb + CB - 1) / CB;
@@ -2502,12 +2507,16 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
   // for one and two routes on every shape measured (H 1024-5120, down rows
   // of 8-448 blocks, 1-3 tokens; Mixtral-8x7B-shaped q4_0 layer: 15.2-16.9
   // -> 11.8 us at one token; top-1, H 5120, I 8192: 9.6 -> 7.2 us, H 4096,
-  // I 14336: 14.1 -> 8.3 us); for four and eight routes over rows of at most
-  // 128 blocks when its 16-row groups give every CU one (Qwen3-235B-shaped
-  // layer, 48-block rows: 8.0 -> 6.4-7.5 us at one token, 23.2 -> 17.3 at
-  // four; H 2048 at one token has 128 such groups, and there the
-  // wave-per-route kernel's 8-row groups are as fast or faster), and only
-  // for calls below CACHED_LOAD_TOKENS (its weight loads are non-temporal).
+  // I 14336: 14.1 -> 8.3 us); for three routes over rows of at most 128
+  // blocks (step per layer, H 2048 / I 1024: 14.1 -> 13.1 us at one token,
+  // 21.6 -> 17.9 at four; H 4096 / I 2048: 23.1 -> 21.1-21.7, 51.7 ->
+  // 40.6-42.0); for four to eight over rows of at most 128 blocks when its
+  // 16-row groups give every CU one (Qwen3-235B-shaped layer, 48-block
+  // rows: down 8.0 -> 6.4-7.5 us at one token, 23.2 -> 17.3 at four; top-7,
+  // H 4096: step 31.4 -> 29.6 us, 69.8 -> 65.1-65.7 at four; H 2048 at one
+  // token has 128 such groups, and there the wave-per-route kernel's 8-row
+  // groups are as fast or faster); from three routes only for calls below
+  // CACHED_LOAD_TOKENS (its weight loads are non-temporal).
   // Work-groups of 16 rows (half a tile) or 32: the size whose busiest CU
   // gets fewer rows, ceil(groups / 256 CUs) x rows per group, 32 on a tie
   // (one token of H 4096: 256 groups of 16 against 128 of 32 that would
@@ -2516,30 +2525,38 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
     const size_t prow = padded_rows((size_t)a.rows);
     const bool spread =
         ((a.slots == 1 || a.slots == 2) && a.nb <= DOWN_TILE_MAX_NB) ||
-        ((a.slots == 4 || a.slots == 8) && a.nb <= 128 && (int)T < CACHED_LOAD_TOKENS &&
-         prow / 16 * T >= 256);
+        (a.slots >= 3 && a.slots <= 8 && a.nb <= 128 && (int)T < CACHED_LOAD_TOKENS &&
+         (a.slots == 3 || prow / 16 * T >= 256));
     if (spread) {
       const uint32_t lds = (uint32_t)down_tile_lds(a.slots, a.nb);
       auto busiest = [&](size_t rw) { return (prow / rw * T + 255) / 256 * rw; };
       const bool half = busiest(16) < busiest(32);
       const dim3 grid((unsigned)(prow / (half ? 16 : 32)), T);
-#define HALE_DOWN_TILE(S_)                                                                          \
+#define HALE_DOWN_TILE(S_, NW_)                                                                     \
   do {                                                                                              \
-    if (half && dtype == Q8_0) return launch(k_down_tile<Q8_0, S_, 16, 16, 1>, grid, 1024, lds, st, a); \
-    if (half && dtype == Q4_0) return launch(k_down_tile<Q4_0, S_, 16, 16, 2>, grid, 1024, lds, st, a); \
-    if (dtype == Q8_0) return launch(k_down_tile<Q8_0, S_, 16, 32, 1>, grid, 1024, lds, st, a);         \
-    if (dtype == Q4_0) return launch(k_down_tile<Q4_0, S_, 16, 32, 2>, grid, 1024, lds, st, a);         \
+    if (half && dtype == Q8_0) return launch(k_down_tile<Q8_0, S_, NW_, 16, 1>, grid, 64 * NW_, lds, st, a); \
+    if (half && dtype == Q4_0) return launch(k_down_tile<Q4_0, S_, NW_, 16, 2>, grid, 64 * NW_, lds, st, a); \
+    if (dtype == Q8_0) return launch(k_down_tile<Q8_0, S_, NW_, 32, 1>, grid, 64 * NW_, lds, st, a);         \
+    if (dtype == Q4_0) return launch(k_down_tile<Q4_0, S_, NW_, 32, 2>, grid, 64 * NW_, lds, st, a);         \
   } while (0)
-      if (a.slots == 1) HALE_DOWN_TILE(1);
-      if (a.slots == 2) HALE_DOWN_TILE(2);
-      if (a.slots == 4) HALE_DOWN_TILE(4);
-      if (a.slots == 8) HALE_DOWN_TILE(8);
+      // sixteen waves, twelve for three slot pairs (five or six routes)
+      switch (a.slots) {
+        case 1: HALE_DOWN_TILE(1, 16); break;
+        case 2: HALE_DOWN_TILE(2, 16); break;
+        case 3: HALE_DOWN_TILE(3, 16); break;
+        case 4: HALE_DOWN_TILE(4, 16); break;
+        case 5: HALE_DOWN_TILE(5, 12); break;
+        case 6: HALE_DOWN_TILE(6, 12); break;
+        case 7: HALE_DOWN_TILE(7, 16); break;
+        case 8: HALE_DOWN_TILE(8, 16); break;
+      }
 #undef HALE_DOWN_TILE
       return hipErrorInvalidValue;
     }
   }
   // A wave per (slot, 8 rows) pays off when few routes leave many rows per
-  // work-group (top-1 and top-3); top-4 and wider use the block-group pipeline.
+  // work-group (three routes that k_down_tile does not take); top-4 and
+  // wider use the block-group pipeline.
   if (a.slots <= 3 && a.nb <= DOWN_CHAIN_MAX_NB && a.slots * a.nb <= DOWN_ACT_MAX &&
       down_chain_waves(a.slots, 8) * a.nb <= DOWN_SCL_MAX) {
     const int rg = down_chain_rows(a.slots);

@@ -341,7 +341,11 @@ def _few_tokens_check(L, moe, xs):
     (H.Q4_0, 2080, 2080, 6, 2, 5),     # top-2: spread-term down, 65 blocks, 132 x 5 16-row groups (no XCD permutation)
     (H.Q8_0, 1024, 16384, 4, 2, 2),    # top-2, down rows of 512 blocks (the most the spread-term kernel stages)
     (H.Q4_0, 512, 16416, 4, 2, 2),     # top-2, 513 blocks: the pipelined down kernel
-    (H.Q8_0, 1024, 1024, 8, 3, 4),     # top-3 whole chain, q8_0
+    (H.Q8_0, 1024, 1024, 8, 3, 4),     # top-3 q8_0: spread-term down (a ghost half-wave)
+    (H.Q4_0, 1024, 8192, 8, 3, 2),     # top-3, 256-block down rows: the whole-chain kernel
+    (H.Q4_0, 4096, 1408, 64, 6, 2),    # top-6: spread-term down, three slot pairs (twelve waves)
+    (H.Q8_0, 4096, 1024, 16, 5, 1),    # top-5 q8_0: twelve waves, a ghost half-wave
+    (H.Q4_0, 4096, 1536, 16, 7, 3),    # top-7: a ghost half-wave, 16-row groups
     (H.Q4_0, 1024, 256, 8, 1, 5),      # top-1: spread-term down, 16-row groups of 4 consecutive blocks per wave-load
     (H.Q8_0, 2048, 4096, 4, 1, 1),     # top-1 q8_0, 128-block down rows, one token
     (H.Q4_0, 5120, 2048, 4, 1, 3),     # top-1, H 5120 (160 tiles): 16-row groups, no XCD permutation
