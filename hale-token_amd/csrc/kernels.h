@@ -113,6 +113,10 @@ struct DownArgs {
   // tokens > 1: token t's routes at route_idx / route_w + t * slots, its h
   // blocks at hact + t * slots * hact_stride, its output at out + t * rows
   int tokens;
+  // WeightMatrix::matvec through the spread-term kernel (one matrix, no
+  // routes or combine): x (f32, 16-byte aligned) quantized by the kernel,
+  // or hact when null
+  const float* x;
 };
 
 hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st);
@@ -137,6 +141,10 @@ struct MatvecArgs {
   const uint16_t* scales2;
 };
 hipError_t launch_matvec(int dtype, const MatvecArgs& a, hipStream_t st);
+// Whether launch_matvec takes x (f32, 16-byte aligned) for rows of nb
+// blocks, quantizing it in the kernel; otherwise the caller quantizes x
+// into act first.
+bool matvec_takes_x(int nb, size_t rows);
 // both matrices of a in one launch, x quantized in the kernel:
 // out[r] = silu(dot(codes row r, x)) * dot(codes2 row r, x)
 hipError_t launch_matvec_pair(int dtype, const MatvecArgs& a, hipStream_t st);

@@ -1580,7 +1580,11 @@ constexpr int DOWN_TILE_MAX_NB = 512;  // blocks per row: two slots' activations
 
 static inline size_t down_tile_lds(int slots, int nb) { return (size_t)slots * nb * sizeof(ActBlock); }
 
-template <int DT, int S, int NW, int RW, int UPW>
+// PLAIN: WeightMatrix::matvec (src/tensor/matrix.rs:115-143) of one matrix
+// (S = 1, no routes): out[row] is the row's sum; x, when given, is
+// quantized into the staging by the work-group (the expressions of
+// k_act_quant, so the same q8 blocks).
+template <int DT, int S, int NW, int RW, int UPW, bool PLAIN = false>
 __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   constexpr int CH = Layout<DT>::CH;
   constexpr int LPS = S == 1 ? 64 : 32;  // lanes per slot
@@ -1598,6 +1602,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   static_assert(RW == 32 || RW == 16 || RW == 8, "a half-wave covers 1, 2 or 4 blocks of RW rows");
   static_assert(UPW % GS == 0, "wave-loads go in whole groups");
   static_assert(FW <= NW, "enough waves to fold");
+  static_assert(!PLAIN || S == 1, "a plain matvec is one matrix");
   __shared__ float terms[2][CB][NCH];
   __shared__ float s_tot[NCH];
   // every slot's activation blocks, sized at launch (down_tile_lds): slot s at [s * nb]
@@ -1621,7 +1626,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   const int r = lane & (RW - 1);                  // row of the work-group's rows
   // the lane's expert first (loads return in order: waiting for it leaves
   // the activation loads behind it in flight)
-  const int ev = a.route_idx[slc];
+  const int ev = PLAIN ? 0 : a.route_idx[slc];
   __builtin_amdgcn_sched_barrier(0);
   // every slot's activation pieces, clamped to the last (no branches, so
   // the waits stay counted)
@@ -1630,11 +1635,24 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
   constexpr int APT = (MAXP + NT - 1) / NT;
   const int npieces = S * nb * 3;
   u32x4 av[APT];
+  // PLAIN with x: 8 lanes per block, each its 4 values (the block of lane
+  // group q = thread / 8, pass m: q + (NT / 8) m), clamped to the last
+  constexpr int XPT = PLAIN ? (DOWN_TILE_MAX_NB * 8 + NT - 1) / NT : 1;
+  f32x4 xv[XPT];
+  const bool from_x = PLAIN && a.x != nullptr;  // uniform
+  if (from_x) {
 #pragma unroll
-  for (int m = 0; m < APT; m++) {
-    const int i = min((int)threadIdx.x + NT * m, npieces - 1);
-    const int s2 = i / (nb * 3), rem = i - s2 * nb * 3;
-    av[m] = ((const u32x4*)(a.hact + (size_t)s2 * a.hact_stride))[rem];
+    for (int m = 0; m < XPT; m++) {
+      const int b = min((int)(threadIdx.x >> 3) + (NT / 8) * m, nb - 1);
+      xv[m] = *(const f32x4*)(a.x + (size_t)b * QK + 4 * (threadIdx.x & 7));
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < APT; m++) {
+      const int i = min((int)threadIdx.x + NT * m, npieces - 1);
+      const int s2 = i / (nb * 3), rem = i - s2 * nb * 3;
+      av[m] = ((const u32x4*)(a.hact + (size_t)s2 * a.hact_stride))[rem];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   // Work-group g runs on XCD g % 8; for RW < 32 the row groups of one tile
@@ -1669,11 +1687,19 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
     load_block(0, s);
     __builtin_amdgcn_sched_barrier(0);
   }
-  const float wv = a.route_w[min(lane, S - 1)];
+  const float wv = PLAIN ? 0.0f : a.route_w[min(lane, S - 1)];
+  if (from_x) {
 #pragma unroll
-  for (int m = 0; m < APT; m++) {
-    const int i = (int)threadIdx.x + NT * m;
-    if (i < npieces) ((u32x4*)s_act)[i] = av[m];
+    for (int m = 0; m < XPT; m++) {
+      const int b = (int)(threadIdx.x >> 3) + (NT / 8) * m;
+      if (b < nb) quant_block8(xv[m], threadIdx.x & 7, s_act + b);  // uniform per 8 lanes
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < APT; m++) {
+      const int i = (int)threadIdx.x + NT * m;
+      if (i < npieces) ((u32x4*)s_act)[i] = av[m];
+    }
   }
   __syncthreads();  // s_act
 
@@ -1714,6 +1740,13 @@ __global__ __launch_bounds__(64 * NW) void k_down_tile(DownArgs a) {
 #pragma unroll
   for (int s2 = 0; s2 < S; s2++) wts[s2] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), s2));
   __syncthreads();
+  if (PLAIN) {
+    if (wave == 0 && lane < RW) {
+      const size_t row = row0 + lane;
+      if (row < (size_t)a.rows) a.out[row] = total;
+    }
+    return;
+  }
   if (wave == 0 && lane < RW) {
     float o = 0.0f;  // out.fill(0.0), then out = out + w * y in route order
 #pragma unroll
@@ -2606,10 +2639,45 @@ hipError_t launch_down_combine(int dtype, const DownArgs& a, hipStream_t st) {
 // 1024 SIMDs; work-groups of one tile (NW = 32 / RPW waves) when that still
 // gives at least 256 work-groups, else half or a quarter of a tile, so
 // small matrices spread over more CUs.
+static bool matvec_spread(int nb, size_t rows) {
+  return nb >= 32 && nb <= DOWN_TILE_MAX_NB && padded_rows(rows) <= 65536;
+}
+
+bool matvec_takes_x(int nb, size_t rows) { return nb <= MATVEC_XQ_MAX_NB || matvec_spread(nb, rows); }
+
 hipError_t launch_matvec(int dtype, const MatvecArgs& a, hipStream_t st) {
   if (a.nb < 1 || a.rows < 1) return hipErrorInvalidValue;
   if (dtype != Q8_0 && dtype != Q4_0) return hipErrorInvalidValue;
   const bool xq = a.x != nullptr;
+  // Rows of 32 to 512 blocks, at most 65,536 of them: the block terms
+  // spread over a work-group's waves (k_down_tile, plain), 512-byte
+  // wave-loads where the chain kernel's read 64- or 128-byte pieces (4096
+  // x 4096, cold: q8_0 7.40 -> 6.20 us, q4_0 5.72 -> 5.25; 14336 x 4096
+  // q4_0 10.7 -> 8.7; 4096 x 14336 13.7 -> 10.3 with x quantized in the
+  // kernel (rows of up to 512 blocks), no quantization launch before it;
+  // 768 x 2048 q8_0 3.8 -> 3.4).  Rows of 24 blocks (2048 x 768: 3.06 against 3.23-3.48 us) and
+  // 151,936 rows (51.9 against 52.5-53.8 us) stay on the chain kernel.
+  if (matvec_spread(a.nb, (size_t)a.rows) && (xq ? ((uintptr_t)a.x & 15) == 0 : a.act != nullptr)) {
+    DownArgs d{};
+    d.codes = a.codes;
+    d.scales = a.scales;
+    d.nb = a.nb;
+    d.rows = a.rows;
+    d.hact = a.act;
+    d.slots = 1;
+    d.out = a.out;
+    d.tokens = 1;
+    d.x = a.x;
+    const size_t prow = padded_rows((size_t)a.rows);
+    auto busiest = [&](size_t rw) { return (prow / rw + 255) / 256 * rw; };
+    const bool half = busiest(16) < busiest(32);
+    const dim3 grid((unsigned)(prow / (half ? 16 : 32)));
+    const uint32_t lds = (uint32_t)down_tile_lds(1, a.nb);
+    if (half && dtype == Q8_0) return launch(k_down_tile<Q8_0, 1, 16, 16, 1, true>, grid, 1024, lds, st, d);
+    if (half) return launch(k_down_tile<Q4_0, 1, 16, 16, 2, true>, grid, 1024, lds, st, d);
+    if (dtype == Q8_0) return launch(k_down_tile<Q8_0, 1, 16, 32, 1, true>, grid, 1024, lds, st, d);
+    return launch(k_down_tile<Q4_0, 1, 16, 32, 2, true>, grid, 1024, lds, st, d);
+  }
   if (xq && (((uintptr_t)a.x & 15) || a.nb > MATVEC_XQ_MAX_NB)) return hipErrorNotSupported;
   if (!xq && (!a.act || a.nb > MATVEC_MAX_NB)) return hipErrorNotSupported;
   const size_t prow = padded_rows((size_t)a.rows);

@@ -812,7 +812,7 @@ static int matvec_enqueue(hale_ctx* c, const hale_matrix* m, const float* dx, fl
   }
   size_t nb = m->cols / HALE_QK;
   MatvecArgs mv{m->codes, m->scales, (int)nb, (int)m->rows, nullptr, nullptr, dout};
-  if (((uintptr_t)dx & 15) == 0 && nb <= (size_t)MATVEC_XQ_MAX_NB) {  // one launch
+  if (((uintptr_t)dx & 15) == 0 && matvec_takes_x((int)nb, m->rows)) {  // one launch
     mv.x = dx;
     LAUNCH(c, K_GEMV, launch_matvec(m->dtype, mv, c->stream));
     return HALE_OK;
