@@ -2485,21 +2485,26 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   // per CU: 256 work-groups of 16 waves, 512 of 8), so that no second round
   // runs on a partly filled GPU.  With routing, one more column of
   // work-groups holds the selector.
-  // q4_0 gate/up rows of more than one 64-block chunk with 257 to 512
+  // q4_0 gate/up rows of more than one 64-block chunk with 257 to 2048
   // tile-slots (eight-wave work-groups of one tile would put two on some
-  // CUs and one on the rest): sixteen waves and two tiles of one slot per
-  // work-group, at most one per CU, each running one selection and four
-  // chunks of loads (Qwen3-235B-shaped layer at one token, 384 tile-slots:
-  // 14.1-14.4 -> 13.2-13.8 us; at two tokens, 768, the eight-wave form
-  // stays faster)
+  // CUs and one on the rest, or run in two rounds): sixteen waves and two
+  // tiles of one slot per work-group when that gives at most 256 of them
+  // (one per CU), else four; each work-group runs one selection and four or
+  // eight chunks of loads.  Per step, graph replay: Qwen3-235B-shaped layer
+  // at one token (384 tile-slots, two tiles) 27.8 -> 27.4 us; at two tokens
+  // (768, four tiles) 45.7 -> 42.4-43.5; Mixtral-shaped layer at one token
+  // (896, four tiles) 43.9 -> 42.4-42.7, at two (1792) 75.8 -> 73.5.
   const long tslots = (long)groups * slots * T;
-  const bool pair16 = dtype == Q4_0 && epi == EPI_GATE_UP && a.nb > 64 && tslots > 256 &&
-                      tslots <= 512 && !(a.logits && a.E > 256);
+  const int ipw16 = dtype == Q4_0 && epi == EPI_GATE_UP && a.nb > 64 && tslots > 256 &&
+                            tslots <= 2048 && !(a.logits && a.E > 256)
+                        ? ((long)((groups + 1) / 2) * slots * T <= 256 ? 2 : 4)
+                        : 0;
+  const bool pair16 = ipw16 > 0;
   auto grid_of = [&](int nw) {
     GemvArgs b = a;
     b.tiles = groups;
     b.ipw = epi == EPI_GATE_UP && (long)groups * slots * T > 256L * (16 / nw) ? 2 : 1;
-    if (pair16) b.ipw = 2;
+    if (pair16) b.ipw = ipw16;
     return std::make_pair(dim3((groups + b.ipw - 1) / b.ipw + (a.logits ? 1 : 0), slots * T), b);
   };
   const bool cached = T >= CACHED_LOAD_TOKENS;

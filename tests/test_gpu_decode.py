@@ -634,13 +634,15 @@ def test_moe_decode_down_whole_chain(ctx, dtype, hidden, inter, E, k):
     (H.Q8_0, 256, 2080, 8, 8),     # 65 tiles x 8 slots = 520 > 512 resident (8 waves): 2 per group, odd
     (H.Q4_0, 2080, 1056, 16, 16),  # 33 x 16 = 528 > 512 (8 waves, two chunks per row): odd
     (H.Q4_0, 1024, 8256, 2, 2),    # 258 x 2 = 516 > 256 resident (16 waves, one chunk)
-    (H.Q4_0, 4096, 1056, 16, 8),   # 33 x 8 = 264 tile-slots of two chunks: 16 waves, odd
+    (H.Q4_0, 4096, 1056, 16, 8),   # 33 x 8 = 264 tile-slots of two chunks: 16 waves, two tiles, odd
+    (H.Q4_0, 4096, 4128, 8, 4),    # 129 x 4 = 516: 16 waves, four tiles, the last group one
 ])
 def test_moe_decode_gate_up_two_tiles_per_group(ctx, dtype, hidden, inter, E, k):
     """Gate/up grids larger than the GPU holds at once give each work-group
     two tiles (the second one's loads issued under the first one's fold),
-    and so do q4_0 rows of two chunks with 257 to 512 tile-slots (sixteen
-    waves): odd tile counts leave the last group one tile."""
+    and so do q4_0 rows of two chunks with 257 to 2048 tile-slots (sixteen
+    waves, two or four tiles): odd tile counts leave the last group one
+    tile."""
     L = O.OracleMoe.synthetic(dtype, hidden, inter, E, k, normalize_topk=True,
                               seed=hidden + inter + k + 11)
     moe = make_layer(ctx, L)
