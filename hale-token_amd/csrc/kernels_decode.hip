@@ -2485,26 +2485,30 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   // per CU: 256 work-groups of 16 waves, 512 of 8), so that no second round
   // runs on a partly filled GPU.  With routing, one more column of
   // work-groups holds the selector.
-  // q4_0 gate/up rows of more than one 64-block chunk with 257 to 2048
-  // tile-slots (eight-wave work-groups of one tile would put two on some
-  // CUs and one on the rest, or run in two rounds): sixteen waves and two
-  // tiles of one slot per work-group when that gives at most 256 of them
-  // (one per CU), else four; each work-group runs one selection and four or
-  // eight chunks of loads.  Per step, graph replay: Qwen3-235B-shaped layer
-  // at one token (384 tile-slots, two tiles) 27.8 -> 27.4 us; at two tokens
-  // (768, four tiles) 45.7 -> 42.4-43.5; Mixtral-shaped layer at one token
-  // (896, four tiles) 43.9 -> 42.4-42.7, at two (1792) 75.8 -> 73.5.
+  // q4_0 gate/up in sixteen-wave work-groups, for rows of one 64-block
+  // chunk and, when it fits, for longer rows with more than 256 tile-slots
+  // (eight-wave work-groups of one tile would put two on some CUs and one on
+  // the rest, or run in two rounds): each work-group takes the fewest tiles
+  // of one slot, 1, 2, 4 or 8, that keep the grid at one work-group per CU
+  // (256), runs one selection and folds its tiles' chunks in sequence.  Per
+  // step, graph replay: Qwen3-30B-shaped layer at 4 / 7 tokens (four /
+  // eight tiles) 31.0-31.5 / 41.9-42.4 -> 28.1 / 38.4 us; Qwen3-235B-shaped
+  // at 1 / 2 / 4 tokens (two / four / eight) 27.8 / 45.7 / 73.1 -> 27.4 /
+  // 42.4-43.5 / 67.7; Mixtral-shaped at 1 / 2 (four / eight) 43.9 / 75.8 ->
+  // 42.4-42.7 / 71.8-72.1.  Longer rows whose tiles do not fit at eight per
+  // work-group keep the eight-wave form.
   const long tslots = (long)groups * slots * T;
-  const int ipw16 = dtype == Q4_0 && epi == EPI_GATE_UP && a.nb > 64 && tslots > 256 &&
-                            tslots <= 2048 && !(a.logits && a.E > 256)
-                        ? ((long)((groups + 1) / 2) * slots * T <= 256 ? 2 : 4)
-                        : 0;
-  const bool pair16 = ipw16 > 0;
+  int ipw16 = 0;  // tiles per sixteen-wave work-group
+  for (int p = 1; p <= 8 && !ipw16; p *= 2)
+    if ((long)((groups + p - 1) / p) * slots * T <= 256) ipw16 = p;
+  const bool q4gu = dtype == Q4_0 && epi == EPI_GATE_UP && !(a.logits && a.E > 256);
+  const bool pair16 = q4gu && a.nb > 64 && tslots > 256 && ipw16 > 0;
+  if (q4gu && a.nb <= 64 && !ipw16) ipw16 = 8;
   auto grid_of = [&](int nw) {
     GemvArgs b = a;
     b.tiles = groups;
     b.ipw = epi == EPI_GATE_UP && (long)groups * slots * T > 256L * (16 / nw) ? 2 : 1;
-    if (pair16) b.ipw = ipw16;
+    if (nw == 16 && q4gu) b.ipw = ipw16;
     return std::make_pair(dim3((groups + b.ipw - 1) / b.ipw + (a.logits ? 1 : 0), slots * T), b);
   };
   const bool cached = T >= CACHED_LOAD_TOKENS;
