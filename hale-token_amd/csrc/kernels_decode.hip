@@ -2468,6 +2468,24 @@ hipError_t launch_route_select(const float* logits, int E, int k, int normalize,
 // tokens (and on Mixtral's top-2 of 8).
 constexpr int CACHED_LOAD_TOKENS = 12;
 
+// Work-groups on the busiest XCD of a grid of width gx and height rows whose
+// columns x < cols hold the tiles (a column past them, the selector's, ends
+// early): work-group x + gx y runs on XCD (x + gx y) % 8.
+static long busiest_xcd(long cols, long gx, long rows) {
+  long cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int j = 0; j < 8; j++) {  // the rows y = j (mod 8)
+    const long ny = rows > j ? (rows - j + 7) / 8 : 0;
+    const int off = (int)((gx % 8) * j % 8);
+    for (int c = 0; c < 8; c++) {  // columns x = c - off (mod 8)
+      const long r0 = (c - off + 8) % 8;
+      cnt[c] += (cols > r0 ? (cols - r0 + 7) / 8 : 0) * ny;
+    }
+  }
+  long m = 0;
+  for (int c = 0; c < 8; c++) m = cnt[c] > m ? cnt[c] : m;
+  return m;
+}
+
 hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int slots,
                        hipStream_t st) {
   if (groups == 0 || slots == 0) return hipSuccess;
@@ -2497,13 +2515,32 @@ hipError_t launch_gemv(int dtype, int epi, const GemvArgs& a, int groups, int sl
   // 42.4-43.5 / 67.7; Mixtral-shaped at 1 / 2 (four / eight) 43.9 / 75.8 ->
   // 42.4-42.7 / 71.8-72.1.  Longer rows whose tiles do not fit at eight per
   // work-group keep the eight-wave form.
+  // "Fits" counts per XCD: work-group x + X y runs on XCD (x + X y) % 8, so
+  // an even grid width X puts whole columns on a few XCDs (Qwen3-30B-shaped
+  // layer at 9 tokens, eight tiles: X = 3 + the selector, 36 work-groups on
+  // each of six XCDs' 32 CUs and the selector column alone on the other
+  // two).  Rows of one chunk whose tiles fit at no width take the fewest
+  // tiles per work-group by rounds x (tiles + one tile's worth for the
+  // work-group's selection and staging): at 9 / 10 tokens of that layer four
+  // tiles, 57.3 / 58.5 -> 48 / 50 us per step.
   const long tslots = (long)groups * slots * T;
+  const bool sel_col = a.logits != nullptr;
+  auto xcd_rounds = [&](int p) {  // rounds of the busiest XCD, 32 CUs each
+    const long cols = (groups + p - 1) / p;
+    return (busiest_xcd(cols, cols + (sel_col ? 1 : 0), (long)slots * T) + 31) / 32;
+  };
   int ipw16 = 0;  // tiles per sixteen-wave work-group
   for (int p = 1; p <= 8 && !ipw16; p *= 2)
-    if ((long)((groups + p - 1) / p) * slots * T <= 256) ipw16 = p;
+    if (xcd_rounds(p) <= 1) ipw16 = p;
   const bool q4gu = dtype == Q4_0 && epi == EPI_GATE_UP && !(a.logits && a.E > 256);
   const bool pair16 = q4gu && a.nb > 64 && tslots > 256 && ipw16 > 0;
-  if (q4gu && a.nb <= 64 && !ipw16) ipw16 = 8;
+  if (q4gu && a.nb <= 64 && !ipw16) {
+    long best = 0;
+    for (int p = 1; p <= 8; p *= 2) {
+      const long cost = xcd_rounds(p) * (p + 1);
+      if (!ipw16 || cost < best) ipw16 = p, best = cost;
+    }
+  }
   auto grid_of = [&](int nw) {
     GemvArgs b = a;
     b.tiles = groups;

@@ -1141,11 +1141,12 @@ static int moe_ws(hale_moe* m, size_t need, void** out) {
 // against 75.7 at 10, 85.1 against 83.1 at 12), a Qwen3-235B-shaped q8_0
 // layer between 7 and 8 (175.6 against 177.4 us at 7, 196.3 against 188.8
 // at 8); Mixtral (top-2 of 8)
-// between 4 and 6 (136 against 166 us at 4, 198 against 184 at 6).
+// between 6 and 7 (173.1 against 180.5 us at 6, 208.8 against 186.9 at 7,
+// with the spread-term down projection and four-tile gate/up work-groups).
 static size_t default_grouped_min(int dtype, size_t E, size_t H, size_t I, size_t k) {
   (void)E;
   (void)I;
-  if (k < 4) return 6;
+  if (k < 4) return 7;
   if (dtype == HALE_Q4_0) return H <= 2048 ? 11 : 9;
   return H <= 2048 ? 12 : 8;
 }

@@ -426,7 +426,7 @@ def test_moe_decode_few_tokens_qwen30b(ctx, qwen30b_q4, T):
     (H.Q4_0, 4096, 1536, 128, 8, 9, 68),    # Qwen3-235B-A22B q4_0: 4.25 E / k
     (H.Q8_0, 2048, 768, 128, 8, 12, 80),    # Qwen3-30B-A3B q8_0: 5 E / k
     (H.Q8_0, 4096, 1536, 128, 8, 8, 60),    # Qwen3-235B-A22B q8_0: 3.75 E / k
-    (H.Q4_0, 4096, 14336, 8, 2, 6, 13),     # Mixtral-8x7B: 3.25 E / k (448-block down rows)
+    (H.Q4_0, 4096, 14336, 8, 2, 7, 13),     # Mixtral-8x7B: 3.25 E / k (448-block down rows)
 ])
 def test_default_thresholds_by_layer_type(ctx, dtype, hidden, inter, E, k, gmin, bmax):
     """A new layer's grouped and row-chain thresholds follow its type and

@@ -146,12 +146,12 @@ def test_band_qwen30b_q4(ctx, T, bmax):
 
 def test_band_mixtral_8_tokens(ctx):
     """Mixtral-8x7B's layer shape (8 q4_0 experts, H 4096, I 14336, top-2)
-    at 8 tokens, its default path (grouped from 6 tokens, row chains up to
+    at 8 tokens, its default path (grouped from 7 tokens, row chains up to
     13; 448-block down rows): every token against the oracle."""
     E, Hd, I, k, T = 8, 4096, 14336, 2, 8
     L = O.OracleMoe.synthetic(H.Q4_0, Hd, I, E, k, normalize_topk=True, seed=88, with_router=True)
     moe = make_layer(ctx, L)
-    assert moe.grouped_min_tokens == 6 and moe.band_max_tokens == 13
+    assert moe.grouped_min_tokens == 7 and moe.band_max_tokens == 13
     check(moe, L, O.normal(89, T * Hd).reshape(T, Hd))
     moe.close()
 
