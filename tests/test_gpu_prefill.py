@@ -1,6 +1,6 @@
 """GPU parity of the expert-grouped multi-token path (ntok at or above the
 layer's grouped threshold: for top-4 and wider 11 tokens (q4_0, hidden
-size up to 2048), 9 (q4_0, wider) or 12 (q8_0), 6 below; the
+size up to 2048), 9 (q4_0, wider) or 12 (q8_0), 7 below; the
 row-chain kernels up to the layer's band threshold, the int8 matrix
 products above it) against the oracle's token-at-a-time prefill
 (src/model/transformer.rs:231-239).
