@@ -272,7 +272,7 @@ int hale_moe_reserve(hale_moe *moe, size_t max_tokens);
 
 /* Fewest tokens per hale_moe_forward* call that take the expert-grouped
  * path (default for top_k >= 4: 11 for q4_0 with hidden <= 2048, 9 for
- * wider q4_0, 12 for q8_0 with hidden <= 2048, 8 for wider q8_0; 6 for
+ * wider q4_0, 12 for q8_0 with hidden <= 2048, 8 for wider q8_0; 7 for
  * top_k < 4); fewer tokens run the decode
  * kernels in one pass over all of them.  Both give the reference's bits; the choice is speed only.
  * n in 2..HALE_DECODE_MAX_TOKENS + 1.  A new threshold re-lays the layer's
