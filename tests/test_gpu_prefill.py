@@ -127,11 +127,11 @@ def test_band_row_chains(ctx, dtype, Hd, I, E, k, T, with_router):
     moe.close()
 
 
-@pytest.mark.parametrize("T,bmax", [(16, None), (24, None), (48, None), (80, 1 << 20)])
+@pytest.mark.parametrize("T,bmax", [(16, None), (24, None), (48, None), (64, None), (80, 1 << 20)])
 def test_band_qwen30b_q4(ctx, T, bmax):
     """Qwen3-30B-A3B's layer shape (128 q4_0 experts, H 2048, I 768, top-8)
-    at 16, 24 (non-temporal weight loads) and 48 tokens (cached loads; the
-    default row-chain range is 11 to 76) and at 80 with the row chains
+    at 16, 24 (non-temporal weight loads), 48 and 64 tokens (cached loads;
+    the default row-chain range is 11 to 76) and at 80 with the row chains
     forced: every token against the oracle."""
     E, Hd, I, k = 128, 2048, 768, 8
     L = O.OracleMoe.synthetic(H.Q4_0, Hd, I, E, k, normalize_topk=True, seed=50 + T, with_router=True)
