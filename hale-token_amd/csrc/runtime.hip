@@ -1135,8 +1135,8 @@ static int moe_ws(hale_moe* m, size_t need, void** out) {
 // then reads each touched expert once; the decode path adds each token's k
 // experts' bytes.  Measured crossovers against the row-chain grouped
 // kernels (graph replay over layers visited in turn, one MI355X):
-// Qwen3-30B q4_0 (top-8 of 128) between 10 and 11 tokens (55.6 against
-// 56.8 us at 10, 62.2 against 59.9 at 11), Qwen3-235B q4_0 at 8 (125.8
+// Qwen3-30B q4_0 (top-8 of 128) between 10 and 11 tokens (49.3 against
+// 55.0 us at 10, 58.9 against 58.2 at 11), Qwen3-235B q4_0 at 8 (125.8
 // both; 153 against 136 at 10), Qwen3-30B q8_0 between 10 and 12 (73.4
 // against 75.7 at 10, 85.1 against 83.1 at 12), a Qwen3-235B-shaped q8_0
 // layer between 7 and 8 (175.6 against 177.4 us at 7, 196.3 against 188.8
